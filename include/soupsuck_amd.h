@@ -1,0 +1,211 @@
+/* soupsuck_amd: C ABI of the MI355X (gfx950) QLoRA NF4 hot path.
+ *
+ * Conventions
+ *   - Every entry point is extern "C", takes plain device pointers, element
+ *     counts and a HIP stream (passed as void*, a hipStream_t; NULL = the
+ *     default stream), enqueues work on that stream and returns immediately.
+ *   - Return value: 0 on success, a negative SS_ERR_* code otherwise.  Invalid
+ *     arguments are rejected BEFORE any launch; ss_last_error() then returns a
+ *     thread-local message.  No entry point throws, allocates device memory,
+ *     synchronizes the stream or keeps mutable global state.
+ *   - fp16 tensors are passed as uint16_t* (IEEE binary16 bits); "dtype" codes
+ *     are SS_F16 / SS_F32.
+ *   - Reference citations are file:line in the reference tree (Khasuetolog/
+ *     soupsuck); each entry point replaces the Triton launch or the library
+ *     call named there, behind the same Python-level interface.
+ */
+#ifndef SOUPSUCK_AMD_H
+#define SOUPSUCK_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SS_ABI_VERSION 1
+
+enum ss_status {
+  SS_OK = 0,
+  SS_ERR_INVALID_ARGUMENT = -1,
+  SS_ERR_LAUNCH = -2,
+  SS_ERR_UNSUPPORTED = -3
+};
+
+enum ss_dtype { SS_F16 = 0, SS_F32 = 1 };
+
+/* Library identity and the last error message of the calling thread. */
+int ss_abi_version(void);
+const char* ss_last_error(void);
+
+/* ---------------------------------------------------------------- NF4 ---
+ * Nested (double-quantized) NF4 state, bitsandbytes 0.50.2 layout
+ * (reference solution/kernels/nf4.py:140-168): packed uint8[ceil(n/2)] with
+ * element 2j in the HIGH nibble of byte j; qabs uint8[ceil(n/64)];
+ * absmax2 fp32[ceil(n/16384)]; code2 fp32[256]; offset fp32[1] (device).
+ */
+
+/* A2. out[i] = fp16(NF4[nib(i)] * fp32(fp32(code2[qabs[i/64]] * absmax2[i/16384]) + offset[0])),
+ * bit-exact, no FMA.  Replaces nf4_decode_kernel[NESTED=True] launched by
+ * dequantize_nf4 (solution/kernels/nf4.py:41-59,190-203).  Any n >= 0 and any
+ * pointer alignment (an aligned vector path is used when possible). */
+int ss_nf4_dequant_nested(const uint8_t* packed, const uint8_t* qabs, const float* absmax2,
+                          const float* code2, const float* offset, uint16_t* out, int64_t n,
+                          void* stream);
+
+/* A3. out[i] = fp16(NF4[nib(i)] * absmax[i/64]) with an already reconstructed
+ * fp32 absmax.  Replaces _dequantize_flat_into / nf4_decode_kernel[NESTED=False]
+ * (solution/kernels/nf4.py:181-187), the bnb backend _dequantize_4bit_impl
+ * entry (solution/nf4_patch.py:89-106). */
+int ss_nf4_dequant_flat(const uint8_t* packed, const float* absmax, uint16_t* out, int64_t n,
+                        void* stream);
+
+/* A7/A9 forward. y[t,n] = fp16(sum_k x[t,k] * Wdec[n,k] + bias[n]) with
+ * Wdec the A2-decoded weight [N,K] (row-major, element n*K+k), fp32
+ * accumulation, bias (fp16, may be NULL) added to the accumulator.
+ * Replaces bnb.matmul_4bit -> gemm_4bit / _dequant_linear_fallback
+ * (solution/nf4_patch.py:108-120) and nf4_tile_matmul_kernel[TRANSPOSE=False]
+ * (solution/kernels/nf4_gemm.py:35-96).  x is [T,K] row-major with row
+ * stride ldx >= K; y is [T,N] with row stride ldy >= N.
+ * workspace: device scratch of at least ss_nf4_gemm_workspace_size(t,n,k)
+ * bytes (may be NULL when that size is 0); used by the large-T path, which
+ * decodes W once into it. */
+int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                    const uint8_t* qabs, const float* absmax2, const float* code2,
+                    const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                    uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* A8/A9 backward.  dx[t,k] = fp16(sum_n dy[t,n] * Wdec[n,k]).  Replaces
+ * MatMul4Bit.backward's dequantize_4bit + torch.matmul(dY, W)
+ * (solution/nf4_patch.py:62-87; tasks/RUNTIME_AUDIT.md:113) and
+ * nf4_tile_matmul_kernel[TRANSPOSE=True] (solution/kernels/nf4_gemm.py:35-118).
+ * If accumulate != 0, dx is read and the result is fp16(dx_old + sum). */
+int ss_nf4_gemm_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                   const uint8_t* qabs, const float* absmax2, const float* code2,
+                   const float* offset, int64_t n, int64_t k, uint16_t* dx, int64_t lddx,
+                   int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+/* NF4 encoder (weight preparation, not on the training path).  Restates
+ * bitsandbytes 0.50.2 quantize_4bit(w, blocksize=64, compress_statistics=True,
+ * quant_type="nf4"), which the reference calls to build its states
+ * (solution/tests/test_nf4.py:40-44; Params4bit in solution/tests/test_unpad.py:
+ * 261-266).  w is fp16/fp32 [n]; code2 (input) is the 256-entry signed dynamic
+ * map; outputs packed, qabs, absmax2 and offset as in the state above;
+ * absmax_workspace is fp32[ceil(n/64)] scratch (it holds the first-level absmax). */
+int ss_nf4_quantize(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint8_t* qabs,
+                    float* absmax2, const float* code2, float* offset, float* absmax_workspace,
+                    void* stream);
+
+/* Workspace bytes the two NF4 GEMM entry points need for this shape. */
+size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k);
+
+/* ------------------------------------------------------- dense fp16 GEMM ---
+ * C[M,N] = alpha * op(A)[M,K] . op(B)[K,N] (+ bias[N]) (+ beta * C), fp16
+ * operands, fp32 accumulation.  a_trans = 0: A stored [M,K] (row stride lda);
+ * a_trans = 1: A stored [K,M].  b_trans = 0: B stored [K,N]; b_trans = 1: B
+ * stored [N,K].  c_dtype SS_F16 or SS_F32; beta must be 0 or 1 (1 reads C).
+ * bias (fp16, length N) may be NULL.  Serves the LoRA products
+ * (solution/lora.py:161, solution/lora_pair.py:34-65) and the vocabulary-chunk
+ * GEMMs of the fused cross-entropy (solution/kernels/cross_entropy.py:149,
+ * 195,202), which the reference sends to cuBLAS. */
+int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
+                const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
+                void* stream);
+
+/* ---------------------------------------------------------- LoRA (A11) ---
+ * out = round_out(fp32(base) + fp32(scaled)), scaled = round_adapter(adapter*s),
+ * rounded again to the base dtype when cast_to_result.  out_dtype is
+ * base_dtype if cast_to_result else promote(base_dtype, adapter_dtype).
+ * Replaces lora_scale_add_kernel (solution/kernels/lora_epilogue.py:24-34). */
+int ss_lora_epilogue_fwd(const void* base, int base_dtype, const void* adapter, int adapter_dtype,
+                         void* out, int out_dtype, int64_t count, float scale, int cast_to_result,
+                         void* stream);
+
+/* d_adapter = round_adapter(fp32(round_adapter(grad)) * s).  Replaces
+ * lora_scale_gradient_kernel (solution/kernels/lora_epilogue.py:37-43). */
+int ss_lora_epilogue_bwd(const void* grad, int grad_dtype, void* d_adapter, int adapter_dtype,
+                         int64_t count, float scale, void* stream);
+
+/* ------------------------------------------------- add + RMSNorm (A13/14) ---
+ * Row-wise over [rows, h] contiguous.  s = cast_s(r + d), rstd[row] =
+ * rsqrt(mean(s^2) + eps), y = cast_y(w * cast_s(s * rstd)); s_dtype must be
+ * promote(r_dtype, d_dtype); y_dtype is promote(s_dtype, w_dtype) or SS_F16.
+ * Replaces add_rmsnorm_forward_kernel (solution/kernels/add_rmsnorm.py:37-51). */
+int ss_add_rmsnorm_fwd(const void* r, int r_dtype, const void* d, int d_dtype, const void* w,
+                       int w_dtype, int64_t w_stride, void* s, int s_dtype, void* y, int y_dtype,
+                       float* rstd, int64_t rows, int64_t h, float eps, void* stream);
+
+/* ds = cast_s(rstd*(u - a*mean(u*a))) + gs, a = s*rstd, u = cast_s(gy*w);
+ * written to dr (dr_dtype) and/or dd (dd_dtype) (either may be NULL); gs or gy
+ * may be NULL (absent upstream).  Strides are in elements.  Replaces
+ * add_rmsnorm_backward_kernel (solution/kernels/add_rmsnorm.py:54-81). */
+int ss_add_rmsnorm_bwd(const void* s, int s_dtype, const void* w, int w_dtype, int64_t w_stride,
+                       const float* rstd, const void* gs, int gs_dtype, int64_t gs_row,
+                       int64_t gs_col, const void* gy, int gy_dtype, int64_t gy_row,
+                       int64_t gy_col, void* dr, int dr_dtype, void* dd, int dd_dtype,
+                       int64_t rows, int64_t h, void* stream);
+
+/* dgamma[c] = sum_rows gy * cast_s(s*rstd) (products rounded to fp16 when
+ * half_products), two-stage and non-atomic: partial fp32[ceil(rows/32), h]
+ * is caller-provided scratch.  Replaces rmsnorm_weight_partials_kernel /
+ * rmsnorm_weight_finalize_kernel (solution/kernels/rmsnorm.py:73-102). */
+int ss_rmsnorm_dgamma(const void* s, int s_dtype, const float* rstd, const void* gy, int gy_dtype,
+                      int64_t gy_row, int64_t gy_col, int half_products, float* partial,
+                      void* dw, int dw_dtype, int64_t rows, int64_t h, void* stream);
+
+/* ------------------------------------------------------------ unpad (A16) ---
+ * Row copies of row_bytes bytes (any even number), bit-exact.
+ * gather:  packed[t] = padded[indices[t]]        (solution/unpad.py:149-150);
+ *          an index outside [0, padded_rows) yields a zero row.
+ * scatter: padded[r] = 0 <= inverse[r] < tokens ? packed[inverse[r]] : 0
+ *                                                 (solution/unpad.py:153-161)
+ * inverse: inverse[r] = t where indices[t] == r, else -1 (int32[rows]);
+ *          out-of-range indices are ignored. */
+int ss_unpad_gather(const void* padded, int64_t padded_rows, void* packed,
+                    const int64_t* indices, int64_t tokens, int64_t row_bytes, void* stream);
+int ss_unpad_inverse(const int64_t* indices, int64_t tokens, int32_t* inverse, int64_t rows,
+                     void* stream);
+int ss_unpad_scatter(const void* packed, int64_t tokens, void* padded, const int32_t* inverse,
+                     int64_t rows, int64_t row_bytes, void* stream);
+
+/* ----------------------------------------------- fused linear CE (A17-19) ---
+ * Online vocabulary statistics over one chunk of fp16 logits z[n, width]
+ * (row stride ldz) whose first column is vocabulary index `start`; state is
+ * fp32[n,4] = (max, sum exp(z-max), sum exp(z-max)*z, target logit), best
+ * int64[n] is the first argmax.  first != 0 initialises the state.
+ * Replaces vocabulary_statistics_kernel (solution/kernels/cross_entropy.py:51-89). */
+int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* targets, float* state,
+                int64_t* best, int64_t n, int64_t width, int64_t start, int64_t ignore_index,
+                int first, void* stream);
+
+/* lse = max + log(sum), entropy = lse - t/sum, loss = lse - z_target (0 when
+ * ignored).  Replaces vocabulary_outputs_kernel (cross_entropy.py:92-105). */
+int ss_ce_outputs(const float* state, const int64_t* targets, float* loss, float* entropy,
+                  float* lse, int64_t n, int64_t ignore_index, void* stream);
+
+/* dz[r, c] = fp16((exp(z - lse[r]) - [start + c == target[r]]) * grad[r] / gain[r]),
+ * gain[r] = max(|grad[r]|, 1e-30) / 1024 (zero on ignored rows); when dz_global
+ * is not NULL it also receives the same derivative scaled by 1/global_gain
+ * instead of 1/gain[r] (for the lm_head gradient).  Replaces
+ * vocabulary_derivative_kernel (solution/kernels/cross_entropy.py:108-122). */
+int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* targets, const float* lse,
+                     const float* grad, uint16_t* dz, uint16_t* dz_global, float global_gain,
+                     int64_t n, int64_t width, int64_t start, int64_t ignore_index,
+                     void* stream);
+
+/* out[r, :] = cast(acc[inverse[r], :] * max(|grad[r]|, 1e-30) / 1024) when
+ * inverse[r] >= 0 (a valid row, compacted to position inverse[r]), else 0:
+ * the dX rescale and scatter of solution/kernels/cross_entropy.py:205-210.
+ * acc is fp32[valid_n, h]; grad fp32[n]; out_dtype SS_F16 or SS_F32. */
+int ss_ce_finalize_dx(const float* acc, int64_t valid_n, const float* grad,
+                      const int32_t* inverse, void* out, int out_dtype, int64_t n, int64_t h,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOUPSUCK_AMD_H */

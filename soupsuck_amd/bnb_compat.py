@@ -1,0 +1,222 @@
+"""bitsandbytes-compatible NF4 surface backed by the HIP library.
+
+bitsandbytes is not available for this ROCm build, so the drop-in keeps the
+call signatures and QuantState fields that the reference's patch surface and
+tests rely on (reference solution/kernels/nf4.py:140-168,
+solution/nf4_patch.py:62-125, solution/tests/test_nf4.py:40-44,136-137,
+solution/tests/test_lora.py:99-100, solution/tests/test_unpad.py:261-266):
+
+  functional.quantize_4bit(A, blocksize=64, compress_statistics=True, quant_type="nf4")
+      -> (packed uint8 [ceil(n/2), 1], QuantState)
+  functional.dequantize_4bit(A, quant_state=None, absmax=None, out=None, blocksize=None,
+                             quant_type="fp4")
+  matmul_4bit(A, B, quant_state, out=None, bias=None)      (B = packed.t())
+  nn.Params4bit(data, requires_grad=False, compress_statistics=True, quant_type="nf4")
+  nn.Linear4bit(in, out, bias=True, compute_dtype=torch.float16,
+                compress_statistics=True, quant_type="nf4")
+
+Only the format on the reference's hot path is implemented: NF4, blocksize
+64, double-quantized statistics (state2 blocksize 256, fp32), fp16 compute.
+Anything else raises NotImplementedError -- there is no CPU path.
+"""
+
+from types import SimpleNamespace
+
+import torch
+
+from . import _lib
+from .kernels.nf4 import _validate_state, dequantize_nf4
+from .kernels.nf4_gemm import NF4Linear
+
+
+def dynamic_map_signed():
+    """The 256-entry signed dynamic 8-bit code used for the second-level statistics.
+
+    bitsandbytes create_dynamic_map(signed=True, max_exponent_bits=7,
+    total_bits=8): for exponent i in 0..6, the 2**i midpoints of
+    linspace(0.1, 1, 2**i + 1) scaled by 10**(i - 6), with both signs, plus
+    0 and 1, sorted.  Format data; computed once per process.
+    """
+    global _DYNAMIC
+    if _DYNAMIC is None:
+        data = []
+        for i in range(7):
+            bounds = torch.linspace(0.1, 1.0, 2 ** i + 1, dtype=torch.float32)
+            means = (bounds[:-1] + bounds[1:]) / 2.0
+            scaled = (10.0 ** (i - 6)) * means
+            data += scaled.tolist() + (-scaled).tolist()
+        data += [0.0, 1.0]
+        _DYNAMIC = torch.tensor(sorted(data), dtype=torch.float32)
+    return _DYNAMIC
+
+
+_DYNAMIC = None
+
+
+class QuantState:
+    """NF4 quantization state with bitsandbytes' attribute names."""
+
+    def __init__(self, absmax, shape=None, code=None, blocksize=None, quant_type=None,
+                 dtype=None, offset=None, state2=None):
+        self.absmax, self.shape, self.code = absmax, shape, code
+        self.blocksize, self.quant_type, self.dtype = blocksize, quant_type, dtype
+        self.offset, self.state2 = offset, state2
+        self.nested = state2 is not None
+
+    def to(self, device):
+        device = torch.device(device)
+        self.absmax = self.absmax.to(device)
+        if self.offset is not None:
+            self.offset = self.offset.to(device)
+        if self.code is not None:
+            self.code = self.code.to(device)
+        if self.state2 is not None:
+            self.state2.absmax = self.state2.absmax.to(device)
+            self.state2.code = self.state2.code.to(device)
+        return self
+
+
+def quantize_4bit(A, absmax=None, out=None, blocksize=64, compress_statistics=True,
+                  quant_type="nf4", quant_storage=torch.uint8):
+    """Quantize a CUDA fp16/fp32 tensor to nested NF4 (ss_nf4_quantize)."""
+    if quant_type != "nf4" or blocksize != 64 or not compress_statistics \
+            or quant_storage != torch.uint8 or absmax is not None or out is not None:
+        raise NotImplementedError("only nested NF4 / blocksize 64 / uint8 storage is supported")
+    if not isinstance(A, torch.Tensor) or not A.is_cuda or A.dtype not in (torch.float16,
+                                                                            torch.float32):
+        raise ValueError("quantize_4bit expects a CUDA fp16/fp32 tensor")
+    device = A.device
+    flat = A.detach().contiguous().reshape(-1)
+    n = flat.numel()
+    if n == 0:
+        raise ValueError("cannot quantize an empty tensor")
+    blocks = -(-n // 64)
+    packed = torch.empty((-(-n // 2), 1), device=device, dtype=torch.uint8)
+    qabs = torch.empty(blocks, device=device, dtype=torch.uint8)
+    absmax2 = torch.empty(-(-blocks // 256), device=device, dtype=torch.float32)
+    code2 = dynamic_map_signed().to(device)
+    offset = torch.empty(1, device=device, dtype=torch.float32)
+    scratch = torch.empty(blocks, device=device, dtype=torch.float32)
+    with torch.cuda.device(device):
+        _lib.call("ss_nf4_quantize", flat.data_ptr(), _lib.dtype_code(flat.dtype), n,
+                  packed.data_ptr(), qabs.data_ptr(), absmax2.data_ptr(), code2.data_ptr(),
+                  offset.data_ptr(), scratch.data_ptr(), _lib.stream(device))
+    state2 = SimpleNamespace(absmax=absmax2, code=code2, blocksize=256, dtype=torch.float32,
+                             nested=False)
+    nf4_code = torch.tensor(_nf4_table(), dtype=torch.float32, device=device)
+    shape = tuple(A.shape) if A.ndim == 2 else (1, n)
+    state = QuantState(qabs, shape=shape, code=nf4_code, blocksize=64, quant_type="nf4",
+                       dtype=torch.float16, offset=offset, state2=state2)
+    return packed, state
+
+
+def _nf4_table():
+    from .kernels.nf4 import NF4_VALUES
+
+    return NF4_VALUES
+
+
+def dequantize_4bit(A, quant_state=None, absmax=None, out=None, blocksize=None, quant_type="fp4"):
+    """Decode a nested NF4 state (ss_nf4_dequant_nested); same view rule as bitsandbytes."""
+    if quant_state is None:
+        raise NotImplementedError("only dequantization from a QuantState is supported")
+    shape = _validate_state(A, quant_state, torch.float16)
+    if out is not None and (out.shape != shape or out.dtype != torch.float16
+                            or out.device != A.device or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous fp16 tensor of quant_state.shape")
+    return dequantize_nf4(A, quant_state, out=out)
+
+
+def matmul_4bit(A, B, quant_state, out=None, bias=None):
+    """A . dequant(B)^T (+bias) with autograd for A; B is the packed weight's .t() view."""
+    if out is not None:
+        raise NotImplementedError("out= is not supported")
+    packed = B.t() if B.ndim == 2 and B.shape[0] == 1 else B
+    return NF4Linear.apply(A, packed, quant_state, bias)
+
+
+class Params4bit(torch.nn.Parameter):
+    """Frozen NF4 weight: holds the fp16/fp32 data until moved to a GPU, then the packed bytes."""
+
+    def __new__(cls, data=None, requires_grad=False, quant_state=None, blocksize=64,
+                compress_statistics=True, quant_type="nf4", quant_storage=torch.uint8, **_):
+        if data is None:
+            data = torch.empty(0)
+        self = torch.Tensor._make_subclass(cls, data, requires_grad)
+        self.quant_state = quant_state
+        self.blocksize, self.compress_statistics = blocksize, compress_statistics
+        self.quant_type, self.quant_storage = quant_type, quant_storage
+        return self
+
+    def _quantize(self, device):
+        packed, state = quantize_4bit(self.data.to(device), blocksize=self.blocksize,
+                                      compress_statistics=self.compress_statistics,
+                                      quant_type=self.quant_type)
+        return Params4bit(packed, requires_grad=False, quant_state=state,
+                          blocksize=self.blocksize, compress_statistics=self.compress_statistics,
+                          quant_type=self.quant_type)
+
+    def cuda(self, device=None, non_blocking=False):
+        target = torch.device("cuda" if device is None else device)
+        if self.quant_state is None:
+            return self._quantize(target)
+        return self
+
+    def to(self, *args, **kwargs):
+        device = kwargs.get("device")
+        if device is None and args and isinstance(args[0], (str, torch.device)):
+            device = args[0]
+        if device is not None and torch.device(device).type == "cuda" and self.quant_state is None:
+            return self._quantize(torch.device(device))
+        return self
+
+
+class Linear4bit(torch.nn.Linear):
+    """bitsandbytes Linear4bit: NF4 frozen weight, fp16 compute, returns the input dtype."""
+
+    def __init__(self, input_features, output_features, bias=True, compute_dtype=None,
+                 compress_statistics=True, quant_type="nf4", quant_storage=torch.uint8,
+                 device=None):
+        super().__init__(input_features, output_features, bias, device)
+        self.weight = Params4bit(self.weight.data, requires_grad=False,
+                                 compress_statistics=compress_statistics, quant_type=quant_type,
+                                 quant_storage=quant_storage)
+        self.compute_dtype = compute_dtype
+        self.compute_type_is_set = compute_dtype is not None
+        self.quant_state = None
+        if self.bias is not None:
+            self.bias.requires_grad_(False)
+
+    def _apply(self, fn, recurse=True):
+        # Module.cuda()/.to()/.half() route through _apply.  The NF4 weight is
+        # handled here: quantized once when it first reaches a GPU, and never
+        # converted by fn afterwards (its bytes are the packed codes).
+        weight = self._parameters.pop("weight")
+        try:
+            result = super()._apply(fn, recurse)
+        finally:
+            self._parameters["weight"] = weight
+        probe = fn(torch.empty(0))
+        if probe.is_cuda:
+            if weight.quant_state is None:
+                self.weight = weight._quantize(probe.device)
+            elif weight.device != probe.device:
+                raise NotImplementedError("moving a quantized Linear4bit between GPUs")
+        return result
+
+    def forward(self, x):
+        state = getattr(self.weight, "quant_state", None)
+        if state is None:
+            raise RuntimeError("Linear4bit weight is not quantized; move the module to a GPU")
+        inp_dtype = x.dtype
+        compute = self.compute_dtype or torch.float16
+        if compute != torch.float16:
+            raise NotImplementedError("only fp16 compute is supported")
+        bias = None if self.bias is None else self.bias.to(torch.float16)
+        x16 = x.to(torch.float16).contiguous()
+        out = matmul_4bit(x16, self.weight.t(), state, bias=bias)
+        return out.to(inp_dtype)
+
+
+functional = SimpleNamespace(quantize_4bit=quantize_4bit, dequantize_4bit=dequantize_4bit)
+nn = SimpleNamespace(Params4bit=Params4bit, Linear4bit=Linear4bit)

@@ -1,0 +1,369 @@
+// Fused residual add + Qwen2 RMSNorm, forward / backward / dgamma (A13-A14).
+//
+// Reference: solution/kernels/add_rmsnorm.py:1-24,37-81 and
+// solution/kernels/rmsnorm.py:73-102.  Every cast follows the reference
+// order; the file is built without contraction (enable_fp_fusion=False in
+// the reference).
+//
+// Layout: one wave64 per row, four rows per 256-thread workgroup.  Lane l
+// owns the 8-element chunks starting at (c*64 + l)*8, so each wave-wide
+// access is 64 x 16 B contiguous for fp16 rows.  The row stays in registers
+// (NCH chunks per lane, H <= 512*NCH), so the forward reads r and d once and
+// writes s and y once: (2+2+2+2)*H + 4 bytes per fp16 row, the HBM floor.
+
+#include "elementwise.h"
+
+namespace ss {
+
+struct F8 {
+  float v[8];
+};
+
+// Load 8 consecutive logical elements starting at element offset `off`
+// (contiguous), `valid` of which exist.
+__device__ __forceinline__ F8 load8(const void* p, int dt, int64_t off, int valid, bool vec) {
+  F8 r;
+  if (vec && valid == 8) {
+    if (dt == SS_F16) {
+      union {
+        uint4 u;
+        half8 h;
+      } t;
+      t.u = *reinterpret_cast<const uint4*>(reinterpret_cast<const half_t*>(p) + off);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r.v[j] = (float)t.h[j];
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off);
+      const float4 b =
+          *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + off + 4);
+      r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+      r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.v[j] = j < valid ? ld_elem(p, dt, off + j) : 0.0f;
+  }
+  return r;
+}
+
+// Strided variant: element j at p[row_off + (col0 + j) * col_stride].
+__device__ __forceinline__ F8 load8s(const void* p, int dt, int64_t row_off, int64_t col0,
+                                     int64_t col_stride, int valid, bool vec) {
+  if (col_stride == 1) return load8(p, dt, row_off + col0, valid, vec);
+  F8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    r.v[j] = j < valid ? ld_elem(p, dt, row_off + (col0 + j) * col_stride) : 0.0f;
+  return r;
+}
+
+__device__ __forceinline__ void store8(void* p, int dt, int64_t off, int valid, const float* v,
+                                       bool vec) {
+  if (vec && valid == 8) {
+    if (dt == SS_F16) {
+      union {
+        uint4 u;
+        half8 h;
+      } t;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t.h[j] = (half_t)v[j];
+      *reinterpret_cast<uint4*>(reinterpret_cast<half_t*>(p) + off) = t.u;
+    } else {
+      float* q = reinterpret_cast<float*>(p) + off;
+      *reinterpret_cast<float4*>(q) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(q + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < valid) st_elem(p, dt, off + j, v[j]);
+  }
+}
+
+struct FwdArgs {
+  const void* r; int rd;
+  const void* d; int dd;
+  const void* w; int wd; int64_t w_stride;
+  void* s; int sd;
+  void* y; int yd;
+  float* rstd;
+  int64_t rows, h;
+  float eps;
+  int vec;
+};
+
+__device__ __forceinline__ int chunk_valid(int64_t h, int64_t col0) {
+  const int64_t left = h - col0;
+  return left <= 0 ? 0 : (left >= 8 ? 8 : (int)left);
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void add_rmsnorm_fwd_kernel(FwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t base = row * a.h;
+  float sv[NCH][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
+    const int valid = chunk_valid(a.h, col0);
+    if (valid > 0) {
+      const F8 r = load8(a.r, a.rd, base + col0, valid, a.vec);
+      const F8 d = load8(a.d, a.dd, base + col0, valid, a.vec);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float s = round_to(a.sd, r.v[j] + d.v[j]);
+        sv[c][j] = s;
+        const float sq = s * s;
+        ss += sq;
+      }
+      store8(a.s, a.sd, base + col0, valid, sv[c], a.vec);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[c][j] = 0.0f;
+    }
+  }
+  ss = wave_sum(ss);
+  const float mean = ss / (float)a.h;
+  const float rstd = rsqrtf(mean + a.eps);
+  if (lane == 0) a.rstd[row] = rstd;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
+    const int valid = chunk_valid(a.h, col0);
+    if (valid > 0) {
+      const F8 w = load8s(a.w, a.wd, 0, col0, a.w_stride, valid, a.vec);
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float q = round_to(a.sd, sv[c][j] * rstd);
+        y[j] = q * w.v[j];
+      }
+      store8(a.y, a.yd, base + col0, valid, y, a.vec);
+    }
+  }
+}
+
+struct BwdArgs {
+  const void* s; int sd;
+  const void* w; int wd; int64_t w_stride;
+  const float* rstd;
+  const void* gs; int gsd; int64_t gs_row, gs_col;
+  const void* gy; int gyd; int64_t gy_row, gy_col;
+  void* dr; int drd;
+  void* dd; int ddd;
+  int64_t rows, h;
+  int vec;
+  int vec_gs, vec_gy;
+};
+
+template <int NCH>
+__global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t base = row * a.h;
+  float ds[NCH][8];
+  if (a.gy) {
+    const float rstd = a.rstd[row];
+    float av[NCH][8];
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
+      const int valid = chunk_valid(a.h, col0);
+      if (valid > 0) {
+        const F8 s = load8(a.s, a.sd, base + col0, valid, a.vec);
+        const F8 g = load8s(a.gy, a.gyd, row * a.gy_row, col0, a.gy_col, valid, a.vec_gy);
+        const F8 w = load8s(a.w, a.wd, 0, col0, a.w_stride, valid, a.vec);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float av_ = s.v[j] * rstd;
+          const float u = round_to(a.sd, g.v[j] * w.v[j]);
+          av[c][j] = av_;
+          ds[c][j] = u;
+          const float ua = u * av_;
+          dot += ua;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          av[c][j] = 0.0f;
+          ds[c][j] = 0.0f;
+        }
+      }
+    }
+    dot = wave_sum(dot);
+    const float proj = dot / (float)a.h;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = av[c][j] * proj;
+        const float diff = ds[c][j] - t;
+        ds[c][j] = round_to(a.sd, rstd * diff);
+      }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ds[c][j] = 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
+    const int valid = chunk_valid(a.h, col0);
+    if (valid <= 0) continue;
+    float out[8];
+    F8 gs;
+    if (a.gs) gs = load8s(a.gs, a.gsd, row * a.gs_row, col0, a.gs_col, valid, a.vec_gs);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = ds[c][j];
+      if (a.gs) v += gs.v[j];
+      out[j] = round_to(a.sd, v);
+    }
+    if (a.dr) store8(a.dr, a.drd, base + col0, valid, out, a.vec);
+    if (a.dd) store8(a.dd, a.ddd, base + col0, valid, out, a.vec);
+  }
+}
+
+__global__ __launch_bounds__(256) void dgamma_partial_kernel(
+    const void* __restrict__ s, int sd, const float* __restrict__ rstd, const void* __restrict__ gy,
+    int gyd, int64_t gy_row, int64_t gy_col, int half_products, float* __restrict__ partial,
+    int64_t rows, int64_t h) {
+  const int64_t c = (int64_t)blockIdx.y * 256 + threadIdx.x;
+  if (c >= h) return;
+  const int64_t r0 = (int64_t)blockIdx.x * 32;
+  const int64_t r1 = r0 + 32 < rows ? r0 + 32 : rows;
+  float acc = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float q = round_to(sd, ld_elem(s, sd, r * h + c) * rstd[r]);
+    float prod = ld_elem(gy, gyd, r * gy_row + c * gy_col) * q;
+    if (half_products) prod = round_to(SS_F16, prod);
+    acc += prod;
+  }
+  partial[blockIdx.x * h + c] = acc;
+}
+
+__global__ __launch_bounds__(256) void dgamma_final_kernel(const float* __restrict__ partial,
+                                                           int64_t groups, int64_t h, void* dw,
+                                                           int dwd) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= h) return;
+  float acc = 0.0f;
+  for (int64_t g = 0; g < groups; ++g) acc += partial[g * h + c];
+  st_elem(dw, dwd, c, acc);
+}
+
+constexpr int kMaxChunks = 16;  // h <= 8192
+
+static bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace ss
+
+using namespace ss;
+
+#define SS_ROW_KERNEL_SWITCH(KERNEL, NCH, ARGS, GRID, STREAM)                                   \
+  switch (NCH) {                                                                                \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 3: hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 5: hipLaunchKernelGGL(KERNEL<5>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 6: hipLaunchKernelGGL(KERNEL<6>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 7: hipLaunchKernelGGL(KERNEL<7>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    case 8: hipLaunchKernelGGL(KERNEL<8>, GRID, dim3(256), 0, STREAM, ARGS); break;             \
+    default: hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(256), 0, STREAM, ARGS); break;           \
+  }
+
+extern "C" int ss_add_rmsnorm_fwd(const void* r, int r_dtype, const void* d, int d_dtype,
+                                  const void* w, int w_dtype, int64_t w_stride, void* s,
+                                  int s_dtype, void* y, int y_dtype, float* rstd, int64_t rows,
+                                  int64_t h, float eps, void* stream) {
+  const char* fn = "ss_add_rmsnorm_fwd";
+  SS_CHECK_ARG(rows >= 0 && h > 0, "%s: need rows >= 0 and h > 0", fn);
+  SS_CHECK_ARG(valid_dtype(r_dtype) && valid_dtype(d_dtype) && valid_dtype(w_dtype) &&
+                   valid_dtype(s_dtype) && valid_dtype(y_dtype),
+               "%s: dtype must be SS_F16 or SS_F32", fn);
+  SS_CHECK_ARG(s_dtype == promote(r_dtype, d_dtype), "%s: s dtype must be promote(r, d)", fn);
+  SS_CHECK_ARG(y_dtype == promote(s_dtype, w_dtype) || y_dtype == SS_F16,
+               "%s: y dtype must be promote(s, w) or fp16", fn);
+  SS_CHECK_ARG(eps >= 0.0f, "%s: eps must be >= 0", fn);
+  if (h > 512 * kMaxChunks) {
+    ss::set_error("%s: h=%lld exceeds the register-resident row limit %d", fn, (long long)h,
+                  512 * kMaxChunks);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return SS_OK;
+  SS_CHECK_ARG(r && d && w && s && y && rstd, "%s: null pointer", fn);
+  FwdArgs a{r, r_dtype, d, d_dtype, w, w_dtype, w_stride, s, s_dtype, y, y_dtype, rstd, rows,
+            h, eps, 0};
+  a.vec = (h % 8 == 0) && al16(r) && al16(d) && al16(s) && al16(y) && (w_stride != 1 || al16(w));
+  const int nch = (int)cdiv(h, 512);
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  hipStream_t st = (hipStream_t)stream;
+  SS_ROW_KERNEL_SWITCH(add_rmsnorm_fwd_kernel, nch, a, grid, st);
+  SS_CHECK_LAUNCH("add_rmsnorm_fwd_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_add_rmsnorm_bwd(const void* s, int s_dtype, const void* w, int w_dtype,
+                                  int64_t w_stride, const float* rstd, const void* gs,
+                                  int gs_dtype, int64_t gs_row, int64_t gs_col, const void* gy,
+                                  int gy_dtype, int64_t gy_row, int64_t gy_col, void* dr,
+                                  int dr_dtype, void* dd, int dd_dtype, int64_t rows, int64_t h,
+                                  void* stream) {
+  const char* fn = "ss_add_rmsnorm_bwd";
+  SS_CHECK_ARG(rows >= 0 && h > 0, "%s: need rows >= 0 and h > 0", fn);
+  SS_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(w_dtype), "%s: bad s/w dtype", fn);
+  SS_CHECK_ARG(!gs || valid_dtype(gs_dtype), "%s: bad gs dtype", fn);
+  SS_CHECK_ARG(!gy || valid_dtype(gy_dtype), "%s: bad gy dtype", fn);
+  SS_CHECK_ARG(!dr || valid_dtype(dr_dtype), "%s: bad dr dtype", fn);
+  SS_CHECK_ARG(!dd || valid_dtype(dd_dtype), "%s: bad dd dtype", fn);
+  if (h > 512 * kMaxChunks) {
+    ss::set_error("%s: h=%lld exceeds the register-resident row limit %d", fn, (long long)h,
+                  512 * kMaxChunks);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (rows == 0 || (!dr && !dd)) return SS_OK;
+  SS_CHECK_ARG(s && w && rstd, "%s: null pointer", fn);
+  BwdArgs a{s, s_dtype, w, w_dtype, w_stride, rstd, gs, gs_dtype, gs_row, gs_col, gy, gy_dtype,
+            gy_row, gy_col, dr, dr_dtype, dd, dd_dtype, rows, h, 0, 0, 0};
+  a.vec = (h % 8 == 0) && al16(s) && (!dr || al16(dr)) && (!dd || al16(dd)) &&
+          (w_stride != 1 || al16(w));
+  a.vec_gs = gs && gs_col == 1 && gs_row % 8 == 0 && al16(gs) && a.vec;
+  a.vec_gy = gy && gy_col == 1 && gy_row % 8 == 0 && al16(gy) && a.vec;
+  const int nch = (int)cdiv(h, 512);
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  hipStream_t st = (hipStream_t)stream;
+  SS_ROW_KERNEL_SWITCH(add_rmsnorm_bwd_kernel, nch, a, grid, st);
+  SS_CHECK_LAUNCH("add_rmsnorm_bwd_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_rmsnorm_dgamma(const void* s, int s_dtype, const float* rstd, const void* gy,
+                                 int gy_dtype, int64_t gy_row, int64_t gy_col, int half_products,
+                                 float* partial, void* dw, int dw_dtype, int64_t rows, int64_t h,
+                                 void* stream) {
+  const char* fn = "ss_rmsnorm_dgamma";
+  SS_CHECK_ARG(rows >= 0 && h > 0, "%s: need rows >= 0 and h > 0", fn);
+  SS_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(gy_dtype) && valid_dtype(dw_dtype),
+               "%s: dtype must be SS_F16 or SS_F32", fn);
+  SS_CHECK_ARG(dw, "%s: null dw", fn);
+  const int64_t groups = cdiv(rows, 32);
+  hipStream_t st = (hipStream_t)stream;
+  if (groups > 0) {
+    SS_CHECK_ARG(s && rstd && gy && partial, "%s: null pointer", fn);
+    hipLaunchKernelGGL(dgamma_partial_kernel, dim3((unsigned)groups, (unsigned)cdiv(h, 256)),
+                       dim3(256), 0, st, s, s_dtype, rstd, gy, gy_dtype, gy_row, gy_col,
+                       half_products, partial, rows, h);
+    SS_CHECK_LAUNCH("dgamma_partial_kernel");
+  }
+  hipLaunchKernelGGL(dgamma_final_kernel, dim3((unsigned)cdiv(h, 256)), dim3(256), 0, st,
+                     partial, groups, h, dw, dw_dtype);
+  SS_CHECK_LAUNCH("dgamma_final_kernel");
+  return SS_OK;
+}

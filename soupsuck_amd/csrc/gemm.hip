@@ -1,0 +1,548 @@
+// MFMA GEMM engine for the NF4 projections and the dense fp16 products.
+//
+// C[M,N] = alpha * A[M,K] . B[K,N] (+ bias) (+ beta * C), fp16 operands on
+// v_mfma_f32_16x16x32_f16 with fp32 accumulation.
+//
+// Operand sources (one loader per kind, chosen at compile time):
+//   OP_ROW      fp16, element (r,k) at ptr[r*ld + k]   (K contiguous)
+//   OP_COL      fp16, element (r,k) at ptr[k*ld + r]   (R contiguous; the
+//               tile is transposed on its way into LDS)
+//   OP_NF4_ROW  NF4 weight W[rows, cols] with r = W row, k = W col: the
+//               forward Y = X . W^T (reference solution/kernels/nf4_gemm.py:
+//               35-71, TRANSPOSE=False)
+//   OP_NF4_COL  NF4 weight with r = W col, k = W row: the backward
+//               dX = dY . W (nf4_gemm.py TRANSPOSE=True)
+// NF4 tiles are decoded in registers with exactly the standalone decoder's
+// arithmetic (fp32 scale, fp32 product, one RNE rounding; no contraction),
+// so the MFMA consumes the bit-exact dequantized weight.
+//
+// Tiling: a 256-thread workgroup (4 wave64) owns a BM x BN output tile; the
+// K loop walks BK=64 slices (exactly one NF4 block per weight row) through
+// two LDS stages.  Global loads for slice k+1 are issued before the MFMAs of
+// slice k and written to the other LDS stage afterwards: one barrier per
+// slice.  LDS rows are padded by 8 halves (16 B) so the 16 lanes that read one
+// MFMA fragment column (16 rows, same k) hit distinct bank groups.
+
+#include "common.h"
+
+namespace ss {
+
+enum Operand { OP_ROW = 0, OP_COL = 1, OP_NF4_ROW = 2, OP_NF4_COL = 3 };
+
+struct Nf4View {
+  const uint8_t* packed;
+  const uint8_t* qabs;
+  const float* absmax2;
+  const float* code2;
+  const float* offset;
+  int64_t cols;  // weight row length (elements); a multiple of 64
+};
+
+struct GemmParams {
+  int64_t M, N, K;
+  const half_t* A;
+  int64_t lda;
+  int a_vec;  // 16-byte vector loads are aligned for A
+  const half_t* B;
+  int64_t ldb;
+  int b_vec;
+  Nf4View w;
+  const half_t* bias;
+  void* C;
+  int64_t ldc;
+  float alpha;
+  int beta;
+};
+
+constexpr int kThreads = 256;
+constexpr int kPad = 8;
+
+union Vec16 {
+  uint4 u;
+  half8 h;
+  uint32_t w[4];
+};
+
+// ------------------------------------------------------------ loaders ----
+// Each loader moves one R x BK tile of its operand (R = BM for A, BN for B)
+// from global memory into registers (load) and from registers into an LDS
+// tile laid out as [R][BK + kPad] with k contiguous (store).
+
+template <int R, int BK, int OP>
+struct Loader;
+
+template <int R, int BK>
+struct Loader<R, BK, OP_ROW> {
+  static constexpr int kChunks = R * BK / 8 / kThreads;
+  static_assert(kChunks >= 1 && R * BK / 8 % kThreads == 0, "tile/thread mismatch");
+  Vec16 v[kChunks];
+  __device__ void load(const half_t* __restrict__ ptr, int64_t ld, int vec, int64_t r0,
+                       int64_t rmax, int64_t k0, int64_t kmax, const Nf4View&) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int row = c / (BK / 8);
+      const int kc = c % (BK / 8);
+      const int64_t gr = r0 + row;
+      const int64_t gk = k0 + kc * 8;
+      if (gr < rmax && vec && gk + 8 <= kmax) {
+        v[i].u = *reinterpret_cast<const uint4*>(ptr + gr * ld + gk);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[i].h[j] = (gr < rmax && gk + j < kmax) ? ptr[gr * ld + gk + j] : (half_t)0.0f;
+      }
+    }
+  }
+  __device__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int row = c / (BK / 8);
+      const int kc = c % (BK / 8);
+      *reinterpret_cast<uint4*>(lds + row * (BK + kPad) + kc * 8) = v[i].u;
+    }
+  }
+};
+
+template <int R, int BK>
+struct Loader<R, BK, OP_COL> {
+  static constexpr int kChunks = R * BK / 8 / kThreads;
+  static_assert(kChunks >= 1 && R * BK / 8 % kThreads == 0, "tile/thread mismatch");
+  Vec16 v[kChunks];
+  // Lanes walk k fastest so that the transposed 2-byte LDS writes of one
+  // instruction land on consecutive addresses (no bank conflicts).
+  __device__ void load(const half_t* __restrict__ ptr, int64_t ld, int vec, int64_t r0,
+                       int64_t rmax, int64_t k0, int64_t kmax, const Nf4View&) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int k = c % BK;
+      const int rc = c / BK;
+      const int64_t gk = k0 + k;
+      const int64_t gr = r0 + rc * 8;
+      if (gk < kmax && vec && gr + 8 <= rmax) {
+        v[i].u = *reinterpret_cast<const uint4*>(ptr + gk * ld + gr);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[i].h[j] = (gk < kmax && gr + j < rmax) ? ptr[gk * ld + gr + j] : (half_t)0.0f;
+      }
+    }
+  }
+  __device__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + kThreads * i;
+      const int k = c % BK;
+      const int rc = c / BK;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lds[(rc * 8 + j) * (BK + kPad) + k] = v[i].h[j];
+    }
+  }
+};
+
+// Decode ELEMS consecutive NF4 codes (ELEMS/2 packed bytes in `words`,
+// element order = byte order, high nibble first) with one fp32 scale.
+template <int ELEMS>
+__device__ __forceinline__ void decode_run(const uint32_t* words, float scale,
+                                           const float* __restrict__ lut, half_t* out) {
+#pragma unroll
+  for (int wi = 0; wi < ELEMS / 8; ++wi) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
+      out[8 * wi + 2 * b] = (half_t)(lut[byte >> 4] * scale);
+      out[8 * wi + 2 * b + 1] = (half_t)(lut[byte & 15u] * scale);
+    }
+  }
+}
+
+struct Nf4Stage {
+  bool valid;
+  uint32_t q;
+  float a2;
+};
+
+// Forward weight tile: r = weight row, k = weight column.  Each thread owns
+// ELEMS consecutive k of one row; BK = 64 means one NF4 block per row.
+template <int R, int BK>
+struct Loader<R, BK, OP_NF4_ROW> {
+  static constexpr int ELEMS = R * BK / kThreads;
+  static_assert(ELEMS == 16 || ELEMS == 32, "NF4 row loader expects 16 or 32 codes per thread");
+  static_assert(64 % ELEMS == 0 && BK % ELEMS == 0, "a thread's run must stay in one block");
+  static constexpr int kParts = BK / ELEMS;
+  uint32_t words[ELEMS / 8];
+  Nf4Stage st;
+  __device__ void load(const half_t*, int64_t, int, int64_t r0, int64_t rmax, int64_t k0,
+                       int64_t kmax, const Nf4View& w) {
+    const int row = threadIdx.x / kParts;
+    const int part = threadIdx.x % kParts;
+    const int64_t gr = r0 + row;
+    const int64_t gk = k0 + part * ELEMS;
+    st.valid = gr < rmax && gk < kmax;
+    if (st.valid) {
+      const int64_t e = gr * w.cols + gk;
+      const uint8_t* src = w.packed + (e >> 1);
+      if constexpr (ELEMS == 32) {
+        uint4 t = *reinterpret_cast<const uint4*>(src);
+        words[0] = t.x; words[1] = t.y; words[2] = t.z; words[3] = t.w;
+      } else {
+        uint2 t = *reinterpret_cast<const uint2*>(src);
+        words[0] = t.x; words[1] = t.y;
+      }
+      const int64_t block = e >> 6;
+      st.q = w.qabs[block];
+      st.a2 = w.absmax2[block >> 8];
+    }
+  }
+  __device__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
+                        const float* __restrict__ lut, float offset) {
+    const int row = threadIdx.x / kParts;
+    const int part = threadIdx.x % kParts;
+    Vec16 out[ELEMS / 8];
+    if (st.valid) {
+      const float product = code2[st.q] * st.a2;
+      const float scale = product + offset;
+      decode_run<ELEMS>(words, scale, lut, reinterpret_cast<half_t*>(out));
+    } else {
+#pragma unroll
+      for (int i = 0; i < ELEMS / 8; ++i) out[i].u = make_uint4(0, 0, 0, 0);
+    }
+    half_t* dst = lds + row * (BK + kPad) + part * ELEMS;
+#pragma unroll
+    for (int i = 0; i < ELEMS / 8; ++i) *reinterpret_cast<uint4*>(dst + 8 * i) = out[i].u;
+  }
+};
+
+// Backward weight tile: r = weight column, k = weight row.  Each thread owns
+// ELEMS consecutive weight columns of one weight row (one NF4 block run) and
+// writes them transposed, so LDS again holds [r][k] with k contiguous.
+template <int R, int BK>
+struct Loader<R, BK, OP_NF4_COL> {
+  static constexpr int ELEMS = R * BK / kThreads;
+  static_assert(ELEMS == 16 || ELEMS == 32, "NF4 column loader expects 16 or 32 codes per thread");
+  static_assert(kThreads % BK == 0 && R / ELEMS == kThreads / BK, "tile/thread mismatch");
+  uint32_t words[ELEMS / 8];
+  Nf4Stage st;
+  __device__ void load(const half_t*, int64_t, int, int64_t r0, int64_t rmax, int64_t k0,
+                       int64_t kmax, const Nf4View& w) {
+    const int krow = threadIdx.x % BK;
+    const int cg = threadIdx.x / BK;
+    const int64_t gk = k0 + krow;
+    const int64_t gr = r0 + cg * ELEMS;
+    st.valid = gk < kmax && gr < rmax;
+    if (st.valid) {
+      const int64_t e = gk * w.cols + gr;
+      const uint8_t* src = w.packed + (e >> 1);
+      if constexpr (ELEMS == 32) {
+        uint4 t = *reinterpret_cast<const uint4*>(src);
+        words[0] = t.x; words[1] = t.y; words[2] = t.z; words[3] = t.w;
+      } else {
+        uint2 t = *reinterpret_cast<const uint2*>(src);
+        words[0] = t.x; words[1] = t.y;
+      }
+      const int64_t block = e >> 6;
+      st.q = w.qabs[block];
+      st.a2 = w.absmax2[block >> 8];
+    }
+  }
+  __device__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
+                        const float* __restrict__ lut, float offset) {
+    const int krow = threadIdx.x % BK;
+    const int cg = threadIdx.x / BK;
+    half_t vals[ELEMS];
+    if (st.valid) {
+      const float product = code2[st.q] * st.a2;
+      const float scale = product + offset;
+      decode_run<ELEMS>(words, scale, lut, vals);
+    } else {
+#pragma unroll
+      for (int j = 0; j < ELEMS; ++j) vals[j] = (half_t)0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < ELEMS; ++j) lds[(cg * ELEMS + j) * (BK + kPad) + krow] = vals[j];
+  }
+};
+
+// ------------------------------------------------------------- kernel ----
+
+template <int BM, int BN, int BK, int WM, int WN>
+struct Tile {
+  static constexpr int kBM = BM, kBN = BN, kBK = BK, kWM = WM, kWN = WN;
+  static constexpr int kWavesN = BN / WN;
+  static constexpr int kWavesM = BM / WM;
+  static_assert(kWavesN * kWavesM == kThreads / kWave, "4 waves per workgroup");
+  static_assert(WM % 16 == 0 && WN % 16 == 0 && BK % 32 == 0, "MFMA 16x16x32 tiling");
+  static constexpr int kLdk = BK + kPad;
+};
+
+template <int CT>
+__device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta) {
+  if constexpr (CT == SS_F16) {
+    half_t* c = reinterpret_cast<half_t*>(C);
+    if (beta) v += (float)c[idx];
+    c[idx] = (half_t)v;
+  } else {
+    float* c = reinterpret_cast<float*>(C);
+    if (beta) v += c[idx];
+    c[idx] = v;
+  }
+}
+
+template <class T, int OPA, int OPB, int CT>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+  constexpr int BM = T::kBM, BN = T::kBN, BK = T::kBK, WM = T::kWM, WN = T::kWN;
+  constexpr int LDK = T::kLdk;
+  constexpr bool kNf4 = OPA >= OP_NF4_ROW || OPB >= OP_NF4_ROW;
+  __shared__ __attribute__((aligned(16))) half_t sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) half_t sB[2][BN * LDK];
+  __shared__ float s_code2[kNf4 ? 256 : 1];
+  __shared__ float s_lut[16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm = wave / T::kWavesN;
+  const int wn = wave % T::kWavesN;
+  const int64_t n0 = (int64_t)blockIdx.x * BN;
+  const int64_t m0 = (int64_t)blockIdx.y * BM;
+
+  float offset = 0.0f;
+  if constexpr (kNf4) {
+    s_code2[tid] = p.w.code2[tid];
+    if (tid < 16) s_lut[tid] = kNF4[tid];
+    offset = p.w.offset[0];
+  }
+
+  Loader<BM, BK, OPA> la;
+  Loader<BN, BK, OPB> lb;
+  const int64_t ktiles = cdiv(p.K, BK);
+
+  la.load(p.A, p.lda, p.a_vec, m0, p.M, 0, p.K, p.w);
+  lb.load(p.B, p.ldb, p.b_vec, n0, p.N, 0, p.K, p.w);
+  __syncthreads();  // code tables visible before the first decode
+  la.store(sA[0], s_code2, s_lut, offset);
+  lb.store(sB[0], s_code2, s_lut, offset);
+  __syncthreads();
+
+  float4v acc[WM / 16][WN / 16];
+#pragma unroll
+  for (int i = 0; i < WM / 16; ++i)
+#pragma unroll
+    for (int j = 0; j < WN / 16; ++j) acc[i][j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  const int frag_row = lane & 15;
+  const int frag_k = (lane >> 4) * 8;
+
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      const int64_t k0 = (kt + 1) * BK;
+      la.load(p.A, p.lda, p.a_vec, m0, p.M, k0, p.K, p.w);
+      lb.load(p.B, p.ldb, p.b_vec, n0, p.N, k0, p.K, p.w);
+    }
+    const half_t* a_tile = sA[cur] + (wm * WM + frag_row) * LDK + frag_k;
+    const half_t* b_tile = sB[cur] + (wn * WN + frag_row) * LDK + frag_k;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      half8 af[WM / 16];
+      half8 bf[WN / 16];
+#pragma unroll
+      for (int i = 0; i < WM / 16; ++i)
+        af[i] = *reinterpret_cast<const half8*>(a_tile + i * 16 * LDK + ks * 32);
+#pragma unroll
+      for (int j = 0; j < WN / 16; ++j)
+        bf[j] = *reinterpret_cast<const half8*>(b_tile + j * 16 * LDK + ks * 32);
+#pragma unroll
+      for (int i = 0; i < WM / 16; ++i)
+#pragma unroll
+        for (int j = 0; j < WN / 16; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      la.store(sA[cur ^ 1], s_code2, s_lut, offset);
+      lb.store(sB[cur ^ 1], s_code2, s_lut, offset);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds D[4*(lane/16) + r][lane%16] of each 16x16 tile.
+  const int crow = (lane >> 4) * 4;
+  const int ccol = lane & 15;
+#pragma unroll
+  for (int i = 0; i < WM / 16; ++i) {
+#pragma unroll
+    for (int j = 0; j < WN / 16; ++j) {
+      const int64_t col = n0 + wn * WN + j * 16 + ccol;
+      if (col >= p.N) continue;
+      const float b = p.bias ? (float)p.bias[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm * WM + i * 16 + crow + r;
+        if (row < p.M) {
+          const float v = acc[i][j][r] * p.alpha + b;
+          store_c<CT>(p.C, row * p.ldc + col, v, p.beta);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- launch ----
+
+using TileBig = Tile<128, 128, 64, 64, 64>;
+using TileSmall = Tile<64, 64, 64, 32, 32>;
+
+template <class T, int OPA, int OPB, int CT>
+static int launch(const GemmParams& p, hipStream_t stream, const char* name) {
+  dim3 grid((unsigned)cdiv(p.N, T::kBN), (unsigned)cdiv(p.M, T::kBM));
+  hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT>), grid, dim3(kThreads), 0, stream, p);
+  SS_CHECK_LAUNCH(name);
+  return SS_OK;
+}
+
+// Pick the tile: the 128x128 tile when it still yields enough workgroups to
+// cover the 256 CUs, the 64x64 tile otherwise.
+static bool use_small_tile(int64_t m, int64_t n) {
+  return cdiv(m, 128) * cdiv(n, 128) < 256;
+}
+
+template <int OPA, int OPB, int CT>
+static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
+  if (use_small_tile(p.M, p.N)) return launch<TileSmall, OPA, OPB, CT>(p, stream, name);
+  return launch<TileBig, OPA, OPB, CT>(p, stream, name);
+}
+
+static bool aligned16(const void* ptr, int64_t ld) {
+  return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && ld % 8 == 0;
+}
+
+static int nf4_decode_first_fwd(const GemmParams& base, void* workspace, hipStream_t stream);
+
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
+  // Large T: decoding W once into fp16 and running the dense GEMM costs one
+  // extra pass over W (2.5 B/weight) but removes ceil(T/BM) redundant decodes.
+  if (t >= 4096 && n > 0 && k > 0) return (size_t)n * (size_t)k * sizeof(uint16_t);
+  return 0;
+}
+
+static int check_nf4(const char* fn, const uint8_t* packed, const uint8_t* qabs,
+                     const float* absmax2, const float* code2, const float* offset, int64_t n,
+                     int64_t k) {
+  SS_CHECK_ARG(packed && qabs && absmax2 && code2 && offset, "%s: null NF4 state pointer", fn);
+  SS_CHECK_ARG(n > 0 && k > 0, "%s: weight shape [%lld,%lld] must be positive", fn,
+               (long long)n, (long long)k);
+  if (k % 64 != 0) {
+    ss::set_error("%s: fused NF4 GEMM needs K %% 64 == 0 (got K=%lld)", fn, (long long)k);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (reinterpret_cast<uintptr_t>(packed) % 16 != 0) {
+    ss::set_error("%s: packed NF4 storage must be 16-byte aligned", fn);
+    return SS_ERR_UNSUPPORTED;
+  }
+  return SS_OK;
+}
+
+extern "C" int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                               const uint8_t* qabs, const float* absmax2, const float* code2,
+                               const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                               uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  const char* fn = "ss_nf4_gemm_fwd";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(x && y, "%s: null activation/output pointer", fn);
+  SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
+  GemmParams p{};
+  p.M = t; p.N = n; p.K = k;
+  p.A = reinterpret_cast<const half_t*>(x); p.lda = ldx; p.a_vec = aligned16(x, ldx);
+  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
+  p.bias = reinterpret_cast<const half_t*>(bias);
+  p.C = y; p.ldc = ldy; p.alpha = 1.0f; p.beta = 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
+    return nf4_decode_first_fwd(p, workspace, s);
+  }
+  return dispatch<OP_ROW, OP_NF4_ROW, SS_F16>(p, s, "gemm_kernel<nf4 fwd>");
+}
+
+extern "C" int ss_nf4_gemm_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                              const uint8_t* qabs, const float* absmax2, const float* code2,
+                              const float* offset, int64_t n, int64_t k, uint16_t* dx,
+                              int64_t lddx, int accumulate, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const char* fn = "ss_nf4_gemm_dx";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(dy && dx, "%s: null gradient pointer", fn);
+  SS_CHECK_ARG(lddy >= n && lddx >= k, "%s: leading dimensions too small", fn);
+  GemmParams p{};
+  p.M = t; p.N = k; p.K = n;
+  p.A = reinterpret_cast<const half_t*>(dy); p.lda = lddy; p.a_vec = aligned16(dy, lddy);
+  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
+  p.C = dx; p.ldc = lddx; p.alpha = 1.0f; p.beta = accumulate ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
+    int r = ss_nf4_dequant_nested(packed, qabs, absmax2, code2, offset,
+                                  reinterpret_cast<uint16_t*>(workspace), n * k, stream);
+    if (r) return r;
+    p.B = reinterpret_cast<const half_t*>(workspace); p.ldb = k; p.b_vec = 1;
+    return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>");
+  }
+  return dispatch<OP_ROW, OP_NF4_COL, SS_F16>(p, s, "gemm_kernel<nf4 dx>");
+}
+
+namespace ss {
+static int nf4_decode_first_fwd(const GemmParams& base, void* workspace, hipStream_t stream) {
+  const Nf4View& w = base.w;
+  int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                reinterpret_cast<uint16_t*>(workspace), base.N * base.K, stream);
+  if (r) return r;
+  GemmParams p = base;
+  p.B = reinterpret_cast<const half_t*>(workspace); p.ldb = base.K; p.b_vec = 1;
+  return dispatch<OP_ROW, OP_ROW, SS_F16>(p, stream, "gemm_kernel<f16 nt>");
+}
+}  // namespace ss
+
+extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
+                           const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                           const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
+                           void* stream) {
+  const char* fn = "ss_gemm_f16";
+  SS_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "%s: negative size", fn);
+  SS_CHECK_ARG(c_dtype == SS_F16 || c_dtype == SS_F32, "%s: c_dtype must be SS_F16/SS_F32", fn);
+  SS_CHECK_ARG(beta == 0.0f || beta == 1.0f, "%s: beta must be 0 or 1", fn);
+  if (m == 0 || n == 0) return SS_OK;
+  SS_CHECK_ARG(c && (k == 0 || (a && b)), "%s: null pointer", fn);
+  SS_CHECK_ARG(lda >= (a_trans ? m : k) && ldb >= (b_trans ? k : n) && ldc >= n,
+               "%s: leading dimensions too small", fn);
+  GemmParams p{};
+  p.M = m; p.N = n; p.K = k;
+  p.A = reinterpret_cast<const half_t*>(a); p.lda = lda; p.a_vec = aligned16(a, lda);
+  p.B = reinterpret_cast<const half_t*>(b); p.ldb = ldb; p.b_vec = aligned16(b, ldb);
+  p.bias = reinterpret_cast<const half_t*>(bias);
+  p.C = c; p.ldc = ldc; p.alpha = alpha; p.beta = beta != 0.0f;
+  hipStream_t s = (hipStream_t)stream;
+  // b_trans = 1: B stored [N,K] -> OP_ROW; b_trans = 0: B stored [K,N] -> OP_COL.
+  const int code = (a_trans ? 2 : 0) + (b_trans ? 0 : 1) + (c_dtype == SS_F32 ? 4 : 0);
+  switch (code) {
+    case 0: return dispatch<OP_ROW, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 nt>");
+    case 1: return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>");
+    case 2: return dispatch<OP_COL, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 tt>");
+    case 3: return dispatch<OP_COL, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 tn>");
+    case 4: return dispatch<OP_ROW, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 nt>");
+    case 5: return dispatch<OP_ROW, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 nn>");
+    case 6: return dispatch<OP_COL, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 tt>");
+    default: return dispatch<OP_COL, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 tn>");
+  }
+}

@@ -1,0 +1,127 @@
+// Standalone NF4 decode (nested A2 and flat A3), bit-exact.
+//
+// Reference: solution/kernels/nf4.py:41-59 (nf4_decode_kernel), formula at
+// :7-10.  HBM-bound: 0.5 B read + 2 B written per element (+1/64 B qabs).
+//
+// Vector path: each lane decodes 8 consecutive elements per step -- one
+// packed dword (4 bytes) in, one 16-byte fp16 store out -- so a wave moves
+// 256 B of nibbles and writes 1 KiB contiguous per step.  The 16-entry NF4
+// table sits in LDS; 16 floats occupy 16 distinct banks, so any per-lane
+// lookup pattern is conflict-free.  8 consecutive elements always share one
+// 64-block (8 divides 64), so each step needs a single scale.
+// Generic path: one element per lane, any alignment / tail.
+
+#include "common.h"
+
+namespace ss {
+
+template <bool NESTED>
+__device__ __forceinline__ float block_scale(const uint8_t* __restrict__ qabs,
+                                             const float* __restrict__ absmax,
+                                             const float* __restrict__ absmax2,
+                                             const float* __restrict__ code2, float offset,
+                                             int64_t block) {
+  if constexpr (NESTED) {
+    return nested_scale(qabs, absmax2, code2, offset, block);
+  } else {
+    return absmax[block];
+  }
+}
+
+template <bool NESTED>
+__global__ __launch_bounds__(256) void nf4_dequant_vec_kernel(
+    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
+    const float* __restrict__ absmax, const float* __restrict__ absmax2,
+    const float* __restrict__ code2, const float* __restrict__ offset_ptr,
+    half8* __restrict__ out, int64_t groups) {
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
+  __syncthreads();
+  const float offset = NESTED ? offset_ptr[0] : 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups; g += stride) {
+    const uint32_t word = __builtin_nontemporal_load(packed + g);
+    const float scale = block_scale<NESTED>(qabs, absmax, absmax2, code2, offset, g >> 3);
+    half8 v;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (word >> (8 * b)) & 0xffu;
+      v[2 * b] = (half_t)(lut[byte >> 4] * scale);
+      v[2 * b + 1] = (half_t)(lut[byte & 15u] * scale);
+    }
+    out[g] = v;
+  }
+}
+
+template <bool NESTED>
+__global__ __launch_bounds__(256) void nf4_dequant_scalar_kernel(
+    const uint8_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
+    const float* __restrict__ absmax, const float* __restrict__ absmax2,
+    const float* __restrict__ code2, const float* __restrict__ offset_ptr,
+    half_t* __restrict__ out, int64_t begin, int64_t n) {
+  const float offset = NESTED ? offset_ptr[0] : 0.0f;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = begin + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t byte = packed[i >> 1];
+    const uint32_t nib = (i & 1) ? (byte & 15u) : (byte >> 4);
+    const float scale = block_scale<NESTED>(qabs, absmax, absmax2, code2, offset, i >> 6);
+    out[i] = (half_t)(kNF4[nib] * scale);
+  }
+}
+
+static int grid_for(int64_t work, int threads) {
+  // Enough waves to cover every CU several times; the loops are grid-stride.
+  int64_t blocks = cdiv(work, threads);
+  const int64_t cap = 256 * 32;
+  return (int)(blocks < cap ? (blocks > 0 ? blocks : 1) : cap);
+}
+
+template <bool NESTED>
+static int launch_dequant(const uint8_t* packed, const uint8_t* qabs, const float* absmax,
+                          const float* absmax2, const float* code2, const float* offset,
+                          uint16_t* out, int64_t n, hipStream_t stream) {
+  if (n == 0) return SS_OK;
+  half_t* o = reinterpret_cast<half_t*>(out);
+  const bool aligned = (reinterpret_cast<uintptr_t>(packed) % 4 == 0) &&
+                       (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  int64_t done = 0;
+  if (aligned) {
+    const int64_t groups = n / 8;
+    if (groups > 0) {
+      hipLaunchKernelGGL(nf4_dequant_vec_kernel<NESTED>, dim3(grid_for(groups, 256)), dim3(256), 0,
+                         stream, reinterpret_cast<const uint32_t*>(packed), qabs, absmax, absmax2,
+                         code2, offset, reinterpret_cast<half8*>(o), groups);
+      SS_CHECK_LAUNCH("nf4_dequant_vec_kernel");
+    }
+    done = groups * 8;
+  }
+  if (done < n) {
+    hipLaunchKernelGGL(nf4_dequant_scalar_kernel<NESTED>, dim3(grid_for(n - done, 256)), dim3(256),
+                       0, stream, packed, qabs, absmax, absmax2, code2, offset, o, done, n);
+    SS_CHECK_LAUNCH("nf4_dequant_scalar_kernel");
+  }
+  return SS_OK;
+}
+
+}  // namespace ss
+
+extern "C" int ss_nf4_dequant_nested(const uint8_t* packed, const uint8_t* qabs,
+                                     const float* absmax2, const float* code2,
+                                     const float* offset, uint16_t* out, int64_t n,
+                                     void* stream) {
+  SS_CHECK_ARG(n >= 0, "ss_nf4_dequant_nested: n=%lld must be >= 0", (long long)n);
+  if (n == 0) return SS_OK;
+  SS_CHECK_ARG(packed && qabs && absmax2 && code2 && offset && out,
+               "ss_nf4_dequant_nested: null pointer");
+  return ss::launch_dequant<true>(packed, qabs, nullptr, absmax2, code2, offset, out, n,
+                                  (hipStream_t)stream);
+}
+
+extern "C" int ss_nf4_dequant_flat(const uint8_t* packed, const float* absmax, uint16_t* out,
+                                   int64_t n, void* stream) {
+  SS_CHECK_ARG(n >= 0, "ss_nf4_dequant_flat: n=%lld must be >= 0", (long long)n);
+  if (n == 0) return SS_OK;
+  SS_CHECK_ARG(packed && absmax && out, "ss_nf4_dequant_flat: null pointer");
+  return ss::launch_dequant<false>(packed, nullptr, absmax, nullptr, nullptr, nullptr, out, n,
+                                   (hipStream_t)stream);
+}

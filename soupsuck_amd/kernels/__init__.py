@@ -1,0 +1,10 @@
+"""Host-side entry points of the HIP kernels (same names as the reference's solution/kernels)."""
+
+from .add_rmsnorm import add_rms_norm
+from .cross_entropy import fused_linear_cross_entropy
+from .lora_epilogue import lora_epilogue
+from .nf4 import dequantize_nf4
+from .nf4_gemm import gemm_f16, nf4_matmul
+
+__all__ = ["add_rms_norm", "fused_linear_cross_entropy", "lora_epilogue", "dequantize_nf4",
+           "gemm_f16", "nf4_matmul"]

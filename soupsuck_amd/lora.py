@@ -1,0 +1,103 @@
+"""QLoRA projection: frozen NF4 base GEMM + LoRA branch in one autograd node (A10-A12).
+
+Forward (reference solution/lora.py:135-163 under CUDA fp16 autocast,
+solution/kernels/lora_epilogue.py:24-34):
+    result = fp16(X . Wdec^T + bias)                    ss_nf4_gemm_fwd
+    Z      = fp16(drop(X) . A^T)                        ss_gemm_f16
+    L      = fp16(Z . B^T)                              ss_gemm_f16
+    out    = fp16(result + fp16(L * s))                 ss_lora_epilogue_fwd
+Backward (reference solution/lora_pair.py:34-65 order, fp16 after each GEMM):
+    dL = fp16(fp16(g) * s)                              ss_lora_epilogue_bwd
+    dZ = fp16(dL . B),  dB = fp16(dL^T . Z),  dA = fp16(dZ^T . drop(X))
+    dX = fp16(g . Wdec + mask * (dZ . A))               ss_nf4_gemm_dx, ss_gemm_f16
+The frozen base contributes no weight gradient.  Dropout (p > 0) uses torch's
+native dropout on an fp32 copy of X, as the reference keeps PEFT's own
+Dropout module and RNG (solution/lora.py:1-40); p = 0 skips it.
+"""
+
+import math
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _lib
+from .kernels.nf4 import _validate_state
+from .kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d
+
+
+class _QLoRAProjection(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling, dropout_p, training):
+        n, k = state.shape
+        t = x.numel() // k
+        x2d = x.reshape(t, k)
+        stream = _lib.stream(x.device)
+        result = nf4_forward_2d(x2d, packed, state, n, k, bias=bias)
+        mask = None
+        if dropout_p > 0.0 and training:
+            dropped = torch.nn.functional.dropout(x2d.float(), dropout_p, True)
+            mask = dropped != 0
+            x_in = dropped.to(torch.float16)
+        else:
+            x_in = x2d
+        a16 = lora_a.to(torch.float16).contiguous()
+        b16 = lora_b.to(torch.float16).contiguous()
+        z = gemm_f16(x_in, a16, b_trans=True)
+        lora = gemm_f16(z, b16, b_trans=True)
+        out = torch.empty_like(result)
+        if t:
+            _lib.call("ss_lora_epilogue_fwd", result.data_ptr(), _lib.F16, lora.data_ptr(),
+                      _lib.F16, out.data_ptr(), _lib.F16, result.numel(), float(scaling), 0,
+                      stream)
+        ctx.save_for_backward(x_in, z, a16, b16, packed, mask)
+        ctx.state, ctx.scaling, ctx.dropout_p = state, float(scaling), dropout_p
+        ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
+        return out.reshape(*x.shape[:-1], n)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad):
+        x_in, z, a16, b16, packed, mask = ctx.saved_tensors
+        state = ctx.state
+        n, k = state.shape
+        t = x_in.shape[0]
+        g = grad.reshape(t, n).to(torch.float16).contiguous()
+        stream = _lib.stream(g.device)
+        d_lora = torch.empty_like(g)
+        if t:
+            _lib.call("ss_lora_epilogue_bwd", g.data_ptr(), _lib.F16, d_lora.data_ptr(), _lib.F16,
+                      g.numel(), ctx.scaling, stream)
+        dz = gemm_f16(d_lora, b16)                          # [T, r]
+        db = gemm_f16(d_lora, z, a_trans=True)              # [N, r]
+        da = gemm_f16(dz, x_in, a_trans=True)               # [r, K]
+        dx = nf4_dx_2d(g, packed, state, n, k)              # [T, K]
+        if mask is None:
+            gemm_f16(dz, a16, out=dx, accumulate=True)
+        else:
+            dx_lora = gemm_f16(dz, a16, out_dtype=torch.float32)
+            dx_lora = dx_lora * mask / (1.0 - ctx.dropout_p)
+            dx = (dx.float() + dx_lora).to(torch.float16)
+        x_dtype, a_dtype, b_dtype = ctx.dtypes
+        return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
+                None, None, None, None, None, None)
+
+
+def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, dropout_p=0.0,
+                     training=True):
+    """out = X . Wdec^T + bias + scaling * (drop(X) . A^T) . B^T with NF4 W (fp16 compute)."""
+    n, k = _validate_state(packed, state, torch.float16)
+    if x.dtype != torch.float16 or not x.is_cuda or x.shape[-1] != k or not x.is_contiguous():
+        raise ValueError("Expected contiguous CUDA fp16 X[..., K]")
+    if lora_a.ndim != 2 or lora_b.ndim != 2 or lora_a.shape[1] != k or lora_b.shape[0] != n \
+            or lora_a.shape[0] != lora_b.shape[1]:
+        raise ValueError("Expected lora_A [r, K] and lora_B [N, r]")
+    if bias is not None and (bias.dtype != torch.float16 or bias.shape != (n,)
+                             or not bias.is_contiguous()):
+        raise ValueError("Expected fp16 bias[N]")
+    if not math.isfinite(scaling):
+        raise ValueError("scaling must be finite")
+    if not 0.0 <= dropout_p < 1.0:
+        raise ValueError("dropout_p must be in [0, 1)")
+    with torch.cuda.device(x.device):
+        return _QLoRAProjection.apply(x, lora_a, lora_b, packed, state, bias, float(scaling),
+                                      float(dropout_p), bool(training))

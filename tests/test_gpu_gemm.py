@@ -1,0 +1,140 @@
+"""GPU parity of the NF4 GEMMs and the dense fp16 MFMA GEMM.
+
+Bar (fixed before any GPU run; the reference's EXP-002 gate,
+experiments/reports/EXP-002.md:60-76): assert_close(rtol=2e-3, atol=2e-3) on
+the fp16 output against the float64 product of the bit-exact decoded weight
+(oracle.gemm), finite output, relative L2 <= 1e-3.  Shapes: the reference's
+EXP-002 table (W 1536x1536, 256x1536, 8960x1536, 1536x8960 at M = 800 and
+2048), configs[0] (gate 8960x1536, X [1024, 1536]), small-T rows (1, 16, 128),
+ragged sizes, the large-T decode-first path, and K % 64 != 0 (dense path).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as ogemm
+from oracle import nf4 as onf4
+from soupsuck_amd import _lib
+from soupsuck_amd.kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d, nf4_matmul
+from tests.gpu_util import device_state, np16, random_weight
+
+pytestmark = pytest.mark.gpu
+
+_CACHE = {}
+
+
+def weight(n, k, seed=11):
+    key = (n, k, seed)
+    if key not in _CACHE:
+        state = onf4.quantize_nested(random_weight(n, k, seed))
+        _CACHE[key] = (state, state.decode())
+    return _CACHE[key]
+
+
+def x_of(t, k, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((t, k), dtype=np.float32) * scale).astype(np.float16)
+
+
+def check(actual, expected, what):
+    ok, max_abs, rel = ogemm.gate(np16(actual).astype(np.float64), expected)
+    assert ok, f"{what}: max_abs={max_abs:.3e} rel_l2={rel:.3e}"
+
+
+@pytest.mark.parametrize("t,n,k", [
+    (1024, 8960, 1536),                                   # configs[0]
+    (800, 1536, 1536), (800, 256, 1536), (800, 8960, 1536), (800, 1536, 8960),
+    (2048, 256, 1536),
+    (1, 1536, 1536), (16, 8960, 1536), (128, 256, 1536), (37, 320, 128), (130, 192, 64),
+])
+def test_forward_matches_oracle(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    x = x_of(t, k, seed=t + n)
+    bias = (np.random.default_rng(5).standard_normal(n) * 0.1).astype(np.float16)
+    xt = torch.from_numpy(x).to(device)
+    bt = torch.from_numpy(bias).to(device)
+    y = nf4_matmul(xt, packed, qs, bias=bt)
+    check(y, ogemm.linear(x, w, bias), f"fwd t={t} n={n} k={k}")
+    y0 = nf4_matmul(xt.view(1, t, k), packed, qs)
+    assert y0.shape == (1, t, n)
+    check(y0[0], ogemm.linear(x, w), f"fwd nobias t={t}")
+
+
+@pytest.mark.parametrize("t,n,k", [
+    (1024, 8960, 1536), (800, 1536, 1536), (800, 256, 1536), (800, 1536, 8960),
+    (1, 1536, 1536), (16, 8960, 1536), (37, 320, 128), (130, 192, 64),
+])
+def test_dx_matches_oracle(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    dy = x_of(t, n, seed=3 * t + k)
+    dx = nf4_matmul(torch.from_numpy(dy).to(device), packed, qs, transpose=True)
+    check(dx, ogemm.linear_dx(dy, w), f"dx t={t} n={n} k={k}")
+
+
+def test_dx_accumulate(device):
+    state, w = weight(256, 1536)
+    packed, qs = device_state(state, device)
+    dy = x_of(64, 256, seed=1)
+    base = x_of(64, 1536, seed=2, scale=0.1)
+    out = torch.from_numpy(base).to(device)
+    nf4_dx_2d(torch.from_numpy(dy).to(device), packed, qs, 256, 1536, out=out, accumulate=True)
+    check(out, ogemm.linear_dx(dy, w) + base.astype(np.float64), "dx accumulate")
+
+
+def test_large_t_decode_first_path(device):
+    t, n, k = 4096, 512, 1536
+    assert _lib.load().ss_nf4_gemm_workspace_size(t, n, k) == n * k * 2
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    x = x_of(t, k, seed=9)
+    y = nf4_forward_2d(torch.from_numpy(x).to(device), packed, qs, n, k)
+    check(y, ogemm.linear(x, w), "fwd decode-first")
+    dy = x_of(t, n, seed=10)
+    dx = nf4_dx_2d(torch.from_numpy(dy).to(device), packed, qs, n, k)
+    check(dx, ogemm.linear_dx(dy, w), "dx decode-first")
+
+
+def test_k_not_multiple_of_64_uses_dense_path(device):
+    state, w = weight(96, 100)
+    packed, qs = device_state(state, device)
+    x = x_of(33, 100, seed=4)
+    check(nf4_matmul(torch.from_numpy(x).to(device), packed, qs), ogemm.linear(x, w), "K=100")
+    dy = x_of(33, 96, seed=5)
+    check(nf4_matmul(torch.from_numpy(dy).to(device), packed, qs, transpose=True),
+          ogemm.linear_dx(dy, w), "K=100 dx")
+
+
+def test_validation_errors(device):
+    state, _ = weight(64, 128)
+    packed, qs = device_state(state, device)
+    with pytest.raises(ValueError):
+        nf4_matmul(torch.zeros((4, 64), device=device, dtype=torch.float16), packed, qs)
+    with pytest.raises(ValueError):
+        nf4_matmul(torch.zeros((4, 128), device=device, dtype=torch.float32), packed, qs)
+
+
+@pytest.mark.parametrize("a_trans", [False, True])
+@pytest.mark.parametrize("b_trans", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("m,n,k", [(37, 45, 70), (256, 16, 1536), (300, 1536, 16), (129, 200, 256)])
+def test_dense_gemm_layouts(device, a_trans, b_trans, out_dtype, m, n, k):
+    rng = np.random.default_rng(m * n + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = (rng.standard_normal((k, n)) * 0.1).astype(np.float16)
+    bias = rng.standard_normal(n).astype(np.float16)
+    ad = torch.from_numpy(np.ascontiguousarray(a.T if a_trans else a)).to(device)
+    bd = torch.from_numpy(np.ascontiguousarray(b.T if b_trans else b)).to(device)
+    c = gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out_dtype=out_dtype, alpha=0.5,
+                 bias=torch.from_numpy(bias).to(device))
+    expected = 0.5 * (a.astype(np.float64) @ b.astype(np.float64)) + bias
+    if out_dtype == torch.float16:
+        check(c, expected, "dense f16")
+    else:
+        np.testing.assert_allclose(np16(c), expected, rtol=1e-5, atol=1e-4)
+        # accumulate into the fp32 output
+        gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out=c, accumulate=True)
+        np.testing.assert_allclose(np16(c), expected + a.astype(np.float64) @ b,
+                                   rtol=1e-5, atol=2e-4)

@@ -1,0 +1,83 @@
+"""GPU parity of the LoRA epilogue (bit-exact) and the QLoRA projection (toleranced).
+
+Epilogue cases mirror solution/tests/test_lora.py:15-49 (every base/adapter
+dtype pair, both cast modes, rtol = atol = 0; the rounded product must cancel
+to exactly zero).  The projection forward is compared with the oracle's
+autocast composition (fp16 after each GEMM) and the backward with the float64
+ideal gradients, within a relative-norm bound of 1e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import lora as olora
+from oracle import nf4 as onf4
+from soupsuck_amd.kernels.lora_epilogue import lora_epilogue
+from soupsuck_amd.lora import qlora_projection
+from tests.gpu_util import bits, device_state, np16, random_weight, rel_norm
+
+pytestmark = pytest.mark.gpu
+
+NP = {torch.float16: np.float16, torch.float32: np.float32}
+
+
+@pytest.mark.parametrize("base_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("adapter_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("cast_to_result", [False, True])
+def test_epilogue_bit_exact(device, base_dtype, adapter_dtype, cast_to_result):
+    rng = np.random.default_rng(175)
+    base = rng.standard_normal((3, 7, 79)).astype(NP[base_dtype])
+    adapter = rng.standard_normal((3, 7, 79)).astype(NP[adapter_dtype])
+    bt = torch.from_numpy(base).to(device).requires_grad_()
+    at = torch.from_numpy(adapter).to(device).requires_grad_()
+    out = lora_epilogue(bt, at, 1.3, cast_to_result=cast_to_result)
+    expected = olora.epilogue_forward(base, adapter, 1.3, cast_to_result)
+    assert out.dtype == torch.from_numpy(expected).dtype
+    np.testing.assert_array_equal(np16(out), expected)
+    grad = rng.standard_normal(out.shape).astype(expected.dtype)
+    out.backward(torch.from_numpy(grad).to(device))
+    d_r, d_a = olora.epilogue_backward(grad, NP[base_dtype], NP[adapter_dtype], 1.3)
+    np.testing.assert_array_equal(np16(bt.grad), d_r)
+    np.testing.assert_array_equal(np16(at.grad), d_a)
+
+
+def test_epilogue_rounded_product_cancels(device):
+    adapter = torch.linspace(-2, 2, 2049, device=device, dtype=torch.float16)
+    result = -(adapter * 1.3)
+    assert torch.count_nonzero(lora_epilogue(result, adapter, 1.3)).item() == 0
+
+
+@pytest.mark.parametrize("t,n,k,bias", [(96, 256, 1536, True), (200, 1536, 1536, False),
+                                        (37, 8960, 1536, False), (64, 1536, 8960, False)])
+def test_qlora_projection_matches_oracle(device, t, n, k, bias):
+    rng = np.random.default_rng(t + n)
+    state = onf4.quantize_nested(random_weight(n, k, seed=3))
+    w = state.decode()
+    packed, qs = device_state(state, device)
+    x = rng.standard_normal((t, k)).astype(np.float16)
+    a = ((rng.random((16, k)) * 2 - 1) / np.sqrt(k)).astype(np.float16)
+    b = (rng.standard_normal((n, 16)) * 0.01).astype(np.float16)
+    bvec = (rng.standard_normal(n) * 0.02).astype(np.float16) if bias else None
+    g = (rng.standard_normal((t, n)) * 0.01).astype(np.float16)
+    xt = torch.from_numpy(x).to(device).requires_grad_()
+    at = torch.from_numpy(a).to(device).requires_grad_()
+    bt = torch.from_numpy(b).to(device).requires_grad_()
+    out = qlora_projection(xt, at, bt, packed, qs,
+                           torch.from_numpy(bvec).to(device) if bias else None, scaling=2.0)
+    # forward: oracle autocast composition
+    base = (x.astype(np.float64) @ w.astype(np.float64).T
+            + (bvec.astype(np.float64) if bias else 0)).astype(np.float16)
+    _, lo = olora.branch_forward(x, a, b)
+    expected = olora.epilogue_forward(base, lo, 2.0)
+    got = np16(out)
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got.astype(np.float64), expected.astype(np.float64),
+                               rtol=2e-3, atol=2e-3)
+    ideal = olora.ideal_projection(x, w, bvec, a, b, 2.0)
+    assert rel_norm(got, ideal) < 1e-3
+    out.backward(torch.from_numpy(g).to(device))
+    dx, da, db = olora.ideal_projection_backward(g, x, w, a, b, 2.0)
+    assert rel_norm(np16(xt.grad), dx) < 1e-2
+    assert rel_norm(np16(at.grad), da) < 1e-2
+    assert rel_norm(np16(bt.grad), db) < 1e-2

@@ -1,0 +1,143 @@
+"""GPU parity of add-RMSNorm (fwd/bwd/dgamma) and the unpad gather/scatter.
+
+add-RMSNorm bar (solution/tests/test_add_rmsnorm.py:10-11): the new residual
+s is bit-exact; y and the input gradients within fp32 1e-5 / fp16 2e-3
+(rtol = atol) of oracle/rmsnorm.py; dgamma within the magnitude-scaled fp32
+reduction budget of that test (:14-44).  Shapes: configs[2] (fp16 [T, 1536],
+T in {826, 4096, 16384}, w = 1 + N(0, 0.1), eps 1e-6) and the reference's
+dtype-promotion grid at (2, 5, 1000).
+Unpad bar: bit-exact; configs[2] batch [4, 360, 1536] fp16 with lengths
+uniform in [80, 360].
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rmsnorm as ormsnorm
+from oracle import unpad as ounpad
+from soupsuck_amd import unpad
+from soupsuck_amd.kernels.add_rmsnorm import add_rms_norm
+from tests.gpu_util import bits, np16
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = dict(rtol=1e-5, atol=1e-5)
+F16_TOL = dict(rtol=2e-3, atol=2e-3)
+NP = {torch.float16: np.float16, torch.float32: np.float32}
+
+
+def run_case(device, shape, rdt, ddt, wdt, out_dtype, train_weight, seed=101):
+    rng = np.random.default_rng(seed)
+    h = shape[-1]
+    r = rng.standard_normal(shape).astype(NP[rdt])
+    d = rng.standard_normal(shape).astype(NP[ddt])
+    w = (1 + 0.1 * rng.standard_normal(h)).astype(NP[wdt])
+    rt = torch.from_numpy(r).to(device).requires_grad_()
+    dt = torch.from_numpy(d).to(device).requires_grad_()
+    wt = torch.from_numpy(w).to(device).requires_grad_(train_weight)
+    s, y = add_rms_norm(rt, dt, wt, 1e-6, out_dtype)
+    es, ey, rstd = ormsnorm.add_rmsnorm_forward(r, d, w, 1e-6, out_dtype is not None)
+    assert s.dtype == torch.from_numpy(es).dtype and y.dtype == torch.from_numpy(ey).dtype
+    np.testing.assert_array_equal(bits(s) if s.dtype == torch.float16 else np16(s),
+                                  es.view(np.int16) if es.dtype == np.float16 else es)
+    tol = F32_TOL if (es.dtype == np.float32 and ey.dtype == np.float32
+                      and w.dtype == np.float32) else F16_TOL
+    np.testing.assert_allclose(np16(y).astype(np.float64), ey.astype(np.float64), **tol)
+    gs = rng.standard_normal(shape).astype(es.dtype)
+    gy = rng.standard_normal(shape).astype(ey.dtype)
+    torch.autograd.backward([s, y], [torch.from_numpy(gs).to(device),
+                                     torch.from_numpy(gy).to(device)])
+    exact = np.promote_types(es.dtype, w.dtype)
+    dr, dd, dg = ormsnorm.add_rmsnorm_backward(gs, gy, es, w, rstd, r.dtype, d.dtype, exact)
+    gtol = F32_TOL if (r.dtype == np.float32 and tol is F32_TOL) else F16_TOL
+    np.testing.assert_allclose(np16(rt.grad).astype(np.float64), dr.astype(np.float64),
+                               **(gtol if r.dtype == np.float32 else F16_TOL))
+    np.testing.assert_allclose(np16(dt.grad).astype(np.float64), dd.astype(np.float64),
+                               **(gtol if d.dtype == np.float32 else F16_TOL))
+    if train_weight:
+        q = (es.astype(np.float64) * rstd[..., None]).astype(es.dtype).astype(np.float64)
+        magnitude = np.abs(gy.astype(np.float64) * q).reshape(-1, h).sum(0)
+        budget = 1e-5 * np.abs(dg) + 32 * np.finfo(np.float32).eps * magnitude
+        if wt.grad.dtype == torch.float16:
+            budget = 2e-3 * np.abs(dg) + 2e-3 + budget
+        err = np.abs(np16(wt.grad).astype(np.float64) - dg)
+        assert np.all(err <= budget), float((err - budget).max())
+
+
+@pytest.mark.parametrize("rows", [826, 4096, 16384])
+def test_config3_fp16(device, rows):
+    run_case(device, (rows, 1536), torch.float16, torch.float16, torch.float16, None, True)
+
+
+@pytest.mark.parametrize("shape", [(4, 512, 1536), (3, 77, 1536), (2, 5, 1000)])
+@pytest.mark.parametrize("ddt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [None, torch.float16])
+@pytest.mark.parametrize("train_weight", [False, True])
+def test_reference_grid(device, shape, ddt, out_dtype, train_weight):
+    run_case(device, shape, torch.float32, ddt, torch.float32, out_dtype, train_weight)
+
+
+@pytest.mark.parametrize("rdt,ddt,wdt", [
+    (torch.float16, torch.float16, torch.float16), (torch.float16, torch.float16, torch.float32),
+    (torch.float16, torch.float32, torch.float16), (torch.float32, torch.float16, torch.float16)])
+@pytest.mark.parametrize("out_dtype", [None, torch.float16])
+def test_dtype_promotion(device, rdt, ddt, wdt, out_dtype):
+    run_case(device, (2, 5, 1000), rdt, ddt, wdt, out_dtype, True)
+
+
+def test_one_output_without_upstream(device):
+    rng = np.random.default_rng(202)
+    r = torch.from_numpy(rng.standard_normal((10, 1000)).astype(np.float32)).to(device)
+    r.requires_grad_()
+    d = torch.from_numpy(rng.standard_normal((10, 1000)).astype(np.float16)).to(device)
+    d.requires_grad_()
+    w = torch.ones(1000, device=device, requires_grad=True)
+    s, y = add_rms_norm(r, d, w, 1e-6)
+    s.backward(torch.ones_like(s))
+    np.testing.assert_array_equal(np16(r.grad), np.ones((10, 1000), np.float32))
+    assert torch.count_nonzero(w.grad).item() == 0
+
+
+def test_invalid_inputs(device):
+    r = torch.ones((2, 5, 1000), device=device)
+    with pytest.raises(ValueError, match="contiguous"):
+        add_rms_norm(r.transpose(0, 1), r.transpose(0, 1), torch.ones(1000, device=device), 1e-6)
+    with pytest.raises(ValueError, match="out_dtype"):
+        add_rms_norm(r, r, torch.ones(1000, device=device), 1e-6, torch.float32)
+
+
+# ------------------------------------------------------------------ unpad ---
+
+def test_config3_unpad_bit_exact(device):
+    rng = np.random.default_rng(0)
+    lengths = tuple(int(v) for v in rng.integers(80, 361, 4))
+    x = rng.standard_normal((4, 360, 1536)).astype(np.float16)
+    batch = unpad.make_batch(lengths, 360, device)
+    idx = ounpad.indices_from_lengths(lengths, 360)
+    assert batch.indices.cpu().numpy().tolist() == idx.tolist()
+    xt = torch.from_numpy(x).to(device).requires_grad_()
+    packed = unpad.pack(xt, batch)
+    assert packed.shape == (1, sum(lengths), 1536)
+    np.testing.assert_array_equal(bits(packed[0]), ounpad.pack(x, idx).view(np.int16))
+    back = unpad.scatter(packed, batch)
+    np.testing.assert_array_equal(bits(back),
+                                  ounpad.scatter(ounpad.pack(x, idx), idx, 4, 360).view(np.int16))
+    g = rng.standard_normal((4, 360, 1536)).astype(np.float16)
+    back.backward(torch.from_numpy(g).to(device))
+    mask = (np.arange(360)[None, :] < np.array(lengths)[:, None])[..., None]
+    np.testing.assert_array_equal(bits(xt.grad), np.where(mask, g, 0).astype(np.float16)
+                                  .view(np.int16))
+
+
+def test_unpad_small_and_integer_rows(device):
+    batch = unpad.make_batch((1, 3), 3, device)
+    assert batch.indices.cpu().tolist() == [0, 3, 4, 5]
+    ids = torch.tensor([[5, 0, 0], [8, 6, 7]], device=device)
+    assert unpad.pack(ids, batch).cpu().tolist() == [[5, 8, 6, 7]]
+    odd = torch.arange(2 * 3 * 3, device=device, dtype=torch.float16).view(2, 3, 3)
+    p = unpad.pack(odd, batch)
+    assert torch.equal(p[0], odd.reshape(6, 3)[[0, 3, 4, 5]])
+    assert torch.equal(unpad.scatter(p, batch)[0, 1:], torch.zeros((2, 3), device=device,
+                                                                   dtype=torch.float16))
+    assert unpad.right_padding_lengths([[1, 1, 1], [1, 0, 0]]) == (3, 1)
