@@ -84,7 +84,7 @@ class KernelTimer:
         end.record()
         _, a, start = self._pending
         self._pending = None
-        kind = "fwd" if name == "ss_nf4_gemm_fwd" else "dx"
+        kind = "fwd" if name in ("ss_nf4_gemm_fwd", "ss_qlora_fwd") else "dx"
         t, n, k = a[2], a[8], a[9]
         self.records.append((tile_name(kind, t, n, k), 2.0 * t * n * k, start, end))
 
@@ -170,8 +170,8 @@ def main():
     torch.cuda.synchronize()
 
     timer = KernelTimer()
-    _lib.hooks["ss_nf4_gemm_fwd"] = (timer.before, timer.after)
-    _lib.hooks["ss_nf4_gemm_dx"] = (timer.before, timer.after)
+    for name in ("ss_nf4_gemm_fwd", "ss_nf4_gemm_dx", "ss_qlora_fwd", "ss_qlora_dx"):
+        _lib.hooks[name] = (timer.before, timer.after)
     timer.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()

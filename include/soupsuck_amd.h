@@ -98,8 +98,51 @@ int ss_nf4_quantize(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint
                     float* absmax2, const float* code2, float* offset, float* absmax_workspace,
                     void* stream);
 
-/* Workspace bytes the two NF4 GEMM entry points need for this shape. */
+/* Workspace bytes the NF4 GEMM entry points (plain and LoRA-fused) need for
+ * this shape (0 when the fused decode-in-GEMM path is used). */
 size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k);
+
+/* A7+A10+A11 fused: the QLoRA projection forward of one Linear4bit with its
+ * LoRA adapter (reference solution/lora.py:135-163 with
+ * solution/kernels/lora_epilogue.py:24-34 under fp16 autocast):
+ *   y = fp16( fp16(x . Wdec^T + bias) + fp16( fp16(z . lora_b^T) * scale ) )
+ * z = fp16(drop(x) . lora_a^T) is [t, 16] contiguous (ss_lora_project);
+ * lora_b is [n, 16] contiguous; rank 16.  Same workspace rule as above. */
+int ss_qlora_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                 const uint8_t* qabs, const float* absmax2, const float* code2,
+                 const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                 const uint16_t* z, const uint16_t* lora_b, float scale, uint16_t* y,
+                 int64_t ldy, void* workspace, size_t workspace_bytes, void* stream);
+
+/* A8+A12 fused: dx = fp16(dy . Wdec + dz . lora_a), the base dX of
+ * MatMul4Bit.backward plus the LoRA input gradient in one accumulator
+ * (reference solution/lora_pair.py:52-65 sums them in fp16 after two
+ * roundings).  dz is [t, 16] contiguous, lora_a is [16, k] contiguous. */
+int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                const uint8_t* qabs, const float* absmax2, const float* code2,
+                const float* offset, int64_t n, int64_t k, const uint16_t* dz,
+                const uint16_t* lora_a, uint16_t* dx, int64_t lddx, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------ rank-16 LoRA products ---
+ * HBM-bound skinny GEMMs of the LoRA branch (reference solution/lora.py:161,
+ * solution/lora_pair.py:52-65), fp32 accumulation, one fp16 rounding.
+ * ss_lora_project: out[m, 16] = fp16(A'[m, k] . W) with A' = A or, when
+ *   scale_a, fp16(A * a_scale) elementwise (dL = fp16(g * s)); W element
+ *   (kk, r) at w[kk*ldw + r] when w_kr (lora_B [N,16]) else w[r*ldw + kk]
+ *   (lora_A [16,K]).  Z = X.A^T and dZ = dL.B.
+ * ss_lora_grad: C[16, n] = fp16(P[t,16]^T . Q'[t, n]) with Q' = Q or
+ *   fp16(Q * q_scale); stored [16][n], or [n][16] when transpose.
+ *   dA = dZ^T.X and dB = dL^T.Z.
+ * workspace: fp32 partials, at least ss_lora_workspace_size(rows, cols) bytes
+ * for an output with rows x 16 or 16 x cols elements. */
+size_t ss_lora_workspace_size(int64_t rows, int64_t cols);
+int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_t k, const uint16_t* w,
+                    int64_t ldw, int w_kr, int scale_a, float a_scale, uint16_t* out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int ss_lora_grad(const uint16_t* p, int64_t ldp, const uint16_t* q, int64_t ldq, int64_t t,
+                 int64_t n, int scale_q, float q_scale, int transpose, uint16_t* out,
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------- dense fp16 GEMM ---
  * C[M,N] = alpha * op(A)[M,K] . op(B)[K,N] (+ bias[N]) (+ beta * C), fp16

@@ -101,28 +101,22 @@ def dynamic_map_signed():
 
     For exponent i in 0..6: 2**i midpoints of linspace(0.1, 1, 2**i + 1),
     scaled by 10**(i-6), with both signs; plus 0 and 1.0; sorted (256 values).
+    The published recipe builds the float32 boundaries with torch.linspace on
+    the CPU, so this restatement does too (its rounding is part of the table).
     """
+    import torch
+
     data = []
     for i in range(7):
         items = 2 ** i + 1
-        bounds = _linspace_f32(0.1, 1.0, items)
-        means = ((bounds[:-1] + bounds[1:]) / np.float32(2.0)).astype(np.float32)
-        scaled = (np.float32(10.0 ** (i - 6)) * means).astype(np.float32)
+        bounds = torch.linspace(0.1, 1.0, items, dtype=torch.float32)
+        means = (bounds[:-1] + bounds[1:]) / 2.0
+        scaled = (10.0 ** (i - 6)) * means
         data += scaled.tolist()
         data += (-scaled).tolist()
     data += [0.0, 1.0]
     assert len(data) == 256
     return np.array(sorted(data), dtype=np.float32)
-
-
-def _linspace_f32(start, end, steps):
-    """float32 linspace computed from both ends (the symmetric float recipe)."""
-    step = np.float32((np.float32(end) - np.float32(start)) / np.float32(steps - 1))
-    i = np.arange(steps)
-    half = steps // 2
-    lo = np.float32(start) + step * i[:half].astype(np.float32)
-    hi = np.float32(end) - step * (steps - 1 - i[half:]).astype(np.float32)
-    return np.concatenate([lo, hi]).astype(np.float32)
 
 
 def nf4_thresholds():

@@ -40,6 +40,17 @@ SIGNATURES = {
                                                                   _int, _c_void_p, _size,
                                                                   _c_void_p],
     "ss_nf4_gemm_workspace_size": [_i64, _i64, _i64],
+    "ss_qlora_fwd": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _c_void_p,
+                                                                _c_void_p, _f32, _c_void_p, _i64,
+                                                                _c_void_p, _size, _c_void_p],
+    "ss_qlora_dx": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _c_void_p,
+                                                               _c_void_p, _i64, _c_void_p, _size,
+                                                               _c_void_p],
+    "ss_lora_workspace_size": [_i64, _i64],
+    "ss_lora_project": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _int, _int, _f32,
+                        _c_void_p, _c_void_p, _size, _c_void_p],
+    "ss_lora_grad": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _f32, _int, _c_void_p,
+                     _c_void_p, _size, _c_void_p],
     "ss_nf4_quantize": [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                         _c_void_p, _c_void_p, _c_void_p],
     "ss_gemm_f16": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
@@ -65,7 +76,8 @@ SIGNATURES = {
     "ss_ce_finalize_dx": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
                           _c_void_p],
 }
-_RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size}
+_RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size,
+             "ss_lora_workspace_size": _size}
 
 _lock = threading.Lock()
 _lib = None

@@ -66,7 +66,7 @@ __device__ __forceinline__ void store8(void* p, int dt, int64_t off, int valid, 
         half8 h;
       } t;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t.h[j] = (half_t)v[j];
+      for (int j = 0; j < 8; ++j) t.h[j] = f32_to_f16(v[j]);
       *reinterpret_cast<uint4*>(reinterpret_cast<half_t*>(p) + off) = t.u;
     } else {
       float* q = reinterpret_cast<float*>(p) + off;

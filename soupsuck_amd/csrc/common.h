@@ -30,6 +30,16 @@ __device__ __constant__ static const float kNF4[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
+// fp32 -> fp16 with round-to-nearest-even as its own instruction.  The empty
+// asm makes the value opaque to instruction selection, which would otherwise
+// fold a preceding fp32 multiply into v_fma_mix*_f16 with a +0 addend: that
+// turns a -0 product into +0 and rounds the exact product once instead of
+// rounding it to fp32 first.  It emits no instruction.
+__device__ __forceinline__ half_t f32_to_f16(float v) {
+  asm("" : "+v"(v));
+  return (half_t)v;
+}
+
 // fp32 scale of one 64-element NF4 block of a nested (double-quantized) state:
 // fp32(fp32(code2[qabs[b]] * absmax2[b / 256]) + offset).  Two separate
 // roundings; the translation unit is built without contraction.

@@ -194,8 +194,8 @@ __global__ __launch_bounds__(256) void ce_derivative_kernel(
       const float onehot = (start + c + j == tgt) ? 1.0f : 0.0f;
       d = (p - onehot) * g;
     }
-    o.h[j] = (half_t)(d / gain);
-    og.h[j] = (half_t)(d / global_gain);
+    o.h[j] = f32_to_f16(d / gain);
+    og.h[j] = f32_to_f16(d / global_gain);
   }
   half_t* out = dz + row * width + c;
   half_t* outg = dzg ? dzg + row * width + c : nullptr;

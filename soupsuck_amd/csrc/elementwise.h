@@ -12,14 +12,14 @@ __device__ __forceinline__ float ld_elem(const void* p, int dt, int64_t i) {
 
 __device__ __forceinline__ void st_elem(void* p, int dt, int64_t i, float v) {
   if (dt == SS_F16)
-    reinterpret_cast<half_t*>(p)[i] = (half_t)v;
+    reinterpret_cast<half_t*>(p)[i] = f32_to_f16(v);
   else
     reinterpret_cast<float*>(p)[i] = v;
 }
 
 // Round an fp32 value to the storage precision of dtype dt (identity for fp32).
 __device__ __forceinline__ float round_to(int dt, float v) {
-  return dt == SS_F16 ? (float)(half_t)v : v;
+  return dt == SS_F16 ? (float)f32_to_f16(v) : v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -38,6 +38,12 @@ struct Nf4View {
   int64_t cols;  // weight row length (elements); a multiple of 64
 };
 
+// Epilogue variants: plain (alpha * acc + bias, + beta * C); the LoRA
+// forward out = fp16(fp16(acc + bias) + fp16(fp16(Z . B^T) * s)) with Z
+// [M,16] and B = lora_B [N,16]; and a rank-16 update out = fp16(acc + dZ . A)
+// with dZ [M,16] and A = lora_A [16, N] (row stride ldlb).
+enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2 };
+
 struct GemmParams {
   int64_t M, N, K;
   const half_t* A;
@@ -52,6 +58,10 @@ struct GemmParams {
   int64_t ldc;
   float alpha;
   int beta;
+  const half_t* lz;   // Z or dZ, [M, 16] contiguous
+  const half_t* lb;   // lora_B [N, 16] (EPI_LORA) or lora_A [16, ldlb] (EPI_RANK)
+  int64_t ldlb;
+  float lscale;
 };
 
 constexpr int kThreads = 256;
@@ -152,8 +162,8 @@ __device__ __forceinline__ void decode_run(const uint32_t* words, float scale,
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
-      out[8 * wi + 2 * b] = (half_t)(lut[byte >> 4] * scale);
-      out[8 * wi + 2 * b + 1] = (half_t)(lut[byte & 15u] * scale);
+      out[8 * wi + 2 * b] = f32_to_f16(lut[byte >> 4] * scale);
+      out[8 * wi + 2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
     }
   }
 }
@@ -282,7 +292,7 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
   if constexpr (CT == SS_F16) {
     half_t* c = reinterpret_cast<half_t*>(C);
     if (beta) v += (float)c[idx];
-    c[idx] = (half_t)v;
+    c[idx] = f32_to_f16(v);
   } else {
     float* c = reinterpret_cast<float*>(C);
     if (beta) v += c[idx];
@@ -290,7 +300,7 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
   }
 }
 
-template <class T, int OPA, int OPB, int CT>
+template <class T, int OPA, int OPB, int CT, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int BM = T::kBM, BN = T::kBN, BK = T::kBK, WM = T::kWM, WN = T::kWN;
   constexpr int LDK = T::kLdk;
@@ -375,15 +385,52 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   for (int i = 0; i < WM / 16; ++i) {
 #pragma unroll
     for (int j = 0; j < WN / 16; ++j) {
-      const int64_t col = n0 + wn * WN + j * 16 + ccol;
+      const int64_t row_base = m0 + wm * WM + i * 16;
+      const int64_t col_base = n0 + wn * WN + j * 16;
+      float4v extra = float4v{0.f, 0.f, 0.f, 0.f};
+      if constexpr (EPI != EPI_PLAIN) {
+        // Rank-16 product for this 16x16 tile on one v_mfma_f32_16x16x16_f16:
+        // A = Z rows (lane: row lane%16, r = 4*(lane/16)..+3), B = (r, column).
+        const int rq = (lane >> 4) * 4;
+        const int64_t zr = row_base + (lane & 15);
+        const int64_t bc = col_base + (lane & 15);
+        half4 za, zb;
+        if (zr < p.M) {
+          za = *reinterpret_cast<const half4*>(p.lz + zr * 16 + rq);
+        } else {
+          za = half4{(half_t)0.0f, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
+        }
+        if (bc < p.N) {
+          if constexpr (EPI == EPI_LORA) {
+            zb = *reinterpret_cast<const half4*>(p.lb + bc * 16 + rq);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) zb[q] = p.lb[(rq + q) * p.ldlb + bc];
+          }
+        } else {
+          zb = half4{(half_t)0.0f, (half_t)0.0f, (half_t)0.0f, (half_t)0.0f};
+        }
+        extra = __builtin_amdgcn_mfma_f32_16x16x16f16(za, zb, extra, 0, 0, 0);
+      }
+      const int64_t col = col_base + ccol;
       if (col >= p.N) continue;
       const float b = p.bias ? (float)p.bias[col] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm * WM + i * 16 + crow + r;
+        const int64_t row = row_base + crow + r;
         if (row < p.M) {
-          const float v = acc[i][j][r] * p.alpha + b;
-          store_c<CT>(p.C, row * p.ldc + col, v, p.beta);
+          const int64_t idx = row * p.ldc + col;
+          if constexpr (EPI == EPI_LORA) {
+            const float y = (float)f32_to_f16(acc[i][j][r] * p.alpha + b);
+            const float lora = (float)f32_to_f16(extra[r]);
+            const float scaled = (float)f32_to_f16(lora * p.lscale);
+            reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
+          } else if constexpr (EPI == EPI_RANK) {
+            store_c<CT>(p.C, idx, acc[i][j][r] + extra[r], p.beta);
+          } else {
+            const float v = acc[i][j][r] * p.alpha + b;
+            store_c<CT>(p.C, idx, v, p.beta);
+          }
         }
       }
     }
@@ -395,10 +442,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 using TileBig = Tile<128, 128, 64, 64, 64>;
 using TileSmall = Tile<64, 64, 64, 32, 32>;
 
-template <class T, int OPA, int OPB, int CT>
+template <class T, int OPA, int OPB, int CT, int EPI>
 static int launch(const GemmParams& p, hipStream_t stream, const char* name) {
   dim3 grid((unsigned)cdiv(p.N, T::kBN), (unsigned)cdiv(p.M, T::kBM));
-  hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT>), grid, dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT, EPI>), grid, dim3(kThreads), 0, stream, p);
   SS_CHECK_LAUNCH(name);
   return SS_OK;
 }
@@ -409,17 +456,15 @@ static bool use_small_tile(int64_t m, int64_t n) {
   return cdiv(m, 128) * cdiv(n, 128) < 256;
 }
 
-template <int OPA, int OPB, int CT>
+template <int OPA, int OPB, int CT, int EPI = EPI_PLAIN>
 static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
-  if (use_small_tile(p.M, p.N)) return launch<TileSmall, OPA, OPB, CT>(p, stream, name);
-  return launch<TileBig, OPA, OPB, CT>(p, stream, name);
+  if (use_small_tile(p.M, p.N)) return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
+  return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
 }
 
 static bool aligned16(const void* ptr, int64_t ld) {
   return reinterpret_cast<uintptr_t>(ptr) % 16 == 0 && ld % 8 == 0;
 }
-
-static int nf4_decode_first_fwd(const GemmParams& base, void* workspace, hipStream_t stream);
 
 }  // namespace ss
 
@@ -449,6 +494,67 @@ static int check_nf4(const char* fn, const uint8_t* packed, const uint8_t* qabs,
   return SS_OK;
 }
 
+namespace ss {
+
+template <int EPI>
+static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const int64_t n = p.N, k = p.K;
+  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
+    const Nf4View& w = p.w;
+    int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                  reinterpret_cast<uint16_t*>(workspace), n * k, s);
+    if (r) return r;
+    p.B = reinterpret_cast<const half_t*>(workspace);
+    p.ldb = k;
+    p.b_vec = 1;
+    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>");
+  }
+  return dispatch<OP_ROW, OP_NF4_ROW, SS_F16, EPI>(p, s, "gemm_kernel<nf4 fwd>");
+}
+
+template <int EPI>
+static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+                  hipStream_t s) {
+  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
+    const Nf4View& w = p.w;
+    int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                  reinterpret_cast<uint16_t*>(workspace), n * k, s);
+    if (r) return r;
+    p.B = reinterpret_cast<const half_t*>(workspace);
+    p.ldb = k;
+    p.b_vec = 1;
+    return dispatch<OP_ROW, OP_COL, SS_F16, EPI>(p, s, "gemm_kernel<f16 nn>");
+  }
+  return dispatch<OP_ROW, OP_NF4_COL, SS_F16, EPI>(p, s, "gemm_kernel<nf4 dx>");
+}
+
+static GemmParams fwd_params(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                             const uint8_t* qabs, const float* absmax2, const float* code2,
+                             const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                             uint16_t* y, int64_t ldy) {
+  GemmParams p{};
+  p.M = t; p.N = n; p.K = k;
+  p.A = reinterpret_cast<const half_t*>(x); p.lda = ldx; p.a_vec = aligned16(x, ldx);
+  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
+  p.bias = reinterpret_cast<const half_t*>(bias);
+  p.C = y; p.ldc = ldy; p.alpha = 1.0f; p.beta = 0;
+  return p;
+}
+
+static GemmParams dx_params(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                            const uint8_t* qabs, const float* absmax2, const float* code2,
+                            const float* offset, int64_t n, int64_t k, uint16_t* dx,
+                            int64_t lddx, int accumulate) {
+  GemmParams p{};
+  p.M = t; p.N = k; p.K = n;
+  p.A = reinterpret_cast<const half_t*>(dy); p.lda = lddy; p.a_vec = aligned16(dy, lddy);
+  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
+  p.C = dx; p.ldc = lddx; p.alpha = 1.0f; p.beta = accumulate ? 1 : 0;
+  return p;
+}
+
+}  // namespace ss
+
 extern "C" int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
                                const uint8_t* qabs, const float* absmax2, const float* code2,
                                const float* offset, int64_t n, int64_t k, const uint16_t* bias,
@@ -461,17 +567,31 @@ extern "C" int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const 
   if (t == 0) return SS_OK;
   SS_CHECK_ARG(x && y, "%s: null activation/output pointer", fn);
   SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
-  GemmParams p{};
-  p.M = t; p.N = n; p.K = k;
-  p.A = reinterpret_cast<const half_t*>(x); p.lda = ldx; p.a_vec = aligned16(x, ldx);
-  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
-  p.bias = reinterpret_cast<const half_t*>(bias);
-  p.C = y; p.ldc = ldy; p.alpha = 1.0f; p.beta = 0;
-  hipStream_t s = (hipStream_t)stream;
-  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
-    return nf4_decode_first_fwd(p, workspace, s);
-  }
-  return dispatch<OP_ROW, OP_NF4_ROW, SS_F16>(p, s, "gemm_kernel<nf4 fwd>");
+  GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, y, ldy);
+  return run_fwd<EPI_PLAIN>(p, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int ss_qlora_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                            const uint8_t* qabs, const float* absmax2, const float* code2,
+                            const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                            const uint16_t* z, const uint16_t* lora_b, float scale, uint16_t* y,
+                            int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "ss_qlora_fwd";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(x && y && z && lora_b, "%s: null pointer", fn);
+  SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
+  SS_CHECK_ARG(reinterpret_cast<uintptr_t>(z) % 8 == 0 &&
+                   reinterpret_cast<uintptr_t>(lora_b) % 8 == 0,
+               "%s: Z and lora_B must be 8-byte aligned", fn);
+  GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, y, ldy);
+  p.lz = reinterpret_cast<const half_t*>(z);
+  p.lb = reinterpret_cast<const half_t*>(lora_b);
+  p.ldlb = 16;
+  p.lscale = scale;
+  return run_fwd<EPI_LORA>(p, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int ss_nf4_gemm_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
@@ -486,33 +606,30 @@ extern "C" int ss_nf4_gemm_dx(const uint16_t* dy, int64_t lddy, int64_t t, const
   if (t == 0) return SS_OK;
   SS_CHECK_ARG(dy && dx, "%s: null gradient pointer", fn);
   SS_CHECK_ARG(lddy >= n && lddx >= k, "%s: leading dimensions too small", fn);
-  GemmParams p{};
-  p.M = t; p.N = k; p.K = n;
-  p.A = reinterpret_cast<const half_t*>(dy); p.lda = lddy; p.a_vec = aligned16(dy, lddy);
-  p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
-  p.C = dx; p.ldc = lddx; p.alpha = 1.0f; p.beta = accumulate ? 1 : 0;
-  hipStream_t s = (hipStream_t)stream;
-  if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
-    int r = ss_nf4_dequant_nested(packed, qabs, absmax2, code2, offset,
-                                  reinterpret_cast<uint16_t*>(workspace), n * k, stream);
-    if (r) return r;
-    p.B = reinterpret_cast<const half_t*>(workspace); p.ldb = k; p.b_vec = 1;
-    return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>");
-  }
-  return dispatch<OP_ROW, OP_NF4_COL, SS_F16>(p, s, "gemm_kernel<nf4 dx>");
+  GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx,
+                           accumulate);
+  return run_dx<EPI_PLAIN>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
-namespace ss {
-static int nf4_decode_first_fwd(const GemmParams& base, void* workspace, hipStream_t stream) {
-  const Nf4View& w = base.w;
-  int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
-                                reinterpret_cast<uint16_t*>(workspace), base.N * base.K, stream);
-  if (r) return r;
-  GemmParams p = base;
-  p.B = reinterpret_cast<const half_t*>(workspace); p.ldb = base.K; p.b_vec = 1;
-  return dispatch<OP_ROW, OP_ROW, SS_F16>(p, stream, "gemm_kernel<f16 nt>");
+extern "C" int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                           const uint8_t* qabs, const float* absmax2, const float* code2,
+                           const float* offset, int64_t n, int64_t k, const uint16_t* dz,
+                           const uint16_t* lora_a, uint16_t* dx, int64_t lddx, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  const char* fn = "ss_qlora_dx";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(dy && dx && dz && lora_a, "%s: null pointer", fn);
+  SS_CHECK_ARG(lddy >= n && lddx >= k, "%s: leading dimensions too small", fn);
+  SS_CHECK_ARG(reinterpret_cast<uintptr_t>(dz) % 8 == 0, "%s: dZ must be 8-byte aligned", fn);
+  GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx, 0);
+  p.lz = reinterpret_cast<const half_t*>(dz);
+  p.lb = reinterpret_cast<const half_t*>(lora_a);
+  p.ldlb = k;
+  return run_dx<EPI_RANK>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
 }
-}  // namespace ss
 
 extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
                            const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,

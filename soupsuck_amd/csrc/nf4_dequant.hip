@@ -46,8 +46,8 @@ __global__ __launch_bounds__(256) void nf4_dequant_vec_kernel(
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const uint32_t byte = (word >> (8 * b)) & 0xffu;
-      v[2 * b] = (half_t)(lut[byte >> 4] * scale);
-      v[2 * b + 1] = (half_t)(lut[byte & 15u] * scale);
+      v[2 * b] = f32_to_f16(lut[byte >> 4] * scale);
+      v[2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
     }
     out[g] = v;
   }
@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void nf4_dequant_scalar_kernel(
     const uint32_t byte = packed[i >> 1];
     const uint32_t nib = (i & 1) ? (byte & 15u) : (byte >> 4);
     const float scale = block_scale<NESTED>(qabs, absmax, absmax2, code2, offset, i >> 6);
-    out[i] = (half_t)(kNF4[nib] * scale);
+    out[i] = f32_to_f16(kNF4[nib] * scale);
   }
 }
 

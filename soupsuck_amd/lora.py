@@ -13,6 +13,12 @@ Backward (reference solution/lora_pair.py:34-65 order, fp16 after each GEMM):
 The frozen base contributes no weight gradient.  Dropout (p > 0) uses torch's
 native dropout on an fp32 copy of X, as the reference keeps PEFT's own
 Dropout module and RNG (solution/lora.py:1-40); p = 0 skips it.
+
+Fast path (rank 16, no active dropout, K % 64 == 0): six launches per
+projection -- forward ss_lora_project (Z) + ss_qlora_fwd (NF4 GEMM with the
+LoRA add in its epilogue); backward ss_lora_project (dZ from fp16(g*s)),
+ss_lora_grad twice (dB, dA) and ss_qlora_dx (g.W + dZ.A in one accumulator).
+Otherwise each GEMM and the epilogue run as separate kernels.
 """
 
 import math
@@ -23,6 +29,86 @@ from torch.autograd.function import once_differentiable
 from . import _lib
 from .kernels.nf4 import _validate_state
 from .kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+def _nf4_args(packed, state):
+    return (packed.data_ptr(), state.absmax.data_ptr(), state.state2.absmax.data_ptr(),
+            state.state2.code.data_ptr(), state.offset.data_ptr())
+
+
+def _gemm_ws(t, n, k, device):
+    size = _lib.load().ss_nf4_gemm_workspace_size(t, n, k)
+    return (_workspace(size, device), size) if size else (None, 0)
+
+
+def project16(a2d, w, w_kr, scale=None):
+    """fp16 [M, 16] = A' . W (ss_lora_project); W is lora_A [16, K] or lora_B [N, 16]."""
+    m, k = a2d.shape
+    out = torch.empty((m, 16), device=a2d.device, dtype=torch.float16)
+    size = _lib.load().ss_lora_workspace_size(m, 0)
+    ws = _workspace(size, a2d.device)
+    _lib.call("ss_lora_project", a2d.data_ptr(), a2d.stride(0), m, k, w.data_ptr(), w.stride(0),
+              int(w_kr), int(scale is not None), float(scale or 1.0), out.data_ptr(),
+              ws.data_ptr(), size, _lib.stream(a2d.device))
+    return out
+
+
+def grad16(p2d, q2d, transpose, scale=None):
+    """fp16 P^T . Q' as [16, N] (or [N, 16] when transpose) (ss_lora_grad)."""
+    t, n = q2d.shape
+    out = torch.empty((n, 16) if transpose else (16, n), device=q2d.device, dtype=torch.float16)
+    size = _lib.load().ss_lora_workspace_size(0, n)
+    ws = _workspace(size, q2d.device)
+    _lib.call("ss_lora_grad", p2d.data_ptr(), p2d.stride(0), q2d.data_ptr(), q2d.stride(0), t, n,
+              int(scale is not None), float(scale or 1.0), int(transpose), out.data_ptr(),
+              ws.data_ptr(), size, _lib.stream(q2d.device))
+    return out
+
+
+class _QLoRAFused(torch.autograd.Function):
+    """Rank-16, dropout-free projection on the fused kernels (six launches)."""
+
+    @staticmethod
+    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling):
+        n, k = state.shape
+        t = x.numel() // k
+        x2d = x.reshape(t, k)
+        a16 = lora_a.to(torch.float16).contiguous()
+        b16 = lora_b.to(torch.float16).contiguous()
+        z = project16(x2d, a16, w_kr=False)
+        y = torch.empty((t, n), device=x.device, dtype=torch.float16)
+        ws, size = _gemm_ws(t, n, k, x.device)
+        _lib.call("ss_qlora_fwd", x2d.data_ptr(), x2d.stride(0), t, *_nf4_args(packed, state), n, k,
+                  _lib.ptr(bias), z.data_ptr(), b16.data_ptr(), float(scaling), y.data_ptr(),
+                  y.stride(0), _lib.ptr(ws), size, _lib.stream(x.device))
+        ctx.save_for_backward(x2d, z, a16, b16, packed)
+        ctx.state, ctx.scaling = state, float(scaling)
+        ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
+        return y.reshape(*x.shape[:-1], n)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad):
+        x2d, z, a16, b16, packed = ctx.saved_tensors
+        state = ctx.state
+        n, k = state.shape
+        t = x2d.shape[0]
+        g = grad.reshape(t, n).to(torch.float16).contiguous()
+        dz = project16(g, b16, w_kr=True, scale=ctx.scaling)        # fp16(fp16(g*s) . B)
+        db = grad16(z, g, transpose=True, scale=ctx.scaling)         # fp16(fp16(g*s)^T . Z)
+        da = grad16(dz, x2d, transpose=False)                        # fp16(dZ^T . X)
+        dx = torch.empty((t, k), device=g.device, dtype=torch.float16)
+        ws, size = _gemm_ws(t, n, k, g.device)
+        _lib.call("ss_qlora_dx", g.data_ptr(), g.stride(0), t, *_nf4_args(packed, state), n, k,
+                  dz.data_ptr(), a16.data_ptr(), dx.data_ptr(), dx.stride(0), _lib.ptr(ws), size,
+                  _lib.stream(g.device))
+        x_dtype, a_dtype, b_dtype = ctx.dtypes
+        return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
+                None, None, None, None)
 
 
 class _QLoRAProjection(torch.autograd.Function):
@@ -98,6 +184,10 @@ def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, d
         raise ValueError("scaling must be finite")
     if not 0.0 <= dropout_p < 1.0:
         raise ValueError("dropout_p must be in [0, 1)")
+    fused = (lora_a.shape[0] == 16 and (dropout_p == 0.0 or not training) and k % 64 == 0
+             and packed.data_ptr() % 16 == 0)
     with torch.cuda.device(x.device):
+        if fused:
+            return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling))
         return _QLoRAProjection.apply(x, lora_a, lora_b, packed, state, bias, float(scaling),
                                       float(dropout_p), bool(training))

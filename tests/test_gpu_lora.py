@@ -81,3 +81,68 @@ def test_qlora_projection_matches_oracle(device, t, n, k, bias):
     assert rel_norm(np16(xt.grad), dx) < 1e-2
     assert rel_norm(np16(at.grad), da) < 1e-2
     assert rel_norm(np16(bt.grad), db) < 1e-2
+
+
+@pytest.mark.parametrize("m,k", [(37, 100), (990, 1536), (990, 8960), (1, 64), (130, 16)])
+@pytest.mark.parametrize("w_kr", [False, True])
+@pytest.mark.parametrize("scale", [None, 2.0, 1.3])
+def test_rank_project_matches_numpy(device, m, k, w_kr, scale):
+    from soupsuck_amd.lora import project16
+
+    rng = np.random.default_rng(m + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    w = (rng.standard_normal((k, 16) if w_kr else (16, k)) * 0.1).astype(np.float16)
+    out = project16(torch.from_numpy(a).to(device), torch.from_numpy(w).to(device), w_kr, scale)
+    a_eff = a if scale is None else (a.astype(np.float32) * np.float32(scale)).astype(np.float16)
+    wm = w.astype(np.float64) if w_kr else w.astype(np.float64).T
+    expected = a_eff.astype(np.float64) @ wm
+    np.testing.assert_allclose(np16(out).astype(np.float64), expected, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("t,n", [(37, 100), (990, 1536), (990, 8960), (1, 64), (300, 16)])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("scale", [None, 2.0])
+def test_rank_grad_matches_numpy(device, t, n, transpose, scale):
+    from soupsuck_amd.lora import grad16
+
+    rng = np.random.default_rng(t * 7 + n)
+    p = (rng.standard_normal((t, 16)) * 0.3).astype(np.float16)
+    q = rng.standard_normal((t, n)).astype(np.float16)
+    out = grad16(torch.from_numpy(p).to(device), torch.from_numpy(q).to(device), transpose, scale)
+    q_eff = q if scale is None else (q.astype(np.float32) * np.float32(scale)).astype(np.float16)
+    expected = p.astype(np.float64).T @ q_eff.astype(np.float64)
+    if transpose:
+        expected = expected.T
+    np.testing.assert_allclose(np16(out).astype(np.float64), expected, rtol=2e-3,
+                               atol=2e-3 * max(1.0, np.sqrt(t)))
+
+
+def test_general_path_matches_fused_and_dropout_runs(device):
+    from soupsuck_amd.lora import _QLoRAProjection
+
+    rng = np.random.default_rng(5)
+    t, n, k = 64, 256, 1536
+    state = onf4.quantize_nested(random_weight(n, k, seed=4))
+    packed, qs = device_state(state, device)
+    x = torch.from_numpy(rng.standard_normal((t, k)).astype(np.float16)).to(device)
+    a = torch.from_numpy(((rng.random((16, k)) * 2 - 1) / 40).astype(np.float16)).to(device)
+    b = torch.from_numpy((rng.standard_normal((n, 16)) * 0.01).astype(np.float16)).to(device)
+    g = torch.from_numpy((rng.standard_normal((t, n)) * 0.01).astype(np.float16)).to(device)
+    outs, grads = [], []
+    for general in (False, True):
+        xs, as_, bs = (v.clone().requires_grad_() for v in (x, a, b))
+        if general:
+            out = _QLoRAProjection.apply(xs, as_, bs, packed, qs, None, 2.0, 0.0, True)
+        else:
+            out = qlora_projection(xs, as_, bs, packed, qs, None, 2.0)
+        out.backward(g)
+        outs.append(np16(out).astype(np.float64))
+        grads.append([np16(v.grad).astype(np.float64) for v in (xs, as_, bs)])
+    np.testing.assert_allclose(outs[0], outs[1], rtol=2e-3, atol=2e-3)
+    for g0, g1 in zip(*grads):
+        assert rel_norm(g0, g1) < 1e-2
+    xs = x.clone().requires_grad_()
+    out = qlora_projection(xs, a.clone().requires_grad_(), b.clone().requires_grad_(), packed, qs,
+                           None, 2.0, dropout_p=0.1)
+    out.backward(g)
+    assert torch.isfinite(out).all() and torch.isfinite(xs.grad).all()
