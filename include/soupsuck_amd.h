@@ -54,6 +54,15 @@ int ss_nf4_dequant_nested(const uint8_t* packed, const uint8_t* qabs, const floa
                           const float* code2, const float* offset, uint16_t* out, int64_t n,
                           void* stream);
 
+/* A2, transposed: out[kk][nn] = Wdec[nn][kk] for a weight of shape [rows, cols]
+ * (out is [cols, rows] row-major), bit-exact like ss_nf4_dequant_nested.  The
+ * backward's large-T path decodes W^T once and runs dX = dY . W as a
+ * K-contiguous GEMM.  Needs cols % 64 == 0, 8-byte aligned packed and 16-byte
+ * aligned out (SS_ERR_UNSUPPORTED otherwise). */
+int ss_nf4_dequant_nested_t(const uint8_t* packed, const uint8_t* qabs, const float* absmax2,
+                            const float* code2, const float* offset, uint16_t* out,
+                            int64_t rows, int64_t cols, void* stream);
+
 /* A3. out[i] = fp16(NF4[nib(i)] * absmax[i/64]) with an already reconstructed
  * fp32 absmax.  Replaces _dequantize_flat_into / nf4_decode_kernel[NESTED=False]
  * (solution/kernels/nf4.py:181-187), the bnb backend _dequantize_4bit_impl

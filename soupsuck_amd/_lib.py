@@ -33,6 +33,7 @@ SIGNATURES = {
     "ss_last_error": [],
     "ss_nf4_dequant_nested": [_c_void_p] * 6 + [_i64, _c_void_p],
     "ss_nf4_dequant_flat": [_c_void_p] * 3 + [_i64, _c_void_p],
+    "ss_nf4_dequant_nested_t": [_c_void_p] * 6 + [_i64, _i64, _c_void_p],
     "ss_nf4_gemm_fwd": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p,
                                                                    _c_void_p, _i64, _c_void_p,
                                                                    _size, _c_void_p],

@@ -23,6 +23,8 @@
 // slice.  LDS rows are padded by 8 halves (16 B) so the 16 lanes that read one
 // MFMA fragment column (16 rows, same k) hit distinct bank groups.
 
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace ss {
@@ -62,6 +64,7 @@ struct GemmParams {
   const half_t* lb;   // lora_B [N, 16] (EPI_LORA) or lora_A [16, ldlb] (EPI_RANK)
   int64_t ldlb;
   float lscale;
+  int remap;   // XCD-aware tile numbering (default on)
 };
 
 constexpr int kThreads = 256;
@@ -81,36 +84,58 @@ union Vec16 {
 template <int R, int BK, int OP>
 struct Loader;
 
+// Loads are branch-free on the vector path: an out-of-range chunk reads a
+// clamped, valid address and is zeroed when it is written to LDS (a per-chunk
+// valid bit).  A divergent vector/scalar if-else writing the same registers
+// would force a wait on every outstanding load (write-after-write across the
+// exec-masked paths) and serialise the tile fetch.  The scalar path is taken
+// only under the uniform `vec` flag (unaligned or K % 8 != 0 operands).
+
 template <int R, int BK>
 struct Loader<R, BK, OP_ROW> {
   static constexpr int kChunks = R * BK / 8 / kThreads;
   static_assert(kChunks >= 1 && R * BK / 8 % kThreads == 0, "tile/thread mismatch");
-  Vec16 v[kChunks];
-  __device__ void load(const half_t* __restrict__ ptr, int64_t ld, int vec, int64_t r0,
+  u32x4 v[kChunks];
+  uint32_t ok;
+  template <bool VEC>
+  __device__ __forceinline__ void load(const half_t* __restrict__ ptr, int64_t ld, int64_t r0,
                        int64_t rmax, int64_t k0, int64_t kmax, const Nf4View&) {
+    ok = 0;
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + kThreads * i;
-      const int row = c / (BK / 8);
-      const int kc = c % (BK / 8);
-      const int64_t gr = r0 + row;
-      const int64_t gk = k0 + kc * 8;
-      if (gr < rmax && vec && gk + 8 <= kmax) {
-        v[i].u = *reinterpret_cast<const uint4*>(ptr + gr * ld + gk);
-      } else {
+      for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int64_t gr = r0 + c / (BK / 8);
+        const int64_t gk = k0 + (c % (BK / 8)) * 8;
+        const bool in = gr < rmax && gk < kmax;
+        ok |= (uint32_t)in << i;
+        const int64_t rr = in ? gr : 0;
+        const int64_t kk = in ? gk : 0;
+        v[i] = *reinterpret_cast<const u32x4*>(ptr + rr * ld + kk);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int64_t gr = r0 + c / (BK / 8);
+        const int64_t gk = k0 + (c % (BK / 8)) * 8;
+        half8 t;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          v[i].h[j] = (gr < rmax && gk + j < kmax) ? ptr[gr * ld + gk + j] : (half_t)0.0f;
+          t[j] = (gr < rmax && gk + j < kmax) ? ptr[gr * ld + gk + j] : (half_t)0.0f;
+        v[i] = __builtin_bit_cast(u32x4, t);
       }
+      ok = ~0u;
     }
   }
-  __device__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
+  __device__ __forceinline__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = threadIdx.x + kThreads * i;
       const int row = c / (BK / 8);
       const int kc = c % (BK / 8);
-      *reinterpret_cast<uint4*>(lds + row * (BK + kPad) + kc * 8) = v[i].u;
+      const u32x4 val = ((ok >> i) & 1u) ? v[i] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(lds + row * (BK + kPad) + kc * 8) = val;
     }
   }
 };
@@ -119,35 +144,51 @@ template <int R, int BK>
 struct Loader<R, BK, OP_COL> {
   static constexpr int kChunks = R * BK / 8 / kThreads;
   static_assert(kChunks >= 1 && R * BK / 8 % kThreads == 0, "tile/thread mismatch");
-  Vec16 v[kChunks];
+  u32x4 v[kChunks];
+  uint32_t ok;
   // Lanes walk k fastest so that the transposed 2-byte LDS writes of one
   // instruction land on consecutive addresses (no bank conflicts).
-  __device__ void load(const half_t* __restrict__ ptr, int64_t ld, int vec, int64_t r0,
+  template <bool VEC>
+  __device__ __forceinline__ void load(const half_t* __restrict__ ptr, int64_t ld, int64_t r0,
                        int64_t rmax, int64_t k0, int64_t kmax, const Nf4View&) {
+    ok = 0;
+    if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + kThreads * i;
-      const int k = c % BK;
-      const int rc = c / BK;
-      const int64_t gk = k0 + k;
-      const int64_t gr = r0 + rc * 8;
-      if (gk < kmax && vec && gr + 8 <= rmax) {
-        v[i].u = *reinterpret_cast<const uint4*>(ptr + gk * ld + gr);
-      } else {
+      for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int64_t gk = k0 + c % BK;
+        const int64_t gr = r0 + (c / BK) * 8;
+        const bool in = gk < kmax && gr < rmax;
+        ok |= (uint32_t)in << i;
+        const int64_t kk = in ? gk : 0;
+        const int64_t rr = in ? gr : 0;
+        v[i] = *reinterpret_cast<const u32x4*>(ptr + kk * ld + rr);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + kThreads * i;
+        const int64_t gk = k0 + c % BK;
+        const int64_t gr = r0 + (c / BK) * 8;
+        half8 t;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          v[i].h[j] = (gk < kmax && gr + j < rmax) ? ptr[gk * ld + gr + j] : (half_t)0.0f;
+          t[j] = (gk < kmax && gr + j < rmax) ? ptr[gk * ld + gr + j] : (half_t)0.0f;
+        v[i] = __builtin_bit_cast(u32x4, t);
       }
+      ok = ~0u;
     }
   }
-  __device__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
+  __device__ __forceinline__ void store(half_t* __restrict__ lds, const float*, const float*, float) {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = threadIdx.x + kThreads * i;
       const int k = c % BK;
       const int rc = c / BK;
+      const u32x4 val = ((ok >> i) & 1u) ? v[i] : u32x4{0u, 0u, 0u, 0u};
+      const half8 h = __builtin_bit_cast(half8, val);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) lds[(rc * 8 + j) * (BK + kPad) + k] = v[i].h[j];
+      for (int j = 0; j < 8; ++j) lds[(rc * 8 + j) * (BK + kPad) + k] = h[j];
     }
   }
 };
@@ -184,29 +225,29 @@ struct Loader<R, BK, OP_NF4_ROW> {
   static constexpr int kParts = BK / ELEMS;
   uint32_t words[ELEMS / 8];
   Nf4Stage st;
-  __device__ void load(const half_t*, int64_t, int, int64_t r0, int64_t rmax, int64_t k0,
+  template <bool VEC>
+  __device__ __forceinline__ void load(const half_t*, int64_t, int64_t r0, int64_t rmax, int64_t k0,
                        int64_t kmax, const Nf4View& w) {
     const int row = threadIdx.x / kParts;
     const int part = threadIdx.x % kParts;
     const int64_t gr = r0 + row;
     const int64_t gk = k0 + part * ELEMS;
     st.valid = gr < rmax && gk < kmax;
-    if (st.valid) {
-      const int64_t e = gr * w.cols + gk;
-      const uint8_t* src = w.packed + (e >> 1);
-      if constexpr (ELEMS == 32) {
-        uint4 t = *reinterpret_cast<const uint4*>(src);
-        words[0] = t.x; words[1] = t.y; words[2] = t.z; words[3] = t.w;
-      } else {
-        uint2 t = *reinterpret_cast<const uint2*>(src);
-        words[0] = t.x; words[1] = t.y;
-      }
-      const int64_t block = e >> 6;
-      st.q = w.qabs[block];
-      st.a2 = w.absmax2[block >> 8];
+    // Clamped, always-valid address; invalid runs are zeroed in store().
+    const int64_t e = st.valid ? gr * w.cols + gk : 0;
+    const uint8_t* src = w.packed + (e >> 1);
+    if constexpr (ELEMS == 32) {
+      const u32x4 t = *reinterpret_cast<const u32x4*>(src);
+      words[0] = t[0]; words[1] = t[1]; words[2] = t[2]; words[3] = t[3];
+    } else {
+      uint2 t = *reinterpret_cast<const uint2*>(src);
+      words[0] = t.x; words[1] = t.y;
     }
+    const int64_t block = e >> 6;
+    st.q = w.qabs[block];
+    st.a2 = w.absmax2[block >> 8];
   }
-  __device__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
+  __device__ __forceinline__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
                         const float* __restrict__ lut, float offset) {
     const int row = threadIdx.x / kParts;
     const int part = threadIdx.x % kParts;
@@ -235,29 +276,28 @@ struct Loader<R, BK, OP_NF4_COL> {
   static_assert(kThreads % BK == 0 && R / ELEMS == kThreads / BK, "tile/thread mismatch");
   uint32_t words[ELEMS / 8];
   Nf4Stage st;
-  __device__ void load(const half_t*, int64_t, int, int64_t r0, int64_t rmax, int64_t k0,
+  template <bool VEC>
+  __device__ __forceinline__ void load(const half_t*, int64_t, int64_t r0, int64_t rmax, int64_t k0,
                        int64_t kmax, const Nf4View& w) {
     const int krow = threadIdx.x % BK;
     const int cg = threadIdx.x / BK;
     const int64_t gk = k0 + krow;
     const int64_t gr = r0 + cg * ELEMS;
     st.valid = gk < kmax && gr < rmax;
-    if (st.valid) {
-      const int64_t e = gk * w.cols + gr;
-      const uint8_t* src = w.packed + (e >> 1);
-      if constexpr (ELEMS == 32) {
-        uint4 t = *reinterpret_cast<const uint4*>(src);
-        words[0] = t.x; words[1] = t.y; words[2] = t.z; words[3] = t.w;
-      } else {
-        uint2 t = *reinterpret_cast<const uint2*>(src);
-        words[0] = t.x; words[1] = t.y;
-      }
-      const int64_t block = e >> 6;
-      st.q = w.qabs[block];
-      st.a2 = w.absmax2[block >> 8];
+    const int64_t e = st.valid ? gk * w.cols + gr : 0;
+    const uint8_t* src = w.packed + (e >> 1);
+    if constexpr (ELEMS == 32) {
+      const u32x4 t = *reinterpret_cast<const u32x4*>(src);
+      words[0] = t[0]; words[1] = t[1]; words[2] = t[2]; words[3] = t[3];
+    } else {
+      uint2 t = *reinterpret_cast<const uint2*>(src);
+      words[0] = t.x; words[1] = t.y;
     }
+    const int64_t block = e >> 6;
+    st.q = w.qabs[block];
+    st.a2 = w.absmax2[block >> 8];
   }
-  __device__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
+  __device__ __forceinline__ void store(half_t* __restrict__ lds, const float* __restrict__ code2,
                         const float* __restrict__ lut, float offset) {
     const int krow = threadIdx.x % BK;
     const int cg = threadIdx.x / BK;
@@ -287,6 +327,13 @@ struct Tile {
   static constexpr int kLdk = BK + kPad;
 };
 
+__device__ __forceinline__ int64_t xcd_remap(int64_t p, int64_t n) {
+  constexpr int64_t kXcd = 8;
+  const int64_t q = n / kXcd, r = n % kXcd;
+  const int64_t x = p % kXcd, local = p / kXcd;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+
 template <int CT>
 __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta) {
   if constexpr (CT == SS_F16) {
@@ -300,7 +347,7 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
   }
 }
 
-template <class T, int OPA, int OPB, int CT, int EPI>
+template <class T, int OPA, int OPB, int CT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int BM = T::kBM, BN = T::kBN, BK = T::kBK, WM = T::kWM, WN = T::kWN;
   constexpr int LDK = T::kLdk;
@@ -315,8 +362,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   const int wave = tid / kWave;
   const int wm = wave / T::kWavesN;
   const int wn = wave % T::kWavesN;
-  const int64_t n0 = (int64_t)blockIdx.x * BN;
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+  // L2).  Renumber so that every XCD owns a contiguous range of tiles, and walk
+  // tiles M-fastest: the M-tiles that share one weight (B) tile run back to
+  // back on the same XCD and re-read it from that XCD's L2.
+  const int64_t mtiles = cdiv(p.M, BM);
+  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
+  const int64_t m0 = (tile % mtiles) * BM;
+  const int64_t n0 = (tile / mtiles) * BN;
 
   float offset = 0.0f;
   if constexpr (kNf4) {
@@ -329,11 +382,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   Loader<BN, BK, OPB> lb;
   const int64_t ktiles = cdiv(p.K, BK);
 
-  la.load(p.A, p.lda, p.a_vec, m0, p.M, 0, p.K, p.w);
-  lb.load(p.B, p.ldb, p.b_vec, n0, p.N, 0, p.K, p.w);
+  if (ktiles > 0) {
+    la.template load<VEC>(p.A, p.lda, m0, p.M, 0, p.K, p.w);
+    lb.template load<VEC>(p.B, p.ldb, n0, p.N, 0, p.K, p.w);
+  }
   __syncthreads();  // code tables visible before the first decode
-  la.store(sA[0], s_code2, s_lut, offset);
-  lb.store(sB[0], s_code2, s_lut, offset);
+  if (ktiles > 0) {
+    la.store(sA[0], s_code2, s_lut, offset);
+    lb.store(sB[0], s_code2, s_lut, offset);
+  }
   __syncthreads();
 
   float4v acc[WM / 16][WN / 16];
@@ -350,8 +407,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
     const bool more = kt + 1 < ktiles;
     if (more) {
       const int64_t k0 = (kt + 1) * BK;
-      la.load(p.A, p.lda, p.a_vec, m0, p.M, k0, p.K, p.w);
-      lb.load(p.B, p.ldb, p.b_vec, n0, p.N, k0, p.K, p.w);
+      la.template load<VEC>(p.A, p.lda, m0, p.M, k0, p.K, p.w);
+      lb.template load<VEC>(p.B, p.ldb, n0, p.N, k0, p.K, p.w);
     }
     const half_t* a_tile = sA[cur] + (wm * WM + frag_row) * LDK + frag_k;
     const half_t* b_tile = sB[cur] + (wn * WN + frag_row) * LDK + frag_k;
@@ -441,25 +498,77 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
 
 using TileBig = Tile<128, 128, 64, 64, 64>;
 using TileSmall = Tile<64, 64, 64, 32, 32>;
+using TileWide = Tile<256, 128, 64, 128, 64>;
+using TileTall = Tile<128, 256, 64, 64, 128>;
+
+static int remap_setting() {
+  static int v = [] {
+    const char* e = getenv("SS_GEMM_REMAP");
+    return e ? atoi(e) : 1;
+  }();
+  return v;
+}
 
 template <class T, int OPA, int OPB, int CT, int EPI>
-static int launch(const GemmParams& p, hipStream_t stream, const char* name) {
-  dim3 grid((unsigned)cdiv(p.N, T::kBN), (unsigned)cdiv(p.M, T::kBM));
-  hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT, EPI>), grid, dim3(kThreads), 0, stream, p);
+static int launch(const GemmParams& p0, hipStream_t stream, const char* name) {
+  GemmParams p = p0;
+  p.remap = remap_setting();
+  dim3 grid((unsigned)(cdiv(p.N, T::kBN) * cdiv(p.M, T::kBM)));
+  // Vector (branch-free, 16-byte) operand loads when both operands allow them;
+  // the scalar variant is a separate instantiation so the hot loop stays small.
+  constexpr bool kAnyNf4 = OPA >= OP_NF4_ROW || OPB >= OP_NF4_ROW;
+  const bool vec = (OPA >= OP_NF4_ROW || p.a_vec) && (OPB >= OP_NF4_ROW || p.b_vec);
+  if (kAnyNf4 || vec) {
+    hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT, EPI, true>), grid, dim3(kThreads), 0, stream,
+                       p);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<T, OPA, OPB, CT, EPI, false>), grid, dim3(kThreads), 0, stream,
+                       p);
+  }
   SS_CHECK_LAUNCH(name);
   return SS_OK;
 }
 
-// Pick the tile: the 128x128 tile when it still yields enough workgroups to
-// cover the 256 CUs, the 64x64 tile otherwise.
-static bool use_small_tile(int64_t m, int64_t n) {
-  return cdiv(m, 128) * cdiv(n, 128) < 256;
+// Tile choice: the largest tile whose workgroup count still covers the 256 CUs
+// (large wave tiles cut LDS traffic per MFMA), else 128x128, else 64x64.
+// SS_GEMM_TILE (1..4 = 64x64, 128x128, 256x128, 128x256) overrides it; it is a
+// tuning knob for the shape sweep, read once per process.
+enum TileId { TILE_AUTO = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_WIDE = 3, TILE_TALL = 4 };
+
+static int tile_override() {
+  static int v = [] {
+    const char* e = getenv("SS_GEMM_TILE");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+static int pick_tile(int64_t m, int64_t n) {
+  const int forced = tile_override();
+  if (forced >= TILE_SMALL && forced <= TILE_TALL) return forced;
+  const int64_t wide = cdiv(m, 256) * cdiv(n, 128);
+  const int64_t tall = cdiv(m, 128) * cdiv(n, 256);
+  if (m >= 1024 && wide >= 240) return TILE_WIDE;
+  if (n >= 1024 && tall >= 240 && m >= 512) return TILE_TALL;
+  if (cdiv(m, 128) * cdiv(n, 128) >= 256) return TILE_BIG;
+  return TILE_SMALL;
 }
 
 template <int OPA, int OPB, int CT, int EPI = EPI_PLAIN>
 static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
-  if (use_small_tile(p.M, p.N)) return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
-  return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
+  if constexpr (OPA >= OP_NF4_ROW || OPB >= OP_NF4_ROW) {
+    // The in-register NF4 decoders handle 128- and 64-row weight tiles.
+    if (cdiv(p.M, 128) * cdiv(p.N, 128) >= 256 || tile_override() == TILE_BIG)
+      return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
+    return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
+  } else {
+    switch (pick_tile(p.M, p.N)) {
+      case TILE_WIDE: return launch<TileWide, OPA, OPB, CT, EPI>(p, stream, name);
+      case TILE_TALL: return launch<TileTall, OPA, OPB, CT, EPI>(p, stream, name);
+      case TILE_BIG: return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
+      default: return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
+    }
+  }
 }
 
 static bool aligned16(const void* ptr, int64_t ld) {
@@ -471,9 +580,16 @@ static bool aligned16(const void* ptr, int64_t ld) {
 using namespace ss;
 
 extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
-  // Large T: decoding W once into fp16 and running the dense GEMM costs one
-  // extra pass over W (2.5 B/weight) but removes ceil(T/BM) redundant decodes.
-  if (t >= 4096 && n > 0 && k > 0) return (size_t)n * (size_t)k * sizeof(uint16_t);
+  // From T rows on, decoding W once into fp16 (one 2.5 B/weight HBM pass)
+  // and running the dense MFMA GEMM beats decoding every W tile again for each
+  // of the ceil(T/BM) row tiles: in-loop decode costs about 1/(2*BM) VALU
+  // decodes per flop, more than the VALU can issue next to full-rate MFMA.
+  // SS_NF4_DECODE_FIRST_T overrides the crossover (tuning knob).
+  static const int64_t threshold = [] {
+    const char* e = getenv("SS_NF4_DECODE_FIRST_T");
+    return e ? (int64_t)atoll(e) : (int64_t)256;
+  }();
+  if (t >= threshold && n > 0 && k > 0) return (size_t)n * (size_t)k * sizeof(uint16_t);
   return 0;
 }
 
@@ -516,14 +632,15 @@ template <int EPI>
 static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                   hipStream_t s) {
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
+    // Decode W^T [k, n] once; dX = dY . W is then the K-contiguous NT product.
     const Nf4View& w = p.w;
-    int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
-                                  reinterpret_cast<uint16_t*>(workspace), n * k, s);
+    int r = ss_nf4_dequant_nested_t(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                    reinterpret_cast<uint16_t*>(workspace), n, k, s);
     if (r) return r;
     p.B = reinterpret_cast<const half_t*>(workspace);
-    p.ldb = k;
-    p.b_vec = 1;
-    return dispatch<OP_ROW, OP_COL, SS_F16, EPI>(p, s, "gemm_kernel<f16 nn>");
+    p.ldb = n;
+    p.b_vec = n % 8 == 0;
+    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>");
   }
   return dispatch<OP_ROW, OP_NF4_COL, SS_F16, EPI>(p, s, "gemm_kernel<nf4 dx>");
 }
@@ -547,7 +664,8 @@ static GemmParams dx_params(const uint16_t* dy, int64_t lddy, int64_t t, const u
                             int64_t lddx, int accumulate) {
   GemmParams p{};
   p.M = t; p.N = k; p.K = n;
-  p.A = reinterpret_cast<const half_t*>(dy); p.lda = lddy; p.a_vec = aligned16(dy, lddy);
+  p.A = reinterpret_cast<const half_t*>(dy); p.lda = lddy;
+  p.a_vec = aligned16(dy, lddy) && n % 8 == 0;
   p.w = Nf4View{packed, qabs, absmax2, code2, offset, k};
   p.C = dx; p.ldc = lddx; p.alpha = 1.0f; p.beta = accumulate ? 1 : 0;
   return p;
@@ -645,8 +763,12 @@ extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64
                "%s: leading dimensions too small", fn);
   GemmParams p{};
   p.M = m; p.N = n; p.K = k;
-  p.A = reinterpret_cast<const half_t*>(a); p.lda = lda; p.a_vec = aligned16(a, lda);
-  p.B = reinterpret_cast<const half_t*>(b); p.ldb = ldb; p.b_vec = aligned16(b, ldb);
+  // Vector loads need 16-byte aligned rows and no 8-element chunk crossing the
+  // end of the contiguous dimension (K for row-major operands, M/N otherwise).
+  p.A = reinterpret_cast<const half_t*>(a); p.lda = lda;
+  p.a_vec = aligned16(a, lda) && (a_trans ? m % 8 == 0 : k % 8 == 0);
+  p.B = reinterpret_cast<const half_t*>(b); p.ldb = ldb;
+  p.b_vec = aligned16(b, ldb) && (b_trans ? k % 8 == 0 : n % 8 == 0);
   p.bias = reinterpret_cast<const half_t*>(bias);
   p.C = c; p.ldc = ldc; p.alpha = alpha; p.beta = beta != 0.0f;
   hipStream_t s = (hipStream_t)stream;

@@ -69,6 +69,70 @@ __global__ __launch_bounds__(256) void nf4_dequant_scalar_kernel(
   }
 }
 
+// Transposed decode: out[k][n] = Wdec[n][k] for W [rows, cols] with cols % 64
+// == 0, so that the backward GEMM dX = dY . W reads W^T with k contiguous.
+// One 256-thread workgroup per 64 x 64 tile: thread (part = tid / 64,
+// row = tid % 64) decodes 16 consecutive columns of one weight row (one
+// 64-block run, one scale) and writes them transposed into LDS, where the 64
+// lanes of a wave touch 64 consecutive halves; the tile then leaves as
+// 16-byte row stores of W^T.
+__global__ __launch_bounds__(256) void nf4_dequant_t_kernel(
+    const uint8_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
+    const float* __restrict__ absmax2, const float* __restrict__ code2,
+    const float* __restrict__ offset_ptr, half_t* __restrict__ out, int64_t rows, int64_t cols) {
+  constexpr int LD = 64 + 8;
+  __shared__ __attribute__((aligned(16))) half_t tile[64 * LD];  // [k][n]
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
+  __syncthreads();
+  const float offset = offset_ptr[0];
+  const int64_t ntiles = cdiv(rows, 64);
+  const int64_t n0 = (blockIdx.x % ntiles) * 64;
+  const int64_t k0 = (blockIdx.x / ntiles) * 64;
+  const int nl = threadIdx.x & 63;
+  const int part = threadIdx.x >> 6;
+  const int64_t n = n0 + nl;
+  half_t vals[16];
+  if (n < rows) {
+    const int64_t e = n * cols + k0 + part * 16;
+    const uint2 w = *reinterpret_cast<const uint2*>(packed + (e >> 1));
+    const float scale = nested_scale(qabs, absmax2, code2, offset, e >> 6);
+    const uint32_t words[2] = {w.x, w.y};
+#pragma unroll
+    for (int wi = 0; wi < 2; ++wi)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
+        vals[8 * wi + 2 * b] = f32_to_f16(lut[byte >> 4] * scale);
+        vals[8 * wi + 2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vals[j] = (half_t)0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) tile[(part * 16 + j) * LD + nl] = vals[j];
+  __syncthreads();
+  // 64 k-rows x 8 chunks of 8 n; two chunks per thread.
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int chunk = threadIdx.x + 256 * c;
+    const int kr = chunk >> 3;
+    const int nc = (chunk & 7) * 8;
+    const int64_t k = k0 + kr;
+    const int64_t nn = n0 + nc;
+    const half8 v = *reinterpret_cast<const half8*>(tile + kr * LD + nc);
+    half_t* dst = out + k * rows + nn;
+    if (nn + 8 <= rows && rows % 8 == 0) {
+      *reinterpret_cast<half8*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (nn + j < rows) dst[j] = v[j];
+    }
+  }
+}
+
 static int grid_for(int64_t work, int threads) {
   // Enough waves to cover every CU several times; the loops are grid-stride.
   int64_t blocks = cdiv(work, threads);
@@ -115,6 +179,27 @@ extern "C" int ss_nf4_dequant_nested(const uint8_t* packed, const uint8_t* qabs,
                "ss_nf4_dequant_nested: null pointer");
   return ss::launch_dequant<true>(packed, qabs, nullptr, absmax2, code2, offset, out, n,
                                   (hipStream_t)stream);
+}
+
+extern "C" int ss_nf4_dequant_nested_t(const uint8_t* packed, const uint8_t* qabs,
+                                       const float* absmax2, const float* code2,
+                                       const float* offset, uint16_t* out, int64_t rows,
+                                       int64_t cols, void* stream) {
+  const char* fn = "ss_nf4_dequant_nested_t";
+  SS_CHECK_ARG(rows >= 0 && cols >= 0, "%s: negative size", fn);
+  if (rows == 0 || cols == 0) return SS_OK;
+  SS_CHECK_ARG(packed && qabs && absmax2 && code2 && offset && out, "%s: null pointer", fn);
+  if (cols % 64 != 0 || reinterpret_cast<uintptr_t>(packed) % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(out) % 16 != 0) {
+    ss::set_error("%s: needs cols %% 64 == 0, 8-byte aligned packed and 16-byte aligned out", fn);
+    return SS_ERR_UNSUPPORTED;
+  }
+  const int64_t tiles = ss::cdiv(rows, 64) * (cols / 64);
+  hipLaunchKernelGGL(ss::nf4_dequant_t_kernel, dim3((unsigned)tiles), dim3(256), 0,
+                     (hipStream_t)stream, packed, qabs, absmax2, code2, offset,
+                     reinterpret_cast<ss::half_t*>(out), rows, cols);
+  SS_CHECK_LAUNCH("nf4_dequant_t_kernel");
+  return SS_OK;
 }
 
 extern "C" int ss_nf4_dequant_flat(const uint8_t* packed, const float* absmax, uint16_t* out,

@@ -155,3 +155,16 @@ def test_gpu_encoder_matches_restated_encoder(device, shape):
     ref_q, ref_a2, _, _ = onf4.double_quant(ref_absmax, offset=offset.cpu().numpy())
     np.testing.assert_array_equal(absmax2.cpu().numpy(), ref_a2)
     np.testing.assert_array_equal(qabs.cpu().numpy(), ref_q)
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (256, 1536), (1536, 8960), (8960, 1536), (37, 128),
+                                   (100, 192)])
+def test_transposed_decode_bit_exact(device, shape):
+    state = onf4.quantize_nested(random_weight(*shape, seed=11))
+    packed, qs = device_state(state, device)
+    rows, cols = shape
+    out = torch.empty((cols, rows), device=device, dtype=torch.float16)
+    _lib.call("ss_nf4_dequant_nested_t", packed.data_ptr(), qs.absmax.data_ptr(),
+              qs.state2.absmax.data_ptr(), qs.state2.code.data_ptr(), qs.offset.data_ptr(),
+              out.data_ptr(), rows, cols, _lib.stream(device))
+    np.testing.assert_array_equal(bits(out), state.decode().T.view(np.int16))
