@@ -42,7 +42,37 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
+                        "FETCH_SIZE / WRITE_SIZE to bytes) and exit")
     return p.parse_args()
+
+
+def copy_calibration(mib):
+    """Plain copy kernel of known size: each dispatch reads and writes exactly mib MiB."""
+    import torch
+
+    n = mib << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    print(json.dumps({"copy_calibration_bytes_per_dispatch": n, "dispatches": 10}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per entry-point call from the committed rocprofv3 --pmc summaries
+    (FETCH_SIZE and WRITE_SIZE passes, each scaled by a copy kernel of known size)."""
+    found = {}
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic-json:"):
+                for key, val in json.loads(line.split(":", 1)[1]).items():
+                    found[key] = (val["traffic_bytes"], path.name)
+    return found
 
 
 def lengths_config1():
@@ -52,15 +82,10 @@ def lengths_config1():
     return [int(v) for v in torch.randint(80, 401, (4,), generator=gen)]
 
 
-def tile_name(kind, t, n, k):
-    """Kernel instantiation the C ABI picks for this call (mirrors csrc/gemm.hip dispatch)."""
-    m_dim, n_dim = (t, n) if kind == "fwd" else (t, k)
-    small = -(-m_dim // 128) * -(-n_dim // 128) < 256
-    return f"nf4_{kind}_{'64x64' if small else '128x128'}"
-
-
 class KernelTimer:
-    """HIP events around every NF4 GEMM launch, on the launch stream (torch's current)."""
+    """HIP events around every NF4 GEMM entry point call, on its launch stream (torch's
+    current stream), keyed by entry point and shape.  One call is one launch sequence
+    (e.g. decode-first: the NF4 decode kernel, then the MFMA GEMM kernel)."""
 
     def __init__(self):
         import torch
@@ -84,9 +109,8 @@ class KernelTimer:
         end.record()
         _, a, start = self._pending
         self._pending = None
-        kind = "fwd" if name in ("ss_nf4_gemm_fwd", "ss_qlora_fwd") else "dx"
         t, n, k = a[2], a[8], a[9]
-        self.records.append((tile_name(kind, t, n, k), 2.0 * t * n * k, start, end))
+        self.records.append((f"{name}[T={t},N={n},K={k}]", 2.0 * t * n * k, start, end))
 
     def summary(self):
         per = {}
@@ -143,6 +167,9 @@ def main():
               f"{world} requested); the multi-GPU sharding is a design note, not a run.",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     import torch
 
@@ -188,9 +215,11 @@ def main():
     kernels = timer.summary()
     dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
     dk = kernels[dominant]
+    traffic, source = measured_traffic().get(dominant, (None, None))
     roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(dk["tflops"], 2),
                 "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(dk["tflops"] / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "frac": round(dk["tflops"] / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
+                "traffic_source": source,
                 "avg_launch_us": round(dk["avg_us"], 3),
                 "gflop_per_launch": round(dk["avg_gflop"], 4)}
 
