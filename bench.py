@@ -9,14 +9,19 @@ followed by their backward (dX, dA, dB).  Inputs are seeded synthetic tensors
 already resident in HBM.
 
 value      = algorithmic TFLOP/s of the whole step (base fwd + dX, LoRA fwd/bwd)
-ms_per_step = the layer's fwd+bwd time (the metric's "QLoRA layer fwd+bwd ms")
-roofline   = the dominant kernel's achieved TFLOP/s (algorithmic flops per
-             launch / average launch duration, HIP events recorded on the
-             launch stream around every launch in the timed region) against
-             the MI355X dense fp16 MFMA peak
+ms_per_step = the layer's fwd+bwd time (the metric's "QLoRA layer fwd+bwd ms"):
+             the step is captured once as a HIP graph and replayed K times
+             (same kernels, same work; no per-launch host cost).
+             eager_ms_per_step is the same step launched from Python.
+roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
+             flops per call / average call duration from HIP events recorded on
+             its launch stream around every call of eager steps queued behind
+             a GPU spin, so the calls run back to back as in the graph; ROCm
+             does not allow timing event nodes inside a captured graph)
+             against the MI355X dense fp16 MFMA peak
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-graph]
 """
 
 import argparse
@@ -41,6 +46,11 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time eager steps instead of HIP-graph replays of the step")
+    p.add_argument("--timing-steps", type=int, default=5,
+                   help="eager steps (queued behind a GPU spin) whose per-call HIP events "
+                        "give the roofline kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
@@ -75,6 +85,20 @@ def measured_traffic():
     return found
 
 
+TIMED_ENTRY_POINTS = ("ss_nf4_gemm_fwd", "ss_nf4_gemm_dx", "ss_qlora_fwd", "ss_qlora_dx")
+
+
+def sleep_cycles_per_ms(torch):
+    """Clock rate of torch.cuda._sleep's spin loop, measured with HIP events."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1000)
+    start.record()
+    torch.cuda._sleep(2_000_000)
+    end.record()
+    end.synchronize()
+    return 2_000_000 / max(start.elapsed_time(end), 1e-3)
+
+
 def lengths_config1():
     import torch
 
@@ -95,17 +119,20 @@ class KernelTimer:
         self.active = False
         self._pending = None
 
+    def _event(self):
+        return self.torch.cuda.Event(enable_timing=True)
+
     def before(self, name, args):
         if not self.active:
             return
-        start = self.torch.cuda.Event(enable_timing=True)
+        start = self._event()
         start.record()
         self._pending = (name, args, start)
 
     def after(self, name, args):
         if not self.active or self._pending is None:
             return
-        end = self.torch.cuda.Event(enable_timing=True)
+        end = self._event()
         end.record()
         _, a, start = self._pending
         self._pending = None
@@ -196,23 +223,67 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    timer = KernelTimer()
-    for name in ("ss_nf4_gemm_fwd", "ss_nf4_gemm_dx", "ss_qlora_fwd", "ss_qlora_dx"):
-        _lib.hooks[name] = (timer.before, timer.after)
-    timer.active = True
-    torch.cuda.synchronize()
+    # Eager steps: every kernel launched from Python through the C ABI.
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
+    eager_ms = 1e3 * (time.perf_counter() - t0) / args.steps
+
+    # Timed region: the same step captured once as a HIP graph
+    # (torch.cuda.CUDAGraph) and replayed K times -- identical kernels and work
+    # per step, without the per-launch host cost of the eager loop above.
+    graph, graph_error = None, None
+    if not args.no_graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            graph.replay()
+            torch.cuda.synchronize()
+        except Exception as exc:  # noqa: BLE001 - reported in the JSON line
+            graph, graph_error = None, f"{type(exc).__name__}: {exc}"[:300]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            step()
+    torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    timer.active = False
+    mode = "hip-graph replay" if graph is not None else "eager"
+
+    # Per-call timing of the NF4 entry points: HIP events recorded on the
+    # launch stream around every call of eager steps.  Each step is queued
+    # behind a GPU spin of a few ms, so the host has enqueued the whole step
+    # (events included) before the GPU reaches it and the calls run back to
+    # back as in the replayed graph: the events see GPU time, not host gaps.
+    timer = KernelTimer()
+    cycles_per_ms = sleep_cycles_per_ms(torch)
+    for name in TIMED_ENTRY_POINTS:
+        _lib.hooks[name] = (timer.before, timer.after)
+    for _ in range(args.timing_steps):
+        torch.cuda._sleep(int(cycles_per_ms * (3 * eager_ms + 2)))
+        timer.active = True
+        step()
+        timer.active = False
+        torch.cuda.synchronize()
     _lib.hooks.clear()
+    kernels = timer.summary()
 
     ms_per_step = 1e3 * elapsed / args.steps
     flops = layer.flops(tokens)
+    for v in kernels.values():
+        v["total_ms"] /= max(args.timing_steps, 1)  # per step
     value = flops / (elapsed / args.steps) / 1e12
-    kernels = timer.summary()
     dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
     dk = kernels[dominant]
     traffic, source = measured_traffic().get(dominant, (None, None))
@@ -221,7 +292,9 @@ def main():
                 "frac": round(dk["tflops"] / PEAK_FP16_TFLOPS, 4), "traffic": traffic,
                 "traffic_source": source,
                 "avg_launch_us": round(dk["avg_us"], 3),
-                "gflop_per_launch": round(dk["avg_gflop"], 4)}
+                "gflop_per_launch": round(dk["avg_gflop"], 4),
+                "timing": (f"HIP events on the launch stream around each call, {args.timing_steps}"
+                           " eager steps each queued behind a GPU spin (calls run back to back)")}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -243,6 +316,9 @@ def main():
                    "tokens": tokens, "lengths": lengths, "hidden": 1536,
                    "intermediate": 8960, "kv_out": 256, "lora_rank": 16},
         "layer_fwd_bwd_ms": round(ms_per_step, 4),
+        "step_mode": mode,
+        "eager_ms_per_step": round(eager_ms, 4),
+        "graph_error": graph_error,
         "nf4_weight_bytes_per_pass": layer.weight_bytes(),
         "roofline": roofline,
         "cpu_baseline": cpu,

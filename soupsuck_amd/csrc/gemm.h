@@ -1,0 +1,76 @@
+// Declarations shared by the GEMM kernels (gemm.hip: general operand
+// sources; gemm_nt.hip: the dense K-contiguous x K-contiguous main loop).
+#pragma once
+
+#include "common.h"
+
+namespace ss {
+
+enum Operand { OP_ROW = 0, OP_COL = 1, OP_NF4_ROW = 2, OP_NF4_COL = 3 };
+
+struct Nf4View {
+  const uint8_t* packed;
+  const uint8_t* qabs;
+  const float* absmax2;
+  const float* code2;
+  const float* offset;
+  int64_t cols;  // weight row length (elements); a multiple of 64
+};
+
+// Epilogue variants: plain (alpha * acc + bias, + beta * C); the LoRA
+// forward out = fp16(fp16(acc + bias) + fp16(fp16(Z . B^T) * s)) with Z
+// [M,16] and B = lora_B [N,16]; and a rank-16 update out = fp16(acc + dZ . A)
+// with dZ [M,16] and A = lora_A [16, N] (row stride ldlb).
+enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2 };
+
+struct GemmParams {
+  int64_t M, N, K;
+  const half_t* A;
+  int64_t lda;
+  int a_vec;  // 16-byte vector loads are aligned for A
+  const half_t* B;
+  int64_t ldb;
+  int b_vec;
+  Nf4View w;
+  const half_t* bias;
+  void* C;
+  int64_t ldc;
+  float alpha;
+  int beta;
+  const half_t* lz;   // Z or dZ, [M, 16] contiguous
+  const half_t* lb;   // lora_B [N, 16] (EPI_LORA) or lora_A [16, ldlb] (EPI_RANK)
+  int64_t ldlb;
+  float lscale;
+  int remap;   // XCD-aware tile numbering (default on)
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2).  xcd_remap renumbers a 1-D grid so that every XCD owns a contiguous
+// range of tile ids.
+__device__ __forceinline__ int64_t xcd_remap(int64_t p, int64_t n) {
+  constexpr int64_t kXcd = 8;
+  const int64_t q = n / kXcd, r = n % kXcd;
+  const int64_t x = p % kXcd, local = p / kXcd;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+
+template <int CT>
+__device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta) {
+  if constexpr (CT == SS_F16) {
+    half_t* c = reinterpret_cast<half_t*>(C);
+    if (beta) v += (float)c[idx];
+    c[idx] = f32_to_f16(v);
+  } else {
+    float* c = reinterpret_cast<float*>(C);
+    if (beta) v += c[idx];
+    c[idx] = v;
+  }
+}
+
+// Dense NT GEMM (A [M,K] and B [N,K] both K-contiguous fp16) on the
+// direct-to-LDS pipelined kernel.  Returns SS_ERR_UNSUPPORTED (nothing
+// launched) when the operands do not meet its requirements: 16-byte aligned
+// rows and K % 32 == 0.
+int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream);
+
+}  // namespace ss

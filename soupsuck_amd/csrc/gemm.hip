@@ -25,47 +25,9 @@
 
 #include <stdlib.h>
 
-#include "common.h"
+#include "gemm.h"
 
 namespace ss {
-
-enum Operand { OP_ROW = 0, OP_COL = 1, OP_NF4_ROW = 2, OP_NF4_COL = 3 };
-
-struct Nf4View {
-  const uint8_t* packed;
-  const uint8_t* qabs;
-  const float* absmax2;
-  const float* code2;
-  const float* offset;
-  int64_t cols;  // weight row length (elements); a multiple of 64
-};
-
-// Epilogue variants: plain (alpha * acc + bias, + beta * C); the LoRA
-// forward out = fp16(fp16(acc + bias) + fp16(fp16(Z . B^T) * s)) with Z
-// [M,16] and B = lora_B [N,16]; and a rank-16 update out = fp16(acc + dZ . A)
-// with dZ [M,16] and A = lora_A [16, N] (row stride ldlb).
-enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2 };
-
-struct GemmParams {
-  int64_t M, N, K;
-  const half_t* A;
-  int64_t lda;
-  int a_vec;  // 16-byte vector loads are aligned for A
-  const half_t* B;
-  int64_t ldb;
-  int b_vec;
-  Nf4View w;
-  const half_t* bias;
-  void* C;
-  int64_t ldc;
-  float alpha;
-  int beta;
-  const half_t* lz;   // Z or dZ, [M, 16] contiguous
-  const half_t* lb;   // lora_B [N, 16] (EPI_LORA) or lora_A [16, ldlb] (EPI_RANK)
-  int64_t ldlb;
-  float lscale;
-  int remap;   // XCD-aware tile numbering (default on)
-};
 
 constexpr int kThreads = 256;
 constexpr int kPad = 8;
@@ -327,26 +289,6 @@ struct Tile {
   static constexpr int kLdk = BK + kPad;
 };
 
-__device__ __forceinline__ int64_t xcd_remap(int64_t p, int64_t n) {
-  constexpr int64_t kXcd = 8;
-  const int64_t q = n / kXcd, r = n % kXcd;
-  const int64_t x = p % kXcd, local = p / kXcd;
-  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
-}
-
-template <int CT>
-__device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta) {
-  if constexpr (CT == SS_F16) {
-    half_t* c = reinterpret_cast<half_t*>(C);
-    if (beta) v += (float)c[idx];
-    c[idx] = f32_to_f16(v);
-  } else {
-    float* c = reinterpret_cast<float*>(C);
-    if (beta) v += c[idx];
-    c[idx] = v;
-  }
-}
-
 template <class T, int OPA, int OPB, int CT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
   constexpr int BM = T::kBM, BN = T::kBN, BK = T::kBK, WM = T::kWM, WN = T::kWN;
@@ -529,10 +471,10 @@ static int launch(const GemmParams& p0, hipStream_t stream, const char* name) {
   return SS_OK;
 }
 
-// Tile choice: the largest tile whose workgroup count still covers the 256 CUs
-// (large wave tiles cut LDS traffic per MFMA), else 128x128, else 64x64.
-// SS_GEMM_TILE (1..4 = 64x64, 128x128, 256x128, 128x256) overrides it; it is a
-// tuning knob for the shape sweep, read once per process.
+// Tile choice: 128x128 when it still gives every CU a workgroup, else 64x64.
+// The 256x128 / 128x256 tiles (one wave per SIMD) measured slower than
+// 128x128 at every Qwen shape, so only SS_GEMM_TILE (1..4 = 64x64, 128x128,
+// 256x128, 128x256) selects them; it is a tuning knob read once per process.
 enum TileId { TILE_AUTO = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_WIDE = 3, TILE_TALL = 4 };
 
 static int tile_override() {
@@ -546,12 +488,18 @@ static int tile_override() {
 static int pick_tile(int64_t m, int64_t n) {
   const int forced = tile_override();
   if (forced >= TILE_SMALL && forced <= TILE_TALL) return forced;
-  const int64_t wide = cdiv(m, 256) * cdiv(n, 128);
-  const int64_t tall = cdiv(m, 128) * cdiv(n, 256);
-  if (m >= 1024 && wide >= 240) return TILE_WIDE;
-  if (n >= 1024 && tall >= 240 && m >= 512) return TILE_TALL;
   if (cdiv(m, 128) * cdiv(n, 128) >= 256) return TILE_BIG;
   return TILE_SMALL;
+}
+
+// SS_GEMM_NT=0 keeps dense NT products on the register-staged kernel (A/B
+// comparison knob, read once per process).
+static bool nt_enabled() {
+  static const bool v = [] {
+    const char* e = getenv("SS_GEMM_NT");
+    return !(e && atoi(e) == 0);
+  }();
+  return v;
 }
 
 template <int OPA, int OPB, int CT, int EPI = EPI_PLAIN>
@@ -562,6 +510,16 @@ static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
       return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
     return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
   } else {
+    if constexpr (OPA == OP_ROW && OPB == OP_ROW) {
+      // Both operands K-contiguous: the pipelined direct-to-LDS kernel when its
+      // alignment / K % 32 requirements hold.
+      if (nt_enabled()) {
+        GemmParams q = p;
+        q.remap = remap_setting();
+        const int rc = gemm_nt(q, CT, EPI, stream);
+        if (rc != SS_ERR_UNSUPPORTED) return rc;
+      }
+    }
     switch (pick_tile(p.M, p.N)) {
       case TILE_WIDE: return launch<TileWide, OPA, OPB, CT, EPI>(p, stream, name);
       case TILE_TALL: return launch<TileTall, OPA, OPB, CT, EPI>(p, stream, name);

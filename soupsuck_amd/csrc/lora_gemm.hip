@@ -23,50 +23,103 @@ namespace ss {
 
 constexpr int kRank = 16;
 
+// 8 consecutive elements p[row*ld + k .. +7], zero outside rows x [.., kend).
+// VEC: the caller guarantees 16-byte aligned rows and kend % 8 == 0, so a
+// chunk is either wholly valid or wholly outside; the load is then branch-free
+// (clamped address + select), which keeps every load of a wave in flight.
+template <bool VEC>
 __device__ __forceinline__ half8 load_row8(const half_t* __restrict__ p, int64_t row,
-                                           int64_t rows, int64_t ld, int64_t k, int64_t kend,
-                                           bool vec) {
-  half8 v;
-  if (row < rows && vec && k + 8 <= kend) {
-    v = *reinterpret_cast<const half8*>(p + row * ld + k);
+                                           int64_t rows, int64_t ld, int64_t k, int64_t kend) {
+  if constexpr (VEC) {
+    const bool ok = row < rows && k < kend;
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(p + (ok ? row * ld + k : 0));
+    const u32x4 v = ok ? raw : u32x4{0u, 0u, 0u, 0u};
+    return __builtin_bit_cast(half8, v);
   } else {
+    half8 v;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       v[i] = (row < rows && k + i < kend) ? p[row * ld + k + i] : (half_t)0.0f;
+    return v;
   }
-  return v;
 }
 
+// Chunk sizes: every wave issues all loads of its chunk before its first MFMA
+// (eight 16-byte loads per lane in flight), so a chunk costs about one memory
+// round trip.  kMaxSplits bounds the fp32 partials.
+constexpr int kProjChunk = 256;  // k per rank_project wave: 8 MFMA steps of 32
+constexpr int kGradChunk = 64;   // t per rank_grad step: 2 MFMA steps of 32
+constexpr int kMaxSplits = 64;
+constexpr int kProjLd = kProjChunk + 8;  // LDS row of the staged W chunk (one rank row)
+constexpr int kGradLd = kGradChunk + 8;  // LDS row of the transposed P tile
+
+// Transposed Q tile [64 n][64 t], rows of 128 B with the 16-byte chunk index
+// XOR-swizzled by (n ^ n/8) & 7: the transposing 2-byte writes (8 rows 8 apart
+// per instruction) and the 16-byte fragment reads (8 consecutive rows) both
+// touch 8 distinct chunks, i.e. no LDS bank conflicts.
+__device__ __forceinline__ int qtile_index(int n, int t) {
+  return n * 64 + ((((t >> 3) ^ n ^ (n >> 3)) & 7) << 3) + (t & 7);
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void rank_project_kernel(
     const half_t* __restrict__ a, int64_t lda, int64_t m, int64_t k, const half_t* __restrict__ w,
-    int64_t ldw, int w_kr, int scale_a, float a_scale, float* __restrict__ part, int64_t splits,
-    int64_t kchunk, int vec) {
+    int64_t ldw, int w_kr, float a_scale, float* __restrict__ part, int64_t splits,
+    int64_t kchunk) {
+  __shared__ __attribute__((aligned(16))) half_t sw[4][kRank * kProjLd];
   const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int64_t mblocks = cdiv(m, 16);
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= mblocks * splits) return;  // the whole wave leaves together
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= mblocks * splits) return;  // no block-wide barrier below: waves are independent
   const int64_t mb = item % mblocks;
   const int64_t s = item / mblocks;
-  const int64_t kbeg = s * kchunk;
-  const int64_t kend = kbeg + kchunk < k ? kbeg + kchunk : k;
+  const int64_t send = (s + 1) * kchunk < k ? (s + 1) * kchunk : k;
   const int r = lane & 15;
   const int kq = (lane >> 4) * 8;
   const int64_t row = mb * 16 + r;
+  half_t* tile = sw[wave];
   float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
-  int it = 0;
-  for (int64_t k0 = kbeg; k0 < kend; k0 += 32, ++it) {
-    half8 av = load_row8(a, row, m, lda, k0 + kq, kend, vec);
-    if (scale_a) {
+  for (int64_t kbeg = s * kchunk; kbeg < send; kbeg += kProjChunk) {
+    const int64_t kend = kbeg + kProjChunk < send ? kbeg + kProjChunk : send;
+    half8 av[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) av[i] = f32_to_f16((float)av[i] * a_scale);
-    }
-    half8 bv;
+    for (int st = 0; st < 8; ++st) av[st] = load_row8<VEC>(a, row, m, lda, kbeg + st * 32 + kq, kend);
+    // Stage W(k, r) for k in [kbeg, kend) as tile[r][k - kbeg] (zero beyond kend).
+    if (w_kr) {
+      // w is [K][ldw]: one 32-byte row of 16 ranks per k; lane takes 8 ranks of one k.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t kk = k0 + kq + i;
-      bv[i] = kk < kend ? (w_kr ? w[kk * ldw + r] : w[r * ldw + kk]) : (half_t)0.0f;
+      for (int it = 0; it < 8; ++it) {
+        const int kk = it * 32 + (lane >> 1);
+        const int rh = (lane & 1) * 8;
+        const half8 v = load_row8<VEC>(w, kbeg + kk, kend, ldw, rh, kRank);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) tile[(rh + i) * kProjLd + kk] = v[i];
+      }
+    } else {
+      // w is [16][ldw]: each rank row is contiguous in k.
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int c = it * 64 + lane;
+        const int rr = c >> 5;
+        const int kc = (c & 31) * 8;
+        const half8 v = load_row8<VEC>(w + rr * ldw, 0, 1, 0, kbeg + kc, kend);
+        *reinterpret_cast<half8*>(tile + rr * kProjLd + kc) = v;
+      }
     }
-    acc[it & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[it & 1], 0, 0, 0);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    // fp16(a * 1.0) == a for every fp16 value, so "no scaling" is a_scale = 1.
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) av[st][i] = f32_to_f16((float)av[st][i] * a_scale);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const half8 bv = *reinterpret_cast<const half8*>(tile + r * kProjLd + st * 32 + kq);
+      acc[st & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[st], bv, acc[st & 1], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
   }
   const float4v c = acc[0] + acc[1];
 #pragma unroll
@@ -76,12 +129,13 @@ __global__ __launch_bounds__(256) void rank_project_kernel(
   }
 }
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void rank_grad_kernel(
     const half_t* __restrict__ p, int64_t ldp, const half_t* __restrict__ q, int64_t ldq,
-    int64_t t, int64_t n, int scale_q, float q_scale, float* __restrict__ part, int64_t splits,
-    int64_t tchunk, int vec) {
-  constexpr int LDT = 40;  // 32 t values + 8 pad per LDS row (one row per column of Q)
-  __shared__ __attribute__((aligned(16))) half_t sq[4][64 * LDT];
+    int64_t t, int64_t n, float q_scale, float* __restrict__ part, int64_t splits,
+    int64_t tchunk) {
+  __shared__ __attribute__((aligned(16))) half_t sq[4][64 * 64];
+  __shared__ __attribute__((aligned(16))) half_t sp[4][kRank * kGradLd];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t nblocks = cdiv(n, 64);
@@ -90,41 +144,50 @@ __global__ __launch_bounds__(256) void rank_grad_kernel(
   const int64_t nb = item % nblocks;
   const int64_t s = item / nblocks;
   const int64_t n0 = nb * 64;
-  const int64_t tbeg = s * tchunk;
-  const int64_t tend = tbeg + tchunk < t ? tbeg + tchunk : t;
+  const int64_t send = (s + 1) * tchunk < t ? (s + 1) * tchunk : t;
   half_t* tile = sq[wave];
+  half_t* ptile = sp[wave];
   const int r = lane & 15;
   const int kq = (lane >> 4) * 8;
   float4v acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = float4v{0.f, 0.f, 0.f, 0.f};
-  for (int64_t t0 = tbeg; t0 < tend; t0 += 32) {
-    // Q tile [32 t x 64 n]: lane loads 8 columns of one row; 4 passes of 8 rows.
+  for (int64_t t0 = s * tchunk; t0 < send; t0 += kGradChunk) {
+    const int64_t tend = t0 + kGradChunk < send ? t0 + kGradChunk : send;
+    // Q tile [64 t x 64 n]: 8 rows of 8 lanes per pass, 16 bytes per lane.
+    half8 v[8];
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const int tl = pass * 8 + (lane >> 3);
+    for (int it = 0; it < 8; ++it)
+      v[it] = load_row8<VEC>(q, t0 + it * 8 + (lane >> 3), tend, ldq, n0 + (lane & 7) * 8, n);
+    // P rows [64 t x 16 r]: lane takes one row (two 16-byte halves).
+    const half8 p0 = load_row8<VEC>(p, t0 + lane, tend, ldp, 0, kRank);
+    const half8 p1 = load_row8<VEC>(p, t0 + lane, tend, ldp, 8, kRank);
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int tl = it * 8 + (lane >> 3);
       const int nl = (lane & 7) * 8;
-      half8 v = load_row8(q, t0 + tl, tend, ldq, n0 + nl, n, vec);
-      if (scale_q) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = f32_to_f16((float)v[i] * q_scale);
+      for (int i = 0; i < 8; ++i) {
+        // fp16(q * 1.0) == q for every fp16 value, so "no scaling" is q_scale = 1.
+        tile[qtile_index(nl + i, tl)] = f32_to_f16((float)v[it][i] * q_scale);
       }
+    }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) tile[(nl + i) * LDT + tl] = v[i];
+    for (int i = 0; i < 8; ++i) {
+      ptile[i * kGradLd + lane] = p0[i];
+      ptile[(8 + i) * kGradLd + lane] = p1[i];
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_s_waitcnt(0);
-    // A operand: P^T (r = lane % 16, t = t0 + kq + i); small and cache resident.
-    half8 av;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t tt = t0 + kq + i;
-      av[i] = tt < tend ? p[tt * ldp + r] : (half_t)0.0f;
-    }
+    for (int kk = 0; kk < 2; ++kk) {
+      const half8 av = *reinterpret_cast<const half8*>(ptile + r * kGradLd + kk * 32 + kq);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const half8 bv = *reinterpret_cast<const half8*>(tile + (c * 16 + r) * LDT + kq);
-      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[c], 0, 0, 0);
+      for (int c = 0; c < 4; ++c) {
+        const half8 bv =
+            *reinterpret_cast<const half8*>(tile + qtile_index(c * 16 + r, kk * 32 + kq));
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[c], 0, 0, 0);
+      }
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -141,37 +204,62 @@ __global__ __launch_bounds__(256) void rank_grad_kernel(
   }
 }
 
+// Sum of part[s * stride + i] over s in split order; eight loads in flight.
+__device__ __forceinline__ float sum_splits(const float* __restrict__ part, int64_t stride,
+                                            int64_t i, int64_t splits) {
+  float acc = 0.0f;
+  int64_t s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = part[(s + j) * stride + i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += v[j];
+  }
+  for (; s < splits; ++s) acc += part[s * stride + i];
+  return acc;
+}
+
 // out[m][r] (project) = fp16(sum_s part[s][m][r]); out row stride 16.
 __global__ __launch_bounds__(256) void rank_project_reduce_kernel(const float* __restrict__ part,
                                                                   int64_t m, int64_t splits,
                                                                   half_t* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= m * kRank) return;
-  float acc = 0.0f;
-  for (int64_t s = 0; s < splits; ++s) acc += part[s * m * kRank + i];
-  out[i] = f32_to_f16(acc);
+  out[i] = f32_to_f16(sum_splits(part, m * kRank, i, splits));
 }
 
 // grad: out = fp16(sum_s part[s][r][c]) stored [16][n] (transpose = 0) or [n][16].
+// A workgroup reduces a 16-rank x 16-column block: thread (r, c) reads a
+// 64-byte run per rank row; the transposed store goes through LDS so that the
+// block writes one contiguous 512-byte run.
 __global__ __launch_bounds__(256) void rank_grad_reduce_kernel(const float* __restrict__ part,
                                                                int64_t n, int64_t splits,
                                                                int transpose,
                                                                half_t* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * kRank) return;
-  float acc = 0.0f;
-  for (int64_t s = 0; s < splits; ++s) acc += part[s * n * kRank + i];
-  const int64_t rr = i / n;
-  const int64_t c = i - rr * n;
-  out[transpose ? c * kRank + rr : i] = f32_to_f16(acc);
+  __shared__ half_t sh[kRank][kRank + 1];
+  const int rr = threadIdx.x >> 4;
+  const int cl = threadIdx.x & 15;
+  const int64_t c0 = (int64_t)blockIdx.x * kRank;
+  const int64_t c = c0 + cl;
+  const half_t v = c < n ? f32_to_f16(sum_splits(part + rr * n, kRank * n, c, splits))
+                         : (half_t)0.0f;
+  if (!transpose) {
+    if (c < n) out[rr * n + c] = v;
+    return;
+  }
+  sh[cl][rr] = v;
+  __syncthreads();
+  const int cw = threadIdx.x >> 4;  // column within the block
+  const int rw = threadIdx.x & 15;  // rank
+  if (c0 + cw < n) out[(c0 + cw) * kRank + rw] = sh[cw][rw];
 }
 
-// Split count so that the grid has about four waves per CU (1024 waves).
-static int64_t pick_splits(int64_t blocks, int64_t len, int64_t step) {
-  int64_t s = cdiv(1024, blocks > 0 ? blocks : 1);
-  const int64_t max_s = cdiv(len, step);
-  if (s > max_s) s = max_s;
-  return s < 1 ? 1 : s;
+// Chunk length along the reduced dimension: a multiple of `unit`, long enough
+// that at most kMaxSplits chunks cover `len`.
+static int64_t pick_chunk(int64_t len, int64_t unit) {
+  const int64_t per = cdiv(len > 0 ? len : 1, kMaxSplits);
+  return cdiv(per, unit) * unit;
 }
 
 static bool al16(const void* p, int64_t ld) {
@@ -184,10 +272,9 @@ using namespace ss;
 
 extern "C" size_t ss_lora_workspace_size(int64_t rows, int64_t cols) {
   // fp32 partials of either kernel for a [rows x 16] or [16 x cols] result:
-  // at most cdiv(1024, blocks) splits, blocks >= cdiv(len, 64).
+  // at most kMaxSplits chunks of the reduced dimension.
   const int64_t m = rows > cols ? rows : cols;
-  const int64_t s = cdiv(1024, cdiv(m > 0 ? m : 1, 64)) + 1;
-  return (size_t)(s * (m > 0 ? m : 1) * kRank) * sizeof(float) + 256;
+  return (size_t)(kMaxSplits * (m > 0 ? m : 1) * kRank) * sizeof(float) + 256;
 }
 
 extern "C" int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_t k,
@@ -200,19 +287,20 @@ extern "C" int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_
   SS_CHECK_ARG(a && w && out && workspace, "%s: null pointer", fn);
   SS_CHECK_ARG(lda >= k && ldw >= (w_kr ? kRank : k), "%s: leading dimension too small", fn);
   const int64_t mblocks = cdiv(m, 16);
-  int64_t splits = pick_splits(mblocks, k, 32);
-  int64_t kchunk = cdiv(cdiv(k, splits), 32) * 32;
-  if (kchunk == 0) kchunk = 32;
-  splits = cdiv(k > 0 ? k : 1, kchunk);
+  const int64_t kchunk = pick_chunk(k, kProjChunk);
+  const int64_t splits = cdiv(k > 0 ? k : 1, kchunk);
   SS_CHECK_ARG((size_t)(splits * m * kRank) * sizeof(float) <= workspace_bytes,
                "%s: workspace too small", fn);
   float* part = reinterpret_cast<float*>(workspace);
   hipStream_t s = (hipStream_t)stream;
   const int64_t waves = mblocks * splits;
-  hipLaunchKernelGGL(rank_project_kernel, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
+  // Vector loads need 16-byte aligned rows of both operands and K % 8 == 0.
+  const bool vec = al16(a, lda) && al16(w, ldw) && k % 8 == 0;
+  auto kern = vec ? rank_project_kernel<true> : rank_project_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
                      reinterpret_cast<const half_t*>(a), lda, m, k,
-                     reinterpret_cast<const half_t*>(w), ldw, w_kr, scale_a, a_scale, part,
-                     splits, kchunk, (int)al16(a, lda));
+                     reinterpret_cast<const half_t*>(w), ldw, w_kr, scale_a ? a_scale : 1.0f,
+                     part, splits, kchunk);
   SS_CHECK_LAUNCH("rank_project_kernel");
   hipLaunchKernelGGL(rank_project_reduce_kernel, dim3((unsigned)cdiv(m * kRank, 256)), dim3(256),
                      0, s, part, m, splits, reinterpret_cast<half_t*>(out));
@@ -230,20 +318,21 @@ extern "C" int ss_lora_grad(const uint16_t* p, int64_t ldp, const uint16_t* q, i
   SS_CHECK_ARG(out && workspace && (t == 0 || (p && q)), "%s: null pointer", fn);
   SS_CHECK_ARG(ldp >= kRank && ldq >= n, "%s: leading dimension too small", fn);
   const int64_t nblocks = cdiv(n, 64);
-  int64_t splits = pick_splits(nblocks, t, 32);
-  int64_t tchunk = cdiv(cdiv(t, splits), 32) * 32;
-  if (tchunk == 0) tchunk = 32;
-  splits = t > 0 ? cdiv(t, tchunk) : 1;
+  const int64_t tchunk = pick_chunk(t, kGradChunk);
+  const int64_t splits = t > 0 ? cdiv(t, tchunk) : 1;
   SS_CHECK_ARG((size_t)(splits * n * kRank) * sizeof(float) <= workspace_bytes,
                "%s: workspace too small", fn);
   float* part = reinterpret_cast<float*>(workspace);
   hipStream_t s = (hipStream_t)stream;
   const int64_t waves = nblocks * splits;
-  hipLaunchKernelGGL(rank_grad_kernel, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
+  // Vector loads need 16-byte aligned rows of P and Q and N % 8 == 0.
+  const bool vec = al16(q, ldq) && al16(p, ldp) && n % 8 == 0;
+  auto kern = vec ? rank_grad_kernel<true> : rank_grad_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
                      reinterpret_cast<const half_t*>(p), ldp, reinterpret_cast<const half_t*>(q),
-                     ldq, t, n, scale_q, q_scale, part, splits, tchunk, (int)al16(q, ldq));
+                     ldq, t, n, scale_q ? q_scale : 1.0f, part, splits, tchunk);
   SS_CHECK_LAUNCH("rank_grad_kernel");
-  hipLaunchKernelGGL(rank_grad_reduce_kernel, dim3((unsigned)cdiv(n * kRank, 256)), dim3(256), 0,
+  hipLaunchKernelGGL(rank_grad_reduce_kernel, dim3((unsigned)cdiv(n, kRank)), dim3(256), 0,
                      s, part, n, splits, transpose, reinterpret_cast<half_t*>(out));
   SS_CHECK_LAUNCH("rank_grad_reduce_kernel");
   return SS_OK;

@@ -138,3 +138,31 @@ def test_dense_gemm_layouts(device, a_trans, b_trans, out_dtype, m, n, k):
         gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out=c, accumulate=True)
         np.testing.assert_allclose(np16(c), expected + a.astype(np.float64) @ b,
                                    rtol=1e-5, atol=2e-4)
+
+
+@pytest.mark.parametrize("m,n,k", [(4100, 4128, 96),    # 256x256 tiles, ragged M and N
+                                   (1000, 2000, 1536),  # 128x128 tiles
+                                   (100, 300, 64),      # 64x64 tiles
+                                   (990, 1536, 8960)])  # long K (a gate/up dX shape)
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_dense_nt_pipeline_tiles(device, m, n, k, out_dtype):
+    """A [M,K] . B[N,K]^T with both operands K-contiguous and K % 32 == 0: the
+    direct-to-LDS pipelined kernel at each of its tile sizes, plus beta = 1."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    bt = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+    bias = rng.standard_normal(n).astype(np.float16)
+    ad, bd = torch.from_numpy(a).to(device), torch.from_numpy(bt).to(device)
+    c = gemm_f16(ad, bd, b_trans=True, out_dtype=out_dtype, bias=torch.from_numpy(bias).to(device))
+    prod = a.astype(np.float64) @ bt.astype(np.float64).T
+    expected = prod + bias
+    if out_dtype == torch.float16:
+        check(c, expected, f"nt {m}x{n}x{k}")
+    else:
+        np.testing.assert_allclose(np16(c), expected, rtol=1e-5, atol=2e-4)
+    gemm_f16(ad, bd, b_trans=True, out=c, accumulate=True)
+    if out_dtype == torch.float16:
+        check(c, np16(torch.from_numpy(expected.astype(np.float16))).astype(np.float64) + prod,
+              f"nt accumulate {m}x{n}x{k}")
+    else:
+        np.testing.assert_allclose(np16(c), expected + prod, rtol=1e-5, atol=4e-4)
