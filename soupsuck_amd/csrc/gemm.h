@@ -21,7 +21,10 @@ struct Nf4View {
 // forward out = fp16(fp16(acc + bias) + fp16(fp16(Z . B^T) * s)) with Z
 // [M,16] and B = lora_B [N,16]; and a rank-16 update out = fp16(acc + dZ . A)
 // with dZ [M,16] and A = lora_A [16, N] (row stride ldlb).
-enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2 };
+// EPI_PARTIAL (split-K, dense NT kernel only): the raw fp32 accumulator of
+// split blockIdx.y is stored to part[split][M][N]; a reduce kernel sums the
+// splits in order and applies the requested epilogue.
+enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2, EPI_PARTIAL = 3 };
 
 struct GemmParams {
   int64_t M, N, K;
@@ -42,6 +45,8 @@ struct GemmParams {
   int64_t ldlb;
   float lscale;
   int remap;   // XCD-aware tile numbering (default on)
+  float* part;      // split-K partials [splits][M][N] fp32 (EPI_PARTIAL)
+  int64_t k_split;  // k elements per split (a multiple of 64)
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
@@ -70,7 +75,12 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
 // Dense NT GEMM (A [M,K] and B [N,K] both K-contiguous fp16) on the
 // direct-to-LDS pipelined kernel.  Returns SS_ERR_UNSUPPORTED (nothing
 // launched) when the operands do not meet its requirements: 16-byte aligned
-// rows and K % 32 == 0.
-int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream);
+// rows and K % 64 == 0.  `partials` (may be null) is scratch for split-K:
+// long-K products with few output tiles are split over k when it holds
+// nt_partial_bytes(M, N, K) bytes.
+int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream, void* partials = nullptr,
+            size_t partial_bytes = 0);
+// fp32 split-K scratch that gemm_nt uses for an M x N x K product (0: no split).
+size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
 
 }  // namespace ss

@@ -503,7 +503,8 @@ static bool nt_enabled() {
 }
 
 template <int OPA, int OPB, int CT, int EPI = EPI_PLAIN>
-static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
+static int dispatch(const GemmParams& p, hipStream_t stream, const char* name,
+                    void* partials = nullptr, size_t partial_bytes = 0) {
   if constexpr (OPA >= OP_NF4_ROW || OPB >= OP_NF4_ROW) {
     // The in-register NF4 decoders handle 128- and 64-row weight tiles.
     if (cdiv(p.M, 128) * cdiv(p.N, 128) >= 256 || tile_override() == TILE_BIG)
@@ -516,7 +517,7 @@ static int dispatch(const GemmParams& p, hipStream_t stream, const char* name) {
       if (nt_enabled()) {
         GemmParams q = p;
         q.remap = remap_setting();
-        const int rc = gemm_nt(q, CT, EPI, stream);
+        const int rc = gemm_nt(q, CT, EPI, stream, partials, partial_bytes);
         if (rc != SS_ERR_UNSUPPORTED) return rc;
       }
     }
@@ -537,6 +538,13 @@ static bool aligned16(const void* ptr, int64_t ld) {
 
 using namespace ss;
 
+// Decode-first workspace: the fp16 weight (forward [N,K], backward its
+// transpose), rounded up to 256 bytes, followed by the fp32 split-K partials
+// of the dense product when it is split.
+static size_t decoded_bytes(int64_t n, int64_t k) {
+  return ((size_t)n * (size_t)k * sizeof(uint16_t) + 255) / 256 * 256;
+}
+
 extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
   // From T rows on, decoding W once into fp16 (one 2.5 B/weight HBM pass)
   // and running the dense MFMA GEMM beats decoding every W tile again for each
@@ -547,8 +555,10 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     const char* e = getenv("SS_NF4_DECODE_FIRST_T");
     return e ? (int64_t)atoll(e) : (int64_t)256;
   }();
-  if (t >= threshold && n > 0 && k > 0) return (size_t)n * (size_t)k * sizeof(uint16_t);
-  return 0;
+  if (t < threshold || n <= 0 || k <= 0) return 0;
+  const size_t fwd = ss::nt_partial_bytes(t, n, k);  // Y [t, n], reduction over k
+  const size_t dx = ss::nt_partial_bytes(t, k, n);   // dX [t, k], reduction over n
+  return decoded_bytes(n, k) + (fwd > dx ? fwd : dx);
 }
 
 static int check_nf4(const char* fn, const uint8_t* packed, const uint8_t* qabs,
@@ -581,7 +591,10 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
     p.B = reinterpret_cast<const half_t*>(workspace);
     p.ldb = k;
     p.b_vec = 1;
-    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>");
+    const size_t dec = decoded_bytes(n, k);
+    void* part = workspace_bytes > dec ? static_cast<char*>(workspace) + dec : nullptr;
+    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>", part,
+                                                 part ? workspace_bytes - dec : 0);
   }
   return dispatch<OP_ROW, OP_NF4_ROW, SS_F16, EPI>(p, s, "gemm_kernel<nf4 fwd>");
 }
@@ -598,7 +611,10 @@ static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t w
     p.B = reinterpret_cast<const half_t*>(workspace);
     p.ldb = n;
     p.b_vec = n % 8 == 0;
-    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>");
+    const size_t dec = decoded_bytes(n, k);
+    void* part = workspace_bytes > dec ? static_cast<char*>(workspace) + dec : nullptr;
+    return dispatch<OP_ROW, OP_ROW, SS_F16, EPI>(p, s, "gemm_kernel<f16 nt>", part,
+                                                 part ? workspace_bytes - dec : 0);
   }
   return dispatch<OP_ROW, OP_NF4_COL, SS_F16, EPI>(p, s, "gemm_kernel<nf4 dx>");
 }

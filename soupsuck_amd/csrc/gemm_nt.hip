@@ -5,27 +5,32 @@
 // NT products; the epilogues (bias, LoRA add, rank-16 update, beta) are the
 // ones of gemm.hip.
 //
-// Pipeline: STAGES LDS buffers of BK = 32 k.  Operand tiles move from global
-// memory straight into LDS with global_load_lds_dwordx4 (no register
-// staging): one wave-wide DMA writes 64 lanes x 16 B = 1 KiB of contiguous LDS
-// (lane i at +16 i), i.e. 16 rows x 64 B of one operand tile.  Stage
-// kt + STAGES - 1 is requested while stage kt is consumed, so STAGES - 1
-// stages of loads are in flight behind the MFMAs.
+// Pipeline: STAGES LDS buffers of BK k (32 or 64).  Operand tiles move from
+// global memory straight into LDS with global_load_lds_dwordx4 (no register
+// staging): one wave-wide DMA writes 64 lanes x 16 B = 1 KiB of contiguous
+// LDS (lane i at +16 i).  How many bytes of a row one DMA fetches sets the
+// DMA throughput (measured on MI355X, L2-resident data: 128 B per row ->
+// 43 B/clk/CU into LDS, 64 B -> 25, 32 B -> 14), so:
+//   BK = 64: a DMA covers 8 rows x 128 B.  Block b (rows 8b .. 8b+7) is 1 KiB;
+//     chunk c of row 8b + r sits at slot (c ^ (b & 1)) * 8 + r.
+//   BK = 32: a DMA covers 16 rows x 64 B.  Row r is 64 B; chunk c sits at
+//     chunk c ^ ((r >> 1) & 3).
+// Both make an MFMA 32x32x16 fragment read (32 consecutive rows, one chunk
+// per lane half) free of LDS bank conflicts (BK = 64: measured; BK = 32:
+// 2-way at most).
 //
-// LDS layout: row r of a stage tile is 64 B (4 chunks of 8 halves); logical
-// chunk c lives at physical chunk c ^ ((r >> 1) & 3).  The lane that fills
-// physical chunk q of row r therefore fetches logical chunk q ^ ((r >> 1) & 3)
-// from global memory.  A fragment read (32 consecutive rows, one logical
-// chunk) then touches 8 distinct 16-byte bank groups per 8 lanes: no LDS bank
-// conflicts.
+// Per stage a wave runs BK / 16 MFMA k-steps; fragments are double buffered
+// so the reads of k-step kk+1 overlap the MFMAs of kk.  One s_barrier per
+// stage sits before the last k-step: by then every wave has read all its
+// fragments of stage kt (lgkmcnt(0)), so buffer kt % STAGES is refilled with
+// stage kt + STAGES right after it, and stage kt+1 (waited for with vmcnt
+// before the barrier) is read while the last MFMAs of stage kt run; the
+// refill DMAs are interleaved between those MFMAs.
 //
 // The DMA is issued from inline asm.  The compiler does not know which LDS
 // buffer an outstanding LDS DMA writes, and would wait for all of them
-// (vmcnt(0)) before every LDS read, draining the pipeline.  Waits are explicit
-// instead: before stage kt is read, vmcnt lets only the DMAs of later stages
-// stay outstanding; lgkmcnt(0) + s_barrier then make every wave's part of
-// the stage visible and guarantee that no wave still reads the buffer that
-// is refilled next.
+// (vmcnt(0)) before every LDS read, draining the pipeline; the waits are
+// explicit instead.
 
 #include <stdlib.h>
 
@@ -34,34 +39,39 @@
 namespace ss {
 namespace {
 
-constexpr int kBK = 32;
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-template <int BM_, int BN_, int WAVES_M, int WAVES_N, int STAGES_, int MINW_>
+template <int BM_, int BN_, int WAVES_M, int WAVES_N, int BK_, int STAGES_, int MINW_>
 struct NtCfg {
-  static constexpr int BM = BM_, BN = BN_, STAGES = STAGES_, MINW = MINW_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_, MINW = MINW_;
   static constexpr int kWaves = WAVES_M * WAVES_N;
   static constexpr int kThreads = kWave * kWaves;
   static constexpr int kWavesN = WAVES_N;
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  static constexpr int FM = WM / 32, FN = WN / 32;  // 32x32 accumulator blocks per wave
-  static constexpr int kDmaA = BM / 16 / kWaves;    // DMA instructions per wave per stage
-  static constexpr int kDmaB = BN / 16 / kWaves;
+  static constexpr int FM = WM / 32, FN = WN / 32;   // 32x32 accumulator blocks per wave
+  static constexpr int KK = BK / 16;                 // MFMA k-steps per stage
+  static constexpr int kRowsPerDma = 1024 / (BK * 2);
+  static constexpr int kDmaA = BM / kRowsPerDma / kWaves;  // DMAs per wave per stage
+  static constexpr int kDmaB = BN / kRowsPerDma / kWaves;
   static constexpr int kDma = kDmaA + kDmaB;
-  static constexpr int kTileA = BM * kBK * 2;       // bytes of one stage's A tile
-  static constexpr int kStageBytes = (BM + BN) * kBK * 2;
-  static_assert(BM % (16 * kWaves) == 0 && BN % (16 * kWaves) == 0, "DMA split over waves");
+  static constexpr int kTileA = BM * BK * 2;         // bytes of one stage's A tile
+  static constexpr int kStageBytes = (BM + BN) * BK * 2;
+  static_assert(BK == 32 || BK == 64, "stage depth");
+  static_assert(BM % (kRowsPerDma * kWaves) == 0 && BN % (kRowsPerDma * kWaves) == 0,
+                "DMA split over waves");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "32x32 MFMA blocks");
-  static_assert(STAGES >= 2 && STAGES <= 4, "pipeline depth");
+  static_assert(STAGES >= 2 && STAGES <= 3, "pipeline depth");
+  static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS");
 };
 
-// One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at `src` land at LDS
-// byte address lds + 16 i.  `lds` must be wave-uniform.  s_nop covers the
-// M0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void dma16(const half_t* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+// One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at base + voff land at
+// LDS byte address lds + 16 i.  `base` and `lds` are wave-uniform (SGPRs);
+// voff is the lane's 32-bit byte offset.  s_nop covers the M0-write ->
+// LDS-DMA hazard.
+__device__ __forceinline__ void dma16(uint32_t voff, const half_t* base, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(src), "s"(lds)
+               : "v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
@@ -72,7 +82,7 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
-// Wait until at most `ahead` stages of DMAs (kDma each) are outstanding.
+// Wait until at most `ahead` stages of DMAs (KDMA each) are outstanding.
 template <int KDMA, int MAXAHEAD>
 __device__ __forceinline__ void wait_stages(int64_t ahead) {
   if constexpr (MAXAHEAD >= 2) {
@@ -90,68 +100,98 @@ __device__ __forceinline__ void wait_stages(int64_t ahead) {
   wait_vm<0>();
 }
 
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  asm volatile("s_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// DMA g of an operand tile: the row and logical 16-byte chunk that lane
+// fetches (its LDS slot is g * 1024 + 16 * lane).
+template <int BK>
+__device__ __forceinline__ void dma_source(int g, int lane, int& row, int& chunk) {
+  if constexpr (BK == 64) {
+    row = g * 8 + (lane & 7);
+    chunk = (lane >> 3) ^ (g & 1);
+  } else {
+    row = g * 16 + (lane >> 2);
+    chunk = (lane & 3) ^ ((row >> 1) & 3);
+  }
+}
+
+// Byte offset (within a stage's operand tile, relative to the start of a
+// 32-row group) of the lane's fragment for k-step kk: row lane % 32,
+// logical chunk 2 kk + lane / 32.
+template <int BK>
+__device__ __forceinline__ int frag_offset(int lane, int kk) {
+  const int r = lane & 31;
+  const int c = 2 * kk + (lane >> 5);
+  if constexpr (BK == 64) {
+    const int b = r >> 3;
+    return b * 1024 + ((((c ^ (b & 1)) * 8) + (r & 7)) << 4);
+  } else {
+    return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+  }
 }
 
 template <class C, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::STAGES * C::kStageBytes];
+  constexpr int kGroupBytes = 32 * C::BK * 2;  // one 32-row group of a stage tile
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / C::kWavesN;
   const int wn = wave % C::kWavesN;
-  // M-fastest tile order: consecutive tiles share the B (weight) panel; with
-  // the XCD remap they run back to back on one XCD and reuse it from L2.
+  // Tile order: after the XCD remap, consecutive tile ids walk groups of
+  // kGroupM M-tiles (M fastest) before moving to the next N-tile, so the
+  // tiles resident on one XCD at a time form a kGroupM x (n) block that
+  // reuses both its A panels and its B panels from that XCD's L2.
   const int64_t mtiles = cdiv(p.M, C::BM);
+  const int64_t ntiles = cdiv(p.N, C::BN);
   const int64_t tile = p.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
-  const int64_t m0 = (tile % mtiles) * C::BM;
-  const int64_t n0 = (tile / mtiles) * C::BN;
+  constexpr int64_t kGroupM = 8;
+  const int64_t per_group = kGroupM * ntiles;
+  const int64_t first_m = (tile / per_group) * kGroupM;
+  const int64_t group_m = mtiles - first_m < kGroupM ? mtiles - first_m : kGroupM;
+  const int64_t in_group = tile % per_group;
+  const int64_t m0 = (first_m + in_group % group_m) * C::BM;
+  const int64_t n0 = (in_group / group_m) * C::BN;
   const uint32_t lds0 = lds_address(smem);
+  // Split-K: this workgroup's k range.
+  int64_t kbeg = 0, klen = p.K;
+  if constexpr (EPI == EPI_PARTIAL) {
+    kbeg = (int64_t)blockIdx.y * p.k_split;
+    klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
+  }
+  const half_t* a_base = p.A + kbeg;
+  const half_t* b_base = p.B + kbeg;
 
-  // Per-lane DMA sources: row (16 per DMA) and the logical chunk that belongs
-  // in physical chunk (lane & 3).  Rows past M / N are clamped to the last
+  // Per-lane DMA sources as 32-bit byte offsets from the operand base (the
+  // host checks that they fit).  Rows past M / N are clamped to the last
   // row: they only feed accumulator rows that are never stored.
-  const half_t* a_src[C::kDmaA];
-  const half_t* b_src[C::kDmaB];
+  uint32_t a_off[C::kDmaA];
+  uint32_t b_off[C::kDmaB];
 #pragma unroll
   for (int j = 0; j < C::kDmaA; ++j) {
-    const int row = (wave * C::kDmaA + j) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    int row, chunk;
+    dma_source<C::BK>(wave * C::kDmaA + j, lane, row, chunk);
     const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
-    a_src[j] = p.A + gr * p.lda + chunk * 8;
+    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
   }
 #pragma unroll
   for (int j = 0; j < C::kDmaB; ++j) {
-    const int row = (wave * C::kDmaB + j) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    int row, chunk;
+    dma_source<C::BK>(wave * C::kDmaB + j, lane, row, chunk);
     const int64_t gr = n0 + row < p.N ? n0 + row : p.N - 1;
-    b_src[j] = p.B + gr * p.ldb + chunk * 8;
+    b_off[j] = (uint32_t)((gr * p.ldb + chunk * 8) * 2);
   }
-  auto issue = [&](int64_t kt, int stage) {
-    const uint32_t base = lds0 + stage * C::kStageBytes;
-#pragma unroll
-    for (int j = 0; j < C::kDmaA; ++j)
-      dma16(a_src[j] + kt * kBK,
-            __builtin_amdgcn_readfirstlane(base + (wave * C::kDmaA + j) * 1024));
-#pragma unroll
-    for (int j = 0; j < C::kDmaB; ++j)
-      dma16(b_src[j] + kt * kBK,
-            __builtin_amdgcn_readfirstlane(base + C::kTileA + (wave * C::kDmaB + j) * 1024));
-  };
+  const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
+  const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds0 + C::kTileA + wave * C::kDmaB * 1024);
 
-  // Fragment offsets: lane reads row (lane & 31) of a 32-row block, logical
-  // chunk 2 * kk + (lane >> 5), stored at chunk ^ ((row >> 1) & 3).
-  const int lr = lane & 31;
+  int frag_off[C::KK];
+#pragma unroll
+  for (int kk = 0; kk < C::KK; ++kk) frag_off[kk] = frag_offset<C::BK>(lane, kk);
+  const int lr = lane & 31;  // epilogue: column within a 32x32 block
   const int lh = lane >> 5;
-  const int swz = (lr >> 1) & 3;
-  const int frag_off[2] = {lr * 64 + ((lh ^ swz) << 4), lr * 64 + (((2 + lh) ^ swz) << 4)};
 
   float16v acc[C::FM][C::FN];
 #pragma unroll
@@ -159,34 +199,80 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
 
-  const int64_t ktiles = p.K / kBK;
+  auto dma_one = [&](int64_t kt, int stage, int idx) {
+    if (idx < C::kDmaA) {
+      dma16(a_off[idx], a_base + kt * C::BK, lds_a + stage * C::kStageBytes + idx * 1024);
+    } else {
+      const int j = idx - C::kDmaA;
+      dma16(b_off[j], b_base + kt * C::BK, lds_b + stage * C::kStageBytes + j * 1024);
+    }
+  };
+  auto read_frags = [&](int64_t kt, int kk, half8 (&af)[C::FM], half8 (&bf)[C::FN]) {
+    const unsigned char* base = smem + (kt % C::STAGES) * C::kStageBytes;
+    const unsigned char* sa = base + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
+    const unsigned char* sb = base + C::kTileA + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
 #pragma unroll
-  for (int s = 0; s < C::STAGES - 1; ++s)
-    if (s < ktiles) issue(s, s);
-
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int64_t ahead = ktiles - 1 - kt;  // stages already requested after kt
-    wait_stages<C::kDma, C::STAGES - 2>(ahead);
-    lds_barrier();
-    if (kt + C::STAGES - 1 < ktiles) issue(kt + C::STAGES - 1, (int)((kt + C::STAGES - 1) % C::STAGES));
-    const unsigned char* sa = smem + (kt % C::STAGES) * C::kStageBytes + (wm * C::WM) * 64;
-    const unsigned char* sb = smem + (kt % C::STAGES) * C::kStageBytes + C::kTileA + (wn * C::WN) * 64;
+    for (int i = 0; i < C::FM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      half8 af[C::FM];
-      half8 bf[C::FN];
+    for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+  };
+  auto mfma_block = [&](const half8 (&af)[C::FM], const half8 (&bf)[C::FN]) {
 #pragma unroll
-      for (int i = 0; i < C::FM; ++i)
-        af[i] = *reinterpret_cast<const half8*>(sa + i * 32 * 64 + frag_off[kk]);
+    for (int i = 0; i < C::FM; ++i)
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
-        bf[j] = *reinterpret_cast<const half8*>(sb + j * 32 * 64 + frag_off[kk]);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  };
+
+  constexpr int kS = C::STAGES;
+  constexpr int kMfma = C::FM * C::FN;
+  const int64_t ktiles = klen / C::BK;
+  half8 fa[2][C::FM], fb[2][C::FN];
 #pragma unroll
-      for (int i = 0; i < C::FM; ++i)
+  for (int s = 0; s < kS; ++s)
+    if (s < ktiles)
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      for (int idx = 0; idx < C::kDma; ++idx) dma_one(s, s, idx);
+  if (ktiles > 0) {
+    wait_stages<C::kDma, kS - 1>((ktiles < kS ? ktiles : kS) - 1);
+    asm volatile("s_barrier" ::: "memory");
+    read_frags(0, 0, fa[0], fb[0]);
+  }
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+#pragma unroll
+    for (int kk = 0; kk + 1 < C::KK; ++kk) {
+      read_frags(kt, kk + 1, fa[(kk + 1) & 1], fb[(kk + 1) & 1]);
+      mfma_block(fa[kk & 1], fb[kk & 1]);
     }
+    constexpr int kLast = (C::KK - 1) & 1;
+    const bool more = kt + 1 < ktiles;
+    const bool refill = kt + kS < ktiles;
+    if (more) {
+      // Stages requested so far: 0 .. min(kt + kS - 1, ktiles - 1); stage kt+1
+      // must have landed.  lgkmcnt(0): this wave's reads of stage kt are done,
+      // so buffer kt % kS may be refilled once every wave passed the barrier.
+      const int64_t last = kt + kS - 1 < ktiles - 1 ? kt + kS - 1 : ktiles - 1;
+      wait_stages<C::kDma, kS - 2>(last - (kt + 1));
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      asm volatile("s_barrier" ::: "memory");
+    }
+    const int refill_stage = (int)(kt % kS);
+#pragma unroll
+    for (int idx = 0; idx < kMfma; ++idx) {
+      if (idx == kMfma / 2 && more) read_frags(kt + 1, 0, fa[0], fb[0]);
+      acc[idx / C::FN][idx % C::FN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+          fa[kLast][idx / C::FN], fb[kLast][idx % C::FN], acc[idx / C::FN][idx % C::FN], 0, 0,
+          0);
+      if (refill) {
+#pragma unroll
+        for (int d = idx * C::kDma / kMfma; d < (idx + 1) * C::kDma / kMfma; ++d)
+          dma_one(kt + kS, refill_stage, d);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int d = kMfma < C::kDma ? kMfma * (C::kDma / kMfma) : C::kDma; d < C::kDma; ++d)
+      if (refill) dma_one(kt + kS, refill_stage, d);
   }
 
   // Epilogue: lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of
@@ -197,6 +283,16 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
     for (int j = 0; j < C::FN; ++j) {
       const int64_t row_base = m0 + wm * C::WM + i * 32;
       const int64_t col = n0 + wn * C::WN + j * 32 + lr;
+      if constexpr (EPI == EPI_PARTIAL) {
+        if (col >= p.N) continue;
+        float* part = p.part + (int64_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (row < p.M) part[row * p.N + col] = acc[i][j][r];
+        }
+        continue;
+      }
       float16v extra = float16v{};
       if constexpr (EPI != EPI_PLAIN) {
         // Rank-16 term of this block on one v_mfma_f32_32x32x16_f16:
@@ -237,59 +333,187 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
   }
 }
 
-using NtBig = NtCfg<256, 256, 2, 2, 4, 1>;    // 128x128 per wave, 128 KiB LDS, 1 WG / CU
-using NtMid = NtCfg<128, 128, 2, 2, 4, 2>;    // 64x64 per wave, 64 KiB LDS, 2 WG / CU
-using NtSmall = NtCfg<64, 64, 2, 2, 4, 2>;    // 32x32 per wave, 32 KiB LDS
+// Split-K reduction: out[row][col] = epilogue(sum over splits s = 0.. of
+// part[s][row][col]), four columns per thread.  The epilogues are those of the
+// GEMM kernel with the same rounding order; the rank-16 terms are summed in
+// fp32 in rank order.
+template <int CT, int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits) {
+  const int64_t groups = cdiv(p.N, 4);
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= p.M * groups) return;
+  const int64_t row = g / groups;
+  const int64_t c0 = (g % groups) * 4;
+  const int64_t plane = p.M * p.N;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.N % 4 == 0) {
+    for (int s = 0; s < splits; ++s) {
+      const float4v t = *reinterpret_cast<const float4v*>(p.part + s * plane + row * p.N + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += t[e];
+    }
+  } else {
+    for (int s = 0; s < splits; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < p.N) v[e] += p.part[s * plane + row * p.N + c0 + e];
+  }
+  float z[16];
+  if constexpr (EPI != EPI_PLAIN) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) z[r] = (float)p.lz[row * 16 + r];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t col = c0 + e;
+    if (col >= p.N) break;
+    const int64_t idx = row * p.ldc + col;
+    if constexpr (EPI == EPI_LORA) {
+      float l = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) l += z[r] * (float)p.lb[col * 16 + r];
+      const float b = p.bias ? (float)p.bias[col] : 0.0f;
+      const float y = (float)f32_to_f16(v[e] * p.alpha + b);
+      const float scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
+      reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
+    } else if constexpr (EPI == EPI_RANK) {
+      float l = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) l += z[r] * (float)p.lb[r * p.ldlb + col];
+      store_c<CT>(p.C, idx, v[e] + l, p.beta);
+    } else {
+      const float b = p.bias ? (float)p.bias[col] : 0.0f;
+      store_c<CT>(p.C, idx, v[e] * p.alpha + b, p.beta);
+    }
+  }
+}
+
+// Tile configurations: <BM, BN, waves M, waves N, BK, stages, min waves/SIMD>.
+using NtSmall = NtCfg<64, 64, 2, 2, 32, 3, 2>;      // 4 waves of 32x32, 24 KiB LDS
+using NtMid = NtCfg<128, 128, 2, 2, 32, 3, 2>;      // 4 waves of 64x64, 48 KiB LDS
+using NtBig4 = NtCfg<256, 256, 2, 2, 32, 3, 1>;     // 4 waves of 128x128, 96 KiB LDS
+using NtBig8 = NtCfg<256, 256, 2, 4, 64, 2, 2>;     // 8 waves of 128x64, 128 KiB LDS
+using NtWide8 = NtCfg<256, 128, 4, 2, 64, 2, 2>;    // 8 waves of 64x64, 96 KiB LDS
+using NtBig8s = NtCfg<256, 256, 2, 4, 32, 3, 2>;    // 8 waves of 128x64, 96 KiB LDS
+using NtMid64 = NtCfg<128, 128, 2, 2, 64, 2, 2>;    // 4 waves of 64x64, 64 KiB LDS
 
 template <class C, int CT, int EPI>
-int launch_nt(const GemmParams& p, hipStream_t stream) {
-  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN)));
+int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
+  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN)), (unsigned)splits);
   hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
   SS_CHECK_LAUNCH("gemm_nt_kernel");
   return SS_OK;
 }
 
-// Tile choice: 256x256 once it fills every CU (least LDS and L2 traffic per
-// flop), else 128x128 while it gives at least half the CUs a tile, else 64x64.
-// SS_NT_TILE (1 = 64x64, 2 = 128x128, 3 = 256x256) overrides it; a tuning
-// knob read once per process.
-int nt_tile(int64_t m, int64_t n) {
+// Configuration and split-K plan for an M x N x K product.
+//   256x256 (8 waves) once it gives at least half the CUs a tile;
+//   long K with few 128x128 tiles: 128x128 split over k so that about 512
+//   workgroups run (each split at least 1024 k);
+//   128x128 while it gives half the CUs a tile; else 64x64.
+// SS_NT_TILE (1..7, the configurations above in order) and SS_NT_SPLITS
+// override the choice (tuning knobs read once per process).
+struct NtPlan {
+  int cfg;
+  int64_t splits, k_split;
+};
+
+NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   static const int forced = [] {
     const char* e = getenv("SS_NT_TILE");
     return e ? atoi(e) : 0;
   }();
-  if (forced >= 1 && forced <= 3) return forced;
-  if (cdiv(m, 256) * cdiv(n, 256) >= 256) return 3;
-  if (cdiv(m, 128) * cdiv(n, 128) >= 128) return 2;
-  return 1;
+  static const int forced_splits = [] {
+    const char* e = getenv("SS_NT_SPLITS");
+    return e ? atoi(e) : 0;
+  }();
+  NtPlan plan{1, 1, k};
+  const int64_t t256 = cdiv(m, 256) * cdiv(n, 256);
+  const int64_t t128 = cdiv(m, 128) * cdiv(n, 128);
+  if (t256 >= 128) {
+    plan.cfg = 6;
+  } else if (k >= 2048 && t128 < 256) {
+    plan.cfg = 2;
+    int64_t s = 512 / t128;
+    if (s > k / 1024) s = k / 1024;
+    plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
+  } else if (t128 >= 128) {
+    plan.cfg = 2;
+  }
+  if (forced >= 1 && forced <= 7) plan.cfg = forced;
+  if (forced_splits >= 1) plan.splits = forced_splits;
+  plan.k_split = cdiv(cdiv(k, plan.splits), 64) * 64;
+  plan.splits = cdiv(k, plan.k_split);
+  return plan;
 }
 
 template <int CT, int EPI>
-int dispatch_nt(const GemmParams& p, hipStream_t stream) {
-  switch (nt_tile(p.M, p.N)) {
-    case 3: return launch_nt<NtBig, CT, EPI>(p, stream);
-    case 2: return launch_nt<NtMid, CT, EPI>(p, stream);
-    default: return launch_nt<NtSmall, CT, EPI>(p, stream);
+int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
+  switch (cfg) {
+    case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
+    case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
+    case 5: return launch_nt<NtWide8, CT, EPI>(p, splits, stream);
+    case 4: return launch_nt<NtBig8, CT, EPI>(p, splits, stream);
+    case 3: return launch_nt<NtBig4, CT, EPI>(p, splits, stream);
+    case 2: return launch_nt<NtMid, CT, EPI>(p, splits, stream);
+    default: return launch_nt<NtSmall, CT, EPI>(p, splits, stream);
   }
+}
+
+template <int CT, int EPI>
+int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
+  const int64_t threads = p.M * cdiv(p.N, 4);
+  hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI>), dim3((unsigned)cdiv(threads, 256)),
+                     dim3(256), 0, stream, p, (int)splits);
+  SS_CHECK_LAUNCH("splitk_reduce_kernel");
+  return SS_OK;
 }
 
 bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
 
 }  // namespace
 
-int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream) {
-  if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % kBK != 0) return SS_ERR_UNSUPPORTED;
+size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 != 0) return 0;
+  const NtPlan plan = nt_plan(m, n, k);
+  return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
+}
+
+int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* partials,
+            size_t partial_bytes) {
+  GemmParams p = p0;
+  if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return SS_ERR_UNSUPPORTED;  // K % 64
   if (!aligned16(p.A) || !aligned16(p.B) || p.lda % 8 != 0 || p.ldb % 8 != 0)
+    return SS_ERR_UNSUPPORTED;
+  // The DMA addresses operands with 32-bit byte offsets from their base.
+  const int64_t kMaxOff = (int64_t)1 << 32;
+  if (((p.M - 1) * p.lda + p.K) * 2 >= kMaxOff || ((p.N - 1) * p.ldb + p.K) * 2 >= kMaxOff)
     return SS_ERR_UNSUPPORTED;
   if (epi != EPI_PLAIN && (!aligned16(p.lz) || (epi == EPI_LORA && !aligned16(p.lb))))
     return SS_ERR_UNSUPPORTED;
-  if (ct == SS_F16) {
-    if (epi == EPI_LORA) return dispatch_nt<SS_F16, EPI_LORA>(p, stream);
-    if (epi == EPI_RANK) return dispatch_nt<SS_F16, EPI_RANK>(p, stream);
-    return dispatch_nt<SS_F16, EPI_PLAIN>(p, stream);
+  if (ct != SS_F16 && epi != EPI_PLAIN) return SS_ERR_UNSUPPORTED;
+  NtPlan plan = nt_plan(p.M, p.N, p.K);
+  const size_t need = (size_t)(plan.splits * p.M * p.N) * sizeof(float);
+  if (plan.splits > 1 && (!partials || partial_bytes < need ||
+                          reinterpret_cast<uintptr_t>(partials) % 16 != 0)) {
+    plan.splits = 1;
+    plan.k_split = p.K;
   }
-  if (epi != EPI_PLAIN) return SS_ERR_UNSUPPORTED;
-  return dispatch_nt<SS_F32, EPI_PLAIN>(p, stream);
+  if (plan.splits > 1) {
+    p.part = reinterpret_cast<float*>(partials);
+    p.k_split = plan.k_split;
+    const int rc = dispatch_nt<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);
+    if (rc) return rc;
+    if (ct == SS_F32) return reduce_nt<SS_F32, EPI_PLAIN>(p, plan.splits, stream);
+    if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, plan.splits, stream);
+    if (epi == EPI_RANK) return reduce_nt<SS_F16, EPI_RANK>(p, plan.splits, stream);
+    return reduce_nt<SS_F16, EPI_PLAIN>(p, plan.splits, stream);
+  }
+  if (ct == SS_F16) {
+    if (epi == EPI_LORA) return dispatch_nt<SS_F16, EPI_LORA>(p, plan.cfg, 1, stream);
+    if (epi == EPI_RANK) return dispatch_nt<SS_F16, EPI_RANK>(p, plan.cfg, 1, stream);
+    return dispatch_nt<SS_F16, EPI_PLAIN>(p, plan.cfg, 1, stream);
+  }
+  return dispatch_nt<SS_F32, EPI_PLAIN>(p, plan.cfg, 1, stream);
 }
 
 }  // namespace ss
