@@ -83,4 +83,24 @@ int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream, void* part
 // fp32 split-K scratch that gemm_nt uses for an M x N x K product (0: no split).
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
 
+// Split-K reduction: C = epilogue(sum over `splits` planes of p.part
+// [splits][M][N]) with the epilogue `epi` (EPI_PLAIN / EPI_LORA / EPI_RANK)
+// and output dtype `ct` (LoRA / rank epilogues: fp16 only).
+int splitk_reduce(const GemmParams& p, int splits, int ct, int epi, hipStream_t stream);
+
+// Skinny NF4 forward (nf4_skinny.hip) for T <= kSkinnyMaxT rows and K % 128
+// == 0: the weight streams from HBM once, decoded in registers; K is split
+// and the fp32 partials are reduced by splitk_reduce.
+constexpr int64_t kSkinnyMaxT = 128;
+struct SkinnyPlan {
+  int mt;                  // 16-row M tiles per workgroup (0: not applicable)
+  int64_t splits, k_split;
+};
+SkinnyPlan skinny_plan(int64_t t, int64_t n, int64_t k);
+size_t skinny_partial_bytes(int64_t t, int64_t n, int64_t k);
+// Y = X . Wdec^T with p.M = T, p.N = N, p.K = K, p.A = X, p.w = the NF4
+// weight and the epilogue fields of p; SS_ERR_UNSUPPORTED when not applicable.
+int nf4_skinny_fwd(const GemmParams& p, int epi, void* partials, size_t partial_bytes,
+                   hipStream_t stream);
+
 }  // namespace ss

@@ -555,7 +555,16 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     const char* e = getenv("SS_NF4_DECODE_FIRST_T");
     return e ? (int64_t)atoll(e) : (int64_t)256;
   }();
-  if (t < threshold || n <= 0 || k <= 0) return 0;
+  if (n <= 0 || k <= 0 || t <= 0) return 0;
+  if (t <= ss::kSkinnyMaxT) {
+    // Forward: skinny-kernel partials.  Backward: decode W^T once and run the
+    // split-K dense product (the in-loop decoder streams the weight with too
+    // little parallelism at small T).
+    const size_t fwd = ss::skinny_partial_bytes(t, n, k);
+    const size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
+    return fwd > dx ? fwd : dx;
+  }
+  if (t < threshold) return 0;
   const size_t fwd = ss::nt_partial_bytes(t, n, k);  // Y [t, n], reduction over k
   const size_t dx = ss::nt_partial_bytes(t, k, n);   // dX [t, k], reduction over n
   return decoded_bytes(n, k) + (fwd > dx ? fwd : dx);
@@ -583,6 +592,10 @@ namespace ss {
 template <int EPI>
 static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
   const int64_t n = p.N, k = p.K;
+  if (p.M <= kSkinnyMaxT && workspace) {
+    const int rc = nf4_skinny_fwd(p, EPI, workspace, workspace_bytes, s);
+    if (rc != SS_ERR_UNSUPPORTED) return rc;
+  }
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
     const Nf4View& w = p.w;
     int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,

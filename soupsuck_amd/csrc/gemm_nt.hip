@@ -472,6 +472,16 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 
 }  // namespace
 
+int splitk_reduce(const GemmParams& p, int splits, int ct, int epi, hipStream_t stream) {
+  if (ct == SS_F32) {
+    if (epi != EPI_PLAIN) return SS_ERR_UNSUPPORTED;
+    return reduce_nt<SS_F32, EPI_PLAIN>(p, splits, stream);
+  }
+  if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, splits, stream);
+  if (epi == EPI_RANK) return reduce_nt<SS_F16, EPI_RANK>(p, splits, stream);
+  return reduce_nt<SS_F16, EPI_PLAIN>(p, splits, stream);
+}
+
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || k % 64 != 0) return 0;
   const NtPlan plan = nt_plan(m, n, k);
