@@ -23,15 +23,37 @@ typedef float float2v __attribute__((ext_vector_type(2)));
 // Native 128-bit vector (HIP's uint4 is a class type; selects and copies of it
 // can be lowered through memory, so register staging uses this type).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
 // Sixteen NF4 code points (format data: reference solution/kernels/nf4.py:32-37).
-__device__ __constant__ static const float kNF4[16] = {
-    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
-    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
-    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
-    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+#define SS_NF4_CODE_POINTS                                                                  \
+  -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,                \
+      -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,           \
+      0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f, \
+      0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f
+__device__ __constant__ static const float kNF4[16] = {SS_NF4_CODE_POINTS};
+
+// fp16(code point) bit patterns (round to nearest even), computed at compile
+// time, for decoders that build their tables without a memory load.
+struct Nf4HalfBits {
+  uint16_t v[16];
+};
+constexpr Nf4HalfBits nf4_half_bits() {
+  constexpr float codes[16] = {SS_NF4_CODE_POINTS};
+  Nf4HalfBits h{};
+  for (int i = 0; i < 16; ++i) h.v[i] = __builtin_bit_cast(uint16_t, (_Float16)codes[i]);
+  return h;
+}
+constexpr Nf4HalfBits kNF4Half = nf4_half_bits();
+// kNF4Half.v[i] for a run-time i, without a memory access (selects).
+__device__ __forceinline__ uint32_t nf4_half_bits_of(int i) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) r = i == q ? kNF4Half.v[q] : r;
+  return r;
+}
 
 // fp32 -> fp16 with round-to-nearest-even as its own instruction.  The empty
 // asm makes the value opaque to instruction selection, which would otherwise

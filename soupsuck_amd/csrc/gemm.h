@@ -59,6 +59,59 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t p, int64_t n) {
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
 }
 
+// LDS DMA (gfx950 global_load_lds_*).  One wave-wide dwordx4 DMA: lane i's
+// 16 bytes at base + voff land at LDS byte address lds + 16 i; the dword form
+// puts lane i's 4 bytes at lds + 4 i.  `base` and `lds` are wave-uniform
+// (SGPRs); voff is the lane's 32-bit byte offset.  s_nop covers the M0-write
+// -> LDS-DMA hazard.  Completion is counted by vmcnt, in issue order with the
+// wave's other vector-memory loads.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* base, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t voff, const void* base, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// Vector loads the compiler does not track: it inserts no wait for them.
+// The caller waits explicitly (wait_vm) and then passes the value through
+// tie() before its first use, so that no use is scheduled ahead of the wait.
+__device__ __forceinline__ u32x4 vload16(const void* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload4(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload_u16(const void* p) {
+  uint32_t v;
+  asm volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+template <class T>
+__device__ __forceinline__ void tie(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 template <int CT>
 __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta) {
   if constexpr (CT == SS_F16) {
@@ -69,6 +122,33 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
     float* c = reinterpret_cast<float*>(C);
     if (beta) v += c[idx];
     c[idx] = v;
+  }
+}
+
+// One fp16 output element of the epilogues, with the rounding order of the
+// GEMM kernels: plain alpha * v + bias (+ C if beta); LoRA fp16(fp16(v +
+// bias) + fp16(fp16(Z[row] . B[col]) * s)); rank fp16(v + dZ[row] . A[:, col])
+// (+ C if beta).  v is the fp32 accumulator of (row, col).
+template <int EPI>
+__device__ __forceinline__ void epilogue_f16(const GemmParams& p, int64_t row, int64_t col,
+                                             float v) {
+  const int64_t idx = row * p.ldc + col;
+  if constexpr (EPI == EPI_LORA) {
+    float l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) l += (float)p.lz[row * 16 + r] * (float)p.lb[col * 16 + r];
+    const float b = p.bias ? (float)p.bias[col] : 0.0f;
+    const float y = (float)f32_to_f16(v * p.alpha + b);
+    const float scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
+    reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
+  } else if constexpr (EPI == EPI_RANK) {
+    float l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) l += (float)p.lz[row * 16 + r] * (float)p.lb[r * p.ldlb + col];
+    store_c<SS_F16>(p.C, idx, v + l, p.beta);
+  } else {
+    const float b = p.bias ? (float)p.bias[col] : 0.0f;
+    store_c<SS_F16>(p.C, idx, v * p.alpha + b, p.beta);
   }
 }
 
@@ -101,6 +181,16 @@ size_t skinny_partial_bytes(int64_t t, int64_t n, int64_t k);
 // Y = X . Wdec^T with p.M = T, p.N = N, p.K = K, p.A = X, p.w = the NF4
 // weight and the epilogue fields of p; SS_ERR_UNSUPPORTED when not applicable.
 int nf4_skinny_fwd(const GemmParams& p, int epi, void* partials, size_t partial_bytes,
+                   hipStream_t stream);
+
+// Streaming NF4 forward (nf4_stream.hip) for T <= kStreamMaxT rows and K % 256
+// == 0: the codes stream through per-wave LDS rings and are decoded with a
+// bank-replicated code table, the block scales applied to the MFMA results;
+// fp32 partial planes, reduced by splitk_reduce.  Same contract as
+// nf4_skinny_fwd.
+constexpr int64_t kStreamMaxT = 32;
+size_t stream_partial_bytes(int64_t t, int64_t n, int64_t k);
+int nf4_stream_fwd(const GemmParams& p, int epi, void* partials, size_t partial_bytes,
                    hipStream_t stream);
 
 }  // namespace ss

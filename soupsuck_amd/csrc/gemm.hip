@@ -560,7 +560,9 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     // Forward: skinny-kernel partials.  Backward: decode W^T once and run the
     // split-K dense product (the in-loop decoder streams the weight with too
     // little parallelism at small T).
-    const size_t fwd = ss::skinny_partial_bytes(t, n, k);
+    size_t fwd = ss::skinny_partial_bytes(t, n, k);
+    const size_t fwd_stream = ss::stream_partial_bytes(t, n, k);
+    if (fwd_stream > fwd) fwd = fwd_stream;
     const size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
     return fwd > dx ? fwd : dx;
   }
@@ -592,6 +594,15 @@ namespace ss {
 template <int EPI>
 static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
   const int64_t n = p.N, k = p.K;
+  // SS_NF4_STREAM=0 turns the streaming kernel off (A/B timing knob).
+  static const bool stream_on = [] {
+    const char* e = getenv("SS_NF4_STREAM");
+    return !(e && e[0] == '0');
+  }();
+  if (p.M <= kStreamMaxT && workspace && stream_on) {
+    const int rc = nf4_stream_fwd(p, EPI, workspace, workspace_bytes, s);
+    if (rc != SS_ERR_UNSUPPORTED) return rc;
+  }
   if (p.M <= kSkinnyMaxT && workspace) {
     const int rc = nf4_skinny_fwd(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;

@@ -64,24 +64,6 @@ struct NtCfg {
   static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS");
 };
 
-// One wave-wide 16-byte-per-lane DMA: lane i's 16 bytes at base + voff land at
-// LDS byte address lds + 16 i.  `base` and `lds` are wave-uniform (SGPRs);
-// voff is the lane's 32-bit byte offset.  s_nop covers the M0-write ->
-// LDS-DMA hazard.
-__device__ __forceinline__ void dma16(uint32_t voff, const half_t* base, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt unconstrained).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
 // Wait until at most `ahead` stages of DMAs (KDMA each) are outstanding.
 template <int KDMA, int MAXAHEAD>
 __device__ __forceinline__ void wait_stages(int64_t ahead) {
@@ -98,10 +80,6 @@ __device__ __forceinline__ void wait_stages(int64_t ahead) {
     }
   }
   wait_vm<0>();
-}
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 // DMA g of an operand tile: the row and logical 16-byte chunk that lane

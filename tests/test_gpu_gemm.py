@@ -62,6 +62,26 @@ def test_forward_matches_oracle(device, t, n, k):
     check(y0[0], ogemm.linear(x, w), f"fwd nobias t={t}")
 
 
+# The streaming T <= 32 forward (post-scaled MFMA on unscaled code values):
+# one or two 16-row M tiles, ragged T and N, one stage (K = 256) up to several
+# stage groups (K = 4608: 18 stages), few row tiles (many groups, tiles split
+# between two workgroups) and many.
+@pytest.mark.parametrize("t,n,k", [
+    (1, 4000, 3584), (5, 200, 256), (16, 8960, 1536), (17, 1000, 3584), (32, 1536, 4608),
+    (9, 64, 8960), (31, 2080, 1536),
+])
+def test_streaming_forward_small_t(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    x = x_of(t, k, seed=7 * t + n)
+    bias = (np.random.default_rng(6).standard_normal(n) * 0.1).astype(np.float16)
+    xt = torch.from_numpy(x).to(device)
+    y = nf4_matmul(xt, packed, qs, bias=torch.from_numpy(bias).to(device))
+    check(y, ogemm.linear(x, w, bias), f"stream fwd t={t} n={n} k={k}")
+    again = nf4_matmul(xt, packed, qs, bias=torch.from_numpy(bias).to(device))
+    assert torch.equal(y, again), "streaming forward is not deterministic"
+
+
 @pytest.mark.parametrize("t,n,k", [
     (1024, 8960, 1536), (800, 1536, 1536), (800, 256, 1536), (800, 1536, 8960),
     (1, 1536, 1536), (16, 8960, 1536), (37, 320, 128), (130, 192, 64),

@@ -51,7 +51,8 @@ def test_epilogue_rounded_product_cancels(device):
 @pytest.mark.parametrize("t,n,k,bias", [(96, 256, 1536, True), (200, 1536, 1536, False),
                                         (37, 8960, 1536, False), (64, 1536, 8960, False),
                                         (300, 256, 1536, True), (990, 8960, 1536, False),
-                                        (990, 1536, 8960, False), (2048, 8960, 256, True)])
+                                        (990, 1536, 8960, False), (2048, 8960, 256, True),
+                                        (16, 8960, 1536, True), (29, 1000, 3584, False)])
 def test_qlora_projection_matches_oracle(device, t, n, k, bias):
     rng = np.random.default_rng(t + n)
     state = onf4.quantize_nested(random_weight(n, k, seed=3))
