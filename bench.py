@@ -21,7 +21,11 @@ roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
              against the MI355X dense fp16 MFMA peak
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
+sweep_configs4 = configs[4]: NF4 forward and dX at the Qwen2.5-7B projection
+             shapes, T in {1, 16, 128, 2048, 16384}, each point timed from HBM
+             (GB/s, TFLOP/s, fraction of its HBM or MFMA roofline)
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-graph]
+       [--no-sweep]
 """
 
 import argparse
@@ -52,6 +56,8 @@ def parse():
                    help="eager steps (queued behind a GPU spin) whose per-call HIP events "
                         "give the roofline kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-sweep", action="store_true",
+                   help="skip the configs[4] NF4 GEMM sweep (7B shapes, T in {1,16,128,2048,16384})")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
                         "FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -151,6 +157,90 @@ class KernelTimer:
                     "avg_gflop": v[1] / v[0] / 1e9,
                     "tflops": v[1] / (v[2] * 1e-3) / 1e12,
                     "total_ms": v[2]} for k, v in per.items()}
+
+
+# Qwen2.5-7B projection shapes (hidden 3584, intermediate 18944,
+# kv 512) as (name, N, K) of W [N, K]; T values of the sweep.
+SWEEP_SHAPES = [("q_o", 3584, 3584), ("k_v", 512, 3584), ("gate_up", 18944, 3584),
+                ("down", 3584, 18944)]
+SWEEP_T = [1, 16, 128, 2048, 16384]
+
+
+def sweep(torch, _lib):
+    """NF4 forward and dX at every configs[4] shape and T through the C ABI.
+
+    Each point is the average of R calls captured in one HIP graph (no host
+    launch cost), rotating over copies of the packed weight whose total
+    exceeds the 256 MB last-level cache, so every call streams its weight
+    from HBM.  Algorithmic bytes: packed codes + qabs + absmax2 + the fp16
+    activation read and output written; flops 2*T*N*K.  roofline_frac =
+    max(bytes / 8 TB/s, flops / 2.5 PFLOP/s) / measured time."""
+    from soupsuck_amd.bnb_compat import quantize_4bit
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    out = {}
+    lib = _lib.load()
+    for name, n, k in SWEEP_SHAPES:
+        w = (torch.randn((n, k), device=dev, generator=gen) * 0.02).half()
+        packed, st = quantize_4bit(w)
+        del w
+        wbytes = n * k // 2 + n * k // 64 + 4 * ((n * k // 64 + 255) // 256)
+        copies = max(1, -(-300_000_000 // wbytes))
+        states = [(packed.clone(), st.absmax.clone()) for _ in range(copies)]
+        rest = (st.state2.absmax.data_ptr(), st.state2.code.data_ptr(), st.offset.data_ptr())
+        for t in SWEEP_T:
+            size = lib.ss_nf4_gemm_workspace_size(t, n, k)
+            ws = torch.empty(max(size, 16), device=dev, dtype=torch.uint8)
+            for mode in ("fwd", "dx"):
+                a = torch.randn((t, n if mode == "dx" else k), device=dev, generator=gen).half()
+                o = torch.empty((t, k if mode == "dx" else n), device=dev, dtype=torch.float16)
+
+                def call(i, stream):
+                    pk, am = states[i % copies]
+                    if mode == "dx":
+                        _lib.call("ss_nf4_gemm_dx", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
+                                  am.data_ptr(), *rest, n, k, o.data_ptr(), o.stride(0), 0,
+                                  ws.data_ptr(), size, stream)
+                    else:
+                        _lib.call("ss_nf4_gemm_fwd", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
+                                  am.data_ptr(), *rest, n, k, None, o.data_ptr(), o.stride(0),
+                                  ws.data_ptr(), size, stream)
+
+                flops = 2.0 * t * n * k
+                reps = max(4, min(64, int(2e10 / max(flops, 1.0))))
+                call(0, _lib.stream(dev))
+                torch.cuda.synchronize()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=side):
+                    sc = _lib.stream(dev)
+                    for i in range(reps):
+                        call(i, sc)
+                graph.replay()
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                graph.replay()
+                e1.record()
+                e1.synchronize()
+                us = e0.elapsed_time(e1) / reps * 1e3
+                moved = wbytes + 2 * t * (n + k)
+                bound_us = max(moved / PEAK_HBM_GBS / 1e3, flops / PEAK_FP16_TFLOPS / 1e6)
+                out[f"{name} T={t} {mode}"] = {
+                    "N": n, "K": k, "us": round(us, 2), "GB/s": round(moved / us / 1e3, 1),
+                    "TFLOP/s": round(flops / us / 1e6, 2),
+                    "bound": "hbm" if moved / PEAK_HBM_GBS / 1e3 >= flops / PEAK_FP16_TFLOPS / 1e6
+                    else "mfma",
+                    "roofline_frac": round(bound_us / us, 4)}
+                del graph, a, o
+            del ws
+        del states, packed, st
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(layer, xs, gs, budget_s):
@@ -296,6 +386,8 @@ def main():
                 "timing": (f"HIP events on the launch stream around each call, {args.timing_steps}"
                            " eager steps each queued behind a GPU spin (calls run back to back)")}
 
+    sweep_res = None if args.no_sweep else sweep(torch, _lib)
+
     cpu = None
     if not args.no_cpu_baseline:
         med, reps, threads = cpu_baseline(layer, xs, gs, args.cpu_seconds)
@@ -323,6 +415,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
+        "sweep_configs4": sweep_res,
     }
     print(json.dumps(line), flush=True)
 
