@@ -193,4 +193,14 @@ size_t stream_partial_bytes(int64_t t, int64_t n, int64_t k);
 int nf4_stream_fwd(const GemmParams& p, int epi, void* partials, size_t partial_bytes,
                    hipStream_t stream);
 
+// Streaming NF4 backward (nf4_stream_dx.hip) for T <= kStreamDxMaxT rows, N %
+// 16 == 0 and K % 256 == 0: dX = dY . Wdec with the codes read transposed from
+// LDS and the block scales folded into dY; fp32 partial planes per row range,
+// reduced (with the epilogue) by splitk_reduce.  p: M = T, N = K (dX columns),
+// K = N (weight rows), A = dY.  SS_ERR_UNSUPPORTED when not applicable.
+constexpr int64_t kStreamDxMaxT = 16;
+size_t stream_dx_partial_bytes(int64_t t, int64_t n, int64_t k);
+int nf4_stream_dx(const GemmParams& p, int epi, void* partials, size_t partial_bytes,
+                  hipStream_t stream);
+
 }  // namespace ss

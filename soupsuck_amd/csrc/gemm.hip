@@ -563,7 +563,9 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     size_t fwd = ss::skinny_partial_bytes(t, n, k);
     const size_t fwd_stream = ss::stream_partial_bytes(t, n, k);
     if (fwd_stream > fwd) fwd = fwd_stream;
-    const size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
+    size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
+    const size_t dx_stream = ss::stream_dx_partial_bytes(t, n, k);
+    if (dx_stream > dx) dx = dx_stream;
     return fwd > dx ? fwd : dx;
   }
   if (t < threshold) return 0;
@@ -591,15 +593,19 @@ static int check_nf4(const char* fn, const uint8_t* packed, const uint8_t* qabs,
 
 namespace ss {
 
-template <int EPI>
-static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
-  const int64_t n = p.N, k = p.K;
-  // SS_NF4_STREAM=0 turns the streaming kernel off (A/B timing knob).
-  static const bool stream_on = [] {
+// SS_NF4_STREAM=0 turns the streaming small-T kernels off (A/B timing knob).
+static bool stream_enabled() {
+  static const bool on = [] {
     const char* e = getenv("SS_NF4_STREAM");
     return !(e && e[0] == '0');
   }();
-  if (p.M <= kStreamMaxT && workspace && stream_on) {
+  return on;
+}
+
+template <int EPI>
+static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const int64_t n = p.N, k = p.K;
+  if (p.M <= kStreamMaxT && workspace && stream_enabled()) {
     const int rc = nf4_stream_fwd(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;
   }
@@ -626,6 +632,10 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
 template <int EPI>
 static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                   hipStream_t s) {
+  if (p.M <= kStreamDxMaxT && workspace && stream_enabled()) {
+    const int rc = nf4_stream_dx(p, EPI, workspace, workspace_bytes, s);
+    if (rc != SS_ERR_UNSUPPORTED) return rc;
+  }
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
     // Decode W^T [k, n] once; dX = dY . W is then the K-contiguous NT product.
     const Nf4View& w = p.w;

@@ -94,6 +94,28 @@ def test_dx_matches_oracle(device, t, n, k):
     check(dx, ogemm.linear_dx(dy, w), f"dx t={t} n={n} k={k}")
 
 
+# The streaming T <= 16 backward (transposed LDS reads of the codes, block
+# scales folded into dY): ragged T, rows not a multiple of the 64-row unit,
+# one to many row ranges, one column stage (K = 256) to many, N % 16 != 0
+# (falls back to decode-first), and accumulation into dX.
+@pytest.mark.parametrize("t,n,k", [
+    (1, 4000, 3584), (16, 8960, 1536), (5, 1536, 256), (9, 64, 8960), (16, 3584, 4608),
+    (3, 200, 512), (12, 1040, 768),
+])
+def test_streaming_dx_small_t(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    dy = x_of(t, n, seed=5 * t + k)
+    dyt = torch.from_numpy(dy).to(device)
+    dx = nf4_matmul(dyt, packed, qs, transpose=True)
+    check(dx, ogemm.linear_dx(dy, w), f"stream dx t={t} n={n} k={k}")
+    assert torch.equal(dx, nf4_matmul(dyt, packed, qs, transpose=True)), "not deterministic"
+    base = x_of(t, k, seed=t, scale=0.1)
+    out = torch.from_numpy(base).to(device)
+    nf4_dx_2d(dyt, packed, qs, n, k, out=out, accumulate=True)
+    check(out, ogemm.linear_dx(dy, w) + base.astype(np.float64), f"stream dx accumulate t={t}")
+
+
 def test_dx_accumulate(device):
     state, w = weight(256, 1536)
     packed, qs = device_state(state, device)
