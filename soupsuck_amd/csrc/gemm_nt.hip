@@ -416,6 +416,13 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   } else if (t128 >= 128) {
     plan.cfg = 2;
+  } else if (t128 < 64 && k >= 1024) {
+    // Few output tiles (e.g. a 256-wide k/v projection): 64x64 tiles split
+    // over K until about 256 workgroups run, each split at least 384 deep.
+    const int64_t t64 = cdiv(m, 64) * cdiv(n, 64);
+    int64_t s = 256 / t64;
+    if (s > k / 384) s = k / 384;
+    plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   }
   if (forced >= 1 && forced <= 7) plan.cfg = forced;
   if (forced_splits >= 1) plan.splits = forced_splits;

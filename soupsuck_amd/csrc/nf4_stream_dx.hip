@@ -295,15 +295,16 @@ int dx_cu_count() {
   return cus;
 }
 
-// Column stages of 256; row ranges so that about one workgroup per CU runs,
-// each range at least 8 units (one per wave) when the rows allow.
+// Column stages of 256; row ranges so that at most one workgroup per CU runs
+// (the LDS holds one), each range at least 8 units (one per wave) when the
+// rows allow.
 StreamDxPlan stream_dx_plan(int64_t t, int64_t nr, int64_t nc) {
   StreamDxPlan plan{};
   if (t < 1 || t > kStreamDxMaxT || nr < 16 || nr % 16 != 0 || nc < kDxCols || nc % kDxCols != 0)
     return plan;
   const int64_t cus = dx_cu_count();
   plan.col_stages = nc / kDxCols;
-  int64_t g = cdiv(cus, plan.col_stages);
+  int64_t g = cus / plan.col_stages;  // at most one workgroup per CU
   const int64_t g_max = cdiv(nr, kDxRows * kDxWaves);
   if (g > g_max) g = g_max;
   if (g < 1) g = 1;
