@@ -21,11 +21,14 @@ roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
              against the MI355X dense fp16 MFMA peak
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
+other_configs = configs[0] (gate dequant GB/s, GEMM T=1024 TFLOP/s), configs[2]
+             (add-RMSNorm fwd/bwd/dgamma and unpad gather/scatter GB/s) and
+             configs[3] (fused chunked CE fwd+bwd ms and TFLOP/s)
 sweep_configs4 = configs[4]: NF4 forward and dX at the Qwen2.5-7B projection
              shapes, T in {1, 16, 128, 2048, 16384}, each point timed from HBM
              (GB/s, TFLOP/s, fraction of its HBM or MFMA roofline)
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-graph]
-       [--no-sweep]
+       [--no-sweep] [--no-other-configs]
 """
 
 import argparse
@@ -58,6 +61,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-sweep", action="store_true",
                    help="skip the configs[4] NF4 GEMM sweep (7B shapes, T in {1,16,128,2048,16384})")
+    p.add_argument("--no-other-configs", action="store_true",
+                   help="skip configs[0], configs[2] and configs[3] (dequant, GEMM T=1024, "
+                        "add-RMSNorm, unpad, fused CE)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
                         "FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -210,24 +216,7 @@ def sweep(torch, _lib):
 
                 flops = 2.0 * t * n * k
                 reps = max(4, min(64, int(2e10 / max(flops, 1.0))))
-                call(0, _lib.stream(dev))
-                torch.cuda.synchronize()
-                side = torch.cuda.Stream()
-                side.wait_stream(torch.cuda.current_stream())
-                graph = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(graph, stream=side):
-                    sc = _lib.stream(dev)
-                    for i in range(reps):
-                        call(i, sc)
-                graph.replay()
-                torch.cuda.synchronize()
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                graph.replay()
-                e1.record()
-                e1.synchronize()
-                us = e0.elapsed_time(e1) / reps * 1e3
+                us = graph_us(torch, _lib, call, reps)
                 moved = wbytes + 2 * t * (n + k)
                 bound_us = max(moved / PEAK_HBM_GBS / 1e3, flops / PEAK_FP16_TFLOPS / 1e6)
                 out[f"{name} T={t} {mode}"] = {
@@ -236,10 +225,226 @@ def sweep(torch, _lib):
                     "bound": "hbm" if moved / PEAK_HBM_GBS / 1e3 >= flops / PEAK_FP16_TFLOPS / 1e6
                     else "mfma",
                     "roofline_frac": round(bound_us / us, 4)}
-                del graph, a, o
+                del a, o
             del ws
         del states, packed, st
         torch.cuda.empty_cache()
+    return out
+
+
+def graph_us(torch, _lib, call, reps):
+    """Average µs of one call(i, stream) over reps calls captured in one HIP graph."""
+    dev = torch.device("cuda:0")
+    call(0, _lib.stream(dev))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        sc = _lib.stream(dev)
+        for i in range(reps):
+            call(i, sc)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    e1.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / reps * 1e3
+
+
+def hbm_point(us, moved, copies):
+    return {"us": round(us, 2), "bytes": int(moved), "GB/s": round(moved / us / 1e3, 1),
+            "bound": "hbm", "roofline_frac": round(moved / PEAK_HBM_GBS / 1e3 / us, 4),
+            "copies_rotated": copies}
+
+
+def other_configs(torch, _lib):
+    """BASELINE.json configs[0], configs[2] and configs[3] on the GPU.
+
+    HBM-bound points rotate over enough copies of their operands (> 300 MB)
+    that each call reads from HBM, not from the 256 MB last-level cache; each
+    is the average of R calls captured in one HIP graph.  Algorithmic bytes:
+      dequant      0.5 + 1/64 B per weight in (codes, qabs) + absmax2 + 2 B out;
+      add-RMSNorm  fwd  r, d in, s, y out (8 H B per row) + rstd 4 B + w 2 H;
+                   bwd  s, gs, gy in, dr, dd out (10 H B per row) + rstd + w;
+                   dgamma s, gy in (4 H B per row) + rstd + partial planes;
+      gather       T rows read + T rows written (4 H B per token);
+      scatter      T rows read + B*S rows written + the int32 inverse map.
+    CE is timed whole through fused_linear_cross_entropy
+    (forward, then backward with the lm_head gradient), host clock around
+    synchronized calls, median of 5; flops 2 T V H forward and 3 x 2 T_valid V H
+    backward (recomputed logits, dX, dW)."""
+    from soupsuck_amd import unpad
+    from soupsuck_amd.bnb_compat import quantize_4bit
+    from soupsuck_amd.kernels.cross_entropy import fused_linear_cross_entropy
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    out = {}
+    f16 = _lib.F16
+
+    # configs[0]: gate [8960, 1536], dequant alone and Y = X W^T at T = 1024.
+    n, k = 8960, 1536
+    w = (torch.randn((n, k), device=dev, generator=gen) * 0.02).half()
+    packed, st = quantize_4bit(w)
+    del w
+    moved = n * k // 2 + n * k // 64 + 4 * (-(-n * k // 16384)) + 1028 + 2 * n * k
+    copies = max(1, -(-300_000_000 // moved))
+    packs = [(packed.clone(), st.absmax.clone()) for _ in range(copies)]
+    outs = [torch.empty((n, k), device=dev, dtype=torch.float16) for _ in range(copies)]
+    rest = (st.state2.absmax.data_ptr(), st.state2.code.data_ptr(), st.offset.data_ptr())
+
+    def dequant(i, stream):
+        pk, am = packs[i % copies]
+        _lib.call("ss_nf4_dequant_nested", pk.data_ptr(), am.data_ptr(), *rest,
+                  outs[i % copies].data_ptr(), n * k, stream)
+
+    us = graph_us(torch, _lib, dequant, 64)
+    out["configs0_dequant_gate_8960x1536"] = hbm_point(us, moved, copies)
+    del outs
+    t = 1024
+    x = torch.randn((t, k), device=dev, generator=gen).half()
+    y = torch.empty((t, n), device=dev, dtype=torch.float16)
+    size = _lib.load().ss_nf4_gemm_workspace_size(t, n, k)
+    ws = torch.empty(max(size, 16), device=dev, dtype=torch.uint8)
+
+    def gemm(i, stream):
+        pk, am = packs[i % copies]
+        _lib.call("ss_nf4_gemm_fwd", x.data_ptr(), x.stride(0), t, pk.data_ptr(),
+                  am.data_ptr(), *rest, n, k, None, y.data_ptr(), y.stride(0),
+                  ws.data_ptr(), size, stream)
+
+    us = graph_us(torch, _lib, gemm, 32)
+    flops = 2.0 * t * n * k
+    out["configs0_gemm_T1024_gate"] = {
+        "us": round(us, 2), "TFLOP/s": round(flops / us / 1e6, 1), "bound": "mfma",
+        "roofline_frac": round(flops / PEAK_FP16_TFLOPS / 1e6 / us, 4)}
+    del packs, packed, st, x, y, ws
+
+    # configs[2]: add-RMSNorm fwd/bwd/dgamma at T in {826, 4096, 16384}, H = 1536.
+    h = 1536
+    wn = (1 + 0.1 * torch.randn(h, device=dev, generator=gen)).half()
+    for t in (826, 4096, 16384):
+        row_fwd = 8 * h + 4
+        copies = max(1, -(-300_000_000 // (t * row_fwd)))
+        bufs = []
+        for _ in range(copies):
+            r = torch.randn((t, h), device=dev, generator=gen).half()
+            d = torch.randn((t, h), device=dev, generator=gen).half()
+            bufs.append((r, d, torch.empty_like(r), torch.empty_like(r),
+                         torch.empty(t, device=dev, dtype=torch.float32)))
+
+        def fwd(i, stream):
+            r, d, s, yy, rstd = bufs[i % copies]
+            _lib.call("ss_add_rmsnorm_fwd", r.data_ptr(), f16, d.data_ptr(), f16, wn.data_ptr(),
+                      f16, 1, s.data_ptr(), f16, yy.data_ptr(), f16, rstd.data_ptr(), t, h,
+                      1e-6, stream)
+
+        us = graph_us(torch, _lib, fwd, 32)
+        out[f"configs2_add_rmsnorm_fwd_T{t}"] = hbm_point(us, t * row_fwd + 2 * h, copies)
+        # Backward reuses the buffers: r -> gs, d -> gy (inputs), and writes
+        # dr, dd into two fresh planes per copy.
+        grads = [(torch.empty_like(b[0]), torch.empty_like(b[0])) for b in bufs]
+
+        def bwd(i, stream):
+            gs, gy, s, _, rstd = bufs[i % copies]
+            dr, dd = grads[i % copies]
+            _lib.call("ss_add_rmsnorm_bwd", s.data_ptr(), f16, wn.data_ptr(), f16, 1,
+                      rstd.data_ptr(), gs.data_ptr(), f16, h, 1, gy.data_ptr(), f16, h, 1,
+                      dr.data_ptr(), f16, dd.data_ptr(), f16, t, h, stream)
+
+        us = graph_us(torch, _lib, bwd, 32)
+        out[f"configs2_add_rmsnorm_bwd_T{t}"] = hbm_point(us, t * (10 * h + 4) + 2 * h, copies)
+        groups = -(-t // 32)
+        partial = torch.empty((groups, h), device=dev, dtype=torch.float32)
+        dw = torch.empty(h, device=dev, dtype=torch.float16)
+
+        def dgamma(i, stream):
+            _, gy, s, _, rstd = bufs[i % copies]
+            _lib.call("ss_rmsnorm_dgamma", s.data_ptr(), f16, rstd.data_ptr(), gy.data_ptr(),
+                      f16, h, 1, 1, partial.data_ptr(), dw.data_ptr(), f16, t, h, stream)
+
+        us = graph_us(torch, _lib, dgamma, 32)
+        out[f"configs2_rmsnorm_dgamma_T{t}"] = hbm_point(
+            us, t * (4 * h + 4) + 2 * groups * h * 4 + 2 * h, copies)
+        del bufs, grads
+
+    # configs[2]: unpad gather/scatter of a [4, 360, 1536] fp16 batch.
+    cg = torch.Generator(device="cpu").manual_seed(0)
+    lengths = [int(v) for v in torch.randint(80, 361, (4,), generator=cg)]
+    batch = unpad.make_batch(lengths, 360, dev)
+    tokens, rows = batch.tokens, batch.rows
+    inverse = batch.inverse()
+    row_bytes = 2 * h
+    moved_g = 2 * tokens * row_bytes + 8 * tokens
+    copies = max(1, -(-300_000_000 // moved_g))
+    padded = [torch.randn((rows, h), device=dev, generator=gen).half() for _ in range(copies)]
+    packed_rows = [torch.empty((tokens, h), device=dev, dtype=torch.float16)
+                   for _ in range(copies)]
+
+    def gather(i, stream):
+        _lib.call("ss_unpad_gather", padded[i % copies].data_ptr(), rows,
+                  packed_rows[i % copies].data_ptr(), batch.indices.data_ptr(), tokens,
+                  row_bytes, stream)
+
+    us = graph_us(torch, _lib, gather, 64)
+    out["configs2_unpad_gather_4x360"] = hbm_point(us, moved_g, copies)
+    out["configs2_unpad_gather_4x360"].update(tokens=tokens, lengths=lengths)
+
+    def scatter(i, stream):
+        _lib.call("ss_unpad_scatter", packed_rows[i % copies].data_ptr(), tokens,
+                  padded[i % copies].data_ptr(), inverse.data_ptr(), rows, row_bytes, stream)
+
+    us = graph_us(torch, _lib, scatter, 64)
+    out["configs2_unpad_scatter_4x360"] = hbm_point(
+        us, tokens * row_bytes + rows * row_bytes + 4 * rows, copies)
+    del padded, packed_rows
+
+    # configs[3]: chunked fused linear CE, hidden [826, 1536], tied head [151936, 1536].
+    t, v = 826, 151936
+    hidden = torch.randn((t, h), device=dev, generator=gen).half()
+    head = (torch.randn((v, h), device=dev, generator=gen) * 0.02).half()
+    labels = torch.randint(0, v, (t,), device=dev, generator=gen)
+    ignored = torch.rand(t, device=dev, generator=gen) < 0.365
+    labels[ignored] = -100
+    valid = int((labels != -100).sum().item())
+    hd = hidden.clone().requires_grad_()
+    hw = head.clone().requires_grad_()
+    fwd_ms, tot_ms = [], []
+    for rep in range(6):
+        hd.grad = None
+        hw.grad = None
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loss, _, _, _ = fused_linear_cross_entropy(hd, hw, labels, chunk=8192, weight_grad=True)
+        mean = loss.sum() / valid
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        mean.backward()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if rep:
+            fwd_ms.append(1e3 * (t1 - t0))
+            tot_ms.append(1e3 * (t2 - t0))
+    fwd = statistics.median(fwd_ms)
+    tot = statistics.median(tot_ms)
+    f_fwd = 2.0 * t * v * h
+    f_bwd = 3 * 2.0 * valid * v * h
+    out["configs3_fused_ce_fwd_bwd"] = {
+        "tokens": t, "valid": valid, "vocab": v, "chunk": 8192,
+        "fwd_ms": round(fwd, 3), "fwd_bwd_ms": round(tot, 3),
+        "fwd_TFLOP/s": round(f_fwd / fwd / 1e9, 1),
+        "fwd_bwd_TFLOP/s": round((f_fwd + f_bwd) / tot / 1e9, 1),
+        "bound": "mfma",
+        "roofline_frac": round((f_fwd + f_bwd) / PEAK_FP16_TFLOPS / 1e9 / tot, 4),
+        "timing": "host clock around synchronized calls (includes the backward's two host "
+                  "syncs), median of 5 after 1 warm-up"}
+    del hidden, head, hd, hw
+    torch.cuda.empty_cache()
     return out
 
 
@@ -387,6 +592,7 @@ def main():
                            " eager steps each queued behind a GPU spin (calls run back to back)")}
 
     sweep_res = None if args.no_sweep else sweep(torch, _lib)
+    others = None if args.no_other_configs else other_configs(torch, _lib)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -416,6 +622,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in kernels.items()},
         "sweep_configs4": sweep_res,
+        "other_configs": others,
     }
     print(json.dumps(line), flush=True)
 

@@ -144,7 +144,11 @@ int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* pack
  *   fp16(Q * q_scale); stored [16][n], or [n][16] when transpose.
  *   dA = dZ^T.X and dB = dL^T.Z.
  * workspace: fp32 partials, at least ss_lora_workspace_size(rows, cols) bytes
- * for an output with rows x 16 or 16 x cols elements. */
+ * for an output with rows x 16 or 16 x cols elements.  It is used only when
+ * the reduction is split over workgroups (few output blocks and a long
+ * reduction: fewer than 32 row blocks with K > 4096, or fewer than 32 column
+ * blocks with T > 4096); otherwise the op is one launch and the workspace
+ * may be NULL. */
 size_t ss_lora_workspace_size(int64_t rows, int64_t cols);
 int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_t k, const uint16_t* w,
                     int64_t ldw, int w_kr, int scale_a, float a_scale, uint16_t* out,

@@ -14,10 +14,15 @@
 //   BK = 64: a DMA covers 8 rows x 128 B.  Block b (rows 8b .. 8b+7) is 1 KiB;
 //     chunk c of row 8b + r sits at slot (c ^ (b & 1)) * 8 + r.
 //   BK = 32: a DMA covers 16 rows x 64 B.  Row r is 64 B; chunk c sits at
-//     chunk c ^ ((r >> 1) & 3).
-// Both make an MFMA 32x32x16 fragment read (32 consecutive rows, one chunk
-// per lane half) free of LDS bank conflicts (BK = 64: measured; BK = 32:
-// 2-way at most).
+//     chunk c ^ swz32(r), swz32(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1).
+// A 128-bit LDS read is served 16 lanes at a time over 64 four-byte banks
+// (256 B): with 64-byte rows, rows r and r + 4 share bank quads, so the 16
+// rows of one pass must cover the four chunk positions once per residue
+// r % 4.  swz32 does that and also keeps each 8-lane group conflict-free
+// (the narrower 128-byte pass); the former c ^ ((r >> 1) & 3) repeated with
+// period 8 and measured a uniform 2-way conflict (SQ_LDS_BANK_CONFLICT =
+// half of SQ_LDS_IDX_ACTIVE).  Both layouts make an MFMA 32x32x16 fragment
+// read (32 consecutive rows, one chunk per lane half) conflict-free.
 //
 // Per stage a wave runs BK / 16 MFMA k-steps; fragments are double buffered
 // so the reads of k-step kk+1 overlap the MFMAs of kk.  One s_barrier per
@@ -60,13 +65,26 @@ struct NtCfg {
   static_assert(BM % (kRowsPerDma * kWaves) == 0 && BN % (kRowsPerDma * kWaves) == 0,
                 "DMA split over waves");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "32x32 MFMA blocks");
-  static_assert(STAGES >= 2 && STAGES <= 3, "pipeline depth");
+  static_assert(STAGES >= 2 && STAGES <= 5, "pipeline depth");
   static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS");
 };
 
 // Wait until at most `ahead` stages of DMAs (KDMA each) are outstanding.
 template <int KDMA, int MAXAHEAD>
 __device__ __forceinline__ void wait_stages(int64_t ahead) {
+  static_assert(MAXAHEAD <= 4, "wait depth");
+  if constexpr (MAXAHEAD >= 4) {
+    if (ahead >= 4) {
+      wait_vm<4 * KDMA>();
+      return;
+    }
+  }
+  if constexpr (MAXAHEAD >= 3) {
+    if (ahead >= 3) {
+      wait_vm<3 * KDMA>();
+      return;
+    }
+  }
   if constexpr (MAXAHEAD >= 2) {
     if (ahead >= 2) {
       wait_vm<2 * KDMA>();
@@ -82,6 +100,9 @@ __device__ __forceinline__ void wait_stages(int64_t ahead) {
   wait_vm<0>();
 }
 
+// Chunk swizzle of the BK = 32 layout (see the layout notes above).
+__device__ __forceinline__ int swz32(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
 // DMA g of an operand tile: the row and logical 16-byte chunk that lane
 // fetches (its LDS slot is g * 1024 + 16 * lane).
 template <int BK>
@@ -91,7 +112,7 @@ __device__ __forceinline__ void dma_source(int g, int lane, int& row, int& chunk
     chunk = (lane >> 3) ^ (g & 1);
   } else {
     row = g * 16 + (lane >> 2);
-    chunk = (lane & 3) ^ ((row >> 1) & 3);
+    chunk = (lane & 3) ^ swz32(row);
   }
 }
 
@@ -106,7 +127,7 @@ __device__ __forceinline__ int frag_offset(int lane, int kk) {
     const int b = r >> 3;
     return b * 1024 + ((((c ^ (b & 1)) * 8) + (r & 7)) << 4);
   } else {
-    return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+    return r * 64 + ((c ^ swz32(r)) << 4);
   }
 }
 
@@ -374,6 +395,10 @@ using NtBig8 = NtCfg<256, 256, 2, 4, 64, 2, 2>;     // 8 waves of 128x64, 128 Ki
 using NtWide8 = NtCfg<256, 128, 4, 2, 64, 2, 2>;    // 8 waves of 64x64, 96 KiB LDS
 using NtBig8s = NtCfg<256, 256, 2, 4, 32, 3, 2>;    // 8 waves of 128x64, 96 KiB LDS
 using NtMid64 = NtCfg<128, 128, 2, 2, 64, 2, 2>;    // 4 waves of 64x64, 64 KiB LDS
+using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 KiB LDS
+using NtBig8s5 = NtCfg<256, 256, 2, 4, 32, 5, 2>;   // 8 waves of 128x64, 160 KiB LDS
+using NtBig4s4 = NtCfg<256, 256, 2, 2, 32, 4, 1>;   // 4 waves of 128x128, 128 KiB LDS
+using NtBig4s5 = NtCfg<256, 256, 2, 2, 32, 5, 1>;   // 4 waves of 128x128, 160 KiB LDS
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
@@ -384,11 +409,12 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
 }
 
 // Configuration and split-K plan for an M x N x K product.
-//   256x256 (8 waves) once it gives at least half the CUs a tile;
+//   256x256 (8 waves, 4-stage ring) once it gives at least half the CUs a
+//   tile;
 //   long K with few 128x128 tiles: 128x128 split over k so that about 512
 //   workgroups run (each split at least 1024 k);
 //   128x128 while it gives half the CUs a tile; else 64x64.
-// SS_NT_TILE (1..7, the configurations above in order) and SS_NT_SPLITS
+// SS_NT_TILE (1..11, the configurations above in order) and SS_NT_SPLITS
 // override the choice (tuning knobs read once per process).
 struct NtPlan {
   int cfg;
@@ -408,7 +434,7 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   const int64_t t256 = cdiv(m, 256) * cdiv(n, 256);
   const int64_t t128 = cdiv(m, 128) * cdiv(n, 128);
   if (t256 >= 128) {
-    plan.cfg = 6;
+    plan.cfg = 8;
   } else if (k >= 2048 && t128 < 256) {
     plan.cfg = 2;
     int64_t s = 512 / t128;
@@ -424,7 +450,7 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     if (s > k / 384) s = k / 384;
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   }
-  if (forced >= 1 && forced <= 7) plan.cfg = forced;
+  if (forced >= 1 && forced <= 11) plan.cfg = forced;
   if (forced_splits >= 1) plan.splits = forced_splits;
   plan.k_split = cdiv(cdiv(k, plan.splits), 64) * 64;
   plan.splits = cdiv(k, plan.k_split);
@@ -434,6 +460,10 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
 template <int CT, int EPI>
 int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
   switch (cfg) {
+    case 11: return launch_nt<NtBig4s5, CT, EPI>(p, splits, stream);
+    case 10: return launch_nt<NtBig4s4, CT, EPI>(p, splits, stream);
+    case 9: return launch_nt<NtBig8s5, CT, EPI>(p, splits, stream);
+    case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
     case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
     case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
     case 5: return launch_nt<NtWide8, CT, EPI>(p, splits, stream);

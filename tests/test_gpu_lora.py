@@ -86,7 +86,9 @@ def test_qlora_projection_matches_oracle(device, t, n, k, bias):
     assert rel_norm(np16(bt.grad), db) < 1e-2
 
 
-@pytest.mark.parametrize("m,k", [(37, 100), (990, 1536), (990, 8960), (1, 64), (130, 16)])
+@pytest.mark.parametrize("m,k", [(37, 100), (990, 1536), (990, 8960), (1, 64), (130, 16),
+                                 (16, 8960),     # few row blocks, long K: split form
+                                 (500, 5000)])   # 32 row blocks: one launch, 16 waves
 @pytest.mark.parametrize("w_kr", [False, True])
 @pytest.mark.parametrize("scale", [None, 2.0, 1.3])
 def test_rank_project_matches_numpy(device, m, k, w_kr, scale):
@@ -102,7 +104,10 @@ def test_rank_project_matches_numpy(device, m, k, w_kr, scale):
     np.testing.assert_allclose(np16(out).astype(np.float64), expected, rtol=2e-3, atol=2e-3)
 
 
-@pytest.mark.parametrize("t,n", [(37, 100), (990, 1536), (990, 8960), (1, 64), (300, 16)])
+@pytest.mark.parametrize("t,n", [(37, 100), (990, 1536), (990, 8960), (1, 64), (300, 16),
+                                 (6000, 64),     # one column block, long T: split form
+                                 (5000, 2048),   # 32 column blocks: one launch
+                                 (0, 64)])       # empty reduction: zeros
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("scale", [None, 2.0])
 def test_rank_grad_matches_numpy(device, t, n, transpose, scale):
