@@ -131,36 +131,42 @@ __device__ __forceinline__ int frag_offset(int lane, int kk) {
   }
 }
 
-template <class C, int CT, int EPI>
-__global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::STAGES * C::kStageBytes];
+template <class C>
+using NtAcc = float16v[C::FM][C::FN];
+
+// Tile id -> (m0, n0).  Consecutive tile ids walk groups of kGroupM M-tiles
+// (M fastest) before moving to the next N-tile, so the tiles resident on one
+// XCD at a time (after the XCD remap of workgroup ids) form a kGroupM x (n)
+// block that reuses both its A panels and its B panels from that XCD's L2.
+template <class C>
+__device__ __forceinline__ void tile_origin(const GemmParams& p, int64_t tile, int64_t& m0,
+                                            int64_t& n0) {
+  const int64_t mtiles = cdiv(p.M, C::BM);
+  const int64_t ntiles = cdiv(p.N, C::BN);
+  constexpr int64_t kGroupM = 8;
+  const int64_t per_group = kGroupM * ntiles;
+  const int64_t first_m = (tile / per_group) * kGroupM;
+  const int64_t group_m = mtiles - first_m < kGroupM ? mtiles - first_m : kGroupM;
+  const int64_t in_group = tile % per_group;
+  m0 = (first_m + in_group % group_m) * C::BM;
+  n0 = (in_group / group_m) * C::BN;
+}
+
+// acc += A[m0.., kbeg .. kbeg+klen) . B[n0.., same k]^T for one output tile:
+// the pipelined direct-to-LDS main loop.  All of the workgroup's LDS DMAs
+// have completed when it returns; the caller puts a barrier between two calls
+// (the last k-step's LDS reads of one call and the first DMAs of the next).
+template <class C>
+__device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
+                                            int64_t kbeg, int64_t klen, unsigned char* smem,
+                                            NtAcc<C>& acc) {
   constexpr int kGroupBytes = 32 * C::BK * 2;  // one 32-row group of a stage tile
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / C::kWavesN;
   const int wn = wave % C::kWavesN;
-  // Tile order: after the XCD remap, consecutive tile ids walk groups of
-  // kGroupM M-tiles (M fastest) before moving to the next N-tile, so the
-  // tiles resident on one XCD at a time form a kGroupM x (n) block that
-  // reuses both its A panels and its B panels from that XCD's L2.
-  const int64_t mtiles = cdiv(p.M, C::BM);
-  const int64_t ntiles = cdiv(p.N, C::BN);
-  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
-  constexpr int64_t kGroupM = 8;
-  const int64_t per_group = kGroupM * ntiles;
-  const int64_t first_m = (tile / per_group) * kGroupM;
-  const int64_t group_m = mtiles - first_m < kGroupM ? mtiles - first_m : kGroupM;
-  const int64_t in_group = tile % per_group;
-  const int64_t m0 = (first_m + in_group % group_m) * C::BM;
-  const int64_t n0 = (in_group / group_m) * C::BN;
   const uint32_t lds0 = lds_address(smem);
-  // Split-K: this workgroup's k range.
-  int64_t kbeg = 0, klen = p.K;
-  if constexpr (EPI == EPI_PARTIAL) {
-    kbeg = (int64_t)blockIdx.y * p.k_split;
-    klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
-  }
   const half_t* a_base = p.A + kbeg;
   const half_t* b_base = p.B + kbeg;
 
@@ -189,14 +195,6 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
   int frag_off[C::KK];
 #pragma unroll
   for (int kk = 0; kk < C::KK; ++kk) frag_off[kk] = frag_offset<C::BK>(lane, kk);
-  const int lr = lane & 31;  // epilogue: column within a 32x32 block
-  const int lh = lane >> 5;
-
-  float16v acc[C::FM][C::FN];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
 
   auto dma_one = [&](int64_t kt, int stage, int idx) {
     if (idx < C::kDmaA) {
@@ -273,9 +271,19 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
     for (int d = kMfma < C::kDma ? kMfma * (C::kDma / kMfma) : C::kDma; d < C::kDma; ++d)
       if (refill) dma_one(kt + kS, refill_stage, d);
   }
+}
 
-  // Epilogue: lane holds D[8 (r / 4) + 4 (lane / 32) + r % 4][lane % 32] of
-  // each 32x32 block in register r.
+// Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
+// 4][lane % 32] of each 32x32 block in register r.
+template <class C, int CT, int EPI>
+__device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
+                                            const NtAcc<C>& acc) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const int lr = lane & 31;  // column within a 32x32 block
+  const int lh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
@@ -330,6 +338,29 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
       }
     }
   }
+}
+
+// Data-parallel / split-K kernel: workgroup = one output tile (blockIdx.x,
+// XCD-remapped) and one k split (blockIdx.y; EPI_PARTIAL stores its fp32
+// accumulator to split plane blockIdx.y).
+template <class C, int CT, int EPI>
+__global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::STAGES * C::kStageBytes];
+  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
+  int64_t m0, n0;
+  tile_origin<C>(p, tile, m0, n0);
+  int64_t kbeg = 0, klen = p.K;
+  if constexpr (EPI == EPI_PARTIAL) {
+    kbeg = (int64_t)blockIdx.y * p.k_split;
+    klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
+  }
+  NtAcc<C> acc;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
+  nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc);
 }
 
 // Split-K reduction: out[row][col] = epilogue(sum over splits s = 0.. of

@@ -116,6 +116,35 @@ def test_streaming_dx_small_t(device, t, n, k):
     check(out, ogemm.linear_dx(dy, w) + base.astype(np.float64), f"stream dx accumulate t={t}")
 
 
+# Decode-first products at the configs[1] layer shapes (T = 990: 256x256
+# tiles for 990x8960x1536, split-K 128x128 for the long-K 990x1536x8960,
+# 64x64 split-K for the narrow 990x256x1536), ragged T and N; split-K sums in
+# split order, so two calls give the same bits; accumulation (beta = 1).
+@pytest.mark.parametrize("t,n,k", [
+    (990, 8960, 1536), (990, 1536, 1536), (990, 1536, 8960), (990, 256, 1536),
+    (4100, 256, 1536), (300, 2000, 1536),
+])
+def test_decode_first_products(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    x = x_of(t, k, seed=t + 2 * n)
+    bias = (np.random.default_rng(9).standard_normal(n) * 0.1).astype(np.float16)
+    xt = torch.from_numpy(x).to(device)
+    bt = torch.from_numpy(bias).to(device)
+    y = nf4_matmul(xt, packed, qs, bias=bt)
+    check(y, ogemm.linear(x, w, bias), f"decode-first fwd t={t} n={n} k={k}")
+    assert torch.equal(y, nf4_matmul(xt, packed, qs, bias=bt)), "decode-first fwd not deterministic"
+    dy = x_of(t, n, seed=t + 3 * k)
+    dyt = torch.from_numpy(dy).to(device)
+    dx = nf4_matmul(dyt, packed, qs, transpose=True)
+    check(dx, ogemm.linear_dx(dy, w), f"decode-first dx t={t} n={n} k={k}")
+    assert torch.equal(dx, nf4_matmul(dyt, packed, qs, transpose=True)), "decode-first dx not deterministic"
+    base = x_of(t, k, seed=t + 1, scale=0.1)
+    out = torch.from_numpy(base).to(device)
+    nf4_dx_2d(dyt, packed, qs, n, k, out=out, accumulate=True)
+    check(out, ogemm.linear_dx(dy, w) + base.astype(np.float64), f"decode-first dx accumulate t={t}")
+
+
 def test_dx_accumulate(device):
     state, w = weight(256, 1536)
     packed, qs = device_state(state, device)
