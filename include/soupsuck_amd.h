@@ -143,12 +143,17 @@ int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* pack
  * ss_lora_grad: C[16, n] = fp16(P[t,16]^T . Q'[t, n]) with Q' = Q or
  *   fp16(Q * q_scale); stored [16][n], or [n][16] when transpose.
  *   dA = dZ^T.X and dB = dL^T.Z.
- * workspace: fp32 partials, at least ss_lora_workspace_size(rows, cols) bytes
- * for an output with rows x 16 or 16 x cols elements.  It is used only when
- * the reduction is split over workgroups (few output blocks and a long
- * reduction: fewer than 32 row blocks with K > 4096, or fewer than 32 column
- * blocks with T > 4096); otherwise the op is one launch and the workspace
- * may be NULL. */
+ * Each op is one launch; the reduction is split over workgroups and the last
+ * workgroup of an output block to arrive adds the splits in split order
+ * (deterministic).
+ * workspace: at least ss_lora_workspace_size(rows, cols) bytes for an output
+ * with rows x 16 or 16 x cols elements.  Its first 256 KiB are arrival
+ * counters (a fixed area shared by both ops and all shapes) that must be
+ * zero when the op starts; the op leaves them zero, so a workspace
+ * zero-filled once serves any sequence of calls that do not overlap in time
+ * (calls on one stream); overlapping calls need separate workspaces.  With a
+ * NULL or smaller workspace the reduction is not split (slower, same
+ * contract otherwise). */
 size_t ss_lora_workspace_size(int64_t rows, int64_t cols);
 int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_t k, const uint16_t* w,
                     int64_t ldw, int w_kr, int scale_a, float a_scale, uint16_t* out,

@@ -4,23 +4,28 @@
 // autocast) and solution/lora_pair.py:52-65 (dZ = dL.B, dB = dL^T.Z,
 // dA = dZ^T.X).  With rank r = 16 these are "skinny" GEMMs: one operand is
 // [T, K] or [T, N] (read once from HBM), the other 16 x K.  They are
-// HBM-bound and, at training shapes (T ~ 1000), short: launch latency is a
-// large share of their time.  Each op is therefore one launch in which a
-// workgroup owns a block of outputs and its waves split the reduced
-// dimension, combining their fp32 sums through LDS in wave order
-// (deterministic).  When few output blocks meet a long reduction (large T
-// with a narrow N in rank_grad) the reduction is instead split over many
-// workgroups whose fp32 partials a second, tiny pass sums in chunk order.
+// HBM-bound and, at training shapes (T ~ 1000), short: launch latency and
+// memory round trips are most of their time.  Each op is one launch over
+// (output block, reduction split) workgroups sized so that each wave streams
+// about one chunk of the reduced dimension (one memory round trip); the
+// waves of a workgroup add their sums through LDS, and when the reduction is
+// split over several workgroups the last of them to arrive (a per-block
+// arrival counter) adds the splits' fp32 sums in split order -- the same sum
+// whichever arrives last -- and stores the fp16 result.  The exchange goes
+// through device-scope stores and loads (global_store/load sc1: coherent
+// across the XCDs' separate L2s, no L2-wide fence), which suits its size
+// (1 KiB or 4 KiB per workgroup).  The counters live at the start of the
+// caller's workspace: zero on entry, zero again on return.
 //
 // rank_project:  C[M, 16] = A[M, K] . W,  W(k, r) = w_kr ? w[k*ldw + r] : w[r*ldw + k],
 //                A optionally replaced by fp16(A * a_scale) (dL = fp16(g * s)).
-//                One wave per (16-row block, K chunk); MFMA operands come
-//                straight from global memory (16 B per lane for A).
+//                Workgroup per (16-row block, K split); A rows come straight
+//                from global memory into MFMA registers (16 B per lane), W is
+//                staged per wave in LDS.
 // rank_grad:     C[16, N] = P[T, 16]^T . Q[T, N] (Q optionally fp16(Q * q_scale)),
-//                stored [16][N] or transposed [N][16].  One wave per
-//                (64-column block, T chunk); Q tiles are loaded coalesced
+//                stored [16][N] or transposed [N][16].  Workgroup per
+//                (64-column block, T split); Q tiles are loaded coalesced
 //                (128 B per row) and transposed through LDS.
-// The final pass sums the partials in chunk order and rounds once to fp16.
 
 #include "common.h"
 
@@ -51,10 +56,11 @@ __device__ __forceinline__ half8 load_row8(const half_t* __restrict__ p, int64_t
 
 // Chunk sizes: every wave issues all loads of its chunk before its first MFMA
 // (eight 16-byte loads per lane in flight), so a chunk costs about one memory
-// round trip.  kMaxSplits bounds the fp32 partials.
+// round trip.  kMaxSplits bounds the splits of one output block (and the
+// fp32 exchange area).
 constexpr int kProjChunk = 256;  // k per rank_project wave: 8 MFMA steps of 32
 constexpr int kGradChunk = 64;   // t per rank_grad step: 2 MFMA steps of 32
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 16;
 constexpr int kProjLd = kProjChunk + 8;  // LDS row of the staged W chunk (one rank row)
 constexpr int kGradLd = kGradChunk + 8;  // LDS row of the transposed P tile
 
@@ -116,60 +122,80 @@ __device__ __forceinline__ void project_chunk(const half_t* __restrict__ a, int6
   __builtin_amdgcn_wave_barrier();
 }
 
-// Split form: one wave per (16-row block, K split); fp32 partials part[s][m][16].
-template <bool VEC>
-__global__ __launch_bounds__(256) void rank_project_kernel(
-    const half_t* __restrict__ a, int64_t lda, int64_t m, int64_t k, const half_t* __restrict__ w,
-    int64_t ldw, int w_kr, float a_scale, float* __restrict__ part, int64_t splits,
-    int64_t kchunk) {
-  __shared__ __attribute__((aligned(16))) half_t sw[4][kRank * kProjLd];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t mblocks = cdiv(m, 16);
-  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= mblocks * splits) return;  // no block-wide barrier below: waves are independent
-  const int64_t mb = item % mblocks;
-  const int64_t s = item / mblocks;
-  const int64_t send = (s + 1) * kchunk < k ? (s + 1) * kchunk : k;
-  const int r = lane & 15;
-  const int64_t row = mb * 16 + r;
-  float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
-  for (int64_t kbeg = s * kchunk; kbeg < send; kbeg += kProjChunk) {
-    const int64_t kend = kbeg + kProjChunk < send ? kbeg + kProjChunk : send;
-    project_chunk<VEC>(a, lda, m, w, ldw, w_kr, a_scale, row, lane, kbeg, kend, sw[wave], acc);
-  }
-  const float4v c = acc[0] + acc[1];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t mm = mb * 16 + (lane >> 4) * 4 + j;
-    if (mm < m) part[(s * m + mm) * kRank + r] = c[j];
-  }
+// Device-scope relaxed accesses for the cross-workgroup exchange of split
+// sums (see the header comment).
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One-launch form: workgroup = one 16-row block, blockDim.x / 64 waves; wave w
-// takes the 256-k chunks w, w + waves, ...; the waves' sums are added in wave
-// order through LDS and rounded once to fp16 (out row stride 16).
-constexpr int kRowWaves = 16;
+// Split exchange of wave 0 of a workgroup that holds `vals` fp32 sums per
+// lane for output block `blk`, split `s` of `splits`: returns true in the
+// workgroup that arrives last, whose `vals` then hold the sum over all
+// splits in split order.  part: [blocks][splits][vals x 64] fp32;
+// counters[blk] counts arrivals and is reset by the last arrival.
+template <int VALS>
+__device__ __forceinline__ bool finish_splits(float (&vals)[VALS], float* __restrict__ part,
+                                              int* __restrict__ counters, int64_t blk,
+                                              int64_t s, int64_t splits, int lane) {
+  float* base = part + blk * splits * (VALS * 64);
+#pragma unroll
+  for (int v = 0; v < VALS; ++v) store_dev(base + s * (VALS * 64) + v * 64 + lane, vals[v]);
+  // This wave's stores are complete before it counts itself.
+  __builtin_amdgcn_s_waitcnt(0);
+  int seen = 0;
+  if (lane == 0)
+    seen = __hip_atomic_fetch_add(counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  seen = __shfl(seen, 0, kWave);
+  if (seen != (int)splits - 1) return false;
+  float sum[VALS];
+#pragma unroll
+  for (int v = 0; v < VALS; ++v) sum[v] = 0.0f;
+  for (int64_t x = 0; x < splits; ++x) {
+#pragma unroll
+    for (int v = 0; v < VALS; ++v)
+      sum[v] += x == s ? vals[v] : load_dev(base + x * (VALS * 64) + v * 64 + lane);
+  }
+#pragma unroll
+  for (int v = 0; v < VALS; ++v) vals[v] = sum[v];
+  if (lane == 0)
+    __hip_atomic_store(counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// Workgroup = (16-row block blockIdx.x, K split blockIdx.y of gridDim.y),
+// blockDim.x / 64 waves.  Split s covers the 256-k chunks [s * cps, (s + 1) *
+// cps); wave w takes chunks w, w + waves, ... of it.  The waves' sums are
+// added in wave order through LDS, the splits' by finish_splits; out row
+// stride 16.
+constexpr int kRowWaves = 4;
 
 template <bool VEC>
-__global__ __launch_bounds__(kRowWaves * 64) void rank_project_rows_kernel(
+__global__ __launch_bounds__(kRowWaves * 64) void rank_project_kernel(
     const half_t* __restrict__ a, int64_t lda, int64_t m, int64_t k, const half_t* __restrict__ w,
-    int64_t ldw, int w_kr, float a_scale, half_t* __restrict__ out) {
+    int64_t ldw, int w_kr, float a_scale, int64_t cps, half_t* __restrict__ out,
+    float* __restrict__ part, int* __restrict__ counters) {
   __shared__ __attribute__((aligned(16))) half_t sw[kRowWaves][kRank * kProjLd];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
   const int64_t mb = blockIdx.x;
+  const int64_t s = blockIdx.y;
+  const int64_t splits = gridDim.y;
   const int r = lane & 15;
   const int64_t row = mb * 16 + r;
+  const int64_t kb = s * cps * kProjChunk;
+  const int64_t ke = kb + cps * kProjChunk < k ? kb + cps * kProjChunk : k;
   float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
-  for (int64_t kbeg = (int64_t)wave * kProjChunk; kbeg < k;
+  for (int64_t kbeg = kb + (int64_t)wave * kProjChunk; kbeg < ke;
        kbeg += (int64_t)waves * kProjChunk) {
-    const int64_t kend = kbeg + kProjChunk < k ? kbeg + kProjChunk : k;
+    const int64_t kend = kbeg + kProjChunk < ke ? kbeg + kProjChunk : ke;
     project_chunk<VEC>(a, lda, m, w, ldw, w_kr, a_scale, row, lane, kbeg, kend, sw[wave], acc);
   }
   // The per-wave tiles are dead once every wave has passed this barrier;
-  // their first 16 KiB hold the waves' 16x16 sums.
+  // their first 4 KiB hold the waves' 16x16 sums.
   __syncthreads();
   float4v* red = reinterpret_cast<float4v*>(&sw[0][0]);
   red[wave * 64 + lane] = acc[0] + acc[1];
@@ -177,10 +203,12 @@ __global__ __launch_bounds__(kRowWaves * 64) void rank_project_rows_kernel(
   if (wave != 0) return;
   float4v c = red[lane];
   for (int w2 = 1; w2 < waves; ++w2) c += red[w2 * 64 + lane];
+  float vals[4] = {c[0], c[1], c[2], c[3]};
+  if (splits > 1 && !finish_splits<4>(vals, part, counters, mb, s, splits, lane)) return;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t mm = mb * 16 + (lane >> 4) * 4 + j;
-    if (mm < m) out[mm * kRank + r] = f32_to_f16(c[j]);
+    if (mm < m) out[mm * kRank + r] = f32_to_f16(vals[j]);
   }
 }
 
@@ -232,152 +260,101 @@ __device__ __forceinline__ void grad_chunk(const half_t* __restrict__ p, int64_t
   __builtin_amdgcn_wave_barrier();
 }
 
-// Split form: one wave per (64-column block, T split); fp32 partials part[s][16][n].
-template <bool VEC>
-__global__ __launch_bounds__(256) void rank_grad_kernel(
-    const half_t* __restrict__ p, int64_t ldp, const half_t* __restrict__ q, int64_t ldq,
-    int64_t t, int64_t n, float q_scale, float* __restrict__ part, int64_t splits,
-    int64_t tchunk) {
-  __shared__ __attribute__((aligned(16))) half_t sq[4][64 * 64];
-  __shared__ __attribute__((aligned(16))) half_t sp[4][kRank * kGradLd];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t nblocks = cdiv(n, 64);
-  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= nblocks * splits) return;  // no block-wide barrier below: waves are independent
-  const int64_t nb = item % nblocks;
-  const int64_t s = item / nblocks;
-  const int64_t n0 = nb * 64;
-  const int64_t send = (s + 1) * tchunk < t ? (s + 1) * tchunk : t;
-  float4v acc[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) acc[c] = float4v{0.f, 0.f, 0.f, 0.f};
-  for (int64_t t0 = s * tchunk; t0 < send; t0 += kGradChunk) {
-    const int64_t tend = t0 + kGradChunk < send ? t0 + kGradChunk : send;
-    grad_chunk<VEC>(p, ldp, q, ldq, n, q_scale, n0, lane, t0, tend, sq[wave], sp[wave], acc);
-  }
-  // lane holds C[r' = 4*(lane/16) + j][n0 + 16c + lane%16]
-  const int r = lane & 15;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int64_t col = n0 + c * 16 + r;
-    if (col >= n) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int rr = (lane >> 4) * 4 + j;
-      part[(s * kRank + rr) * n + col] = acc[c][j];
-    }
-  }
-}
-
-// One-launch form: workgroup = one 64-column block, blockDim.x / 64 waves;
-// wave w takes the 64-t chunks w, w + waves, ...; the waves' sums are added in
-// wave order through LDS and rounded once to fp16, stored [16][n] or [n][16].
-constexpr int kColWaves = 8;
+// Workgroup = (64-column block blockIdx.x, T split blockIdx.y of gridDim.y),
+// blockDim.x / 64 waves.  Split s covers the 64-t chunks [s * cps, (s + 1) *
+// cps); wave w takes chunks w, w + waves, ... of it.  The waves' sums are
+// added in wave order through LDS, the splits' by finish_splits; the result
+// is stored [16][n] or transposed [n][16].
+constexpr int kColWaves = 4;
 
 template <bool VEC>
-__global__ __launch_bounds__(kColWaves * 64) void rank_grad_cols_kernel(
+__global__ __launch_bounds__(kColWaves * 64) void rank_grad_kernel(
     const half_t* __restrict__ p, int64_t ldp, const half_t* __restrict__ q, int64_t ldq,
-    int64_t t, int64_t n, float q_scale, int transpose, half_t* __restrict__ out) {
+    int64_t t, int64_t n, float q_scale, int64_t cps, int transpose, half_t* __restrict__ out,
+    float* __restrict__ part, int* __restrict__ counters) {
   __shared__ __attribute__((aligned(16))) half_t sq[kColWaves][64 * 64];
   __shared__ __attribute__((aligned(16))) half_t sp[kColWaves][kRank * kGradLd];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int waves = blockDim.x >> 6;
-  const int64_t n0 = (int64_t)blockIdx.x * 64;
+  const int64_t nb = blockIdx.x;
+  const int64_t s = blockIdx.y;
+  const int64_t splits = gridDim.y;
+  const int64_t n0 = nb * 64;
+  const int64_t tb = s * cps * kGradChunk;
+  const int64_t te = tb + cps * kGradChunk < t ? tb + cps * kGradChunk : t;
   float4v acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = float4v{0.f, 0.f, 0.f, 0.f};
-  for (int64_t t0 = (int64_t)wave * kGradChunk; t0 < t; t0 += (int64_t)waves * kGradChunk) {
-    const int64_t tend = t0 + kGradChunk < t ? t0 + kGradChunk : t;
+  for (int64_t t0 = tb + (int64_t)wave * kGradChunk; t0 < te; t0 += (int64_t)waves * kGradChunk) {
+    const int64_t tend = t0 + kGradChunk < te ? t0 + kGradChunk : te;
     grad_chunk<VEC>(p, ldp, q, ldq, n, q_scale, n0, lane, t0, tend, sq[wave], sp[wave], acc);
   }
   // The Q tiles are dead once every wave has passed this barrier; their first
-  // 32 KiB hold the waves' 16x64 sums.
+  // 16 KiB hold the waves' 16x64 sums.
   __syncthreads();
   float4v* red = reinterpret_cast<float4v*>(&sq[0][0]);
 #pragma unroll
   for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
   __syncthreads();
   if (wave != 0) return;
-  const int r = lane & 15;
+  float vals[16];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     float4v v = red[c * 64 + lane];
     for (int w2 = 1; w2 < waves; ++w2) v += red[(w2 * 4 + c) * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vals[c * 4 + j] = v[j];
+  }
+  if (splits > 1 && !finish_splits<16>(vals, part, counters, nb, s, splits, lane)) return;
+  // lane holds C[r' = 4*(lane/16) + j][n0 + 16c + lane%16] in vals[4c + j]
+  const int r = lane & 15;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
     const int64_t col = n0 + c * 16 + r;
     if (col >= n) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int rr = (lane >> 4) * 4 + j;
-      out[transpose ? col * kRank + rr : rr * n + col] = f32_to_f16(v[j]);
+      out[transpose ? col * kRank + rr : rr * n + col] = f32_to_f16(vals[c * 4 + j]);
     }
   }
 }
 
-// Sum of part[s * stride + i] over s in split order; eight loads in flight.
-__device__ __forceinline__ float sum_splits(const float* __restrict__ part, int64_t stride,
-                                            int64_t i, int64_t splits) {
-  float acc = 0.0f;
-  int64_t s = 0;
-  for (; s + 8 <= splits; s += 8) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = part[(s + j) * stride + i];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc += v[j];
-  }
-  for (; s < splits; ++s) acc += part[s * stride + i];
-  return acc;
+// Split plan: each wave of a split gets one chunk (cps = waves per
+// workgroup chunks per split) unless that needs more than kMaxSplits splits.
+struct RankPlan {
+  int64_t splits, cps;
+  int waves;
+};
+
+static RankPlan rank_plan(int64_t len, int64_t unit, int max_waves, bool can_split) {
+  const int64_t chunks = cdiv(len > 0 ? len : 1, unit);
+  RankPlan plan;
+  plan.splits = can_split ? cdiv(chunks, max_waves) : 1;
+  if (plan.splits > kMaxSplits) plan.splits = kMaxSplits;
+  plan.cps = cdiv(chunks, plan.splits);
+  plan.splits = cdiv(chunks, plan.cps);
+  plan.waves = (int)(plan.cps < max_waves ? plan.cps : max_waves);
+  return plan;
 }
 
-// out[m][r] (project) = fp16(sum_s part[s][m][r]); out row stride 16.
-__global__ __launch_bounds__(256) void rank_project_reduce_kernel(const float* __restrict__ part,
-                                                                  int64_t m, int64_t splits,
-                                                                  half_t* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= m * kRank) return;
-  out[i] = f32_to_f16(sum_splits(part, m * kRank, i, splits));
+// Workspace layout: a fixed area of kCounters arrival counters (one int per
+// output block; the same for every op and shape, so ops of different shapes
+// can share one workspace without one's exchange data landing on another's
+// counters), then the fp32 exchange area [blocks][splits][vals x 64].  Ops
+// with more output blocks than kCounters do not split.
+constexpr int64_t kCounters = 65536;
+constexpr size_t kCounterBytes = kCounters * sizeof(int);
+
+static size_t project_bytes(int64_t m) {
+  const int64_t blocks = cdiv(m > 0 ? m : 1, 16);
+  return kCounterBytes + (size_t)(blocks * kMaxSplits * 4 * 64) * sizeof(float);
 }
 
-// grad: out = fp16(sum_s part[s][r][c]) stored [16][n] (transpose = 0) or [n][16].
-// A workgroup reduces a 16-rank x 16-column block: thread (r, c) reads a
-// 64-byte run per rank row; the transposed store goes through LDS so that the
-// block writes one contiguous 512-byte run.
-__global__ __launch_bounds__(256) void rank_grad_reduce_kernel(const float* __restrict__ part,
-                                                               int64_t n, int64_t splits,
-                                                               int transpose,
-                                                               half_t* __restrict__ out) {
-  __shared__ half_t sh[kRank][kRank + 1];
-  const int rr = threadIdx.x >> 4;
-  const int cl = threadIdx.x & 15;
-  const int64_t c0 = (int64_t)blockIdx.x * kRank;
-  const int64_t c = c0 + cl;
-  const half_t v = c < n ? f32_to_f16(sum_splits(part + rr * n, kRank * n, c, splits))
-                         : (half_t)0.0f;
-  if (!transpose) {
-    if (c < n) out[rr * n + c] = v;
-    return;
-  }
-  sh[cl][rr] = v;
-  __syncthreads();
-  const int cw = threadIdx.x >> 4;  // column within the block
-  const int rw = threadIdx.x & 15;  // rank
-  if (c0 + cw < n) out[(c0 + cw) * kRank + rw] = sh[cw][rw];
-}
-
-// The one-launch forms are used while they give at least this many
-// workgroups, or when the reduction is short enough that a few workgroups
-// finish it in a couple of memory round trips (K <= 16 x 256 for project,
-// T <= 8 x 8 x 64 for grad); otherwise the split form spreads the reduction.
-constexpr int64_t kMinRowBlocks = 32;
-constexpr int64_t kMinColBlocks = 32;
-
-// Chunk length along the reduced dimension: a multiple of `unit`, long enough
-// that at most kMaxSplits chunks cover `len`.
-static int64_t pick_chunk(int64_t len, int64_t unit) {
-  const int64_t per = cdiv(len > 0 ? len : 1, kMaxSplits);
-  return cdiv(per, unit) * unit;
+static size_t grad_bytes(int64_t n) {
+  const int64_t blocks = cdiv(n > 0 ? n : 1, 64);
+  return kCounterBytes + (size_t)(blocks * kMaxSplits * 16 * 64) * sizeof(float);
 }
 
 static bool al16(const void* p, int64_t ld) {
@@ -389,10 +366,10 @@ static bool al16(const void* p, int64_t ld) {
 using namespace ss;
 
 extern "C" size_t ss_lora_workspace_size(int64_t rows, int64_t cols) {
-  // fp32 partials of either kernel for a [rows x 16] or [16 x cols] result:
-  // at most kMaxSplits chunks of the reduced dimension.
-  const int64_t m = rows > cols ? rows : cols;
-  return (size_t)(kMaxSplits * (m > 0 ? m : 1) * kRank) * sizeof(float) + 256;
+  // Counters and exchange area of either op: project for a [rows x 16]
+  // result, grad for a [16 x cols] result.
+  const size_t a = project_bytes(rows), b = grad_bytes(cols);
+  return a > b ? a : b;
 }
 
 extern "C" int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_t k,
@@ -405,37 +382,19 @@ extern "C" int ss_lora_project(const uint16_t* a, int64_t lda, int64_t m, int64_
   SS_CHECK_ARG(a && w && out, "%s: null pointer", fn);
   SS_CHECK_ARG(lda >= k && ldw >= (w_kr ? kRank : k), "%s: leading dimension too small", fn);
   const int64_t mblocks = cdiv(m, 16);
-  hipStream_t s = (hipStream_t)stream;
+  const bool can_split =
+      workspace && workspace_bytes >= project_bytes(m) && mblocks <= kCounters;
+  const RankPlan plan = rank_plan(k, kProjChunk, kRowWaves, can_split);
+  int* counters = reinterpret_cast<int*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   // Vector loads need 16-byte aligned rows of both operands and K % 8 == 0.
   const bool vec = al16(a, lda) && al16(w, ldw) && k % 8 == 0;
-  if (mblocks >= kMinRowBlocks || k <= kRowWaves * kProjChunk) {
-    // One launch: a workgroup per 16-row block, up to 16 waves over K.
-    const int64_t chunks = cdiv(k > 0 ? k : 1, kProjChunk);
-    const int waves = (int)(chunks < kRowWaves ? chunks : kRowWaves);
-    auto kern = vec ? rank_project_rows_kernel<true> : rank_project_rows_kernel<false>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)mblocks), dim3(64 * waves), 0, s,
-                       reinterpret_cast<const half_t*>(a), lda, m, k,
-                       reinterpret_cast<const half_t*>(w), ldw, w_kr, scale_a ? a_scale : 1.0f,
-                       reinterpret_cast<half_t*>(out));
-    SS_CHECK_LAUNCH("rank_project_rows_kernel");
-    return SS_OK;
-  }
-  SS_CHECK_ARG(workspace, "%s: null workspace", fn);
-  const int64_t kchunk = pick_chunk(k, kProjChunk);
-  const int64_t splits = cdiv(k > 0 ? k : 1, kchunk);
-  SS_CHECK_ARG((size_t)(splits * m * kRank) * sizeof(float) <= workspace_bytes,
-               "%s: workspace too small", fn);
-  float* part = reinterpret_cast<float*>(workspace);
-  const int64_t waves = mblocks * splits;
   auto kern = vec ? rank_project_kernel<true> : rank_project_kernel<false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
-                     reinterpret_cast<const half_t*>(a), lda, m, k,
+  hipLaunchKernelGGL(kern, dim3((unsigned)mblocks, (unsigned)plan.splits), dim3(64 * plan.waves),
+                     0, (hipStream_t)stream, reinterpret_cast<const half_t*>(a), lda, m, k,
                      reinterpret_cast<const half_t*>(w), ldw, w_kr, scale_a ? a_scale : 1.0f,
-                     part, splits, kchunk);
+                     plan.cps, reinterpret_cast<half_t*>(out), part, counters);
   SS_CHECK_LAUNCH("rank_project_kernel");
-  hipLaunchKernelGGL(rank_project_reduce_kernel, dim3((unsigned)cdiv(m * kRank, 256)), dim3(256),
-                     0, s, part, m, splits, reinterpret_cast<half_t*>(out));
-  SS_CHECK_LAUNCH("rank_project_reduce_kernel");
   return SS_OK;
 }
 
@@ -449,35 +408,17 @@ extern "C" int ss_lora_grad(const uint16_t* p, int64_t ldp, const uint16_t* q, i
   SS_CHECK_ARG(out && (t == 0 || (p && q)), "%s: null pointer", fn);
   SS_CHECK_ARG(t == 0 || (ldp >= kRank && ldq >= n), "%s: leading dimension too small", fn);
   const int64_t nblocks = cdiv(n, 64);
-  hipStream_t s = (hipStream_t)stream;
+  const bool can_split = workspace && workspace_bytes >= grad_bytes(n) && nblocks <= kCounters;
+  const RankPlan plan = rank_plan(t, kGradChunk, kColWaves, can_split);
+  int* counters = reinterpret_cast<int*>(workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
   // Vector loads need 16-byte aligned rows of P and Q and N % 8 == 0.
   const bool vec = al16(q, ldq) && al16(p, ldp) && n % 8 == 0;
-  if (nblocks >= kMinColBlocks || t <= kColWaves * kGradChunk * 8) {
-    // One launch: a workgroup per 64-column block, up to 8 waves over T.
-    const int64_t chunks = cdiv(t > 0 ? t : 1, kGradChunk);
-    const int waves = (int)(chunks < kColWaves ? chunks : kColWaves);
-    auto kern = vec ? rank_grad_cols_kernel<true> : rank_grad_cols_kernel<false>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(64 * waves), 0, s,
-                       reinterpret_cast<const half_t*>(p), ldp,
-                       reinterpret_cast<const half_t*>(q), ldq, t, n,
-                       scale_q ? q_scale : 1.0f, transpose, reinterpret_cast<half_t*>(out));
-    SS_CHECK_LAUNCH("rank_grad_cols_kernel");
-    return SS_OK;
-  }
-  SS_CHECK_ARG(workspace, "%s: null workspace", fn);
-  const int64_t tchunk = pick_chunk(t, kGradChunk);
-  const int64_t splits = t > 0 ? cdiv(t, tchunk) : 1;
-  SS_CHECK_ARG((size_t)(splits * n * kRank) * sizeof(float) <= workspace_bytes,
-               "%s: workspace too small", fn);
-  float* part = reinterpret_cast<float*>(workspace);
-  const int64_t waves = nblocks * splits;
   auto kern = vec ? rank_grad_kernel<true> : rank_grad_kernel<false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s,
-                     reinterpret_cast<const half_t*>(p), ldp, reinterpret_cast<const half_t*>(q),
-                     ldq, t, n, scale_q ? q_scale : 1.0f, part, splits, tchunk);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblocks, (unsigned)plan.splits), dim3(64 * plan.waves),
+                     0, (hipStream_t)stream, reinterpret_cast<const half_t*>(p), ldp,
+                     reinterpret_cast<const half_t*>(q), ldq, t, n, scale_q ? q_scale : 1.0f,
+                     plan.cps, transpose, reinterpret_cast<half_t*>(out), part, counters);
   SS_CHECK_LAUNCH("rank_grad_kernel");
-  hipLaunchKernelGGL(rank_grad_reduce_kernel, dim3((unsigned)cdiv(n, kRank)), dim3(256), 0,
-                     s, part, n, splits, transpose, reinterpret_cast<half_t*>(out));
-  SS_CHECK_LAUNCH("rank_grad_reduce_kernel");
   return SS_OK;
 }

@@ -45,15 +45,32 @@ def _gemm_ws(t, n, k, device):
     return (_workspace(size, device), size) if size else (None, 0)
 
 
+_RANK_WORKSPACE = {}
+
+
+def _rank_workspace(nbytes, device):
+    """Zero-filled workspace of the rank-16 ops, one per device, grown on demand.
+
+    Its leading arrival counters must be zero when an op starts and the op
+    leaves them zero, so one zero-filled buffer serves every call issued in
+    order on the device's stream (torch's current stream)."""
+    key = (device.type, device.index)
+    ws = _RANK_WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)
+        _RANK_WORKSPACE[key] = ws
+    return ws
+
+
 def project16(a2d, w, w_kr, scale=None):
     """fp16 [M, 16] = A' . W (ss_lora_project); W is lora_A [16, K] or lora_B [N, 16]."""
     m, k = a2d.shape
     out = torch.empty((m, 16), device=a2d.device, dtype=torch.float16)
     size = _lib.load().ss_lora_workspace_size(m, 0)
-    ws = _workspace(size, a2d.device)
+    ws = _rank_workspace(size, a2d.device)
     _lib.call("ss_lora_project", a2d.data_ptr(), a2d.stride(0), m, k, w.data_ptr(), w.stride(0),
               int(w_kr), int(scale is not None), float(scale or 1.0), out.data_ptr(),
-              ws.data_ptr(), size, _lib.stream(a2d.device))
+              ws.data_ptr(), ws.numel(), _lib.stream(a2d.device))
     return out
 
 
@@ -62,10 +79,10 @@ def grad16(p2d, q2d, transpose, scale=None):
     t, n = q2d.shape
     out = torch.empty((n, 16) if transpose else (16, n), device=q2d.device, dtype=torch.float16)
     size = _lib.load().ss_lora_workspace_size(0, n)
-    ws = _workspace(size, q2d.device)
+    ws = _rank_workspace(size, q2d.device)
     _lib.call("ss_lora_grad", p2d.data_ptr(), p2d.stride(0), q2d.data_ptr(), q2d.stride(0), t, n,
               int(scale is not None), float(scale or 1.0), int(transpose), out.data_ptr(),
-              ws.data_ptr(), size, _lib.stream(q2d.device))
+              ws.data_ptr(), ws.numel(), _lib.stream(q2d.device))
     return out
 
 

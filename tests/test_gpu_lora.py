@@ -125,6 +125,28 @@ def test_rank_grad_matches_numpy(device, t, n, transpose, scale):
                                atol=2e-3 * max(1.0, np.sqrt(t)))
 
 
+def test_rank_ops_deterministic_and_leave_counters_zero(device):
+    """Split reductions finished by the last workgroup to arrive: repeated calls
+    give the same bits, and the workspace's arrival counters are zero again
+    after every call (the contract that lets one zero-filled workspace serve
+    all calls on a stream)."""
+    from soupsuck_amd import lora
+
+    rng = np.random.default_rng(12)
+    a = torch.from_numpy(rng.standard_normal((990, 8960)).astype(np.float16)).to(device)
+    w = torch.from_numpy((rng.standard_normal((8960, 16)) * 0.1).astype(np.float16)).to(device)
+    z = torch.from_numpy((rng.standard_normal((990, 16)) * 0.3).astype(np.float16)).to(device)
+    first_p = lora.project16(a, w, True, 2.0)
+    first_g = lora.grad16(z, a, True, 2.0)
+    for _ in range(3):
+        assert torch.equal(lora.project16(a, w, True, 2.0), first_p)
+        assert torch.equal(lora.grad16(z, a, True, 2.0), first_g)
+    torch.cuda.synchronize()
+    ws = lora._RANK_WORKSPACE[(device.type, device.index if device.index is not None else 0)]
+    counters = ws[:256 * 1024].view(torch.int32)  # the fixed counter area
+    assert int(torch.count_nonzero(counters)) == 0
+
+
 def test_general_path_matches_fused_and_dropout_runs(device):
     from soupsuck_amd.lora import _QLoRAProjection
 
