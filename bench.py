@@ -97,7 +97,13 @@ def measured_traffic():
     return found
 
 
-TIMED_ENTRY_POINTS = ("ss_nf4_gemm_fwd", "ss_nf4_gemm_dx", "ss_qlora_fwd", "ss_qlora_dx")
+TIMED_ENTRY_POINTS = ("ss_nf4_gemm_fwd", "ss_nf4_gemm_dx", "ss_qlora_fwd", "ss_qlora_dx",
+                      "ss_qlora_forward", "ss_qlora_backward")
+
+# Rank-16 LoRA flops an entry point performs besides the base 2*T*N*K:
+# forward Z = X.A^T and Z.B^T; backward dZ, dB, dA and dZ.A.
+LORA_FLOPS = {"ss_qlora_forward": lambda t, n, k: 2 * t * 16 * (k + n),
+              "ss_qlora_backward": lambda t, n, k: 2 * t * 16 * (2 * n + 2 * k)}
 
 
 def sleep_cycles_per_ms(torch):
@@ -121,7 +127,8 @@ def lengths_config1():
 class KernelTimer:
     """HIP events around every NF4 GEMM entry point call, on its launch stream (torch's
     current stream), keyed by entry point and shape.  One call is one launch sequence
-    (e.g. decode-first: the NF4 decode kernel, then the MFMA GEMM kernel)."""
+    (e.g. the QLoRA backward: the preparation launch with dZ, dB and the transposed
+    decode, the MFMA GEMM, then dA)."""
 
     def __init__(self):
         import torch
@@ -149,7 +156,8 @@ class KernelTimer:
         _, a, start = self._pending
         self._pending = None
         t, n, k = a[2], a[8], a[9]
-        self.records.append((f"{name}[T={t},N={n},K={k}]", 2.0 * t * n * k, start, end))
+        flops = 2.0 * t * n * k + LORA_FLOPS.get(name, lambda *_: 0)(t, n, k)
+        self.records.append((f"{name}[T={t},N={n},K={k}]", flops, start, end))
 
     def summary(self):
         per = {}

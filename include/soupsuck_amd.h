@@ -133,6 +133,39 @@ int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* pack
                 const uint16_t* lora_a, uint16_t* dx, int64_t lddx, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* A10-A12 as one projection step (forward / backward of the rank-16 QLoRA
+ * projection out = fp16(X . Wdec^T + bias) + fp16(fp16(Z . lora_b^T) * scale),
+ * Z = fp16(X . lora_a^T); reference solution/lora.py:135-163 forward and
+ * solution/lora_pair.py:34-65 backward order).  The rank-16 jobs that do not
+ * depend on each other run in one launch with the NF4 decode of the
+ * decode-first path, ahead of the NF4 GEMM:
+ * ss_qlora_forward: z [t,16] (written, kept for the backward) and y [t,n] as
+ *   ss_lora_project (Z) followed by ss_qlora_fwd.
+ * ss_qlora_backward: dz [t,16] = fp16(fp16(dy*scale) . lora_b), db [n,16] =
+ *   fp16(fp16(dy*scale)^T . z), dx [t,k] = fp16(dy . Wdec + dz . lora_a),
+ *   da [16,k] = fp16(dz^T . x), as ss_lora_project, ss_lora_grad (twice) and
+ *   ss_qlora_dx.
+ * x, lora_a [16,k], lora_b [n,16], z, dz contiguous rows; workspace as for
+ * ss_qlora_fwd / ss_qlora_dx (ss_nf4_gemm_workspace_size); rank_workspace:
+ * ss_qlora_rank_workspace_size(t, n, k) bytes with the contract of the
+ * rank-16 products' workspace below (zero-filled once, left zero).  No
+ * counterpart in the reference: it is the fused form of the entry points it
+ * composes. */
+size_t ss_qlora_rank_workspace_size(int64_t t, int64_t n, int64_t k);
+int ss_qlora_forward(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                     const uint8_t* qabs, const float* absmax2, const float* code2,
+                     const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                     const uint16_t* lora_a, const uint16_t* lora_b, float scale, uint16_t* z,
+                     uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                     void* rank_workspace, size_t rank_workspace_bytes, void* stream);
+int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                      const uint8_t* qabs, const float* absmax2, const float* code2,
+                      const float* offset, int64_t n, int64_t k, const uint16_t* x, int64_t ldx,
+                      const uint16_t* z, const uint16_t* lora_a, const uint16_t* lora_b,
+                      float scale, uint16_t* dx, int64_t lddx, uint16_t* dz, uint16_t* da,
+                      uint16_t* db, void* workspace, size_t workspace_bytes,
+                      void* rank_workspace, size_t rank_workspace_bytes, void* stream);
+
 /* ------------------------------------------------ rank-16 LoRA products ---
  * HBM-bound skinny GEMMs of the LoRA branch (reference solution/lora.py:161,
  * solution/lora_pair.py:52-65), fp32 accumulation, one fp16 rounding.

@@ -47,6 +47,13 @@ SIGNATURES = {
     "ss_qlora_dx": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _c_void_p,
                                                                _c_void_p, _i64, _c_void_p, _size,
                                                                _c_void_p],
+    "ss_qlora_forward": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64] + [_c_void_p] * 3
+                        + [_f32, _c_void_p, _c_void_p, _i64, _c_void_p, _size, _c_void_p, _size,
+                           _c_void_p],
+    "ss_qlora_backward": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _i64]
+                         + [_c_void_p] * 3 + [_f32, _c_void_p, _i64] + [_c_void_p] * 3
+                         + [_c_void_p, _size, _c_void_p, _size, _c_void_p],
+    "ss_qlora_rank_workspace_size": [_i64, _i64, _i64],
     "ss_lora_workspace_size": [_i64, _i64],
     "ss_lora_project": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _int, _int, _f32,
                         _c_void_p, _c_void_p, _size, _c_void_p],
@@ -78,7 +85,7 @@ SIGNATURES = {
                           _c_void_p],
 }
 _RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size,
-             "ss_lora_workspace_size": _size}
+             "ss_lora_workspace_size": _size, "ss_qlora_rank_workspace_size": _size}
 
 _lock = threading.Lock()
 _lib = None

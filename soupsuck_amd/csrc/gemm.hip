@@ -26,6 +26,7 @@
 #include <stdlib.h>
 
 #include "gemm.h"
+#include "rank16.h"
 
 namespace ss {
 
@@ -602,9 +603,27 @@ static bool stream_enabled() {
   return on;
 }
 
+// Decode-first path with the decode fused into the preparation launch of the
+// QLoRA step (rank-16 jobs + decode in one launch): T above the skinny range,
+// aligned decode destination.
+static bool fuse_decode(const GemmParams& p, int64_t n, int64_t k, void* workspace,
+                        size_t workspace_bytes) {
+  return p.M > kSkinnyMaxT && workspace && workspace_bytes >= (size_t)n * (size_t)k * 2 &&
+         reinterpret_cast<uintptr_t>(workspace) % 16 == 0 && k % 64 == 0;
+}
+
+// prep (may be null): rank-16 jobs that must complete before the GEMM; they
+// run in one launch ahead of it, together with the decode when the
+// decode-first path is taken.
 template <int EPI>
-static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s) {
+static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipStream_t s,
+                   PrepJobs* prep = nullptr, bool vp = false, bool vg = false) {
   const int64_t n = p.N, k = p.K;
+  const bool fused = prep && fuse_decode(p, n, k, workspace, workspace_bytes);
+  if (prep && !fused) {
+    const int r = launch_prep(*prep, vp, vg, s);
+    if (r) return r;
+  }
   if (p.M <= kStreamMaxT && workspace && stream_enabled()) {
     const int rc = nf4_stream_fwd(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;
@@ -615,8 +634,18 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
   }
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
     const Nf4View& w = p.w;
-    int r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
-                                  reinterpret_cast<uint16_t*>(workspace), n * k, s);
+    int r;
+    if (fused) {
+      prep->dec_kind = kDecodeRows;
+      prep->dec_w = w;
+      prep->dec_out = reinterpret_cast<half_t*>(workspace);
+      prep->dec_rows = n;
+      prep->dec_cols = k;
+      r = launch_prep(*prep, vp, vg, s);
+    } else {
+      r = ss_nf4_dequant_nested(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                reinterpret_cast<uint16_t*>(workspace), n * k, s);
+    }
     if (r) return r;
     p.B = reinterpret_cast<const half_t*>(workspace);
     p.ldb = k;
@@ -631,7 +660,13 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
 
 template <int EPI>
 static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
-                  hipStream_t s) {
+                  hipStream_t s, PrepJobs* prep = nullptr, bool vp = false, bool vg = false) {
+  const bool fused = prep && fuse_decode(p, n, k, workspace, workspace_bytes) &&
+                     reinterpret_cast<uintptr_t>(p.w.packed) % 8 == 0;
+  if (prep && !fused) {
+    const int r = launch_prep(*prep, vp, vg, s);
+    if (r) return r;
+  }
   if (p.M <= kStreamDxMaxT && workspace && stream_enabled()) {
     const int rc = nf4_stream_dx(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;
@@ -639,8 +674,18 @@ static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t w
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
     // Decode W^T [k, n] once; dX = dY . W is then the K-contiguous NT product.
     const Nf4View& w = p.w;
-    int r = ss_nf4_dequant_nested_t(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
-                                    reinterpret_cast<uint16_t*>(workspace), n, k, s);
+    int r;
+    if (fused) {
+      prep->dec_kind = kDecodeTransposed;
+      prep->dec_w = w;
+      prep->dec_out = reinterpret_cast<half_t*>(workspace);
+      prep->dec_rows = n;
+      prep->dec_cols = k;
+      r = launch_prep(*prep, vp, vg, s);
+    } else {
+      r = ss_nf4_dequant_nested_t(w.packed, w.qabs, w.absmax2, w.code2, w.offset,
+                                  reinterpret_cast<uint16_t*>(workspace), n, k, s);
+    }
     if (r) return r;
     p.B = reinterpret_cast<const half_t*>(workspace);
     p.ldb = n;
@@ -755,6 +800,90 @@ extern "C" int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const ui
   p.lb = reinterpret_cast<const half_t*>(lora_a);
   p.ldlb = k;
   return run_dx<EPI_RANK>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" size_t ss_qlora_rank_workspace_size(int64_t t, int64_t n, int64_t k) {
+  const size_t fwd = ss_lora_workspace_size(t, 0);
+  const size_t bwd = ss_lora_workspace_size(t, n);
+  const size_t da = ss_lora_workspace_size(0, k);
+  size_t m = fwd > bwd ? fwd : bwd;
+  return m > da ? m : da;
+}
+
+extern "C" int ss_qlora_forward(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                                const uint8_t* qabs, const float* absmax2, const float* code2,
+                                const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                                const uint16_t* lora_a, const uint16_t* lora_b, float scale,
+                                uint16_t* z, uint16_t* y, int64_t ldy, void* workspace,
+                                size_t workspace_bytes, void* rank_workspace,
+                                size_t rank_workspace_bytes, void* stream) {
+  const char* fn = "ss_qlora_forward";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(x && y && z && lora_a && lora_b, "%s: null pointer", fn);
+  SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
+  SS_CHECK_ARG(reinterpret_cast<uintptr_t>(z) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(lora_b) % 16 == 0,
+               "%s: Z and lora_B must be 16-byte aligned", fn);
+  GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, y, ldy);
+  p.lz = reinterpret_cast<const half_t*>(z);
+  p.lb = reinterpret_cast<const half_t*>(lora_b);
+  p.ldlb = 16;
+  p.lscale = scale;
+  PrepJobs pj{};
+  bool vp = false, vg = false;
+  // Z = fp16(X . A^T): the rank-16 job the LoRA epilogue reads.
+  pj.proj_blocks = rank_project_setup(pj.proj, x, ldx, t, k, lora_a, k, 0, 1.0f, z,
+                                      rank_workspace, rank_workspace_bytes, t, vp);
+  pj.grad_blocks = 0;
+  pj.dec_kind = kDecodeNone;
+  return run_fwd<EPI_LORA>(p, workspace, workspace_bytes, (hipStream_t)stream, &pj, vp, vg);
+}
+
+extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
+                                 const uint8_t* packed, const uint8_t* qabs,
+                                 const float* absmax2, const float* code2, const float* offset,
+                                 int64_t n, int64_t k, const uint16_t* x, int64_t ldx,
+                                 const uint16_t* z, const uint16_t* lora_a,
+                                 const uint16_t* lora_b, float scale, uint16_t* dx, int64_t lddx,
+                                 uint16_t* dz, uint16_t* da, uint16_t* db, void* workspace,
+                                 size_t workspace_bytes, void* rank_workspace,
+                                 size_t rank_workspace_bytes, void* stream) {
+  const char* fn = "ss_qlora_backward";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  SS_CHECK_ARG(da && db && lora_a && lora_b, "%s: null pointer", fn);
+  if (t == 0) {
+    // No rows: the adapter gradients are zero and dX is empty.
+    rc = ss_lora_grad(nullptr, 16, nullptr, n, 0, k, 0, 1.0f, 0, da, nullptr, 0, stream);
+    if (rc) return rc;
+    return ss_lora_grad(nullptr, 16, nullptr, n, 0, n, 0, 1.0f, 1, db, nullptr, 0, stream);
+  }
+  SS_CHECK_ARG(dy && dx && dz && x && z, "%s: null pointer", fn);
+  SS_CHECK_ARG(lddy >= n && lddx >= k && ldx >= k, "%s: leading dimensions too small", fn);
+  SS_CHECK_ARG(reinterpret_cast<uintptr_t>(dz) % 16 == 0, "%s: dZ must be 16-byte aligned", fn);
+  hipStream_t s = (hipStream_t)stream;
+  PrepJobs pj{};
+  bool vp = false, vg = false;
+  // dZ = fp16(fp16(g * s) . B) and dB = fp16(fp16(g * s)^T . Z): both read g
+  // once, neither depends on the other; the dX epilogue reads dZ.
+  pj.proj_blocks = rank_project_setup(pj.proj, dy, lddy, t, n, lora_b, 16, 1, scale, dz,
+                                      rank_workspace, rank_workspace_bytes, t, vp);
+  pj.grad_blocks = rank_grad_setup(pj.grad, z, 16, dy, lddy, t, n, scale, 1, db, rank_workspace,
+                                   rank_workspace_bytes, t, vg);
+  pj.dec_kind = kDecodeNone;
+  GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx, 0);
+  p.lz = reinterpret_cast<const half_t*>(dz);
+  p.lb = reinterpret_cast<const half_t*>(lora_a);
+  p.ldlb = k;
+  rc = run_dx<EPI_RANK>(p, n, k, workspace, workspace_bytes, s, &pj, vp, vg);
+  if (rc) return rc;
+  // dA = fp16(dZ^T . X), after dZ.
+  return ss_lora_grad(dz, 16, x, ldx, t, k, 0, 1.0f, 0, da, rank_workspace, rank_workspace_bytes,
+                      stream);
 }
 
 extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,

@@ -11,22 +11,9 @@
 // 64-block (8 divides 64), so each step needs a single scale.
 // Generic path: one element per lane, any alignment / tail.
 
-#include "common.h"
+#include "decode_blocks.h"
 
 namespace ss {
-
-template <bool NESTED>
-__device__ __forceinline__ float block_scale(const uint8_t* __restrict__ qabs,
-                                             const float* __restrict__ absmax,
-                                             const float* __restrict__ absmax2,
-                                             const float* __restrict__ code2, float offset,
-                                             int64_t block) {
-  if constexpr (NESTED) {
-    return nested_scale(qabs, absmax2, code2, offset, block);
-  } else {
-    return absmax[block];
-  }
-}
 
 template <bool NESTED>
 __global__ __launch_bounds__(256) void nf4_dequant_vec_kernel(
@@ -34,23 +21,9 @@ __global__ __launch_bounds__(256) void nf4_dequant_vec_kernel(
     const float* __restrict__ absmax, const float* __restrict__ absmax2,
     const float* __restrict__ code2, const float* __restrict__ offset_ptr,
     half8* __restrict__ out, int64_t groups) {
-  __shared__ float lut[16];
-  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
-  __syncthreads();
-  const float offset = NESTED ? offset_ptr[0] : 0.0f;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < groups; g += stride) {
-    const uint32_t word = __builtin_nontemporal_load(packed + g);
-    const float scale = block_scale<NESTED>(qabs, absmax, absmax2, code2, offset, g >> 3);
-    half8 v;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (word >> (8 * b)) & 0xffu;
-      v[2 * b] = f32_to_f16(lut[byte >> 4] * scale);
-      v[2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
-    }
-    out[g] = v;
-  }
+  __shared__ __attribute__((aligned(16))) unsigned char smem[64];
+  decode_vec_block<NESTED>(packed, qabs, absmax, absmax2, code2, offset_ptr, out, groups,
+                           blockIdx.x, gridDim.x, smem);
 }
 
 template <bool NESTED>
@@ -80,57 +53,8 @@ __global__ __launch_bounds__(256) void nf4_dequant_t_kernel(
     const uint8_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ absmax2, const float* __restrict__ code2,
     const float* __restrict__ offset_ptr, half_t* __restrict__ out, int64_t rows, int64_t cols) {
-  constexpr int LD = 64 + 8;
-  __shared__ __attribute__((aligned(16))) half_t tile[64 * LD];  // [k][n]
-  __shared__ float lut[16];
-  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
-  __syncthreads();
-  const float offset = offset_ptr[0];
-  const int64_t ntiles = cdiv(rows, 64);
-  const int64_t n0 = (blockIdx.x % ntiles) * 64;
-  const int64_t k0 = (blockIdx.x / ntiles) * 64;
-  const int nl = threadIdx.x & 63;
-  const int part = threadIdx.x >> 6;
-  const int64_t n = n0 + nl;
-  half_t vals[16];
-  if (n < rows) {
-    const int64_t e = n * cols + k0 + part * 16;
-    const uint2 w = *reinterpret_cast<const uint2*>(packed + (e >> 1));
-    const float scale = nested_scale(qabs, absmax2, code2, offset, e >> 6);
-    const uint32_t words[2] = {w.x, w.y};
-#pragma unroll
-    for (int wi = 0; wi < 2; ++wi)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
-        vals[8 * wi + 2 * b] = f32_to_f16(lut[byte >> 4] * scale);
-        vals[8 * wi + 2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
-      }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) vals[j] = (half_t)0.0f;
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) tile[(part * 16 + j) * LD + nl] = vals[j];
-  __syncthreads();
-  // 64 k-rows x 8 chunks of 8 n; two chunks per thread.
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int chunk = threadIdx.x + 256 * c;
-    const int kr = chunk >> 3;
-    const int nc = (chunk & 7) * 8;
-    const int64_t k = k0 + kr;
-    const int64_t nn = n0 + nc;
-    const half8 v = *reinterpret_cast<const half8*>(tile + kr * LD + nc);
-    half_t* dst = out + k * rows + nn;
-    if (nn + 8 <= rows && rows % 8 == 0) {
-      *reinterpret_cast<half8*>(dst) = v;
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (nn + j < rows) dst[j] = v[j];
-    }
-  }
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kDecodeSmem];
+  decode_t_block(packed, qabs, absmax2, code2, offset_ptr, out, rows, cols, blockIdx.x, smem);
 }
 
 static int grid_for(int64_t work, int threads) {

@@ -14,10 +14,11 @@ The frozen base contributes no weight gradient.  Dropout (p > 0) uses torch's
 native dropout on an fp32 copy of X, as the reference keeps PEFT's own
 Dropout module and RNG (solution/lora.py:1-40); p = 0 skips it.
 
-Fast path (rank 16, no active dropout, K % 64 == 0): six launches per
-projection -- forward ss_lora_project (Z) + ss_qlora_fwd (NF4 GEMM with the
-LoRA add in its epilogue); backward ss_lora_project (dZ from fp16(g*s)),
-ss_lora_grad twice (dB, dA) and ss_qlora_dx (g.W + dZ.A in one accumulator).
+Fast path (rank 16, no active dropout, K % 64 == 0): two entry points per
+projection -- forward ss_qlora_forward (Z, then the NF4 GEMM with the LoRA
+add in its epilogue; Z runs in one launch with the NF4 decode); backward
+ss_qlora_backward (dZ from fp16(g*s) and dB in one launch with the
+transposed decode, the dX GEMM g.W + dZ.A in one accumulator, then dA).
 Otherwise each GEMM and the epilogue run as separate kernels.
 """
 
@@ -86,8 +87,14 @@ def grad16(p2d, q2d, transpose, scale=None):
     return out
 
 
+def _qlora_rank_ws(t, n, k, device):
+    return _rank_workspace(_lib.load().ss_qlora_rank_workspace_size(t, n, k), device)
+
+
 class _QLoRAFused(torch.autograd.Function):
-    """Rank-16, dropout-free projection on the fused kernels (six launches)."""
+    """Rank-16, dropout-free projection on the fused entry points: forward
+    ss_qlora_forward (Z and the NF4 GEMM with the LoRA epilogue), backward
+    ss_qlora_backward (dZ, dB, dX with the rank-16 update, dA)."""
 
     @staticmethod
     def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling):
@@ -96,12 +103,14 @@ class _QLoRAFused(torch.autograd.Function):
         x2d = x.reshape(t, k)
         a16 = lora_a.to(torch.float16).contiguous()
         b16 = lora_b.to(torch.float16).contiguous()
-        z = project16(x2d, a16, w_kr=False)
+        z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
         y = torch.empty((t, n), device=x.device, dtype=torch.float16)
         ws, size = _gemm_ws(t, n, k, x.device)
-        _lib.call("ss_qlora_fwd", x2d.data_ptr(), x2d.stride(0), t, *_nf4_args(packed, state), n, k,
-                  _lib.ptr(bias), z.data_ptr(), b16.data_ptr(), float(scaling), y.data_ptr(),
-                  y.stride(0), _lib.ptr(ws), size, _lib.stream(x.device))
+        rws = _qlora_rank_ws(t, n, k, x.device)
+        _lib.call("ss_qlora_forward", x2d.data_ptr(), x2d.stride(0), t, *_nf4_args(packed, state),
+                  n, k, _lib.ptr(bias), a16.data_ptr(), b16.data_ptr(), float(scaling),
+                  z.data_ptr(), y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(),
+                  rws.numel(), _lib.stream(x.device))
         ctx.save_for_backward(x2d, z, a16, b16, packed)
         ctx.state, ctx.scaling = state, float(scaling)
         ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
@@ -115,14 +124,18 @@ class _QLoRAFused(torch.autograd.Function):
         n, k = state.shape
         t = x2d.shape[0]
         g = grad.reshape(t, n).to(torch.float16).contiguous()
-        dz = project16(g, b16, w_kr=True, scale=ctx.scaling)        # fp16(fp16(g*s) . B)
-        db = grad16(z, g, transpose=True, scale=ctx.scaling)         # fp16(fp16(g*s)^T . Z)
-        da = grad16(dz, x2d, transpose=False)                        # fp16(dZ^T . X)
-        dx = torch.empty((t, k), device=g.device, dtype=torch.float16)
-        ws, size = _gemm_ws(t, n, k, g.device)
-        _lib.call("ss_qlora_dx", g.data_ptr(), g.stride(0), t, *_nf4_args(packed, state), n, k,
-                  dz.data_ptr(), a16.data_ptr(), dx.data_ptr(), dx.stride(0), _lib.ptr(ws), size,
-                  _lib.stream(g.device))
+        dev = g.device
+        dz = torch.empty((t, 16), device=dev, dtype=torch.float16)   # fp16(fp16(g*s) . B)
+        db = torch.empty((n, 16), device=dev, dtype=torch.float16)   # fp16(fp16(g*s)^T . Z)
+        da = torch.empty((16, k), device=dev, dtype=torch.float16)   # fp16(dZ^T . X)
+        dx = torch.empty((t, k), device=dev, dtype=torch.float16)
+        ws, size = _gemm_ws(t, n, k, dev)
+        rws = _qlora_rank_ws(t, n, k, dev)
+        _lib.call("ss_qlora_backward", g.data_ptr(), g.stride(0), t, *_nf4_args(packed, state), n,
+                  k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(), a16.data_ptr(), b16.data_ptr(),
+                  ctx.scaling, dx.data_ptr(), dx.stride(0), dz.data_ptr(), da.data_ptr(),
+                  db.data_ptr(), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
+                  _lib.stream(dev))
         x_dtype, a_dtype, b_dtype = ctx.dtypes
         return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
                 None, None, None, None)
