@@ -64,6 +64,11 @@ def parse():
     p.add_argument("--no-other-configs", action="store_true",
                    help="skip configs[0], configs[2] and configs[3] (dequant, GEMM T=1024, "
                         "add-RMSNorm, unpad, fused CE)")
+    p.add_argument("--profile-call", default="", metavar="DIR:N:K",
+                   help="only run one configs[1] projection entry point (DIR forward or "
+                        "backward, weight [N,K]) --reps times at the bench's T and exit (for "
+                        "rocprofv3 counter passes that attribute every kernel to one call)")
+    p.add_argument("--reps", type=int, default=20)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
                         "FETCH_SIZE / WRITE_SIZE to bytes) and exit")
@@ -83,6 +88,37 @@ def copy_calibration(mib):
     torch.cuda.synchronize()
     assert torch.equal(dst, src)
     print(json.dumps({"copy_calibration_bytes_per_dispatch": n, "dispatches": 10}), flush=True)
+
+
+def profile_call(spec, reps):
+    """Repeat one ss_qlora_forward / ss_qlora_backward call of the configs[1] layer."""
+    import torch
+
+    from soupsuck_amd import _lib
+    from soupsuck_amd.layer import QLoRALayer
+
+    direction, n, k = spec.split(":")
+    n, k = int(n), int(k)
+    device = torch.device("cuda:0")
+    layer = QLoRALayer(device)
+    tokens = sum(lengths_config1())
+    xs, gs = layer.inputs(tokens, device)
+    idx = next(i for i, p in enumerate(layer.projections) if (p.n, p.k) == (n, k))
+    proj, x, g = layer.projections[idx], xs[idx], gs[idx]
+    from soupsuck_amd.lora import qlora_projection
+
+    x.requires_grad_(direction == "backward")
+    out = qlora_projection(x, proj.lora_a, proj.lora_b, proj.packed, proj.state, proj.bias,
+                           layer.scaling)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        if direction == "backward":
+            out.backward(g, retain_graph=True)
+        else:
+            qlora_projection(x, proj.lora_a, proj.lora_b, proj.packed, proj.state, proj.bias,
+                             layer.scaling)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_call": spec, "tokens": tokens, "reps": reps}), flush=True)
 
 
 def measured_traffic():
@@ -499,6 +535,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.profile_call:
+        profile_call(args.profile_call, args.reps)
         return
 
     import torch
