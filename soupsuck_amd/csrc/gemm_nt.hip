@@ -388,10 +388,41 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
       for (int e = 0; e < 4; ++e)
         if (c0 + e < p.N) v[e] += p.part[s * plane + row * p.N + c0 + e];
   }
+  // Rank-16 operands with 16-byte (Z, lora_B rows) and 8-byte (four lora_A
+  // columns) loads where aligned; the products are summed in rank order as in
+  // the GEMM epilogue.
   float z[16];
   if constexpr (EPI != EPI_PLAIN) {
+    const half_t* zr = p.lz + row * 16;
+    if (reinterpret_cast<uintptr_t>(p.lz) % 16 == 0) {
+      const half8 z0 = *reinterpret_cast<const half8*>(zr);
+      const half8 z1 = *reinterpret_cast<const half8*>(zr + 8);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) z[r] = (float)p.lz[row * 16 + r];
+      for (int r = 0; r < 8; ++r) {
+        z[r] = (float)z0[r];
+        z[8 + r] = (float)z1[r];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) z[r] = (float)zr[r];
+    }
+  }
+  float a4[16][4];  // EPI_RANK: lora_A[r][c0 .. c0 + 3]
+  if constexpr (EPI == EPI_RANK) {
+    if (c0 + 4 <= p.N && p.ldlb % 4 == 0 && reinterpret_cast<uintptr_t>(p.lb) % 8 == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const half4 v4 = *reinterpret_cast<const half4*>(p.lb + r * p.ldlb + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a4[r][e] = (float)v4[e];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          a4[r][e] = c0 + e < p.N ? (float)p.lb[r * p.ldlb + c0 + e] : 0.0f;
+    }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -399,9 +430,23 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
     if (col >= p.N) break;
     const int64_t idx = row * p.ldc + col;
     if constexpr (EPI == EPI_LORA) {
+      float bl[16];
+      const half_t* br = p.lb + col * 16;
+      if (reinterpret_cast<uintptr_t>(p.lb) % 16 == 0) {
+        const half8 b0 = *reinterpret_cast<const half8*>(br);
+        const half8 b1 = *reinterpret_cast<const half8*>(br + 8);
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          bl[r] = (float)b0[r];
+          bl[8 + r] = (float)b1[r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bl[r] = (float)br[r];
+      }
       float l = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) l += z[r] * (float)p.lb[col * 16 + r];
+      for (int r = 0; r < 16; ++r) l += z[r] * bl[r];
       const float b = p.bias ? (float)p.bias[col] : 0.0f;
       const float y = (float)f32_to_f16(v[e] * p.alpha + b);
       const float scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
@@ -409,7 +454,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
     } else if constexpr (EPI == EPI_RANK) {
       float l = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) l += z[r] * (float)p.lb[r * p.ldlb + col];
+      for (int r = 0; r < 16; ++r) l += z[r] * a4[r][e];
       store_c<CT>(p.C, idx, v[e] + l, p.beta);
     } else {
       const float b = p.bias ? (float)p.bias[col] : 0.0f;

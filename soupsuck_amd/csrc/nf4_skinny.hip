@@ -160,22 +160,29 @@ __global__ __launch_bounds__(256, 2) void nf4_skinny_fwd_kernel(
         }
       }
     }
+    // k-step j outermost: the MT x NB MFMAs of one k-step update distinct
+    // accumulators, so each MFMA's dependency on the previous update of its
+    // accumulator is MT x NB instructions back (m-tile outermost left only
+    // NB = 2 independent chains and stalled on every other MFMA).  The X
+    // fragments of a k-step are read before its MFMAs.
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int j = 0; j < 4; ++j) {
+      half8 af[MT];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        half8 af;
+      for (int mt = 0; mt < MT; ++mt) {
         if constexpr (XLDS) {
-          af = *reinterpret_cast<const half8*>(
+          af[mt] = *reinterpret_cast<const half8*>(
               &sx[it & 1][(mt * 16 + r16) * kSkPitch + 32 * g + 8 * j]);
         } else {
-          af = __builtin_bit_cast(half8, sl.x[mt * 4 + j]);
+          af[mt] = __builtin_bit_cast(half8, sl.x[mt * 4 + j]);
         }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nb = 0; nb < kSkNB; ++nb)
           acc[mt][nb] =
-              __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bfrag[nb][j], acc[mt][nb], 0, 0, 0);
-      }
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], bfrag[nb][j], acc[mt][nb], 0, 0, 0);
     }
     // Refill with iteration it + PF, clamped to a valid iteration so that the
     // loads are always issued (the load counts stay the same every
@@ -259,7 +266,7 @@ int nf4_skinny_fwd(const GemmParams& p, int epi, void* partials, size_t partial_
                          p.lda, p.M, p.w, p.N, p.K, plan.k_split, part);
       break;
     default:
-      hipLaunchKernelGGL((nf4_skinny_fwd_kernel<8, true, 3>), grid, dim3(256), 0, stream, p.A,
+      hipLaunchKernelGGL((nf4_skinny_fwd_kernel<8, true, 2>), grid, dim3(256), 0, stream, p.A,
                          p.lda, p.M, p.w, p.N, p.K, plan.k_split, part);
       break;
   }
