@@ -464,7 +464,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
 }
 
 // Tile configurations: <BM, BN, waves M, waves N, BK, stages, min waves/SIMD>.
-using NtSmall = NtCfg<64, 64, 2, 2, 32, 3, 2>;      // 4 waves of 32x32, 24 KiB LDS
+using NtSmall = NtCfg<64, 64, 2, 2, 32, 4, 2>;      // 4 waves of 32x32, 32 KiB LDS
 using NtMid = NtCfg<128, 128, 2, 2, 32, 3, 2>;      // 4 waves of 64x64, 48 KiB LDS
 using NtBig4 = NtCfg<256, 256, 2, 2, 32, 3, 1>;     // 4 waves of 128x128, 96 KiB LDS
 using NtBig8 = NtCfg<256, 256, 2, 4, 64, 2, 2>;     // 8 waves of 128x64, 128 KiB LDS
@@ -472,9 +472,6 @@ using NtWide8 = NtCfg<256, 128, 4, 2, 64, 2, 2>;    // 8 waves of 64x64, 96 KiB 
 using NtBig8s = NtCfg<256, 256, 2, 4, 32, 3, 2>;    // 8 waves of 128x64, 96 KiB LDS
 using NtMid64 = NtCfg<128, 128, 2, 2, 64, 2, 2>;    // 4 waves of 64x64, 64 KiB LDS
 using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 KiB LDS
-using NtBig8s5 = NtCfg<256, 256, 2, 4, 32, 5, 2>;   // 8 waves of 128x64, 160 KiB LDS
-using NtBig4s4 = NtCfg<256, 256, 2, 2, 32, 4, 1>;   // 4 waves of 128x128, 128 KiB LDS
-using NtBig4s5 = NtCfg<256, 256, 2, 2, 32, 5, 1>;   // 4 waves of 128x128, 160 KiB LDS
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
@@ -490,7 +487,7 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
 //   long K with few 128x128 tiles: 128x128 split over k so that about 512
 //   workgroups run (each split at least 1024 k);
 //   128x128 while it gives half the CUs a tile; else 64x64.
-// SS_NT_TILE (1..11, the configurations above in order) and SS_NT_SPLITS
+// SS_NT_TILE (1..8, the configurations above in order) and SS_NT_SPLITS
 // override the choice (tuning knobs read once per process).
 struct NtPlan {
   int cfg;
@@ -526,7 +523,7 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     if (s > k / 384) s = k / 384;
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   }
-  if (forced >= 1 && forced <= 11) plan.cfg = forced;
+  if (forced >= 1 && forced <= 8) plan.cfg = forced;
   if (forced_splits >= 1) plan.splits = forced_splits;
   plan.k_split = cdiv(cdiv(k, plan.splits), 64) * 64;
   plan.splits = cdiv(k, plan.k_split);
@@ -536,9 +533,6 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
 template <int CT, int EPI>
 int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
   switch (cfg) {
-    case 11: return launch_nt<NtBig4s5, CT, EPI>(p, splits, stream);
-    case 10: return launch_nt<NtBig4s4, CT, EPI>(p, splits, stream);
-    case 9: return launch_nt<NtBig8s5, CT, EPI>(p, splits, stream);
     case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
     case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
     case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
