@@ -26,6 +26,34 @@ struct Nf4View {
 // splits in order and applies the requested epilogue.
 enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2, EPI_PARTIAL = 3 };
 
+// Arguments of one rank-16 product; splits / cps from the host plan,
+// part / counters inside a zero-filled rank workspace (rank16.h, lora_gemm.hip).
+struct RankProjectArgs {
+  const half_t* a;
+  int64_t lda, m, k;
+  const half_t* w;
+  int64_t ldw;
+  int w_kr;
+  float a_scale;
+  int64_t cps, splits;
+  half_t* out;
+  float* part;
+  int* counters;
+};
+
+struct RankGradArgs {
+  const half_t* p;
+  int64_t ldp;
+  const half_t* q;
+  int64_t ldq, t, n;
+  float q_scale;
+  int64_t cps, splits;
+  int transpose;
+  half_t* out;
+  float* part;
+  int* counters;
+};
+
 struct GemmParams {
   int64_t M, N, K;
   const half_t* A;
@@ -47,6 +75,13 @@ struct GemmParams {
   int remap;   // XCD-aware tile numbering (default on)
   float* part;      // split-K partials [splits][M][N] fp32 (EPI_PARTIAL)
   int64_t k_split;  // k elements per split (a multiple of 64)
+  // Optional rank-16 grad riding on the dense NT launch: tail_blocks extra
+  // workgroups (unsplit launches, after the GEMM tiles) each run one block
+  // of `tail` (rank_grad_block, vector loads).  tail_ran (host side) is set
+  // when a launch took the tail.
+  RankGradArgs tail;
+  int64_t tail_blocks;
+  int* tail_ran;
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own

@@ -879,9 +879,19 @@ extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
   p.lz = reinterpret_cast<const half_t*>(dz);
   p.lb = reinterpret_cast<const half_t*>(lora_a);
   p.ldlb = k;
+  // dA = fp16(dZ^T . X) needs dZ from the preparation launch, as the dX GEMM
+  // does: its workgroups ride on the dense dX launch when that path runs
+  // (vector loads), else it is launched on its own afterwards.
+  bool vda = false;
+  int da_ran = 0;
+  const int64_t da_blocks = rank_grad_setup(p.tail, dz, 16, x, ldx, t, k, 1.0f, 0, da,
+                                            rank_workspace, rank_workspace_bytes, 0, vda);
+  if (vda) {
+    p.tail_blocks = da_blocks;
+    p.tail_ran = &da_ran;
+  }
   rc = run_dx<EPI_RANK>(p, n, k, workspace, workspace_bytes, s, &pj, vp, vg);
-  if (rc) return rc;
-  // dA = fp16(dZ^T . X), after dZ.
+  if (rc || da_ran) return rc;
   return ss_lora_grad(dz, 16, x, ldx, t, k, 0, 1.0f, 0, da, rank_workspace, rank_workspace_bytes,
                       stream);
 }

@@ -39,7 +39,7 @@
 
 #include <stdlib.h>
 
-#include "gemm.h"
+#include "rank16.h"
 
 namespace ss {
 namespace {
@@ -340,13 +340,32 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
   }
 }
 
+// LDS of a GEMM workgroup: the stage ring; for the dX epilogue (rank-16
+// update) also room for a rank-16 grad tail block.
+template <class C, int EPI>
+constexpr int nt_smem_bytes() {
+  constexpr int ring = C::STAGES * C::kStageBytes;
+  return EPI == EPI_RANK && kRankGradSmem > ring ? kRankGradSmem : ring;
+}
+
 // Data-parallel / split-K kernel: workgroup = one output tile (blockIdx.x,
 // XCD-remapped) and one k split (blockIdx.y; EPI_PARTIAL stores its fp32
-// accumulator to split plane blockIdx.y).
+// accumulator to split plane blockIdx.y).  Workgroups past the tiles run the
+// optional rank-16 grad tail (p.tail; rank-16 epilogue, unsplit launches)
+// after the GEMM tiles, filling CUs the GEMM leaves idle.
 template <class C, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::STAGES * C::kStageBytes];
-  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, gridDim.x) : (int64_t)blockIdx.x;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[nt_smem_bytes<C, EPI>()];
+  const int64_t tiles = gridDim.x - p.tail_blocks;
+  if constexpr (EPI == EPI_RANK) {
+    if ((int64_t)blockIdx.x >= tiles) {
+      const int64_t b = blockIdx.x - tiles;
+      const int64_t nblocks = cdiv(p.tail.n, 64);
+      rank_grad_block<true>(p.tail, b % nblocks, b / nblocks, smem);
+      return;
+    }
+  }
+  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
   int64_t m0, n0;
   tile_origin<C>(p, tile, m0, n0);
   int64_t kbeg = 0, klen = p.K;
@@ -475,7 +494,8 @@ using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 Ki
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
-  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN)), (unsigned)splits);
+  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN) + p.tail_blocks),
+                  (unsigned)splits);
   hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
   SS_CHECK_LAUNCH("gemm_nt_kernel");
   return SS_OK;
@@ -593,6 +613,12 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
     plan.splits = 1;
     plan.k_split = p.K;
   }
+  // The rank-16 grad tail rides only on unsplit dX products (rank-16
+  // epilogue): measured, it fills idle CUs there (down / q / o / k / v
+  // backward 6-11 us faster), but slowed the split-K launches of the long-K
+  // dX more than a launch of its own costs.
+  if (epi != EPI_RANK || plan.splits > 1) p.tail_blocks = 0;
+  if (p.tail_blocks > 0 && p.tail_ran) *p.tail_ran = 1;
   if (plan.splits > 1) {
     p.part = reinterpret_cast<float*>(partials);
     p.k_split = plan.k_split;

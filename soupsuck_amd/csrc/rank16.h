@@ -9,8 +9,8 @@
 //   : w[r*ldw + k], A' = A or fp16(A * a_scale); one (16-row block, K split).
 // rank_grad_block: C[16, N] = P[T, 16]^T . Q'[T, N], Q' = Q or fp16(Q * q_scale),
 //   stored [16][N] or [N][16]; one (64-column block, T split).
-// Both expect blockDim.x = 64 * waves (waves <= 4) and `smem` of at least
-// kRankProjSmem / kRankGradSmem bytes.  A split's waves stream one chunk each
+// Both run on blocks of 64 * waves threads (waves past 4 only join the
+// barriers) with `smem` of at least kRankProjSmem / kRankGradSmem bytes.  A split's waves stream one chunk each
 // (one memory round trip), add their sums through LDS, and the splits of an
 // output block are added by the last workgroup to arrive (finish_splits).
 #pragma once
@@ -201,34 +201,6 @@ __device__ __forceinline__ void grad_chunk(const half_t* __restrict__ p, int64_t
   __builtin_amdgcn_wave_barrier();
 }
 
-// Arguments of one rank-16 product; splits / cps from the host plan,
-// part / counters inside a zero-filled rank workspace (see lora_gemm.hip).
-struct RankProjectArgs {
-  const half_t* a;
-  int64_t lda, m, k;
-  const half_t* w;
-  int64_t ldw;
-  int w_kr;
-  float a_scale;
-  int64_t cps, splits;
-  half_t* out;
-  float* part;
-  int* counters;
-};
-
-struct RankGradArgs {
-  const half_t* p;
-  int64_t ldp;
-  const half_t* q;
-  int64_t ldq, t, n;
-  float q_scale;
-  int64_t cps, splits;
-  int transpose;
-  half_t* out;
-  float* part;
-  int* counters;
-};
-
 constexpr int kRankMaxWaves = 4;
 constexpr int kRankProjSmem = kRankMaxWaves * kRank * kProjLd * 2;
 constexpr int kRankGradSmem = kRankMaxWaves * (64 * 64 + kRank * kGradLd) * 2;
@@ -241,13 +213,15 @@ __device__ __forceinline__ void rank_project_block(const RankProjectArgs& g, int
   half_t (*sw)[kRank * kProjLd] = reinterpret_cast<half_t (*)[kRank * kProjLd]>(smem);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
+  // Waves past kRankMaxWaves (a block shared with a wider kernel) take no
+  // chunk but join the barriers.
+  const int waves = (int)(blockDim.x >> 6) < kRankMaxWaves ? (int)(blockDim.x >> 6) : kRankMaxWaves;
   const int r = lane & 15;
   const int64_t row = mb * 16 + r;
   const int64_t kb = s * g.cps * kProjChunk;
   const int64_t ke = kb + g.cps * kProjChunk < g.k ? kb + g.cps * kProjChunk : g.k;
   float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
-  for (int64_t kbeg = kb + (int64_t)wave * kProjChunk; kbeg < ke;
+  for (int64_t kbeg = kb + (int64_t)wave * kProjChunk; wave < waves && kbeg < ke;
        kbeg += (int64_t)waves * kProjChunk) {
     const int64_t kend = kbeg + kProjChunk < ke ? kbeg + kProjChunk : ke;
     project_chunk<VEC>(g.a, g.lda, g.m, g.w, g.ldw, g.w_kr, g.a_scale, row, lane, kbeg, kend,
@@ -257,7 +231,7 @@ __device__ __forceinline__ void rank_project_block(const RankProjectArgs& g, int
   // their first 4 KiB hold the waves' 16x16 sums.
   __syncthreads();
   float4v* red = reinterpret_cast<float4v*>(smem);
-  red[wave * 64 + lane] = acc[0] + acc[1];
+  if (wave < waves) red[wave * 64 + lane] = acc[0] + acc[1];
   __syncthreads();
   if (wave != 0) return;
   float4v c = red[lane];
@@ -281,14 +255,17 @@ __device__ __forceinline__ void rank_grad_block(const RankGradArgs& g, int64_t n
       smem + kRankMaxWaves * 64 * 64 * 2);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
+  // Waves past kRankMaxWaves (a block shared with a wider kernel) take no
+  // chunk but join the barriers.
+  const int waves = (int)(blockDim.x >> 6) < kRankMaxWaves ? (int)(blockDim.x >> 6) : kRankMaxWaves;
   const int64_t n0 = nb * 64;
   const int64_t tb = s * g.cps * kGradChunk;
   const int64_t te = tb + g.cps * kGradChunk < g.t ? tb + g.cps * kGradChunk : g.t;
   float4v acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = float4v{0.f, 0.f, 0.f, 0.f};
-  for (int64_t t0 = tb + (int64_t)wave * kGradChunk; t0 < te; t0 += (int64_t)waves * kGradChunk) {
+  for (int64_t t0 = tb + (int64_t)wave * kGradChunk; wave < waves && t0 < te;
+       t0 += (int64_t)waves * kGradChunk) {
     const int64_t tend = t0 + kGradChunk < te ? t0 + kGradChunk : te;
     grad_chunk<VEC>(g.p, g.ldp, g.q, g.ldq, g.n, g.q_scale, n0, lane, t0, tend, sq[wave],
                     sp[wave], acc);
@@ -297,8 +274,10 @@ __device__ __forceinline__ void rank_grad_block(const RankGradArgs& g, int64_t n
   // 16 KiB hold the waves' 16x64 sums.
   __syncthreads();
   float4v* red = reinterpret_cast<float4v*>(smem);
+  if (wave < waves) {
 #pragma unroll
-  for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+    for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+  }
   __syncthreads();
   if (wave != 0) return;
   float vals[16];
