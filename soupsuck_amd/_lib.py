@@ -63,6 +63,10 @@ SIGNATURES = {
                         _c_void_p, _c_void_p, _c_void_p],
     "ss_gemm_f16": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
                     _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p],
+    "ss_gemm_f16_workspace_size": [_int, _int, _i64, _i64, _i64],
+    "ss_gemm_f16_split": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
+                          _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p, _size, _c_void_p],
+    "ss_transpose_f16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "ss_lora_epilogue_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _f32, _int,
                              _c_void_p],
     "ss_lora_epilogue_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _f32, _c_void_p],
@@ -85,7 +89,8 @@ SIGNATURES = {
                           _c_void_p],
 }
 _RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size,
-             "ss_lora_workspace_size": _size, "ss_qlora_rank_workspace_size": _size}
+             "ss_lora_workspace_size": _size, "ss_qlora_rank_workspace_size": _size,
+             "ss_gemm_f16_workspace_size": _size}
 
 _lock = threading.Lock()
 _lib = None

@@ -896,11 +896,10 @@ extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
                       stream);
 }
 
-extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
-                           const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                           const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
-                           void* stream) {
-  const char* fn = "ss_gemm_f16";
+static int gemm_f16_impl(const char* fn, int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,
+                         float alpha, const uint16_t* a, int64_t lda, const uint16_t* b,
+                         int64_t ldb, const uint16_t* bias, float beta, void* c, int c_dtype,
+                         int64_t ldc, void* workspace, size_t workspace_bytes, void* stream) {
   SS_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "%s: negative size", fn);
   SS_CHECK_ARG(c_dtype == SS_F16 || c_dtype == SS_F32, "%s: c_dtype must be SS_F16/SS_F32", fn);
   SS_CHECK_ARG(beta == 0.0f || beta == 1.0f, "%s: beta must be 0 or 1", fn);
@@ -922,13 +921,38 @@ extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64
   // b_trans = 1: B stored [N,K] -> OP_ROW; b_trans = 0: B stored [K,N] -> OP_COL.
   const int code = (a_trans ? 2 : 0) + (b_trans ? 0 : 1) + (c_dtype == SS_F32 ? 4 : 0);
   switch (code) {
-    case 0: return dispatch<OP_ROW, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 nt>");
+    case 0: return dispatch<OP_ROW, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 nt>", workspace,
+                                                    workspace_bytes);
     case 1: return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>");
     case 2: return dispatch<OP_COL, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 tt>");
     case 3: return dispatch<OP_COL, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 tn>");
-    case 4: return dispatch<OP_ROW, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 nt>");
+    case 4: return dispatch<OP_ROW, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 nt>", workspace,
+                                                    workspace_bytes);
     case 5: return dispatch<OP_ROW, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 nn>");
     case 6: return dispatch<OP_COL, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 tt>");
     default: return dispatch<OP_COL, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 tn>");
   }
+}
+
+extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
+                           const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                           const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
+                           void* stream) {
+  return gemm_f16_impl("ss_gemm_f16", a_trans, b_trans, m, n, k, alpha, a, lda, b, ldb, bias,
+                       beta, c, c_dtype, ldc, nullptr, 0, stream);
+}
+
+extern "C" size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m, int64_t n,
+                                             int64_t k) {
+  // Split-K partials of the dense NT kernel (both operands K-contiguous).
+  return !a_trans && b_trans ? ss::nt_partial_bytes(m, n, k) : 0;
+}
+
+extern "C" int ss_gemm_f16_split(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,
+                                 float alpha, const uint16_t* a, int64_t lda, const uint16_t* b,
+                                 int64_t ldb, const uint16_t* bias, float beta, void* c,
+                                 int c_dtype, int64_t ldc, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  return gemm_f16_impl("ss_gemm_f16_split", a_trans, b_trans, m, n, k, alpha, a, lda, b, ldb,
+                       bias, beta, c, c_dtype, ldc, workspace, workspace_bytes, stream);
 }

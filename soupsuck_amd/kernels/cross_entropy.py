@@ -21,7 +21,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
-from .nf4_gemm import gemm_f16
+from .nf4_gemm import gemm_f16, transpose_f16
 
 
 def _chunk_size(n, h):
@@ -118,6 +118,17 @@ class _LinearCrossEntropy(torch.autograd.Function):
         z = torch.empty((valid_n, width_max), device=device, dtype=torch.float16)
         dz = torch.empty((valid_n, width_max), device=device, dtype=torch.float16)
         dzg = torch.empty_like(dz) if need_w else None
+        # The chunk products go to the dense NT kernel, which wants both operands
+        # contiguous along the reduced dimension: dX = dz . W_c reduces over the
+        # chunk (W_c^T [H, width] per chunk), dW_c = dzg^T . h reduces over the
+        # valid rows (dzg^T [width, T'] and h^T [H, T'], T' = valid rows padded
+        # to 64 with zero columns, so K % 64 == 0).
+        wt = torch.empty((h, width_max), device=device, dtype=torch.float16) if need_x else None
+        if need_w:
+            t_pad = -(-valid_n // 64) * 64
+            ht = torch.zeros((h, t_pad), device=device, dtype=torch.float16)
+            transpose_f16(work_hidden, out=ht[:, :valid_n])
+            dzgt = torch.zeros((width_max, t_pad), device=device, dtype=torch.float16)
         for start in range(0, v, ctx.chunk):
             w = _chunk_weight(weight, start, ctx.chunk)
             width = w.shape[0]
@@ -130,15 +141,17 @@ class _LinearCrossEntropy(torch.autograd.Function):
                       _lib.ptr(dzgc), float(global_gain), valid_n, width, start,
                       ctx.ignore_index, stream)
             if need_x:
-                gemm_f16(dzc, w, out=acc, accumulate=True)
+                wtc = transpose_f16(w, out=wt[:, :width])
+                gemm_f16(dzc, wtc, b_trans=True, out=acc, accumulate=True, split_k=True)
             if need_w:
                 dw_chunk = dw[start:start + width]
+                transpose_f16(dzgc, out=dzgt[:width, :valid_n])
+                dzgtc = dzgt[:width]
                 if dw.dtype == torch.float16 or dw.dtype == torch.float32:
-                    gemm_f16(dzgc, work_hidden, a_trans=True, out=dw_chunk,
-                             alpha=float(global_gain))
+                    gemm_f16(dzgtc, ht, b_trans=True, out=dw_chunk, alpha=float(global_gain))
                 else:
-                    dw_chunk.copy_(gemm_f16(dzgc, work_hidden, a_trans=True,
-                                            out_dtype=torch.float32, alpha=float(global_gain)))
+                    dw_chunk.copy_(gemm_f16(dzgtc, ht, b_trans=True, out_dtype=torch.float32,
+                                            alpha=float(global_gain)))
         if need_x:
             _lib.call("ss_ce_finalize_dx", acc.data_ptr(), valid_n, grad.data_ptr(),
                       inverse.data_ptr(), dx.data_ptr(), _lib.dtype_code(dx.dtype), n, h, stream)

@@ -43,11 +43,13 @@ def _dense_weight(packed, state, n, k):
 
 
 def gemm_f16(a, b, *, a_trans=False, b_trans=False, out=None, out_dtype=torch.float16,
-             alpha=1.0, accumulate=False, bias=None):
+             alpha=1.0, accumulate=False, bias=None, split_k=False):
     """C = alpha * op(A) . op(B) (+bias) (+C) on the MFMA engine (ss_gemm_f16).
 
     a: [M,K] (or [K,M] when a_trans), b: [K,N] (or [N,K] when b_trans); fp16,
     row-major with unit column stride.  Returns C [M,N] of out_dtype.
+    split_k: give the dense NT kernel scratch to split a long reduction over
+    workgroups when the output has few tiles (ss_gemm_f16_split).
     """
     if a.dtype != torch.float16 or b.dtype != torch.float16:
         raise ValueError("gemm_f16 expects fp16 operands")
@@ -63,9 +65,34 @@ def gemm_f16(a, b, *, a_trans=False, b_trans=False, out=None, out_dtype=torch.fl
         out = torch.empty((m, n), device=a.device, dtype=out_dtype)
     if out.shape != (m, n) or out.stride(-1) != 1:
         raise ValueError("gemm_f16: bad output buffer")
+    size = _lib.load().ss_gemm_f16_workspace_size(int(a_trans), int(b_trans), m, n, k) \
+        if split_k else 0
+    if size:
+        ws = torch.empty(size, dtype=torch.uint8, device=a.device)
+        _lib.call("ss_gemm_f16_split", int(a_trans), int(b_trans), m, n, k, float(alpha),
+                  a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), _lib.ptr(bias),
+                  1.0 if accumulate else 0.0, out.data_ptr(), _lib.dtype_code(out.dtype),
+                  out.stride(0), ws.data_ptr(), size, _lib.stream(a.device))
+        return out
     _lib.call("ss_gemm_f16", int(a_trans), int(b_trans), m, n, k, float(alpha), a.data_ptr(),
               a.stride(0), b.data_ptr(), b.stride(0), _lib.ptr(bias), 1.0 if accumulate else 0.0,
               out.data_ptr(), _lib.dtype_code(out.dtype), out.stride(0), _lib.stream(a.device))
+    return out
+
+
+def transpose_f16(src, out=None):
+    """out[c, r] = src[r, c] for a 2-D fp16 tensor with unit column stride (ss_transpose_f16);
+    ``out`` may be a strided view (unit column stride), e.g. the leading block of a
+    wider zero-padded buffer."""
+    if src.dtype != torch.float16 or src.ndim != 2 or src.stride(-1) != 1:
+        raise ValueError("transpose_f16 expects a 2-D fp16 tensor with unit column stride")
+    rows, cols = src.shape
+    if out is None:
+        out = torch.empty((cols, rows), device=src.device, dtype=torch.float16)
+    if out.shape != (cols, rows) or out.stride(-1) != 1 or out.dtype != torch.float16:
+        raise ValueError("transpose_f16: bad output buffer")
+    _lib.call("ss_transpose_f16", src.data_ptr(), src.stride(0), rows, cols, out.data_ptr(),
+              out.stride(0), _lib.stream(src.device))
     return out
 
 

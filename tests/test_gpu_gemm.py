@@ -16,7 +16,8 @@ import torch
 from oracle import gemm as ogemm
 from oracle import nf4 as onf4
 from soupsuck_amd import _lib
-from soupsuck_amd.kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d, nf4_matmul
+from soupsuck_amd.kernels.nf4_gemm import (gemm_f16, nf4_dx_2d, nf4_forward_2d, nf4_matmul,
+                                           transpose_f16)
 from tests.gpu_util import device_state, np16, random_weight
 
 pytestmark = pytest.mark.gpu
@@ -237,3 +238,41 @@ def test_dense_nt_pipeline_tiles(device, m, n, k, out_dtype):
               f"nt accumulate {m}x{n}x{k}")
     else:
         np.testing.assert_allclose(np16(c), expected + prod, rtol=1e-5, atol=4e-4)
+
+
+@pytest.mark.parametrize("m,n,k", [(518, 1536, 8192),   # CE dX chunk: valid rows x H over a vocab chunk
+                                   (64, 64, 4096), (200, 136, 1024), (300, 2000, 64)])
+def test_dense_split_k(device, m, n, k):
+    """ss_gemm_f16_split: the long reduction over few output tiles split over
+    workgroups (partials in the caller's scratch), fp32 accumulate and fp16 out."""
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    bt = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+    ad, bd = torch.from_numpy(a).to(device), torch.from_numpy(bt).to(device)
+    prod = a.astype(np.float64) @ bt.astype(np.float64).T
+    base = rng.standard_normal((m, n)).astype(np.float32)
+    c = torch.from_numpy(base).to(device)
+    gemm_f16(ad, bd, b_trans=True, out=c, accumulate=True, split_k=True)
+    np.testing.assert_allclose(np16(c), base + prod, rtol=1e-5, atol=5e-4)
+    h = gemm_f16(ad, bd, b_trans=True, alpha=0.25, split_k=True)
+    check(h, 0.25 * prod, f"split fp16 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 130), (64, 64), (518, 1536), (1536, 518),
+                                       (100, 8192), (65, 63)])
+def test_transpose_f16(device, rows, cols):
+    """ss_transpose_f16 is a bit-exact permutation, also into a strided view of a
+    wider buffer whose padding it must leave untouched."""
+    rng = np.random.default_rng(rows * 131 + cols)
+    a = rng.standard_normal((rows, cols)).astype(np.float16)
+    src = torch.from_numpy(a).to(device)
+    out = transpose_f16(src)
+    assert np.array_equal(np16(out), a.T)
+    pad = torch.full((cols, rows + 70), 7.0, device=device, dtype=torch.float16)
+    transpose_f16(src, out=pad[:, :rows])
+    got = np16(pad)
+    assert np.array_equal(got[:, :rows], a.T)
+    assert np.all(got[:, rows:] == 7.0)
+    # a strided source (a column window of a wider matrix)
+    wide = torch.from_numpy(rng.standard_normal((rows, cols + 9)).astype(np.float16)).to(device)
+    assert np.array_equal(np16(transpose_f16(wide[:, 3:3 + cols])), np16(wide)[:, 3:3 + cols].T)
