@@ -197,6 +197,29 @@ int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream, void* part
             size_t partial_bytes = 0);
 // fp32 split-K scratch that gemm_nt uses for an M x N x K product (0: no split).
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
+// Tile configuration (1..8 in gemm_nt.hip's list) and split-K plan of an
+// M x N x K product on the NT kernels.
+struct NtPlan {
+  int cfg;
+  int64_t splits, k_split;
+};
+NtPlan nt_plan(int64_t m, int64_t n, int64_t k);
+
+// Fused NF4 forward (gemm_nf4.hip): Y = X . Wdec^T with p.M = T, p.N = N,
+// p.K = K, p.A = X, p.w = the NF4 weight, the NT kernel's tile plan and
+// epilogues (EPI_PLAIN / EPI_LORA); the weight is decoded into LDS tiles, never
+// written to memory.  `partials` (may be null) holds the split-K planes
+// (nt_partial_bytes).  SS_ERR_UNSUPPORTED (nothing launched) unless
+// gemm_nf4_fwd_ok.
+bool gemm_nf4_fwd_ok(const GemmParams& p, int epi);
+// Whether the fused kernel is the faster path for this product (tile plan and
+// M tiles; measured).
+bool gemm_nf4_fwd_preferred(const GemmParams& p);
+// The fused kernel's tile / split plan and its split-K scratch (0: no split).
+NtPlan nf4_plan(int64_t m, int64_t n, int64_t k);
+size_t nf4_fused_partial_bytes(int64_t m, int64_t n, int64_t k);
+int gemm_nf4_fwd(const GemmParams& p, int epi, hipStream_t stream, void* partials,
+                 size_t partial_bytes);
 
 // Split-K reduction: C = epilogue(sum over `splits` planes of p.part
 // [splits][M][N]) with the epilogue `epi` (EPI_PLAIN / EPI_LORA / EPI_RANK)

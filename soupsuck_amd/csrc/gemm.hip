@@ -564,12 +564,16 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     size_t fwd = ss::skinny_partial_bytes(t, n, k);
     const size_t fwd_stream = ss::stream_partial_bytes(t, n, k);
     if (fwd_stream > fwd) fwd = fwd_stream;
+    const size_t fwd_fused = ss::nf4_fused_partial_bytes(t, n, k);
+    if (fwd_fused > fwd) fwd = fwd_fused;
     size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
     const size_t dx_stream = ss::stream_dx_partial_bytes(t, n, k);
     if (dx_stream > dx) dx = dx_stream;
     return fwd > dx ? fwd : dx;
   }
-  if (t < threshold) return 0;
+  // Below the threshold the forward may run the fused kernel (its split-K
+  // partials); the backward runs the in-loop decoder without scratch.
+  if (t < threshold) return ss::nf4_fused_partial_bytes(t, n, k);
   const size_t fwd = ss::nt_partial_bytes(t, n, k);  // Y [t, n], reduction over k
   const size_t dx = ss::nt_partial_bytes(t, k, n);   // dX [t, k], reduction over n
   return decoded_bytes(n, k) + (fwd > dx ? fwd : dx);
@@ -603,6 +607,24 @@ static bool stream_enabled() {
   return on;
 }
 
+// SS_NF4_FUSED=0 turns the fused NF4 GEMM off (decode-first instead; A/B knob).
+static bool nf4_fused_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SS_NF4_FUSED");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+// SS_NF4_FUSED=2 takes the fused NF4 GEMM wherever it applies (A/B knob).
+static bool nf4_fused_forced() {
+  static const bool on = [] {
+    const char* e = getenv("SS_NF4_FUSED");
+    return e && e[0] == '2';
+  }();
+  return on;
+}
+
 // Decode-first path with the decode fused into the preparation launch of the
 // QLoRA step (rank-16 jobs + decode in one launch): T above the skinny range,
 // aligned decode destination.
@@ -628,9 +650,19 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
     const int rc = nf4_stream_fwd(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;
   }
-  if (p.M <= kSkinnyMaxT && workspace) {
+  if (p.M <= kSkinnyMaxT && workspace && !nf4_fused_forced()) {
     const int rc = nf4_skinny_fwd(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;
+  }
+  if (nf4_fused_enabled() && gemm_nf4_fwd_ok(p, EPI) &&
+      (nf4_fused_forced() || (p.M > kSkinnyMaxT && gemm_nf4_fwd_preferred(p)))) {
+    // The weight is decoded inside the GEMM; the workspace holds split-K
+    // partials only.  A deferred preparation launch carries no decode.
+    if (fused) {
+      const int r = launch_prep(*prep, vp, vg, s);
+      if (r) return r;
+    }
+    return gemm_nf4_fwd(p, EPI, s, workspace, workspace_bytes);
   }
   if (workspace && workspace_bytes >= (size_t)n * (size_t)k * 2) {
     const Nf4View& w = p.w;

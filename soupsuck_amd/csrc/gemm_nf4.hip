@@ -1,0 +1,420 @@
+// Fused NF4 GEMM for gfx950: Y[T, N] = X[T, K] . Wdec^T with the NF4 weight
+// decoded inside the GEMM, for T above the streaming / skinny kernels' range.
+//
+// Reference: bnb.matmul_4bit's forward (solution/nf4_patch.py:108-120) and
+// the fused tile analogue nf4_tile_matmul_kernel (solution/kernels/
+// nf4_gemm.py:35-71: decode a tile, cast to fp16, dot with fp32
+// accumulation).  The decode-first path writes the decoded fp16 weight (2 B
+// per weight) to memory and reads it back in the GEMM; here the weight moves
+// as its codes (0.5 B + 1/64 B of qabs per weight) and the fp16 tile exists
+// only in LDS.
+//
+// The A operand (X rows) and the MFMA / epilogue part are those of the dense
+// NT kernel (nt_core.h, same tile configurations, stage depth BK = 32), so a
+// launch computes exactly what the decode-first path computes with the same
+// configuration: identical fp16 B values (the standalone decoder's
+// arithmetic: fp16_rne(fp32(NF4[c]) * fp32(fp32(code2[q] * absmax2) +
+// offset))), identical k order.
+//
+// Per stage kt (32 k) each thread owns DPT = BN * 16 / threads code bytes of
+// one weight row (TPR = 16 / DPT threads per row): they come with the row's
+// qabs byte and absmax2 entry as plain vector loads into a register ring
+// issued D stages ahead (D >= STAGES, the A tile ring's depth), in the same
+// per-iteration pattern as the A tile DMAs, so one vmcnt wait covers both.  The thread decodes them (16-entry fp32 code table
+// and the 256-entry code2 table in LDS) and writes 2 * DPT fp16 values into
+// a double-buffered B tile with the dense kernel's BK = 32 layout.
+//
+// Loop, iteration kt: read the fragments of stage kt; wait for stage kt + 1;
+// decode stage kt + 1 into the other B tile, its arithmetic interleaved with
+// the MFMAs of stage kt (the two waves of a SIMD leave the barrier together,
+// so each wave must overlap its own decode with its MFMAs); one barrier (the
+// B tile of kt + 1 is complete, every wave is done with A slot kt % STAGES
+// and B tile kt % 2); refill the A slot with stage kt + STAGES and the
+// register slot with the codes of stage kt + D.
+
+#include "nt_core.h"
+
+namespace ss {
+namespace {
+
+__device__ __forceinline__ u32x2 vload8_off(uint32_t voff, const void* base) {
+  u32x2 v;
+  asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload4_off(uint32_t voff, const void* base) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t vload1_off(uint32_t voff, const void* base) {
+  uint32_t v;
+  asm volatile("global_load_ubyte %0, %1, %2" : "=v"(v) : "v"(voff), "s"(base) : "memory");
+  return v;
+}
+
+// Code bytes, qabs byte and absmax2 bits of one stage (codes.y unused when
+// DPT == 4).
+struct Nf4Slot {
+  u32x2 codes;
+  uint32_t q;
+  uint32_t a2;
+};
+
+template <class C>
+struct Nf4Layout {
+  static_assert(C::BK == 32, "fused NF4 stages are 32 k deep");
+  static constexpr int DPT = C::BN * 16 / C::kThreads;  // code bytes per thread per stage
+  static constexpr int TPR = 16 / DPT;                  // threads per weight row
+  static_assert(DPT == 4 || DPT == 8, "decode split");
+  static constexpr int kTileA = C::BM * 64;
+  static constexpr int kTileB = C::BN * 64;
+  static constexpr int kOffB = C::STAGES * kTileA;
+  static constexpr int kOffLut = kOffB + 2 * kTileB;
+  static constexpr int kOffCode2 = kOffLut + 64;
+  static constexpr int kSmem = kOffCode2 + 1024;
+  static constexpr int kOps = C::kDmaA + 3;  // vector-memory ops per stage and wave
+  static_assert(kSmem <= 160 * 1024, "LDS");
+};
+
+template <class C, int CD>
+__device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
+                                             int64_t kbeg, int64_t klen, unsigned char* smem,
+                                             NtAcc<C>& acc) {
+  using L = Nf4Layout<C>;
+  constexpr int kS = C::STAGES;
+  constexpr int kD = CD;  // code ring depth (stages of codes in flight)
+  static_assert(kD >= kS && kD % kS == 0, "code ring depth");
+  constexpr int kGroupBytes = 32 * 64;  // one 32-row group of a BK = 32 tile
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const Nf4View& w = p.w;
+  float* const lut = reinterpret_cast<float*>(smem + L::kOffLut);
+  float* const code2 = reinterpret_cast<float*>(smem + L::kOffCode2);
+
+  // Tables first, with tracked loads, before any untracked load is issued.
+  if (tid < 16) lut[tid] = kNF4[tid];
+  for (int i = tid; i < 256; i += C::kThreads) code2[i] = w.code2[i];
+  float offset = w.offset[0];
+  tie(offset);
+  __syncthreads();
+
+  // A tile DMA sources (rows past M clamped; never stored).
+  const uint32_t lds0 = lds_address(smem);
+  const half_t* a_base = p.A + kbeg;
+  uint32_t a_off[C::kDmaA];
+#pragma unroll
+  for (int j = 0; j < C::kDmaA; ++j) {
+    int row, chunk;
+    dma_source<32>(wave * C::kDmaA + j, lane, row, chunk);
+    const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
+    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
+  }
+  const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
+
+  // This thread's weight row (clamped) and byte range within a stage.
+  const int brow = tid / L::TPR;
+  const int bpart = tid % L::TPR;
+  const int64_t wrow = n0 + brow < p.N ? n0 + brow : p.N - 1;
+  const int64_t kq = p.K >> 6;  // scale blocks per weight row
+  const uint32_t code_off = (uint32_t)(wrow * (p.K >> 1) + (kbeg >> 1) + bpart * L::DPT);
+  const int64_t block0 = wrow * kq + (kbeg >> 6);
+  const uint32_t q_off = (uint32_t)block0;
+
+  auto issue_a = [&](int64_t kt, int slot_a) {
+#pragma unroll
+    for (int j = 0; j < C::kDmaA; ++j)
+      dma16(a_off[j], a_base + kt * 32, lds_a + slot_a * L::kTileA + j * 1024);
+  };
+  auto issue_c = [&](int64_t kt, Nf4Slot& sl) {
+    const uint8_t* cbase = w.packed + kt * 16;
+    if constexpr (L::DPT == 8) {
+      sl.codes = vload8_off(code_off, cbase);
+    } else {
+      sl.codes[0] = vload4_off(code_off, cbase);
+    }
+    sl.q = vload1_off(q_off, w.qabs + (kt >> 1));
+    sl.a2 = vload4_off((uint32_t)(((block0 + (kt >> 1)) >> 8) * 4), w.absmax2);
+  };
+
+  // Decode one stage's codes into B tile `buf`: fp16_rne(NF4[c] * scale),
+  // element 2j of a byte in its high nibble.
+  auto decode = [&](Nf4Slot& sl, int buf) {
+    tie(sl.codes);
+    tie(sl.q);
+    tie(sl.a2);
+    const float scale = code2[sl.q & 0xffu] * __builtin_bit_cast(float, sl.a2) + offset;
+    unsigned char* bt = smem + L::kOffB + buf * L::kTileB + brow * 64;
+#pragma unroll
+    for (int h = 0; h < L::DPT / 4; ++h) {
+      const uint32_t word = sl.codes[h];
+      half8 v;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (word >> (8 * b)) & 0xffu;
+        const float hi = lut[byte >> 4] * scale;
+        const float lo = lut[byte & 15u] * scale;
+        v[2 * b] = f32_to_f16(hi);
+        v[2 * b + 1] = f32_to_f16(lo);
+      }
+      const int chunk = bpart * (L::DPT / 4) + h;
+      *reinterpret_cast<half8*>(bt + ((chunk ^ swz32(brow)) << 4)) = v;
+    }
+  };
+
+  int frag_off[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) frag_off[kk] = frag_offset<32>(lane, kk);
+  auto read_frags = [&](int slot_a, int buf, int kk, half8 (&af)[C::FM], half8 (&bf)[C::FN]) {
+    const unsigned char* sa =
+        smem + slot_a * L::kTileA + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
+    const unsigned char* sb =
+        smem + L::kOffB + buf * L::kTileB + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+  };
+
+  // Every iteration issues the A tile of stage kt + kS and the codes of stage
+  // kt + kD (past the end: the last stage again, into slots nobody reads), so
+  // the wait counts are the same every time.  The codes run further ahead
+  // than the A tiles: at small T they stream from HBM and their latency,
+  // not the MFMA, sets the pace.  The prologue is kD virtual iterations
+  // -kD .. -1 of the same pattern (the first kD - kS without A tiles).
+  const int64_t ktiles = klen / 32;
+  auto clampk = [&](int64_t kt) { return kt < ktiles ? kt : ktiles - 1; };
+  Nf4Slot ring[kD];
+#pragma unroll
+  for (int v = -kD; v < 0; ++v) {
+    if (v + kS >= 0) issue_a(clampk(v + kS), v + kS);
+    issue_c(clampk(v + kD), ring[v + kD]);
+  }
+  // A tile 0 was followed by the codes of one virtual iteration and kS - 1
+  // whole virtual iterations.
+  wait_vm<3 + (kS - 1) * L::kOps>();
+  decode(ring[0], 0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+
+  // Iteration kt; j = kt % kD is a compile-time constant (the register ring
+  // is indexed statically).  The decode of stage kt + 1 (after the last
+  // stage: of a repeated stage, into the B tile nobody reads) runs as
+  // kSteps micro-steps -- code2 read, per code byte the two table reads, the
+  // scale, per byte two products and a packed conversion, the tile writes --
+  // spread between the MFMAs of stage kt (sched_barrier keeps the order):
+  // the two waves of a SIMD leave the barrier together, so a wave must
+  // overlap its own decode with its MFMAs.
+  constexpr int kBytes = L::DPT;
+  constexpr int kChunks = L::DPT / 4;
+  constexpr int kSteps = 2 * kBytes + 2 + kChunks;
+  constexpr int kMfma = 2 * C::FM * C::FN;
+  auto iteration = [&](int64_t kt, int j, Nf4Slot& next, Nf4Slot& own) {
+    const int sa = j % kS;  // A slot of stage kt
+    half8 fa[2][C::FM], fb[2][C::FN];
+    read_frags(sa, (int)(kt & 1), 0, fa[0], fb[0]);
+    read_frags(sa, (int)(kt & 1), 1, fa[1], fb[1]);
+    // Stage kt + 1: its A tile was followed by one iteration's codes and kS - 2
+    // whole iterations; its codes were issued before its A tile.
+    wait_vm<3 + (kS - 2) * L::kOps>();
+    tie(next.codes);
+    tie(next.q);
+    tie(next.a2);
+    unsigned char* const bt = smem + L::kOffB + (int)((kt + 1) & 1) * L::kTileB + brow * 64;
+    float c2 = 0.0f, scale = 0.0f;
+    float tv[2 * kBytes];
+    half8 outv[kChunks];
+    auto micro = [&](int st) {
+      if (st == 0) {
+        c2 = code2[next.q & 0xffu];
+      } else if (st <= kBytes) {
+        const int b = st - 1;
+        const uint32_t byte = (next.codes[b >> 2] >> (8 * (b & 3))) & 0xffu;
+        tv[2 * b] = lut[byte >> 4];
+        tv[2 * b + 1] = lut[byte & 15u];
+      } else if (st == kBytes + 1) {
+        scale = c2 * __builtin_bit_cast(float, next.a2) + offset;
+      } else if (st <= 2 * kBytes + 1) {
+        const int b = st - kBytes - 2;
+        outv[b >> 2][2 * (b & 3)] = f32_to_f16(tv[2 * b] * scale);
+        outv[b >> 2][2 * (b & 3) + 1] = f32_to_f16(tv[2 * b + 1] * scale);
+      } else {
+        const int h = st - 2 * kBytes - 2;
+        const int chunk = bpart * kChunks + h;
+        *reinterpret_cast<half8*>(bt + ((chunk ^ swz32(brow)) << 4)) = outv[h];
+      }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < kMfma; ++m) {
+      const int kk = m / (C::FM * C::FN);
+      const int i = (m / C::FN) % C::FM;
+      const int jj = m % C::FN;
+      acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][jj], acc[i][jj], 0,
+                                                          0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int st = m * kSteps / kMfma; st < (m + 1) * kSteps / kMfma; ++st) micro(st);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    issue_a(clampk(kt + kS), sa);
+    issue_c(clampk(kt + kD), own);
+  };
+
+  for (int64_t kt0 = 0; kt0 < ktiles; kt0 += kD) {
+#pragma unroll
+    for (int j = 0; j < kD; ++j) {
+      if (kt0 + j >= ktiles) break;
+      iteration(kt0 + j, j, ring[(j + 1) % kD], ring[j]);
+    }
+  }
+  // No LDS DMA may land after the workgroup ends, and no register load after
+  // its register is reused: the loads issued in the last iterations are never
+  // decoded, so to the compiler their results are dead as soon as the asm
+  // that "produced" them, and it would hand their registers to other values
+  // (epilogue addresses) while the loads are still in flight.  The ties keep
+  // every ring register allocated until the wait has retired its load.
+  wait_vm<0>();
+#pragma unroll
+  for (int s = 0; s < kD; ++s) {
+    tie(ring[s].codes);
+    tie(ring[s].q);
+    tie(ring[s].a2);
+  }
+}
+
+template <class C, int CD, int CT, int EPI>
+__global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4Layout<C>::kSmem];
+  const int64_t tiles = gridDim.x;
+  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
+  int64_t m0, n0;
+  tile_origin<C>(p, tile, m0, n0);
+  int64_t kbeg = 0, klen = p.K;
+  if constexpr (EPI == EPI_PARTIAL) {
+    kbeg = (int64_t)blockIdx.y * p.k_split;
+    klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
+  }
+  NtAcc<C> acc;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
+  nf4_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc);
+}
+
+// Configurations (same tiles, waves and stage depth as the dense kernel's
+// configurations 1, 2 and 8).
+using Nf4Small = NtCfg<64, 64, 2, 2, 32, 4, 2>;
+using Nf4Mid = NtCfg<128, 128, 2, 2, 32, 4, 2>;
+using Nf4Big = NtCfg<256, 256, 2, 4, 32, 4, 2>;
+
+template <class C, int CD, int CT, int EPI>
+int launch_nf4(const GemmParams& p, int64_t splits, hipStream_t stream) {
+  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN)), (unsigned)splits);
+  hipLaunchKernelGGL((gemm_nf4_kernel<C, CD, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
+  SS_CHECK_LAUNCH("gemm_nf4_kernel");
+  return SS_OK;
+}
+
+template <int CT, int EPI>
+int dispatch_nf4(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
+  switch (cfg) {
+    case 8: return launch_nf4<Nf4Big, 8, CT, EPI>(p, splits, stream);
+    case 2: return launch_nf4<Nf4Mid, 12, CT, EPI>(p, splits, stream);
+    default: return launch_nf4<Nf4Small, 12, CT, EPI>(p, splits, stream);
+  }
+}
+
+}  // namespace
+
+// Tile plan of the fused kernel: the NT kernel's plan (configurations 1, 2
+// and 8 only), except for one or two 128-row tiles, where streaming the
+// weight sets the pace: 64x64 tiles up to 64 rows, 128x128 above, split over
+// k until about 512 workgroups run, each split at least 512 deep.
+NtPlan nf4_plan(int64_t m, int64_t n, int64_t k) {
+  if (m > 256) {
+    NtPlan plan = nt_plan(m, n, k);
+    if (plan.cfg != 1 && plan.cfg != 2 && plan.cfg != 8) plan.cfg = 2;
+    return plan;
+  }
+  NtPlan plan{m <= 64 ? 1 : 2, 1, k};
+  const int64_t bm = plan.cfg == 1 ? 64 : 128;
+  const int64_t tiles = cdiv(m, bm) * cdiv(n, bm);
+  int64_t s = 512 / tiles;
+  if (s > k / 512) s = k / 512;
+  if (s < 1) s = 1;
+  plan.k_split = cdiv(cdiv(k, s), 64) * 64;
+  plan.splits = cdiv(k, plan.k_split);
+  return plan;
+}
+
+bool gemm_nf4_fwd_ok(const GemmParams& p, int epi) {
+  if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return false;
+  if (reinterpret_cast<uintptr_t>(p.A) % 16 != 0 || p.lda % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(p.w.packed) % 8 != 0)
+    return false;
+  // 32-bit offsets: A rows (DMA), code bytes and qabs from their bases.
+  const int64_t kMaxOff = (int64_t)1 << 32;
+  if (((p.M - 1) * p.lda + p.K) * 2 >= kMaxOff || p.N * (p.K / 2) >= kMaxOff) return false;
+  if (epi != EPI_PLAIN && epi != EPI_LORA) return false;
+  if (epi == EPI_LORA && (reinterpret_cast<uintptr_t>(p.lz) % 16 != 0 ||
+                          reinterpret_cast<uintptr_t>(p.lb) % 16 != 0))
+    return false;
+  return true;
+}
+
+// The fused kernel decodes each weight once per M tile, on the VALU of the
+// GEMM's own waves; the decode-first path decodes it once (2 B written and
+// read back per weight) and runs the dense GEMM.  Measured on MI355X (HIP
+// graph, one call at a time, weights rotated through HBM for the 7B shapes):
+//   T in (128, 256] (one or two 128-row tiles): fused ahead at every shape
+//     (7B gate 18944 x 3584 at T = 256: 88 vs 103 us; 1.5B gate: 34 vs 44);
+//   larger T: ahead for 64x64 tiles (990 x 1536 x 1536: 23.4 vs 25.2 us) and
+//     for 256x256 tiles with at most 4 M tiles (990 x 8960 x 1536: 61.9 vs
+//     66.1), behind for 128x128 tiles (990 x 1536 x 8960: 73.7 vs 66.5) and
+//     8 M tiles of 256 (2048 x 18944 x 3584: 392 vs 360).
+// T <= 128 stays on the streaming / skinny kernels (7B gate at T = 33: 32 vs
+// 48 us fused).
+bool gemm_nf4_fwd_preferred(const GemmParams& p) {
+  if (p.M <= kSkinnyMaxT) return false;
+  if (p.M <= 256) return true;
+  const NtPlan plan = nf4_plan(p.M, p.N, p.K);
+  return plan.cfg == 1 || (plan.cfg == 8 && cdiv(p.M, 256) <= 4);
+}
+
+size_t nf4_fused_partial_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 64 != 0) return 0;
+  const NtPlan plan = nf4_plan(m, n, k);
+  return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
+}
+
+int gemm_nf4_fwd(const GemmParams& p0, int epi, hipStream_t stream, void* partials,
+                 size_t partial_bytes) {
+  if (!gemm_nf4_fwd_ok(p0, epi)) return SS_ERR_UNSUPPORTED;
+  GemmParams p = p0;
+  NtPlan plan = nf4_plan(p.M, p.N, p.K);
+  const size_t need = (size_t)(plan.splits * p.M * p.N) * sizeof(float);
+  if (plan.splits > 1 && (!partials || partial_bytes < need ||
+                          reinterpret_cast<uintptr_t>(partials) % 16 != 0)) {
+    plan.splits = 1;
+    plan.k_split = p.K;
+  }
+  if (plan.splits > 1) {
+    p.part = reinterpret_cast<float*>(partials);
+    p.k_split = plan.k_split;
+    const int rc = dispatch_nf4<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);
+    if (rc) return rc;
+    return splitk_reduce(p, (int)plan.splits, SS_F16, epi, stream);
+  }
+  if (epi == EPI_LORA) return dispatch_nf4<SS_F16, EPI_LORA>(p, plan.cfg, 1, stream);
+  return dispatch_nf4<SS_F16, EPI_PLAIN>(p, plan.cfg, 1, stream);
+}
+
+}  // namespace ss

@@ -5,24 +5,7 @@
 // NT products; the epilogues (bias, LoRA add, rank-16 update, beta) are the
 // ones of gemm.hip.
 //
-// Pipeline: STAGES LDS buffers of BK k (32 or 64).  Operand tiles move from
-// global memory straight into LDS with global_load_lds_dwordx4 (no register
-// staging): one wave-wide DMA writes 64 lanes x 16 B = 1 KiB of contiguous
-// LDS (lane i at +16 i).  How many bytes of a row one DMA fetches sets the
-// DMA throughput (measured on MI355X, L2-resident data: 128 B per row ->
-// 43 B/clk/CU into LDS, 64 B -> 25, 32 B -> 14), so:
-//   BK = 64: a DMA covers 8 rows x 128 B.  Block b (rows 8b .. 8b+7) is 1 KiB;
-//     chunk c of row 8b + r sits at slot (c ^ (b & 1)) * 8 + r.
-//   BK = 32: a DMA covers 16 rows x 64 B.  Row r is 64 B; chunk c sits at
-//     chunk c ^ swz32(r), swz32(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1).
-// A 128-bit LDS read is served 16 lanes at a time over 64 four-byte banks
-// (256 B): with 64-byte rows, rows r and r + 4 share bank quads, so the 16
-// rows of one pass must cover the four chunk positions once per residue
-// r % 4.  swz32 does that and also keeps each 8-lane group conflict-free
-// (the narrower 128-byte pass); the former c ^ ((r >> 1) & 3) repeated with
-// period 8 and measured a uniform 2-way conflict (SQ_LDS_BANK_CONFLICT =
-// half of SQ_LDS_IDX_ACTIVE).  Both layouts make an MFMA 32x32x16 fragment
-// read (32 consecutive rows, one chunk per lane half) conflict-free.
+// Operand layouts, configurations and the epilogue: nt_core.h.
 //
 // Per stage a wave runs BK / 16 MFMA k-steps; fragments are double buffered
 // so the reads of k-step kk+1 overlap the MFMAs of kk.  One s_barrier per
@@ -39,118 +22,10 @@
 
 #include <stdlib.h>
 
-#include "rank16.h"
+#include "nt_core.h"
 
 namespace ss {
 namespace {
-
-typedef float float16v __attribute__((ext_vector_type(16)));
-
-template <int BM_, int BN_, int WAVES_M, int WAVES_N, int BK_, int STAGES_, int MINW_>
-struct NtCfg {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_, MINW = MINW_;
-  static constexpr int kWaves = WAVES_M * WAVES_N;
-  static constexpr int kThreads = kWave * kWaves;
-  static constexpr int kWavesN = WAVES_N;
-  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  static constexpr int FM = WM / 32, FN = WN / 32;   // 32x32 accumulator blocks per wave
-  static constexpr int KK = BK / 16;                 // MFMA k-steps per stage
-  static constexpr int kRowsPerDma = 1024 / (BK * 2);
-  static constexpr int kDmaA = BM / kRowsPerDma / kWaves;  // DMAs per wave per stage
-  static constexpr int kDmaB = BN / kRowsPerDma / kWaves;
-  static constexpr int kDma = kDmaA + kDmaB;
-  static constexpr int kTileA = BM * BK * 2;         // bytes of one stage's A tile
-  static constexpr int kStageBytes = (BM + BN) * BK * 2;
-  static_assert(BK == 32 || BK == 64, "stage depth");
-  static_assert(BM % (kRowsPerDma * kWaves) == 0 && BN % (kRowsPerDma * kWaves) == 0,
-                "DMA split over waves");
-  static_assert(WM % 32 == 0 && WN % 32 == 0, "32x32 MFMA blocks");
-  static_assert(STAGES >= 2 && STAGES <= 5, "pipeline depth");
-  static_assert(STAGES * kStageBytes <= 160 * 1024, "LDS");
-};
-
-// Wait until at most `ahead` stages of DMAs (KDMA each) are outstanding.
-template <int KDMA, int MAXAHEAD>
-__device__ __forceinline__ void wait_stages(int64_t ahead) {
-  static_assert(MAXAHEAD <= 4, "wait depth");
-  if constexpr (MAXAHEAD >= 4) {
-    if (ahead >= 4) {
-      wait_vm<4 * KDMA>();
-      return;
-    }
-  }
-  if constexpr (MAXAHEAD >= 3) {
-    if (ahead >= 3) {
-      wait_vm<3 * KDMA>();
-      return;
-    }
-  }
-  if constexpr (MAXAHEAD >= 2) {
-    if (ahead >= 2) {
-      wait_vm<2 * KDMA>();
-      return;
-    }
-  }
-  if constexpr (MAXAHEAD >= 1) {
-    if (ahead >= 1) {
-      wait_vm<KDMA>();
-      return;
-    }
-  }
-  wait_vm<0>();
-}
-
-// Chunk swizzle of the BK = 32 layout (see the layout notes above).
-__device__ __forceinline__ int swz32(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
-
-// DMA g of an operand tile: the row and logical 16-byte chunk that lane
-// fetches (its LDS slot is g * 1024 + 16 * lane).
-template <int BK>
-__device__ __forceinline__ void dma_source(int g, int lane, int& row, int& chunk) {
-  if constexpr (BK == 64) {
-    row = g * 8 + (lane & 7);
-    chunk = (lane >> 3) ^ (g & 1);
-  } else {
-    row = g * 16 + (lane >> 2);
-    chunk = (lane & 3) ^ swz32(row);
-  }
-}
-
-// Byte offset (within a stage's operand tile, relative to the start of a
-// 32-row group) of the lane's fragment for k-step kk: row lane % 32,
-// logical chunk 2 kk + lane / 32.
-template <int BK>
-__device__ __forceinline__ int frag_offset(int lane, int kk) {
-  const int r = lane & 31;
-  const int c = 2 * kk + (lane >> 5);
-  if constexpr (BK == 64) {
-    const int b = r >> 3;
-    return b * 1024 + ((((c ^ (b & 1)) * 8) + (r & 7)) << 4);
-  } else {
-    return r * 64 + ((c ^ swz32(r)) << 4);
-  }
-}
-
-template <class C>
-using NtAcc = float16v[C::FM][C::FN];
-
-// Tile id -> (m0, n0).  Consecutive tile ids walk groups of kGroupM M-tiles
-// (M fastest) before moving to the next N-tile, so the tiles resident on one
-// XCD at a time (after the XCD remap of workgroup ids) form a kGroupM x (n)
-// block that reuses both its A panels and its B panels from that XCD's L2.
-template <class C>
-__device__ __forceinline__ void tile_origin(const GemmParams& p, int64_t tile, int64_t& m0,
-                                            int64_t& n0) {
-  const int64_t mtiles = cdiv(p.M, C::BM);
-  const int64_t ntiles = cdiv(p.N, C::BN);
-  constexpr int64_t kGroupM = 8;
-  const int64_t per_group = kGroupM * ntiles;
-  const int64_t first_m = (tile / per_group) * kGroupM;
-  const int64_t group_m = mtiles - first_m < kGroupM ? mtiles - first_m : kGroupM;
-  const int64_t in_group = tile % per_group;
-  m0 = (first_m + in_group % group_m) * C::BM;
-  n0 = (in_group / group_m) * C::BN;
-}
 
 // acc += A[m0.., kbeg .. kbeg+klen) . B[n0.., same k]^T for one output tile:
 // the pipelined direct-to-LDS main loop.  All of the workgroup's LDS DMAs
@@ -270,73 +145,6 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
 #pragma unroll
     for (int d = kMfma < C::kDma ? kMfma * (C::kDma / kMfma) : C::kDma; d < C::kDma; ++d)
       if (refill) dma_one(kt + kS, refill_stage, d);
-  }
-}
-
-// Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
-// 4][lane % 32] of each 32x32 block in register r.
-template <class C, int CT, int EPI>
-__device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
-                                            const NtAcc<C>& acc) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int wm = wave / C::kWavesN;
-  const int wn = wave % C::kWavesN;
-  const int lr = lane & 31;  // column within a 32x32 block
-  const int lh = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int64_t row_base = m0 + wm * C::WM + i * 32;
-      const int64_t col = n0 + wn * C::WN + j * 32 + lr;
-      if constexpr (EPI == EPI_PARTIAL) {
-        if (col >= p.N) continue;
-        float* part = p.part + (int64_t)blockIdx.y * p.M * p.N;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (row < p.M) part[row * p.N + col] = acc[i][j][r];
-        }
-        continue;
-      }
-      float16v extra = float16v{};
-      if constexpr (EPI != EPI_PLAIN) {
-        // Rank-16 term of this block on one v_mfma_f32_32x32x16_f16:
-        // A = Z rows (row lane%32, ranks 8 (lane/32)..+7), B = (rank, column).
-        const int64_t zr = row_base + lr;
-        const half8 zero = half8{};
-        const half8 za = zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
-        half8 zb = zero;
-        if (col < p.N) {
-          if constexpr (EPI == EPI_LORA) {
-            zb = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
-          }
-        }
-        extra = __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, extra, 0, 0, 0);
-      }
-      if (col >= p.N) continue;
-      const float b = p.bias ? (float)p.bias[col] : 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (row >= p.M) continue;
-        const int64_t idx = row * p.ldc + col;
-        if constexpr (EPI == EPI_LORA) {
-          const float y = (float)f32_to_f16(acc[i][j][r] * p.alpha + b);
-          const float lora = (float)f32_to_f16(extra[r]);
-          const float scaled = (float)f32_to_f16(lora * p.lscale);
-          reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
-        } else if constexpr (EPI == EPI_RANK) {
-          store_c<CT>(p.C, idx, acc[i][j][r] + extra[r], p.beta);
-        } else {
-          store_c<CT>(p.C, idx, acc[i][j][r] * p.alpha + b, p.beta);
-        }
-      }
-    }
   }
 }
 
@@ -501,6 +309,33 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
   return SS_OK;
 }
 
+template <int CT, int EPI>
+int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
+  switch (cfg) {
+    case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
+    case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
+    case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
+    case 5: return launch_nt<NtWide8, CT, EPI>(p, splits, stream);
+    case 4: return launch_nt<NtBig8, CT, EPI>(p, splits, stream);
+    case 3: return launch_nt<NtBig4, CT, EPI>(p, splits, stream);
+    case 2: return launch_nt<NtMid, CT, EPI>(p, splits, stream);
+    default: return launch_nt<NtSmall, CT, EPI>(p, splits, stream);
+  }
+}
+
+template <int CT, int EPI>
+int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
+  const int64_t threads = p.M * cdiv(p.N, 4);
+  hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI>), dim3((unsigned)cdiv(threads, 256)),
+                     dim3(256), 0, stream, p, (int)splits);
+  SS_CHECK_LAUNCH("splitk_reduce_kernel");
+  return SS_OK;
+}
+
+bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
+
+}  // namespace
+
 // Configuration and split-K plan for an M x N x K product.
 //   256x256 (8 waves, 4-stage ring) once it gives at least half the CUs a
 //   tile;
@@ -509,11 +344,6 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
 //   128x128 while it gives half the CUs a tile; else 64x64.
 // SS_NT_TILE (1..8, the configurations above in order) and SS_NT_SPLITS
 // override the choice (tuning knobs read once per process).
-struct NtPlan {
-  int cfg;
-  int64_t splits, k_split;
-};
-
 NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   static const int forced = [] {
     const char* e = getenv("SS_NT_TILE");
@@ -549,33 +379,6 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   plan.splits = cdiv(k, plan.k_split);
   return plan;
 }
-
-template <int CT, int EPI>
-int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
-  switch (cfg) {
-    case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
-    case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
-    case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
-    case 5: return launch_nt<NtWide8, CT, EPI>(p, splits, stream);
-    case 4: return launch_nt<NtBig8, CT, EPI>(p, splits, stream);
-    case 3: return launch_nt<NtBig4, CT, EPI>(p, splits, stream);
-    case 2: return launch_nt<NtMid, CT, EPI>(p, splits, stream);
-    default: return launch_nt<NtSmall, CT, EPI>(p, splits, stream);
-  }
-}
-
-template <int CT, int EPI>
-int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
-  const int64_t threads = p.M * cdiv(p.N, 4);
-  hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI>), dim3((unsigned)cdiv(threads, 256)),
-                     dim3(256), 0, stream, p, (int)splits);
-  SS_CHECK_LAUNCH("splitk_reduce_kernel");
-  return SS_OK;
-}
-
-bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; }
-
-}  // namespace
 
 int splitk_reduce(const GemmParams& p, int splits, int ct, int epi, hipStream_t stream) {
   if (ct == SS_F32) {

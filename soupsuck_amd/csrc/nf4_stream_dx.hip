@@ -246,6 +246,9 @@ __global__ __launch_bounds__(kDxWaves * kWave) void nf4_stream_dx_kernel(GemmPar
     }
   }
   wait_vm<0>();
+  // A wave without units never consumed the offset load: keep its register
+  // allocated until the wait above has retired it.
+  tie(offset_bits);
 
   // Cross-wave sums in rounds of column chunks through the slot region:
   // wave w's value for dY row m, chunk cc, lane column c at

@@ -276,3 +276,25 @@ def test_transpose_f16(device, rows, cols):
     # a strided source (a column window of a wider matrix)
     wide = torch.from_numpy(rng.standard_normal((rows, cols + 9)).astype(np.float16)).to(device)
     assert np.array_equal(np16(transpose_f16(wide[:, 3:3 + cols])), np16(wide)[:, 3:3 + cols].T)
+
+
+@pytest.mark.parametrize("t,n,k", [(990, 8960, 1536),   # 256x256 tiles, 4 M tiles
+                                   (1024, 8960, 1536),  # configs[0]
+                                   (800, 1536, 1536),   # 64x64 tiles
+                                   (300, 256, 1536),    # 64x64 tiles split over k
+                                   (990, 1536, 8960)])  # decode-first (long k)
+def test_forward_bitwise_equals_decode_then_dense(device, t, n, k):
+    """The NF4 forward (fused decode or decode-first, as dispatched) equals,
+    bit for bit, the stand-alone decode followed by the dense NT GEMM with the
+    same tile plan: the fused kernel's fp16 B tiles are the decoder's values
+    and its k order is the dense kernel's."""
+    state, _ = weight(n, k)
+    packed, qs = device_state(state, device)
+    x = torch.from_numpy(x_of(t, k, seed=7)).to(device)
+    y = nf4_matmul(x, packed, qs)
+    wd = torch.empty((n, k), device=device, dtype=torch.float16)
+    _lib.call("ss_nf4_dequant_nested", packed.data_ptr(), qs.absmax.data_ptr(),
+              qs.state2.absmax.data_ptr(), qs.state2.code.data_ptr(), qs.offset.data_ptr(),
+              wd.data_ptr(), n * k, _lib.stream(device))
+    ref = gemm_f16(x, wd, b_trans=True, split_k=True)
+    assert torch.equal(y, ref)
