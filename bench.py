@@ -22,7 +22,7 @@ roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
 other_configs = configs[0] (gate dequant GB/s, GEMM T=1024 TFLOP/s), configs[2]
-             (add-RMSNorm fwd/bwd/dgamma and unpad gather/scatter GB/s) and
+             (add-RMSNorm fwd/bwd/bwd+dgamma and unpad gather/scatter GB/s) and
              configs[3] (fused chunked CE fwd+bwd ms and TFLOP/s)
 sweep_configs4 = configs[4]: NF4 forward and dX at the Qwen2.5-7B projection
              shapes, T in {1, 16, 128, 2048, 16384}, each point timed from HBM
@@ -314,7 +314,8 @@ def other_configs(torch, _lib):
       dequant      0.5 + 1/64 B per weight in (codes, qabs) + absmax2 + 2 B out;
       add-RMSNorm  fwd  r, d in, s, y out (8 H B per row) + rstd 4 B + w 2 H;
                    bwd  s, gs, gy in, dr, dd out (10 H B per row) + rstd + w;
-                   dgamma s, gy in (4 H B per row) + rstd + partial planes;
+                   bwd + dgamma: the backward's bytes + the per-wave fp32 column sums
+                   written and read back + dw;
       gather       T rows read + T rows written (4 H B per token);
       scatter      T rows read + B*S rows written + the int32 inverse map.
     CE is timed whole through fused_linear_cross_entropy
@@ -369,7 +370,7 @@ def other_configs(torch, _lib):
         "roofline_frac": round(flops / PEAK_FP16_TFLOPS / 1e6 / us, 4)}
     del packs, packed, st, x, y, ws
 
-    # add-RMSNorm fwd/bwd/dgamma at T in {826, 4096, 16384}, H = 1536.
+    # add-RMSNorm fwd/bwd/bwd+dgamma at T in {826, 4096, 16384}, H = 1536.
     h = 1536
     wn = (1 + 0.1 * torch.randn(h, device=dev, generator=gen)).half()
     for t in (826, 4096, 16384):
@@ -403,18 +404,21 @@ def other_configs(torch, _lib):
 
         us = graph_us(torch, _lib, bwd, 32)
         out[f"configs2_add_rmsnorm_bwd_T{t}"] = hbm_point(us, t * (10 * h + 4) + 2 * h, copies)
-        groups = -(-t // 32)
-        partial = torch.empty((groups, h), device=dev, dtype=torch.float32)
+        waves = _lib.load().ss_add_rmsnorm_dgamma_waves(t)
+        partial = torch.empty((waves, h), device=dev, dtype=torch.float32)
         dw = torch.empty(h, device=dev, dtype=torch.float16)
 
-        def dgamma(i, stream):
-            _, gy, s, _, rstd = bufs[i % copies]
-            _lib.call("ss_rmsnorm_dgamma", s.data_ptr(), f16, rstd.data_ptr(), gy.data_ptr(),
-                      f16, h, 1, 1, partial.data_ptr(), dw.data_ptr(), f16, t, h, stream)
+        def bwd_dgamma(i, stream):
+            gs, gy, s, _, rstd = bufs[i % copies]
+            dr, dd = grads[i % copies]
+            _lib.call("ss_add_rmsnorm_bwd_dgamma", s.data_ptr(), f16, wn.data_ptr(), f16, 1,
+                      rstd.data_ptr(), gs.data_ptr(), f16, h, 1, gy.data_ptr(), f16, h, 1,
+                      dr.data_ptr(), f16, dd.data_ptr(), f16, 1, partial.data_ptr(),
+                      dw.data_ptr(), f16, t, h, stream)
 
-        us = graph_us(torch, _lib, dgamma, 32)
-        out[f"configs2_rmsnorm_dgamma_T{t}"] = hbm_point(
-            us, t * (4 * h + 4) + 2 * groups * h * 4 + 2 * h, copies)
+        us = graph_us(torch, _lib, bwd_dgamma, 32)
+        out[f"configs2_add_rmsnorm_bwd_dgamma_T{t}"] = hbm_point(
+            us, t * (10 * h + 4) + 2 * h + 2 * waves * h * 4 + 2 * h, copies)
         del bufs, grads
 
     # unpad gather/scatter of a [4, 360, 1536] fp16 batch.

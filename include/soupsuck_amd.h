@@ -261,6 +261,22 @@ int ss_add_rmsnorm_bwd(const void* s, int s_dtype, const void* w, int w_dtype, i
                        int64_t gy_col, void* dr, int dr_dtype, void* dd, int dd_dtype,
                        int64_t rows, int64_t h, void* stream);
 
+/* The backward of ss_add_rmsnorm_bwd and the weight gradient in one pass over
+ * s and gy: dr / dd as there (either may be NULL) and
+ * dgamma[c] = sum_rows gy * cast_s(s*rstd) (products rounded to fp16 when
+ * half_products), summed per group of consecutive rows in fp32 into partial
+ * fp32[ss_add_rmsnorm_dgamma_waves(rows), h] (caller-provided scratch, no
+ * initialisation needed) and those sums added in group order (deterministic).
+ * Replaces add_rmsnorm_backward_kernel followed by the two dgamma kernels
+ * (solution/kernels/add_rmsnorm.py:54-81,123-135; rmsnorm.py:73-102). */
+int64_t ss_add_rmsnorm_dgamma_waves(int64_t rows);
+int ss_add_rmsnorm_bwd_dgamma(const void* s, int s_dtype, const void* w, int w_dtype,
+                              int64_t w_stride, const float* rstd, const void* gs, int gs_dtype,
+                              int64_t gs_row, int64_t gs_col, const void* gy, int gy_dtype,
+                              int64_t gy_row, int64_t gy_col, void* dr, int dr_dtype, void* dd,
+                              int dd_dtype, int half_products, float* partial, void* dw,
+                              int dw_dtype, int64_t rows, int64_t h, void* stream);
+
 /* dgamma[c] = sum_rows gy * cast_s(s*rstd) (products rounded to fp16 when
  * half_products), two-stage and non-atomic: partial fp32[ceil(rows/32), h]
  * is caller-provided scratch.  Replaces rmsnorm_weight_partials_kernel /

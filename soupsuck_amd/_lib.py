@@ -75,6 +75,11 @@ SIGNATURES = {
     "ss_add_rmsnorm_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _c_void_p, _c_void_p, _int,
                            _i64, _i64, _c_void_p, _int, _i64, _i64, _c_void_p, _int, _c_void_p,
                            _int, _i64, _i64, _c_void_p],
+    "ss_add_rmsnorm_dgamma_waves": [_i64],
+    "ss_add_rmsnorm_bwd_dgamma": [_c_void_p, _int, _c_void_p, _int, _i64, _c_void_p, _c_void_p,
+                                  _int, _i64, _i64, _c_void_p, _int, _i64, _i64, _c_void_p, _int,
+                                  _c_void_p, _int, _int, _c_void_p, _c_void_p, _int, _i64, _i64,
+                                  _c_void_p],
     "ss_rmsnorm_dgamma": [_c_void_p, _int, _c_void_p, _c_void_p, _int, _i64, _i64, _int,
                           _c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p],
     "ss_unpad_gather": [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
@@ -90,7 +95,7 @@ SIGNATURES = {
 }
 _RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size,
              "ss_lora_workspace_size": _size, "ss_qlora_rank_workspace_size": _size,
-             "ss_gemm_f16_workspace_size": _size}
+             "ss_gemm_f16_workspace_size": _size, "ss_add_rmsnorm_dgamma_waves": _i64}
 
 _lock = threading.Lock()
 _lib = None

@@ -159,11 +159,12 @@ struct BwdArgs {
   int vec_gs, vec_gy;
 };
 
-template <int NCH>
-__global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
+// One row of the backward, on one wave: ds into dr / dd (when present) and,
+// with DG, gy * cast_s(s * rstd) added to the lane's column sums dg
+// (rounded to fp16 first when half_products).
+template <int NCH, bool DG>
+__device__ __forceinline__ void bwd_row(const BwdArgs& a, int64_t row, int lane,
+                                        float (&dg)[NCH][8], int half_products) {
   const int64_t base = row * a.h;
   float ds[NCH][8];
   if (a.gy) {
@@ -186,6 +187,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
           ds[c][j] = u;
           const float ua = u * av_;
           dot += ua;
+          if constexpr (DG) {
+            float prod = g.v[j] * round_to(a.sd, av_);
+            if (half_products) prod = round_to(SS_F16, prod);
+            dg[c][j] += prod;
+          }
         }
       } else {
 #pragma unroll
@@ -211,6 +217,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ds[c][j] = 0.0f;
   }
+  if (!a.dr && !a.dd) return;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
@@ -229,6 +236,89 @@ __global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
     if (a.dd) store8(a.dd, a.ddd, base + col0, valid, out, a.vec);
   }
 }
+
+template <int NCH>
+__global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  float unused[NCH][8];
+  bwd_row<NCH, false>(a, row, lane, unused, 0);
+}
+
+// Backward with the weight gradient in the same pass over s and gy: a
+// workgroup of kDgWaves waves owns kDgWaves consecutive rows (one per wave,
+// like the plain backward) and keeps fp32 column sums of gy * cast_s(s *
+// rstd); the waves' sums are added through LDS in wave order into
+// partial[workgroup][h].
+constexpr int kDgWaves = 8;
+
+template <int NCH>
+__global__ __launch_bounds__(kDgWaves * 64) void add_rmsnorm_bwd_dg_kernel(
+    BwdArgs a, int half_products, float* __restrict__ partial) {
+  extern __shared__ float s_dg[];  // [kDgWaves][h]
+  const int lane = threadIdx.x & 63;
+  const int k = threadIdx.x >> 6;
+  float dg[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dg[c][j] = 0.0f;
+  const int64_t row = (int64_t)blockIdx.x * kDgWaves + k;
+  if (row < a.rows) bwd_row<NCH, true>(a, row, lane, dg, half_products);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (col0 + j < a.h) s_dg[k * a.h + col0 + j] = dg[c][j];
+  }
+  __syncthreads();
+  for (int64_t col = threadIdx.x; col < a.h; col += kDgWaves * 64) {
+    float v = s_dg[col];
+#pragma unroll
+    for (int q = 1; q < kDgWaves; ++q) v += s_dg[q * a.h + col];
+    partial[(int64_t)blockIdx.x * a.h + col] = v;
+  }
+}
+
+// dw[c] = sum over g = 0 .. groups-1 of partial[g][c]: 64 columns per
+// workgroup of 16 waves; wave k takes g = k, k + 16, ... in batches of eight
+// loads (in flight together) added in order, and the 16 wave sums are added
+// in wave order.
+__global__ __launch_bounds__(1024) void dgamma_groups_final_kernel(
+    const float* __restrict__ partial, int64_t groups, int64_t h, void* dw, int dwd) {
+  __shared__ float part[16][64];
+  const int lane = threadIdx.x & 63;
+  const int k = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t cc = c < h ? c : h - 1;
+  float acc = 0.0f;
+  int64_t g = k;
+  for (; g + 16 * 7 < groups; g += 16 * 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = partial[(g + 16 * j) * h + cc];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += v[j];
+  }
+  for (; g < groups; g += 16) acc += partial[g * h + cc];
+  part[k][lane] = acc;
+  __syncthreads();
+  if (k == 0 && c < h) {
+    float v = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v += part[q][lane];
+    st_elem(dw, dwd, c, v);
+  }
+}
+
+// Partial rows of the fused backward + dgamma pass (one per workgroup).  One
+// row per wave: a wave's rows would run one after the other (each a chain of
+// loads, a wave reduction and stores), cutting the waves in flight more than
+// it saves in partial rows (measured at T = 16384: 196 us with four rows per
+// wave).
+int64_t dgamma_groups(int64_t rows) { return rows > 0 ? cdiv(rows, kDgWaves) : 0; }
 
 __global__ __launch_bounds__(256) void dgamma_partial_kernel(
     const void* __restrict__ s, int sd, const float* __restrict__ rstd, const void* __restrict__ gy,
@@ -341,6 +431,82 @@ extern "C" int ss_add_rmsnorm_bwd(const void* s, int s_dtype, const void* w, int
   hipStream_t st = (hipStream_t)stream;
   SS_ROW_KERNEL_SWITCH(add_rmsnorm_bwd_kernel, nch, a, grid, st);
   SS_CHECK_LAUNCH("add_rmsnorm_bwd_kernel");
+  return SS_OK;
+}
+
+extern "C" int64_t ss_add_rmsnorm_dgamma_waves(int64_t rows) { return ss::dgamma_groups(rows); }
+
+extern "C" int ss_add_rmsnorm_bwd_dgamma(const void* s, int s_dtype, const void* w, int w_dtype,
+                                         int64_t w_stride, const float* rstd, const void* gs,
+                                         int gs_dtype, int64_t gs_row, int64_t gs_col,
+                                         const void* gy, int gy_dtype, int64_t gy_row,
+                                         int64_t gy_col, void* dr, int dr_dtype, void* dd,
+                                         int dd_dtype, int half_products, float* partial,
+                                         void* dw, int dw_dtype, int64_t rows, int64_t h,
+                                         void* stream) {
+  const char* fn = "ss_add_rmsnorm_bwd_dgamma";
+  SS_CHECK_ARG(rows >= 0 && h > 0, "%s: need rows >= 0 and h > 0", fn);
+  SS_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(w_dtype) && valid_dtype(dw_dtype),
+               "%s: bad s/w/dw dtype", fn);
+  SS_CHECK_ARG(!gs || valid_dtype(gs_dtype), "%s: bad gs dtype", fn);
+  SS_CHECK_ARG(!gy || valid_dtype(gy_dtype), "%s: bad gy dtype", fn);
+  SS_CHECK_ARG(!dr || valid_dtype(dr_dtype), "%s: bad dr dtype", fn);
+  SS_CHECK_ARG(!dd || valid_dtype(dd_dtype), "%s: bad dd dtype", fn);
+  if (h > 512 * kMaxChunks) {
+    ss::set_error("%s: h=%lld exceeds the register-resident row limit %d", fn, (long long)h,
+                  512 * kMaxChunks);
+    return SS_ERR_UNSUPPORTED;
+  }
+  SS_CHECK_ARG(dw, "%s: null dw", fn);
+  hipStream_t st = (hipStream_t)stream;
+  if ((size_t)kDgWaves * h * sizeof(float) > 160 * 1024) {
+    // Rows too wide for the LDS combine: the backward, then the two-stage
+    // dgamma (ceil(rows / 32) partial rows, within the partial scratch).
+    const int rc = ss_add_rmsnorm_bwd(s, s_dtype, w, w_dtype, w_stride, rstd, gs, gs_dtype, gs_row,
+                                      gs_col, gy, gy_dtype, gy_row, gy_col, dr, dr_dtype, dd,
+                                      dd_dtype, rows, h, stream);
+    if (rc) return rc;
+    if (!gy) {
+      hipLaunchKernelGGL(dgamma_final_kernel, dim3((unsigned)cdiv(h, 256)), dim3(256), 0, st,
+                         partial, (int64_t)0, h, dw, dw_dtype);
+      SS_CHECK_LAUNCH("dgamma_final_kernel");
+      return SS_OK;
+    }
+    return ss_rmsnorm_dgamma(s, s_dtype, rstd, gy, gy_dtype, gy_row, gy_col, half_products,
+                             partial, dw, dw_dtype, rows, h, stream);
+  }
+  const int64_t groups = dgamma_groups(rows);
+  if (rows > 0) {
+    SS_CHECK_ARG(s && w && rstd && partial, "%s: null pointer", fn);
+    BwdArgs a{s, s_dtype, w, w_dtype, w_stride, rstd, gs, gs_dtype, gs_row, gs_col, gy,
+              gy_dtype, gy_row, gy_col, dr, dr_dtype, dd, dd_dtype, rows, h, 0, 0, 0};
+    a.vec = (h % 8 == 0) && al16(s) && (!dr || al16(dr)) && (!dd || al16(dd)) &&
+            (w_stride != 1 || al16(w));
+    a.vec_gs = gs && gs_col == 1 && gs_row % 8 == 0 && al16(gs) && a.vec;
+    a.vec_gy = gy && gy_col == 1 && gy_row % 8 == 0 && al16(gy) && a.vec;
+    const int nch = (int)cdiv(h, 512);
+    const size_t lds = (size_t)kDgWaves * h * sizeof(float);
+    const dim3 grid((unsigned)groups);
+    const dim3 block(kDgWaves * 64);
+#define SS_DG_CASE(N)                                                                           \
+  case N:                                                                                       \
+    hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<N>), grid, block, lds, st, a, half_products,  \
+                       partial);                                                                \
+    break;
+    switch (nch) {
+      SS_DG_CASE(1) SS_DG_CASE(2) SS_DG_CASE(3) SS_DG_CASE(4) SS_DG_CASE(5) SS_DG_CASE(6)
+      SS_DG_CASE(7) SS_DG_CASE(8)
+      default:
+        hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<16>), grid, block, lds, st, a,
+                           half_products, partial);
+        break;
+    }
+#undef SS_DG_CASE
+    SS_CHECK_LAUNCH("add_rmsnorm_bwd_dg_kernel");
+  }
+  hipLaunchKernelGGL(dgamma_groups_final_kernel, dim3((unsigned)cdiv(h, 64)), dim3(1024), 0, st,
+                     partial, groups, h, dw, dw_dtype);
+  SS_CHECK_LAUNCH("dgamma_groups_final_kernel");
   return SS_OK;
 }
 

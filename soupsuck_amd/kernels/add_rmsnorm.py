@@ -6,8 +6,10 @@ s = cast(residual + delta, promote), y = weight * cast(s * rstd, s.dtype) in
 promote(s, weight) or fp16 when out_dtype=torch.float16; backward
 ds = cast(rstd (u - a mean(u a))) + g_s with u = cast(g_y w); dgamma is the
 two-stage non-atomic reduction of g_y * q (products rounded to fp16 when the
-exact output dtype is fp16).  Kernels: ss_add_rmsnorm_fwd / _bwd and
-ss_rmsnorm_dgamma.  Saves only s, the weight and one fp32 rstd per row.
+exact output dtype is fp16).  Kernels: ss_add_rmsnorm_fwd / _bwd, and
+ss_add_rmsnorm_bwd_dgamma when the weight is trained (input gradients and the
+per-wave column sums of dgamma in one pass over s and gy, then an in-order
+sum of the wave partials).  Saves only s, the weight and one fp32 rstd per row.
 """
 
 import math
@@ -56,6 +58,23 @@ class _AddRMSNorm(torch.autograd.Function):
         dd = torch.empty(s.shape, device=s.device, dtype=ctx.delta_dtype) if need_d else None
         dw = None
         stream = _lib.stream(s.device)
+        if need_w and rows and grad_normed is not None:
+            # dr / dd and the weight gradient in one pass over s and gy.
+            gs = grad_residual.reshape(rows, h) if grad_residual is not None else None
+            gy = grad_normed.reshape(rows, h)
+            waves = _lib.load().ss_add_rmsnorm_dgamma_waves(rows)
+            partial = torch.empty((waves, h), device=s.device, dtype=torch.float32)
+            dw = torch.empty(weight.shape, device=weight.device, dtype=weight.dtype)
+            _lib.call("ss_add_rmsnorm_bwd_dgamma", s.data_ptr(), _code(s), weight.data_ptr(),
+                      _code(weight), weight.stride(0), rstd.data_ptr(), _lib.ptr(gs),
+                      _code(gs) if gs is not None else 0,
+                      gs.stride(0) if gs is not None else 0, gs.stride(1) if gs is not None else 0,
+                      gy.data_ptr(), _code(gy), gy.stride(0), gy.stride(1),
+                      _lib.ptr(dr), _code(dr) if dr is not None else 0, _lib.ptr(dd),
+                      _code(dd) if dd is not None else 0,
+                      int(ctx.exact_dtype == torch.float16), partial.data_ptr(), dw.data_ptr(),
+                      _code(dw), rows, h, stream)
+            return dr, dd, dw, None, None
         if rows and (need_r or need_d):
             gs = grad_residual.reshape(rows, h) if grad_residual is not None else None
             gy = grad_normed.reshape(rows, h) if grad_normed is not None else None
