@@ -75,6 +75,7 @@ struct GemmParams {
   int remap;   // XCD-aware tile numbering (default on)
   float* part;      // split-K partials [splits][M][N] fp32 (EPI_PARTIAL)
   int64_t k_split;  // k elements per split (a multiple of 64)
+  int fold_rank;    // EPI_PARTIAL: split 0 adds the rank-16 term lz . lb (EPI_RANK layout)
   // Optional rank-16 grad riding on the dense NT launch: tail_blocks extra
   // workgroups (unsplit launches, after the GEMM tiles) each run one block
   // of `tail` (rank_grad_block, vector loads).  tail_ran (host side) is set

@@ -425,11 +425,19 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
   if (plan.splits > 1) {
     p.part = reinterpret_cast<float*>(partials);
     p.k_split = plan.k_split;
+    // The rank-16 update is folded into split 0's partial (the reduce then
+    // only sums: its lora_A column loads dominated its load count).
+    p.fold_rank = epi == EPI_RANK;
     const int rc = dispatch_nt<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);
     if (rc) return rc;
     if (ct == SS_F32) return reduce_nt<SS_F32, EPI_PLAIN>(p, plan.splits, stream);
     if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, plan.splits, stream);
-    if (epi == EPI_RANK) return reduce_nt<SS_F16, EPI_RANK>(p, plan.splits, stream);
+    if (epi == EPI_RANK) {
+      GemmParams q = p;
+      q.alpha = 1.0f;
+      q.bias = nullptr;
+      return reduce_nt<SS_F16, EPI_PLAIN>(q, plan.splits, stream);
+    }
     return reduce_nt<SS_F16, EPI_PLAIN>(p, plan.splits, stream);
   }
   if (ct == SS_F16) {

@@ -153,12 +153,27 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
       const int64_t row_base = m0 + wm * C::WM + i * 32;
       const int64_t col = n0 + wn * C::WN + j * 32 + lr;
       if constexpr (EPI == EPI_PARTIAL) {
+        // Split 0 of a rank-16 (dX) product adds dZ . A to its partial, so the
+        // reduce is a plain sum (fold_rank; same MFMA as the unsplit epilogue).
+        float16v extra = float16v{};
+        if (p.fold_rank && blockIdx.y == 0) {
+          const int64_t zr = row_base + lr;
+          const half8 zero = half8{};
+          const half8 za =
+              zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
+          half8 zb = zero;
+          if (col < p.N) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
+          }
+          extra = __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, extra, 0, 0, 0);
+        }
         if (col >= p.N) continue;
         float* part = p.part + (int64_t)blockIdx.y * p.M * p.N;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
-          if (row < p.M) part[row * p.N + col] = acc[i][j][r];
+          if (row < p.M) part[row * p.N + col] = acc[i][j][r] + extra[r];
         }
         continue;
       }
