@@ -88,12 +88,17 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
   };
+  // MFMA phases raise the wave's issue priority (s_setprio 1), so a SIMD's
+  // other wave, in its load / LDS phase, does not delay them (measured +7 % at
+  // 8192^3, neutral at the layer shapes).
   auto mfma_block = [&](const half8 (&af)[C::FM], const half8 (&bf)[C::FN]) {
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
   };
 
   constexpr int kS = C::STAGES;
@@ -129,6 +134,7 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
       asm volatile("s_barrier" ::: "memory");
     }
     const int refill_stage = (int)(kt % kS);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int idx = 0; idx < kMfma; ++idx) {
       if (idx == kMfma / 2 && more) read_frags(kt + 1, 0, fa[0], fb[0]);
@@ -142,6 +148,7 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int d = kMfma < C::kDma ? kMfma * (C::kDma / kMfma) : C::kDma; d < C::kDma; ++d)
       if (refill) dma_one(kt + kS, refill_stage, d);
@@ -194,10 +201,23 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
 // part[s][row][col]), four columns per thread.  The epilogues are those of the
 // GEMM kernel with the same rounding order; the rank-16 terms are summed in
 // fp32 in rank order.
-template <int CT, int EPI>
+// TAIL: the first p.tail_blocks workgroups run the rank-16 grad p.tail
+// (rank_grad_block, vector loads) instead, overlapping the reduce: used for
+// split-K dX products, whose dA would otherwise need a launch of its own.
+template <int CT, int EPI, bool TAIL = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits) {
+  int64_t block = blockIdx.x;
+  if constexpr (TAIL) {
+    __shared__ __attribute__((aligned(16))) unsigned char smem[kRankGradSmem];
+    if (block < p.tail_blocks) {
+      const int64_t nblocks = cdiv(p.tail.n, 64);
+      rank_grad_block<true>(p.tail, block % nblocks, block / nblocks, smem);
+      return;
+    }
+    block -= p.tail_blocks;
+  }
   const int64_t groups = cdiv(p.N, 4);
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t g = block * 256 + threadIdx.x;
   if (g >= p.M * groups) return;
   const int64_t row = g / groups;
   const int64_t c0 = (g % groups) * 4;
@@ -323,11 +343,12 @@ int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream
   }
 }
 
-template <int CT, int EPI>
+template <int CT, int EPI, bool TAIL = false>
 int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
   const int64_t threads = p.M * cdiv(p.N, 4);
-  hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI>), dim3((unsigned)cdiv(threads, 256)),
-                     dim3(256), 0, stream, p, (int)splits);
+  const int64_t blocks = cdiv(threads, 256) + (TAIL ? p.tail_blocks : 0);
+  hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI, TAIL>), dim3((unsigned)blocks), dim3(256), 0,
+                     stream, p, (int)splits);
   SS_CHECK_LAUNCH("splitk_reduce_kernel");
   return SS_OK;
 }
@@ -416,11 +437,12 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
     plan.splits = 1;
     plan.k_split = p.K;
   }
-  // The rank-16 grad tail rides only on unsplit dX products (rank-16
-  // epilogue): measured, it fills idle CUs there (down / q / o / k / v
-  // backward 6-11 us faster), but slowed the split-K launches of the long-K
-  // dX more than a launch of its own costs.
-  if (epi != EPI_RANK || plan.splits > 1) p.tail_blocks = 0;
+  // The rank-16 grad tail rides on unsplit dX products (rank-16 epilogue)
+  // after the GEMM tiles: measured, it fills idle CUs there (down / q / o / k
+  // / v backward 6-11 us faster).  On the split-K launches of the long-K dX it
+  // slowed the GEMM more than a launch of its own costs; there it leads the
+  // reduce launch instead.
+  if (epi != EPI_RANK) p.tail_blocks = 0;
   if (p.tail_blocks > 0 && p.tail_ran) *p.tail_ran = 1;
   if (plan.splits > 1) {
     p.part = reinterpret_cast<float*>(partials);
@@ -428,14 +450,18 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
     // The rank-16 update is folded into split 0's partial (the reduce then
     // only sums: its lora_A column loads dominated its load count).
     p.fold_rank = epi == EPI_RANK;
+    const int64_t tail = p.tail_blocks;
+    p.tail_blocks = 0;
     const int rc = dispatch_nt<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);
     if (rc) return rc;
+    p.tail_blocks = tail;
     if (ct == SS_F32) return reduce_nt<SS_F32, EPI_PLAIN>(p, plan.splits, stream);
     if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, plan.splits, stream);
     if (epi == EPI_RANK) {
       GemmParams q = p;
       q.alpha = 1.0f;
       q.bias = nullptr;
+      if (q.tail_blocks > 0) return reduce_nt<SS_F16, EPI_PLAIN, true>(q, plan.splits, stream);
       return reduce_nt<SS_F16, EPI_PLAIN>(q, plan.splits, stream);
     }
     return reduce_nt<SS_F16, EPI_PLAIN>(p, plan.splits, stream);
