@@ -76,6 +76,7 @@ struct GemmParams {
   float* part;      // split-K partials [splits][M][N] fp32 (EPI_PARTIAL)
   int64_t k_split;  // k elements per split (a multiple of 64)
   int fold_rank;    // EPI_PARTIAL: split 0 adds the rank-16 term lz . lb (EPI_RANK layout)
+  int pingpong;     // 8-wave NT configurations: ping-pong main loop (set by gemm_nt)
   // Optional rank-16 grad riding on the dense NT launch: tail_blocks extra
   // workgroups (unsplit launches, after the GEMM tiles) each run one block
   // of `tail` (rank_grad_block, vector loads).  tail_ran (host side) is set

@@ -155,6 +155,121 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
   }
 }
 
+// Ping-pong main loop of the 8-wave configurations (two waves per SIMD:
+// wave w and w + 4).  Run in lockstep, the two waves of a SIMD issue their
+// MFMAs, LDS reads and barrier waits at the same time, and the MFMA pipe
+// idles while both wait.  Here every wave runs the same body per stage kt,
+//   read the fragments of stage kt, issue its DMAs of stage kt - 1 + STAGES,
+//   wait for its DMAs of stage kt + 1, barrier, the 16 MFMAs of stage kt,
+//   barrier,
+// but waves 4-7 pass one extra barrier before the first stage and waves 0-3
+// one after the last.  The barrier instances then pair each MFMA phase of
+// one group with a read phase of the other: on every SIMD one wave computes
+// while the other loads.  Stage kt's buffer is read by waves 0-3 in phase 2kt
+// and by waves 4-7 in phase 2kt + 1, and refilled (stage kt + STAGES) in read
+// phases from 2kt + 2 on; each wave's wait for its DMAs of stage kt + 1
+// precedes a barrier that ends before either group reads that stage.  The
+// MFMAs of every accumulator run in the order of nt_mainloop, so the results
+// are the same bit for bit.
+template <class C>
+__device__ __forceinline__ void nt_mainloop_pp(const GemmParams& p, int64_t m0, int64_t n0,
+                                               int64_t kbeg, int64_t klen, unsigned char* smem,
+                                               NtAcc<C>& acc) {
+  static_assert(C::kWaves == 8 && C::KK == 2, "ping-pong: 8 waves, two k-steps per stage");
+  constexpr int kGroupBytes = 32 * C::BK * 2;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: scalar branches
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const bool late = wave >= 4;  // SIMD partner of wave - 4
+  const uint32_t lds0 = lds_address(smem);
+  const half_t* a_base = p.A + kbeg;
+  const half_t* b_base = p.B + kbeg;
+  uint32_t a_off[C::kDmaA];
+  uint32_t b_off[C::kDmaB];
+#pragma unroll
+  for (int j = 0; j < C::kDmaA; ++j) {
+    int row, chunk;
+    dma_source<C::BK>(wave * C::kDmaA + j, lane, row, chunk);
+    const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
+    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < C::kDmaB; ++j) {
+    int row, chunk;
+    dma_source<C::BK>(wave * C::kDmaB + j, lane, row, chunk);
+    const int64_t gr = n0 + row < p.N ? n0 + row : p.N - 1;
+    b_off[j] = (uint32_t)((gr * p.ldb + chunk * 8) * 2);
+  }
+  const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
+  const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds0 + C::kTileA + wave * C::kDmaB * 1024);
+  int frag_off[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) frag_off[kk] = frag_offset<C::BK>(lane, kk);
+
+  constexpr int kS = C::STAGES;
+  const int64_t ktiles = klen / C::BK;
+  auto issue_stage = [&](int64_t kt) {
+    if (kt >= ktiles) return;
+    const int stage = (int)(kt % kS);
+#pragma unroll
+    for (int j = 0; j < C::kDmaA; ++j)
+      dma16(a_off[j], a_base + kt * C::BK, lds_a + stage * C::kStageBytes + j * 1024);
+#pragma unroll
+    for (int j = 0; j < C::kDmaB; ++j)
+      dma16(b_off[j], b_base + kt * C::BK, lds_b + stage * C::kStageBytes + j * 1024);
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+#pragma unroll
+  for (int st = 0; st < kS; ++st) issue_stage(st);
+  if (ktiles <= 0) return;
+  wait_stages<C::kDma, kS - 1>((ktiles < kS ? ktiles : kS) - 1);
+  barrier();  // stage 0 is in LDS
+  if (late) barrier();
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    half8 fa[2][C::FM], fb[2][C::FN];
+    const unsigned char* base = smem + (kt % kS) * C::kStageBytes;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const unsigned char* sa = base + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
+      const unsigned char* sb = base + C::kTileA + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+        fa[kk][i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+        fb[kk][j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+    }
+    if (kt >= 1) issue_stage(kt - 1 + kS);
+    {
+      // Stages this wave has issued: up to min(kt + kS - 1, ktiles - 1);
+      // stage kt + 1 must have landed.
+      const int64_t last = kt + kS - 1 < ktiles - 1 ? kt + kS - 1 : ktiles - 1;
+      wait_stages<C::kDma, kS - 2>(last - (kt + 1));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the fragments are in
+    barrier();
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][j], acc[i][j], 0,
+                                                             0, 0);
+    __builtin_amdgcn_s_setprio(0);
+    barrier();
+  }
+  if (!late) barrier();
+}
+
 // LDS of a GEMM workgroup: the stage ring; for the dX epilogue (rank-16
 // update) also room for a rank-16 grad tail block.
 template <class C, int EPI>
@@ -193,7 +308,14 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
-  nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+  if constexpr (C::kWaves == 8 && C::KK == 2) {
+    if (p.pingpong)
+      nt_mainloop_pp<C>(p, m0, n0, kbeg, klen, smem, acc);
+    else
+      nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+  } else {
+    nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+  }
   nt_epilogue<C, CT, EPI>(p, m0, n0, acc);
 }
 
@@ -417,9 +539,20 @@ size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k) {
   return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
 }
 
+// SS_NT_PINGPONG=0 keeps the 8-wave configurations on the lockstep main loop
+// (A/B knob, read once per process).
+static bool pingpong_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SS_NT_PINGPONG");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* partials,
             size_t partial_bytes) {
   GemmParams p = p0;
+  p.pingpong = pingpong_enabled();
   if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return SS_ERR_UNSUPPORTED;  // K % 64
   if (!aligned16(p.A) || !aligned16(p.B) || p.lda % 8 != 0 || p.ldb % 8 != 0)
     return SS_ERR_UNSUPPORTED;
