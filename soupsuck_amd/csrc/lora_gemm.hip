@@ -42,13 +42,19 @@ __global__ __launch_bounds__(kRankMaxWaves * 64) void rank_grad_kernel(RankGradA
   rank_grad_block<VEC>(g, blockIdx.x, blockIdx.y, smem);
 }
 
-constexpr int kPrepSmem = kRankGradSmem > kRankProjSmem
-                              ? (kRankGradSmem > kDecodeSmem ? kRankGradSmem : kDecodeSmem)
-                              : (kRankProjSmem > kDecodeSmem ? kRankProjSmem : kDecodeSmem);
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int kPrepSmem = cmax(cmax(kRankGradSmem, kRankProjSmem), cmax(kDecodeSmem, kDecodeT2Smem));
+
+// The wide transposed decode tile (64 n x 128 k) applies to cols % 128 == 0
+// and 16-byte aligned codes.
+static bool wide_t(const Nf4View& w, int64_t cols) {
+  return cols % 128 == 0 && reinterpret_cast<uintptr_t>(w.packed) % 16 == 0;
+}
 
 // Blocks [0, proj_blocks): project (mblocks x splits, block-major); then
 // grad blocks; then decode blocks (row-major decode: grid-stride over
-// dec_blocks; transposed decode: one 64x64 tile each).
+// dec_blocks; transposed decode: one 64 x 128 tile each, 64 x 64 when the
+// columns are not a multiple of 128).
 template <bool VP, bool VG>
 __global__ __launch_bounds__(256) void qlora_prep_kernel(PrepJobs pj) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[kPrepSmem];
@@ -70,6 +76,9 @@ __global__ __launch_bounds__(256) void qlora_prep_kernel(PrepJobs pj) {
     decode_vec_block<true>(reinterpret_cast<const uint32_t*>(w.packed), w.qabs, nullptr,
                            w.absmax2, w.code2, w.offset, reinterpret_cast<half8*>(pj.dec_out),
                            pj.dec_rows * pj.dec_cols / 8, b, pj.dec_blocks, smem);
+  } else if (pj.dec_cols % 128 == 0 && reinterpret_cast<uintptr_t>(w.packed) % 16 == 0) {
+    decode_t2_block(w.packed, w.qabs, w.absmax2, w.code2, w.offset, pj.dec_out, pj.dec_rows,
+                    pj.dec_cols, b, smem);
   } else {
     decode_t_block(w.packed, w.qabs, w.absmax2, w.code2, w.offset, pj.dec_out, pj.dec_rows,
                    pj.dec_cols, b, smem);
@@ -131,7 +140,8 @@ int launch_prep(PrepJobs& pj, bool vp, bool vg, hipStream_t stream) {
     pj.dec_blocks = cdiv(groups, 256) < cap ? cdiv(groups, 256) : cap;
     dec = pj.dec_blocks;
   } else if (pj.dec_kind == kDecodeTransposed) {
-    pj.dec_blocks = cdiv(pj.dec_rows, 64) * (pj.dec_cols / 64);
+    pj.dec_blocks = cdiv(pj.dec_rows, 64) *
+                    (wide_t(pj.dec_w, pj.dec_cols) ? pj.dec_cols / 128 : pj.dec_cols / 64);
     dec = pj.dec_blocks;
   }
   const int64_t blocks = pj.proj_blocks + pj.grad_blocks + dec;

@@ -44,17 +44,22 @@ __global__ __launch_bounds__(256) void nf4_dequant_scalar_kernel(
 
 // Transposed decode: out[k][n] = Wdec[n][k] for W [rows, cols] with cols % 64
 // == 0, so that the backward GEMM dX = dY . W reads W^T with k contiguous.
-// One 256-thread workgroup per 64 x 64 tile: thread (part = tid / 64,
-// row = tid % 64) decodes 16 consecutive columns of one weight row (one
-// 64-block run, one scale) and writes them transposed into LDS, where the 64
-// lanes of a wave touch 64 consecutive halves; the tile then leaves as
-// 16-byte row stores of W^T.
+// One 256-thread workgroup per 64 x 64 tile (WIDE: 64 x 128 tiles, 32
+// columns per thread from one 16-byte code load, decode_t2_block): thread
+// (part = tid / 64, row = tid % 64) decodes consecutive columns of one weight
+// row (one scale) and writes them transposed into LDS, where the 64 lanes of a
+// wave touch 64 consecutive halves; the tile then leaves as 16-byte row
+// stores of W^T.
+template <bool WIDE>
 __global__ __launch_bounds__(256) void nf4_dequant_t_kernel(
     const uint8_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ absmax2, const float* __restrict__ code2,
     const float* __restrict__ offset_ptr, half_t* __restrict__ out, int64_t rows, int64_t cols) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[kDecodeSmem];
-  decode_t_block(packed, qabs, absmax2, code2, offset_ptr, out, rows, cols, blockIdx.x, smem);
+  __shared__ __attribute__((aligned(16))) unsigned char smem[WIDE ? kDecodeT2Smem : kDecodeSmem];
+  if constexpr (WIDE)
+    decode_t2_block(packed, qabs, absmax2, code2, offset_ptr, out, rows, cols, blockIdx.x, smem);
+  else
+    decode_t_block(packed, qabs, absmax2, code2, offset_ptr, out, rows, cols, blockIdx.x, smem);
 }
 
 static int grid_for(int64_t work, int threads) {
@@ -118,10 +123,12 @@ extern "C" int ss_nf4_dequant_nested_t(const uint8_t* packed, const uint8_t* qab
     ss::set_error("%s: needs cols %% 64 == 0, 8-byte aligned packed and 16-byte aligned out", fn);
     return SS_ERR_UNSUPPORTED;
   }
-  const int64_t tiles = ss::cdiv(rows, 64) * (cols / 64);
-  hipLaunchKernelGGL(ss::nf4_dequant_t_kernel, dim3((unsigned)tiles), dim3(256), 0,
-                     (hipStream_t)stream, packed, qabs, absmax2, code2, offset,
-                     reinterpret_cast<ss::half_t*>(out), rows, cols);
+  // 64 x 128 tiles (16-byte code loads) when the columns allow, else 64 x 64.
+  const bool wide = cols % 128 == 0 && reinterpret_cast<uintptr_t>(packed) % 16 == 0;
+  const int64_t tiles = ss::cdiv(rows, 64) * (wide ? cols / 128 : cols / 64);
+  hipLaunchKernelGGL(wide ? ss::nf4_dequant_t_kernel<true> : ss::nf4_dequant_t_kernel<false>,
+                     dim3((unsigned)tiles), dim3(256), 0, (hipStream_t)stream, packed, qabs,
+                     absmax2, code2, offset, reinterpret_cast<ss::half_t*>(out), rows, cols);
   SS_CHECK_LAUNCH("nf4_dequant_t_kernel");
   return SS_OK;
 }
