@@ -452,6 +452,32 @@ def other_configs(torch, _lib):
         us, tokens * row_bytes + rows * row_bytes + 4 * rows, copies)
     del padded, packed_rows
 
+    # The MLP activation between the configs[1] gate/up and down projections:
+    # SwiGLU forward (g, u in, a out: 6 B per element) and backward (g, u, da
+    # in, dg, du out: 10 B) on [T, 8960] fp16, T = the configs[1] token count.
+    t, inter = sum(lengths_config1()), 8960
+    per = t * inter * 2
+    copies = max(1, -(-300_000_000 // (5 * per)))
+    planes = [[torch.randn((t, inter), device=dev, generator=gen).half() for _ in range(5)]
+              for _ in range(copies)]
+    mat = (f16, inter, 1)
+
+    def swiglu_fwd(i, stream):
+        g, u, _, a, _ = planes[i % copies]
+        _lib.call("ss_swiglu_fwd", g.data_ptr(), *mat, u.data_ptr(), *mat, a.data_ptr(), *mat, t,
+                  inter, stream)
+
+    def swiglu_bwd(i, stream):
+        g, u, da, dg, du = planes[i % copies]
+        _lib.call("ss_swiglu_bwd", g.data_ptr(), *mat, u.data_ptr(), *mat, da.data_ptr(), *mat,
+                  dg.data_ptr(), *mat, du.data_ptr(), *mat, t, inter, stream)
+
+    out[f"mlp_swiglu_fwd_T{t}x{inter}"] = hbm_point(graph_us(torch, _lib, swiglu_fwd, 32),
+                                                    3 * per, copies)
+    out[f"mlp_swiglu_bwd_T{t}x{inter}"] = hbm_point(graph_us(torch, _lib, swiglu_bwd, 32),
+                                                    5 * per, copies)
+    del planes
+
     # chunked fused linear CE, hidden [826, 1536], tied head [151936, 1536].
     t, v = 826, 151936
     hidden = torch.randn((t, h), device=dev, generator=gen).half()

@@ -242,6 +242,24 @@ int ss_lora_epilogue_fwd(const void* base, int base_dtype, const void* adapter, 
 int ss_lora_epilogue_bwd(const void* grad, int grad_dtype, void* d_adapter, int adapter_dtype,
                          int64_t count, float scale, void* stream);
 
+/* ------------------------------------------------------------ SwiGLU ---
+ * Qwen2 MLP activation on rows x cols matrices with independent row/column
+ * strides (elements) and dtypes (SS_F16 / SS_F32), fp32 arithmetic:
+ * p = 1/(1+exp(-g)), act = g*p; forward out = act*u; backward
+ * dgate = (grad*u)*(p + act*(1-p)), dup = grad*act.  Empty extents are a
+ * no-op.  Replace swiglu_tile_engine (solution/kernels/swiglu_fused.py:20-46)
+ * as called by swiglu_fused_forward (:52-64) and swiglu_fused_backward
+ * (:67-78). */
+int ss_swiglu_fwd(const void* gate, int gate_dtype, int64_t g_rs, int64_t g_cs, const void* up,
+                  int up_dtype, int64_t u_rs, int64_t u_cs, void* out, int out_dtype, int64_t o_rs,
+                  int64_t o_cs, int64_t rows, int64_t cols, void* stream);
+
+int ss_swiglu_bwd(const void* gate, int gate_dtype, int64_t g_rs, int64_t g_cs, const void* up,
+                  int up_dtype, int64_t u_rs, int64_t u_cs, const void* grad, int grad_dtype,
+                  int64_t d_rs, int64_t d_cs, void* dgate, int dgate_dtype, int64_t dg_rs,
+                  int64_t dg_cs, void* dup, int dup_dtype, int64_t du_rs, int64_t du_cs,
+                  int64_t rows, int64_t cols, void* stream);
+
 /* ------------------------------------------------- add + RMSNorm (A13/14) ---
  * Row-wise over [rows, h] contiguous.  s = cast_s(r + d), rstd[row] =
  * rsqrt(mean(s^2) + eps), y = cast_y(w * cast_s(s * rstd)); s_dtype must be
