@@ -22,8 +22,11 @@ roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
 other_configs = configs[0] (gate dequant GB/s, GEMM T=1024 TFLOP/s), configs[2]
-             (add-RMSNorm fwd/bwd/bwd+dgamma and unpad gather/scatter GB/s) and
-             configs[3] (fused chunked CE fwd+bwd ms and TFLOP/s)
+             (add-RMSNorm fwd/bwd/bwd+dgamma and unpad gather/scatter GB/s),
+             configs[3] (fused chunked CE fwd+bwd ms and TFLOP/s), and the
+             configs[1] layer's MLP activation: SwiGLU fwd/bwd GB/s and the frozen
+             NF4 MLP fwd+bwd with the SwiGLU in the GEMM epilogues or as its own
+             kernels
 sweep_configs4 = configs[4]: NF4 forward and dX at the Qwen2.5-7B projection
              shapes, T in {1, 16, 128, 2048, 16384}, each point timed from HBM
              (GB/s, TFLOP/s, fraction of its HBM or MFMA roofline)
@@ -477,6 +480,38 @@ def other_configs(torch, _lib):
     out[f"mlp_swiglu_bwd_T{t}x{inter}"] = hbm_point(graph_us(torch, _lib, swiglu_bwd, 32),
                                                     5 * per, copies)
     del planes
+
+    # The frozen NF4 MLP of the configs[1] layer (gate/up 8960x1536, down
+    # 1536x8960) forward + input-gradient backward at the same T, with the
+    # SwiGLU in the GEMM epilogues and as its own kernels between plain GEMMs
+    # (soupsuck_amd.mlp, the second is its default).  Weights stay resident
+    # (as in the layer step); flops 7 x 2 T H I.
+    from soupsuck_amd import mlp as fmlp
+
+    parts = []
+    for n_, k_ in ((inter, h), (inter, h), (h, inter)):
+        wq = (torch.randn((n_, k_), device=dev, generator=gen) * 0.02).half()
+        pk, stq = quantize_4bit(wq)
+        parts.append((pk, stq, n_, k_))
+        del wq
+    xm = torch.randn((t, h), device=dev, generator=gen).half()
+    gm = torch.randn((t, h), device=dev, generator=gen).half()
+
+    def mlp_epilogue(i, stream):
+        _, gate, up = fmlp.mlp_forward_2d(xm, parts, keep=True, fuse=True)
+        fmlp.mlp_backward_2d(gm, parts, gate, up, fuse=True)
+
+    def mlp_kernels(i, stream):
+        _, gate, up = fmlp.mlp_forward_2d(xm, parts, keep=True, fuse=False)
+        fmlp.mlp_backward_2d(gm, parts, gate, up, fuse=False)
+
+    flops = fmlp.mlp_flops(t, h, inter)
+    for name, fn in (("in_epilogue", mlp_epilogue), ("own_kernels", mlp_kernels)):
+        us = graph_us(torch, _lib, fn, 8)
+        out[f"mlp_fwd_bwd_T{t}_swiglu_{name}"] = {
+            "us": round(us, 2), "TFLOP/s": round(flops / us / 1e6, 1), "bound": "mfma",
+            "roofline_frac": round(flops / us / 1e6 / PEAK_FP16_TFLOPS, 4)}
+    del parts, xm, gm
 
     # chunked fused linear CE, hidden [826, 1536], tied head [151936, 1536].
     t, v = 826, 151936

@@ -242,6 +242,30 @@ int ss_lora_epilogue_fwd(const void* base, int base_dtype, const void* adapter, 
 int ss_lora_epilogue_bwd(const void* grad, int grad_dtype, void* d_adapter, int adapter_dtype,
                          int64_t count, float scale, void* stream);
 
+/* ---------------------------------------------- NF4 GEMM + SwiGLU (MLP) ---
+ * Forward: up = fp16(X . W_up^T) (W_up the NF4 weight [n, k], X [t, k]),
+ * act = fp16(silu(gate) * up) with gate [t, n] fp16; `up` may be NULL (not
+ * kept, e.g. recomputed in backward).  Backward: dact = fp16(dY . W_down)
+ * (W_down [n, k], dY [t, n]), then dgate = fp16((dact up) slope(gate)),
+ * dup = fp16(dact silu(gate)) over [t, k].  The activation is applied in the
+ * GEMM epilogue where the chosen kernel supports it, else by the SwiGLU
+ * kernel in place; results are bit-identical to ss_nf4_gemm_fwd / _dx
+ * followed by ss_swiglu_fwd / _bwd.  Workspace as ss_nf4_gemm_workspace_size.
+ * Replace the projection + swiglu_fused_forward / swiglu_fused_backward pairs
+ * of the frozen MLP node (solution/mlp.py:500-576). */
+int ss_nf4_gemm_fwd_swiglu(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                           const uint8_t* qabs, const float* absmax2, const float* code2,
+                           const float* offset, int64_t n, int64_t k, const uint16_t* gate,
+                           int64_t ldgate, uint16_t* up, int64_t ldup, uint16_t* act,
+                           int64_t ldact, void* workspace, size_t workspace_bytes, void* stream);
+
+int ss_nf4_gemm_dx_swiglu(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                          const uint8_t* qabs, const float* absmax2, const float* code2,
+                          const float* offset, int64_t n, int64_t k, const uint16_t* gate,
+                          int64_t ldgate, const uint16_t* up, int64_t ldup, uint16_t* dgate,
+                          int64_t lddgate, uint16_t* dup, int64_t lddup, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------ SwiGLU ---
  * Qwen2 MLP activation on rows x cols matrices with independent row/column
  * strides (elements) and dtypes (SS_F16 / SS_F32), fp32 arithmetic:

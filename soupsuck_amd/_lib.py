@@ -70,6 +70,13 @@ SIGNATURES = {
     "ss_lora_epilogue_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _f32, _int,
                              _c_void_p],
     "ss_lora_epilogue_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _f32, _c_void_p],
+    "ss_nf4_gemm_fwd_swiglu": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p,
+                                                                           _i64, _c_void_p, _i64,
+                                                                           _c_void_p, _i64,
+                                                                           _c_void_p, _size,
+                                                                           _c_void_p],
+    "ss_nf4_gemm_dx_swiglu": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64]
+                             + [_c_void_p, _i64] * 4 + [_c_void_p, _size, _c_void_p],
     "ss_swiglu_fwd": ([_c_void_p, _int, _i64, _i64] * 3) + [_i64, _i64, _c_void_p],
     "ss_swiglu_bwd": ([_c_void_p, _int, _i64, _i64] * 5) + [_i64, _i64, _c_void_p],
     "ss_add_rmsnorm_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _c_void_p,

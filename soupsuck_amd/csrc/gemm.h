@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.h"
+#include "swiglu.h"
 
 namespace ss {
 
@@ -24,7 +25,11 @@ struct Nf4View {
 // EPI_PARTIAL (split-K, dense NT kernel only): the raw fp32 accumulator of
 // split blockIdx.y is stored to part[split][M][N]; a reduce kernel sums the
 // splits in order and applies the requested epilogue.
-enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2, EPI_PARTIAL = 3 };
+// EPI_GLU (dense NT, fused NF4, split-K reduce): the plain value passed
+// through glu_apply; entry points request it with EPI_PLAIN and p.glu set, the
+// launchers pick the EPI_GLU instantiation (the plain kernels carry no
+// activation code, which would cost the 256x256 tiles registers).
+enum Epilogue { EPI_PLAIN = 0, EPI_LORA = 1, EPI_RANK = 2, EPI_PARTIAL = 3, EPI_GLU = 4 };
 
 // Arguments of one rank-16 product; splits / cps from the host plan,
 // part / counters inside a zero-filled rank workspace (rank16.h, lora_gemm.hip).
@@ -84,6 +89,22 @@ struct GemmParams {
   RankGradArgs tail;
   int64_t tail_blocks;
   int* tail_ran;
+  // Gated (SwiGLU) store of an fp16, beta = 0 output (glu_apply): glu = 1
+  // forward, the product is `up` -- act = silu(gate) up goes to glu_out and
+  // up to C when glu_store_c; glu = 2 backward, the product is dact -- dgate
+  // to C, dup to glu_out.  Applied by the EPI_GLU instantiations of the dense
+  // NT and fused NF4 kernels and of the split-K reduce, whose host launchers
+  // set *glu_done; other kernels store C unchanged and leave the activation
+  // to the caller.
+  int glu;
+  int glu_store_c;
+  const half_t* glu_gate;
+  int64_t ldgate;
+  const half_t* glu_up;
+  int64_t ldup;
+  half_t* glu_out;
+  int64_t ldglu;
+  int* glu_done;
 };
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
@@ -159,6 +180,26 @@ __device__ __forceinline__ void store_c(void* C, int64_t idx, float v, int beta)
     float* c = reinterpret_cast<float*>(C);
     if (beta) v += c[idx];
     c[idx] = v;
+  }
+}
+
+// Gated store of output element (row, col) with value v = alpha acc + bias
+// and the element's gate g (and, backward, up u) already loaded: v is
+// rounded to fp16 first (the product as the unfused path stores it), then the
+// activation of swiglu.hip is applied to that fp16 value.  Callers load the
+// gate / up values of a whole fragment before its first store: a load placed
+// after a store through another pointer of the struct cannot be moved above
+// it, and one memory round trip per element serialises the epilogue.
+__device__ __forceinline__ void glu_apply(const GemmParams& p, int64_t row, int64_t col,
+                                          int64_t idx, float v, half_t g, half_t u) {
+  const half_t h = f32_to_f16(v);
+  const SwigluTerms t = swiglu_terms((float)g);
+  if (p.glu == 1) {
+    if (p.glu_store_c) reinterpret_cast<half_t*>(p.C)[idx] = h;
+    p.glu_out[row * p.ldglu + col] = f32_to_f16(t.act * (float)h);
+  } else {
+    reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(((float)h * (float)u) * swiglu_slope(t));
+    p.glu_out[row * p.ldglu + col] = f32_to_f16((float)h * t.act);
   }
 }
 

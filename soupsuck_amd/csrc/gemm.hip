@@ -26,6 +26,7 @@
 #include <stdlib.h>
 
 #include "gemm.h"
+#include "soupsuck_amd.h"
 #include "rank16.h"
 
 namespace ss {
@@ -817,6 +818,78 @@ extern "C" int ss_nf4_gemm_dx(const uint16_t* dy, int64_t lddy, int64_t t, const
   GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx,
                            accumulate);
   return run_dx<EPI_PLAIN>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// The MLP's SwiGLU riding on the GEMM that produces its last operand.  The
+// dense NT and fused NF4 epilogues (and the split-K reduce) apply it as they
+// store (glu_apply); a path whose kernel stores plainly (streaming / skinny
+// small-T kernels, the generic loader) leaves its output where the
+// activation kernel then reads and overwrites it in place.  Either way the
+// result is bit-identical to the product followed by ss_swiglu_fwd/bwd.
+extern "C" int ss_nf4_gemm_fwd_swiglu(const uint16_t* x, int64_t ldx, int64_t t,
+                                      const uint8_t* packed, const uint8_t* qabs,
+                                      const float* absmax2, const float* code2,
+                                      const float* offset, int64_t n, int64_t k,
+                                      const uint16_t* gate, int64_t ldgate, uint16_t* up,
+                                      int64_t ldup, uint16_t* act, int64_t ldact, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  const char* fn = "ss_nf4_gemm_fwd_swiglu";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(x && gate && act, "%s: null pointer", fn);
+  SS_CHECK_ARG(ldx >= k && ldgate >= n && ldact >= n && (!up || ldup >= n),
+               "%s: leading dimensions too small", fn);
+  uint16_t* c = up ? up : act;
+  const int64_t ldc = up ? ldup : ldact;
+  GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, nullptr, c,
+                            ldc);
+  int done = 0;
+  p.glu = 1;
+  p.glu_store_c = up != nullptr;
+  p.glu_gate = reinterpret_cast<const half_t*>(gate);
+  p.ldgate = ldgate;
+  p.glu_out = reinterpret_cast<half_t*>(act);
+  p.ldglu = ldact;
+  p.glu_done = &done;
+  rc = run_fwd<EPI_PLAIN>(p, workspace, workspace_bytes, (hipStream_t)stream);
+  if (rc || done) return rc;
+  return ss_swiglu_fwd(gate, SS_F16, ldgate, 1, c, SS_F16, ldc, 1, act, SS_F16, ldact, 1, t, n,
+                       stream);
+}
+
+extern "C" int ss_nf4_gemm_dx_swiglu(const uint16_t* dy, int64_t lddy, int64_t t,
+                                     const uint8_t* packed, const uint8_t* qabs,
+                                     const float* absmax2, const float* code2,
+                                     const float* offset, int64_t n, int64_t k,
+                                     const uint16_t* gate, int64_t ldgate, const uint16_t* up,
+                                     int64_t ldup, uint16_t* dgate, int64_t lddgate,
+                                     uint16_t* dup, int64_t lddup, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  const char* fn = "ss_nf4_gemm_dx_swiglu";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(dy && gate && up && dgate && dup, "%s: null pointer", fn);
+  SS_CHECK_ARG(lddy >= n && ldgate >= k && ldup >= k && lddgate >= k && lddup >= k,
+               "%s: leading dimensions too small", fn);
+  GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dgate,
+                           lddgate, 0);
+  int done = 0;
+  p.glu = 2;
+  p.glu_gate = reinterpret_cast<const half_t*>(gate);
+  p.ldgate = ldgate;
+  p.glu_up = reinterpret_cast<const half_t*>(up);
+  p.ldup = ldup;
+  p.glu_out = reinterpret_cast<half_t*>(dup);
+  p.ldglu = lddup;
+  p.glu_done = &done;
+  rc = run_dx<EPI_PLAIN>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
+  if (rc || done) return rc;
+  return ss_swiglu_bwd(gate, SS_F16, ldgate, 1, up, SS_F16, ldup, 1, dgate, SS_F16, lddgate, 1,
+                       dgate, SS_F16, lddgate, 1, dup, SS_F16, lddup, 1, t, k, stream);
 }
 
 extern "C" int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,

@@ -414,6 +414,11 @@ int gemm_nf4_fwd(const GemmParams& p0, int epi, hipStream_t stream, void* partia
     return splitk_reduce(p, (int)plan.splits, SS_F16, epi, stream);
   }
   if (epi == EPI_LORA) return dispatch_nf4<SS_F16, EPI_LORA>(p, plan.cfg, 1, stream);
+  if (p.glu) {
+    const int rc = dispatch_nf4<SS_F16, EPI_GLU>(p, plan.cfg, 1, stream);
+    if (rc == SS_OK && p.glu_done) *p.glu_done = 1;
+    return rc;
+  }
   return dispatch_nf4<SS_F16, EPI_PLAIN>(p, plan.cfg, 1, stream);
 }
 

@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
   // columns) loads where aligned; the products are summed in rank order as in
   // the GEMM epilogue.
   float z[16];
-  if constexpr (EPI != EPI_PLAIN) {
+  if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
     const half_t* zr = p.lz + row * 16;
     if (reinterpret_cast<uintptr_t>(p.lz) % 16 == 0) {
       const half8 z0 = *reinterpret_cast<const half8*>(zr);
@@ -391,6 +391,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           a4[r][e] = c0 + e < p.N ? (float)p.lb[r * p.ldlb + c0 + e] : 0.0f;
+    }
+  }
+  half_t gg[4], uu[4];  // EPI_GLU: gate / up of the four columns, loaded before any store
+  if constexpr (EPI == EPI_GLU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool in = c0 + e < p.N;
+      gg[e] = in ? p.glu_gate[row * p.ldgate + c0 + e] : (half_t)0;
+      uu[e] = in && p.glu == 2 ? p.glu_up[row * p.ldup + c0 + e] : (half_t)0;
     }
   }
 #pragma unroll
@@ -427,7 +436,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
       store_c<CT>(p.C, idx, v[e] + l, p.beta);
     } else {
       const float b = p.bias ? (float)p.bias[col] : 0.0f;
-      store_c<CT>(p.C, idx, v[e] * p.alpha + b, p.beta);
+      if constexpr (EPI == EPI_GLU)
+        glu_apply(p, row, col, idx, v[e] * p.alpha + b, gg[e], uu[e]);
+      else
+        store_c<CT>(p.C, idx, v[e] * p.alpha + b, p.beta);
     }
   }
 }
@@ -448,6 +460,7 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
                   (unsigned)splits);
   hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
   SS_CHECK_LAUNCH("gemm_nt_kernel");
+  if (EPI == EPI_GLU && p.glu_done) *p.glu_done = 1;
   return SS_OK;
 }
 
@@ -472,6 +485,7 @@ int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
   hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI, TAIL>), dim3((unsigned)blocks), dim3(256), 0,
                      stream, p, (int)splits);
   SS_CHECK_LAUNCH("splitk_reduce_kernel");
+  if (EPI == EPI_GLU && p.glu_done) *p.glu_done = 1;
   return SS_OK;
 }
 
@@ -530,6 +544,7 @@ int splitk_reduce(const GemmParams& p, int splits, int ct, int epi, hipStream_t 
   }
   if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, splits, stream);
   if (epi == EPI_RANK) return reduce_nt<SS_F16, EPI_RANK>(p, splits, stream);
+  if (p.glu) return reduce_nt<SS_F16, EPI_GLU>(p, splits, stream);
   return reduce_nt<SS_F16, EPI_PLAIN>(p, splits, stream);
 }
 
@@ -597,11 +612,13 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
       if (q.tail_blocks > 0) return reduce_nt<SS_F16, EPI_PLAIN, true>(q, plan.splits, stream);
       return reduce_nt<SS_F16, EPI_PLAIN>(q, plan.splits, stream);
     }
+    if (p.glu) return reduce_nt<SS_F16, EPI_GLU>(p, plan.splits, stream);
     return reduce_nt<SS_F16, EPI_PLAIN>(p, plan.splits, stream);
   }
   if (ct == SS_F16) {
     if (epi == EPI_LORA) return dispatch_nt<SS_F16, EPI_LORA>(p, plan.cfg, 1, stream);
     if (epi == EPI_RANK) return dispatch_nt<SS_F16, EPI_RANK>(p, plan.cfg, 1, stream);
+    if (p.glu) return dispatch_nt<SS_F16, EPI_GLU>(p, plan.cfg, 1, stream);
     return dispatch_nt<SS_F16, EPI_PLAIN>(p, plan.cfg, 1, stream);
   }
   return dispatch_nt<SS_F32, EPI_PLAIN>(p, plan.cfg, 1, stream);

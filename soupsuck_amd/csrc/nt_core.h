@@ -135,11 +135,52 @@ __device__ __forceinline__ void tile_origin(const GemmParams& p, int64_t tile, i
   n0 = (in_group / group_m) * C::BN;
 }
 
+// EPI_GLU epilogue: the gate (and up) values of each 32x32 block are loaded
+// before the block's first store.
+template <class C>
+__device__ __forceinline__ void nt_glu_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
+                                                const NtAcc<C>& acc) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int64_t row_base = m0 + wm * C::WM + i * 32;
+      const int64_t col = n0 + wn * C::WN + j * 32 + lr;
+      if (col >= p.N) continue;
+      half_t g[16], u[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const bool in = row < p.M;
+        g[r] = in ? p.glu_gate[row * p.ldgate + col] : (half_t)0;
+        u[r] = in && p.glu == 2 ? p.glu_up[row * p.ldup + col] : (half_t)0;
+      }
+      const float b = p.bias ? (float)p.bias[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (row >= p.M) continue;
+        glu_apply(p, row, col, row * p.ldc + col, acc[i][j][r] * p.alpha + b, g[r], u[r]);
+      }
+    }
+  }
+}
+
 // Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
 // 4][lane % 32] of each 32x32 block in register r.
 template <class C, int CT, int EPI>
 __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
                                             const NtAcc<C>& acc) {
+  if constexpr (EPI == EPI_GLU) {
+    nt_glu_epilogue<C>(p, m0, n0, acc);
+    return;
+  }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int wm = wave / C::kWavesN;
@@ -178,7 +219,7 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
         continue;
       }
       float16v extra = float16v{};
-      if constexpr (EPI != EPI_PLAIN) {
+      if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
         // Rank-16 term of this block on one v_mfma_f32_32x32x16_f16:
         // A = Z rows (row lane%32, ranks 8 (lane/32)..+7), B = (rank, column).
         const int64_t zr = row_base + lr;

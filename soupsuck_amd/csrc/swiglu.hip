@@ -24,6 +24,7 @@
 
 #include "common.h"
 #include "elementwise.h"
+#include "swiglu.h"
 
 namespace ss {
 namespace {
@@ -31,23 +32,12 @@ namespace {
 constexpr int kCols = 256;       // columns per workgroup tile
 constexpr int kRows = 16;        // rows per workgroup tile
 constexpr int kChunk = 8;        // elements per vector access
-constexpr float kLog2e = 1.4426950408889634f;
 
 struct Mat {
   void* p;
   int dt;
   int64_t rs, cs;
 };
-
-struct Terms {
-  float p, act;
-};
-
-__device__ __forceinline__ Terms gate_terms(float g) {
-  const float e = __builtin_amdgcn_exp2f(g * -kLog2e);
-  const float p = __builtin_amdgcn_rcpf(1.0f + e);
-  return {p, g * p};
-}
 
 __device__ __forceinline__ void load8(const Mat& m, int64_t off, float (&v)[kChunk]) {
   if (m.dt == SS_F16) {
@@ -110,9 +100,9 @@ __global__ __launch_bounds__(256) void swiglu_vec_kernel(Mat g, Mat u, Mat da, M
     float a[kChunk], b[kChunk];
 #pragma unroll
     for (int e = 0; e < kChunk; ++e) {
-      const Terms t = gate_terms(gv[k][e]);
+      const SwigluTerms t = swiglu_terms(gv[k][e]);
       if (BWD) {
-        const float slope = t.p + t.act * (1.0f - t.p);
+        const float slope = swiglu_slope(t);
         a[e] = (dv[k][e] * uv[k][e]) * slope;
         b[e] = dv[k][e] * t.act;
       } else {
@@ -133,11 +123,11 @@ __global__ __launch_bounds__(256) void swiglu_any_kernel(Mat g, Mat u, Mat da, M
   for (int k = 0; k < kRows; ++k) {
     const int64_t r = blockIdx.x * (int64_t)kRows + k;
     if (r >= rows) break;
-    const Terms t = gate_terms(ld_elem(g.p, g.dt, r * g.rs + c * g.cs));
+    const SwigluTerms t = swiglu_terms(ld_elem(g.p, g.dt, r * g.rs + c * g.cs));
     const float uu = ld_elem(u.p, u.dt, r * u.rs + c * u.cs);
     if (BWD) {
       const float d = ld_elem(da.p, da.dt, r * da.rs + c * da.cs);
-      const float slope = t.p + t.act * (1.0f - t.p);
+      const float slope = swiglu_slope(t);
       st_elem(o0.p, o0.dt, r * o0.rs + c * o0.cs, (d * uu) * slope);
       st_elem(o1.p, o1.dt, r * o1.rs + c * o1.cs, d * t.act);
     } else {

@@ -1,0 +1,240 @@
+"""Frozen Qwen2 MLP on NF4 projections with the SwiGLU fused into the GEMMs.
+
+Mirrors the reference's solution/mlp.py:500-612 (``_FrozenMLP``,
+``fused_qwen2_mlp``, ``patch_qwen2_mlp_fused``): down(silu(gate(x)) * up(x))
+for frozen bias-free NF4 Linear4bit projections, as one autograd node that
+keeps gate and up (fp16) for the backward, or only x with ``recompute=True``
+(gate and up are recomputed in the backward).  Kernels per direction:
+
+  forward   gate = X Wg^T                         ss_nf4_gemm_fwd
+            up, act = X Wu^T, silu(gate) * up     ss_nf4_gemm_fwd + ss_swiglu_fwd
+                                                  (or ss_nf4_gemm_fwd_swiglu)
+            out = act Wd^T                        ss_nf4_gemm_fwd
+  backward  dgate, dup from dact = dY Wd          ss_nf4_gemm_dx + ss_swiglu_bwd
+                                                  (or ss_nf4_gemm_dx_swiglu)
+            dX = dgate Wg + dup Wu                ss_nf4_gemm_dx (twice, the
+                                                  second accumulating in fp32)
+
+The activation in the GEMM epilogue (the ``*_swiglu`` entry points,
+SS_MLP_GLU_EPILOGUE=1) gives bit-identical results; it is off by default
+because it measured slower (see ``_epilogue_fusion``).
+
+Numerics follow the reference's node (bnb fp16 projections, the fp32 SwiGLU
+tile engine of solution/kernels/swiglu_fused.py): every projection output is
+rounded to fp16 before the activation reads it.  One difference: the two
+input-gradient products are summed as fp16(fp16(dgate Wg) + fp32(dup Wu))
+instead of two fp16 results added in fp16 (one rounding fewer).  The
+reference's pinned-host offload pools (solution/mlp.py:105-359) are a memory
+policy outside this path; ``offload`` is accepted and ignored.
+"""
+
+import importlib
+import os
+from functools import wraps
+from types import ModuleType
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _lib
+from .kernels.nf4 import _validate_state
+from .kernels.nf4_gemm import nf4_dx_2d, nf4_forward_2d
+from .kernels.swiglu import swiglu_fused_backward, swiglu_fused_forward
+from .utils import enabled
+
+_MARKER = "_solution_fused_original"
+
+
+def _nf4(module):
+    """(packed, state, n, k) of a frozen bias-free NF4 Linear4bit, else None."""
+    weight = getattr(module, "weight", None)
+    state = getattr(weight, "quant_state", None)
+    if state is None or getattr(module, "bias", None) is not None:
+        return None
+    if weight.requires_grad or module._forward_hooks or module._forward_pre_hooks:
+        return None
+    packed = weight.data if isinstance(weight, torch.nn.Parameter) else weight
+    try:
+        n, k = _validate_state(packed, state, torch.float16)
+    except ValueError:
+        return None
+    if k % 64 or packed.data_ptr() % 16:
+        return None
+    return packed, state, n, k
+
+
+def _projections(mlp):
+    parts = [_nf4(getattr(mlp, name, None)) for name in ("gate_proj", "up_proj", "down_proj")]
+    return None if any(p is None for p in parts) else parts
+
+
+def _eligible(mlp, x):
+    if not isinstance(x, torch.Tensor) or not x.is_cuda or x.dtype not in (torch.float16,
+                                                                          torch.float32):
+        return False
+    act = getattr(getattr(mlp, "config", None), "hidden_act", "silu")
+    if act != "silu":
+        return False
+    parts = _projections(mlp)
+    if parts is None:
+        return False
+    (_, _, ng, kg), (_, _, nu, ku), (_, _, nd, kd) = parts
+    return (kg == ku == nd == x.shape[-1] and ng == nu == kd
+            and all(p[0].device == x.device for p in parts))
+
+
+def _workspace(t, n, k, device):
+    size = _lib.load().ss_nf4_gemm_workspace_size(t, n, k)
+    ws = torch.empty(max(size, 1), dtype=torch.uint8, device=device) if size else None
+    return ws, size
+
+
+def _state_args(packed, state):
+    return (packed.data_ptr(), state.absmax.data_ptr(), state.state2.absmax.data_ptr(),
+            state.state2.code.data_ptr(), state.offset.data_ptr())
+
+
+def _epilogue_fusion():
+    """SS_MLP_GLU_EPILOGUE=1 applies the SwiGLU in the GEMM epilogues; the
+    default runs it as its own HBM-bound kernels (measured faster at the
+    configs[1] shapes: the epilogue's 2-byte gate / up accesses are latency
+    bound once every tile reaches its epilogue together)."""
+    return os.environ.get("SS_MLP_GLU_EPILOGUE", "0") == "1"
+
+
+def gate_up_swiglu(x2d, gate_proj, up_proj, keep=True, fuse=None):
+    """(gate, up, act) for x2d [T, H] fp16; gate/up are None unless ``keep``."""
+    packed_g, state_g, n, k = gate_proj
+    packed_u, state_u, _, _ = up_proj
+    t = x2d.shape[0]
+    gate = nf4_forward_2d(x2d, packed_g, state_g, n, k)
+    if not (_epilogue_fusion() if fuse is None else fuse):
+        up = nf4_forward_2d(x2d, packed_u, state_u, n, k)
+        act = swiglu_fused_forward(gate, up)
+        return (gate if keep else None), (up if keep else None), act
+    act = torch.empty((t, n), device=x2d.device, dtype=torch.float16)
+    up = torch.empty_like(act) if keep else None
+    if t:
+        ws, size = _workspace(t, n, k, x2d.device)
+        _lib.call("ss_nf4_gemm_fwd_swiglu", x2d.data_ptr(), x2d.stride(0), t,
+                  *_state_args(packed_u, state_u), n, k, gate.data_ptr(), gate.stride(0),
+                  _lib.ptr(up), n, act.data_ptr(), n, _lib.ptr(ws), size,
+                  _lib.stream(x2d.device))
+    return (gate if keep else None), up, act
+
+
+def down_dx_swiglu(dy2d, down_proj, gate, up, fuse=None):
+    """(dgate, dup) from dact = dy2d . Wd, fp16 [T, I]."""
+    packed, state, n, k = down_proj
+    t = dy2d.shape[0]
+    if not (_epilogue_fusion() if fuse is None else fuse):
+        return swiglu_fused_backward(gate, up, nf4_dx_2d(dy2d, packed, state, n, k))
+    dgate = torch.empty((t, k), device=dy2d.device, dtype=torch.float16)
+    dup = torch.empty_like(dgate)
+    if t:
+        ws, size = _workspace(t, n, k, dy2d.device)
+        _lib.call("ss_nf4_gemm_dx_swiglu", dy2d.data_ptr(), dy2d.stride(0), t,
+                  *_state_args(packed, state), n, k, gate.data_ptr(), gate.stride(0),
+                  up.data_ptr(), up.stride(0), dgate.data_ptr(), k, dup.data_ptr(), k,
+                  _lib.ptr(ws), size, _lib.stream(dy2d.device))
+    return dgate, dup
+
+
+def mlp_forward_2d(x2d, parts, keep=True, fuse=None):
+    """(out, gate, up) of the MLP on x2d [T, H] fp16 contiguous."""
+    gate_p, up_p, down_p = parts
+    gate, up, act = gate_up_swiglu(x2d, gate_p, up_p, keep, fuse)
+    packed, state, n, k = down_p
+    out = nf4_forward_2d(act, packed, state, n, k)
+    return out, gate, up
+
+
+def mlp_backward_2d(grad2d, parts, gate, up, fuse=None):
+    """dX [T, H] fp16 of the MLP given the saved (or recomputed) gate and up."""
+    gate_p, up_p, down_p = parts
+    dgate, dup = down_dx_swiglu(grad2d, down_p, gate, up, fuse)
+    dx = nf4_dx_2d(dgate, gate_p[0], gate_p[1], gate_p[2], gate_p[3])
+    nf4_dx_2d(dup, up_p[0], up_p[1], up_p[2], up_p[3], out=dx, accumulate=True)
+    return dx
+
+
+class _FrozenMLP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, mlp, recompute):
+        parts = _projections(mlp)
+        shape = x.shape
+        x2d = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+        out, gate, up = mlp_forward_2d(x2d, parts, keep=not recompute)
+        ctx.mlp, ctx.recompute, ctx.input_dtype, ctx.shape = mlp, recompute, x.dtype, shape
+        if recompute:
+            ctx.save_for_backward(x2d)
+        else:
+            ctx.save_for_backward(gate, up)
+        return out.reshape(*shape[:-1], out.shape[-1]).to(x.dtype)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad):
+        parts = _projections(ctx.mlp)
+        if parts is None:
+            raise RuntimeError("MLP projections changed between forward and backward")
+        grad2d = grad.reshape(-1, grad.shape[-1]).to(torch.float16).contiguous()
+        if ctx.recompute:
+            (x2d,) = ctx.saved_tensors
+            gate = nf4_forward_2d(x2d, *parts[0])
+            up = nf4_forward_2d(x2d, *parts[1])
+        else:
+            gate, up = ctx.saved_tensors
+        dx = mlp_backward_2d(grad2d, parts, gate, up)
+        return dx.reshape(ctx.shape).to(ctx.input_dtype), None, None
+
+
+def fused_qwen2_mlp(mlp, x, recompute=None, offload=None):
+    """Run an eligible frozen NF4 MLP; raise ValueError otherwise (solution/mlp.py:579-594)."""
+    del offload  # pinned-host offload is a memory policy outside this path
+    if not _eligible(mlp, x):
+        raise ValueError("Expected frozen bias-free fp16 NF4 Linear4bit projections on CUDA")
+    if recompute is None:
+        recompute = os.environ.get("SOUP_MLP_RECOMPUTE") == "1"
+    with torch.cuda.device(x.device):
+        if not torch.is_grad_enabled() or not x.requires_grad:
+            shape = x.shape
+            x2d = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
+            out, _, _ = mlp_forward_2d(x2d, _projections(mlp), keep=False)
+            return out.reshape(*shape[:-1], out.shape[-1]).to(x.dtype)
+        return _FrozenMLP.apply(x, mlp, bool(recompute))
+
+
+def patch_qwen2_mlp_fused(module=None):
+    """Route Qwen2MLP.forward through fused_qwen2_mlp for eligible modules (idempotent)."""
+    try:
+        module = module or importlib.import_module("transformers.models.qwen2.modeling_qwen2")
+    except (ImportError, AttributeError):
+        return False
+    if not isinstance(module, ModuleType):
+        return False
+    cls = getattr(module, "Qwen2MLP", None)
+    if not isinstance(cls, type) or not issubclass(cls, torch.nn.Module):
+        return False
+    original = cls.forward
+    if hasattr(original, _MARKER):
+        return True
+
+    @wraps(original)
+    def forward(self, x):
+        if not enabled() or type(self) is not cls or not _eligible(self, x):
+            return original(self, x)
+        return fused_qwen2_mlp(self, x)
+
+    setattr(forward, _MARKER, original)
+    cls.forward = forward
+    return True
+
+
+def mlp_flops(t, hidden, inter):
+    """Forward + backward (dX only) flops of the frozen MLP: 3 + 4 products of 2 t h i."""
+    return 7 * 2 * t * hidden * inter
+
+
+__all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "gate_up_swiglu", "down_dx_swiglu",
+           "mlp_forward_2d", "mlp_backward_2d", "mlp_flops"]

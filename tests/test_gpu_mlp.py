@@ -1,0 +1,143 @@
+"""GPU parity of the frozen NF4 MLP with the SwiGLU in the GEMM epilogues.
+
+* ss_nf4_gemm_fwd_swiglu / ss_nf4_gemm_dx_swiglu equal, bit for bit, the
+  unfused composition (ss_nf4_gemm_fwd or _dx, then ss_swiglu_fwd or _bwd,
+  both pinned against the oracles in their own tests) at T values that take
+  each GEMM path: streaming (T <= 32), skinny (33-128), fused NF4 (129-256),
+  decode-first + dense NT (larger T), at the configs[1] shapes
+  (gate/up 8960 x 1536, down 1536 x 8960).
+* fused_qwen2_mlp against the eager fp32 module on the decoded weights, with
+  the reference's tolerance (solution/tests/test_mlp.py:12, 63-89): outputs
+  and input gradients within rtol = atol = 2e-3, relative L2 error of dX
+  <= 1e-2, for fp16 and fp32 inputs, with and without recompute.
+"""
+
+import pytest
+import torch
+
+from soupsuck_amd import _lib
+from soupsuck_amd.bnb_compat import Linear4bit, dequantize_4bit, quantize_4bit
+from soupsuck_amd.kernels.nf4_gemm import nf4_dx_2d, nf4_forward_2d
+from soupsuck_amd.kernels.swiglu import swiglu_fused_backward, swiglu_fused_forward
+from soupsuck_amd.mlp import down_dx_swiglu, fused_qwen2_mlp, gate_up_swiglu, patch_qwen2_mlp_fused
+
+pytestmark = pytest.mark.gpu
+
+HIDDEN, INTER = 1536, 8960
+
+
+def _weight(n, k, seed, device):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    w = (torch.randn((n, k), device=device, generator=gen) * 0.02).half()
+    packed, state = quantize_4bit(w)
+    return packed, state, n, k
+
+
+@pytest.fixture(scope="module")
+def weights(device):
+    return {"gate": _weight(INTER, HIDDEN, 1, device), "up": _weight(INTER, HIDDEN, 2, device),
+            "down": _weight(HIDDEN, INTER, 3, device)}
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("t", [1, 16, 100, 200, 990, 2048])
+def test_forward_swiglu_bitwise_equals_gemm_then_swiglu(device, weights, t):
+    print(f"case fwd_swiglu T={t}", flush=True)
+    gen = torch.Generator(device=device).manual_seed(t)
+    x = torch.randn((t, HIDDEN), device=device, generator=gen).half()
+    gate, up, act = gate_up_swiglu(x, weights["gate"], weights["up"], keep=True, fuse=True)
+    up_ref = nf4_forward_2d(x, *weights["up"])
+    act_ref = swiglu_fused_forward(gate, up_ref)
+    assert torch.equal(_bits(up), _bits(up_ref))
+    assert torch.equal(_bits(act), _bits(act_ref))
+    _, none_up, act2 = gate_up_swiglu(x, weights["gate"], weights["up"], keep=False,
+                                      fuse=True)
+    assert none_up is None and torch.equal(_bits(act2), _bits(act_ref))
+
+
+@pytest.mark.parametrize("t", [1, 16, 100, 200, 990, 2048])
+def test_dx_swiglu_bitwise_equals_dx_then_swiglu(device, weights, t):
+    print(f"case dx_swiglu T={t}", flush=True)
+    gen = torch.Generator(device=device).manual_seed(100 + t)
+    dy = torch.randn((t, HIDDEN), device=device, generator=gen).half()
+    gate = (torch.randn((t, INTER), device=device, generator=gen) * 3).half()
+    up = torch.randn((t, INTER), device=device, generator=gen).half()
+    dgate, dup = down_dx_swiglu(dy, weights["down"], gate, up, fuse=True)
+    dact = nf4_dx_2d(dy, *weights["down"])
+    dg_ref, du_ref = swiglu_fused_backward(gate, up, dact)
+    assert torch.equal(_bits(dgate), _bits(dg_ref))
+    assert torch.equal(_bits(dup), _bits(du_ref))
+
+
+class _MLP(torch.nn.Module):
+    def __init__(self, hidden, inter):
+        super().__init__()
+        self.config = type("Cfg", (), {"hidden_act": "silu"})()
+        self.gate_proj = Linear4bit(hidden, inter, bias=False, compute_dtype=torch.float16)
+        self.up_proj = Linear4bit(hidden, inter, bias=False, compute_dtype=torch.float16)
+        self.down_proj = Linear4bit(inter, hidden, bias=False, compute_dtype=torch.float16)
+
+
+def _dense(proj):
+    st = proj.weight.quant_state
+    return dequantize_4bit(proj.weight.data, st).float()
+
+
+@pytest.mark.parametrize("epilogue", ["0", "1"])
+@pytest.mark.parametrize("recompute", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(2, 5, 128), (3, 77, 128)])
+def test_fused_mlp_matches_fp32_module(device, monkeypatch, epilogue, recompute, dtype, shape):
+    print(f"case mlp epilogue={epilogue} recompute={recompute} dtype={dtype} shape={shape}",
+          flush=True)
+    monkeypatch.setenv("SS_MLP_GLU_EPILOGUE", epilogue)
+    torch.manual_seed(777)
+    mlp = _MLP(128, 320).to(device)
+    x = torch.randn(shape, device=device, dtype=dtype, requires_grad=True)
+    out = fused_qwen2_mlp(mlp, x, recompute)
+    assert out.dtype == dtype and out.shape == shape
+    wg, wu, wd = (_dense(p) for p in (mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+    rx = x.detach().float().requires_grad_()
+    ref = torch.nn.functional.linear(
+        torch.nn.functional.silu(rx @ wg.t()) * (rx @ wu.t()), wd)
+    torch.testing.assert_close(out.float(), ref, rtol=2e-3, atol=2e-3)
+    upstream = torch.randn_like(out)
+    out.backward(upstream)
+    ref.backward(upstream.float())
+    assert x.grad.dtype == dtype
+    torch.testing.assert_close(x.grad.float(), rx.grad, rtol=2e-3, atol=2e-3)
+    rel = (x.grad.float() - rx.grad).norm() / rx.grad.norm()
+    assert rel.item() <= 1e-2
+
+
+def test_rejects_ineligible_modules(device):
+    mlp = _MLP(128, 320).to(device)
+    mlp.down_proj = torch.nn.Linear(320, 128, bias=False).to(device).half()
+    x = torch.randn((2, 128), device=device, dtype=torch.float16)
+    with pytest.raises(ValueError):
+        fused_qwen2_mlp(mlp, x)
+
+
+def test_patched_qwen2_mlp_routes_through_the_fused_node(device):
+    modeling = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
+    config = modeling.Qwen2Config(hidden_size=128, intermediate_size=320, hidden_act="silu")
+    layer = modeling.Qwen2MLP(config)
+    for name, (i, o) in {"gate_proj": (128, 320), "up_proj": (128, 320),
+                         "down_proj": (320, 128)}.items():
+        setattr(layer, name, Linear4bit(i, o, bias=False, compute_dtype=torch.float16))
+    layer = layer.to(device)
+    x = torch.randn((2, 9, 128), device=device, dtype=torch.float16, requires_grad=True)
+    original = modeling.Qwen2MLP.forward
+    expected = original(layer, x)
+    assert patch_qwen2_mlp_fused(modeling)
+    try:
+        assert modeling.Qwen2MLP.forward is not original
+        actual = layer(x)
+        assert actual.grad_fn is not None and "FrozenMLP" in type(actual.grad_fn).__name__
+    finally:
+        modeling.Qwen2MLP.forward = original
+    torch.testing.assert_close(actual, expected, rtol=2e-3, atol=2e-3)
+    assert _lib.load() is not None
