@@ -98,6 +98,7 @@ struct GemmParams {
   // to the caller.
   int glu;
   int glu_store_c;
+  int glu_vec;  // N, ldc / ldgate / ldup / ldglu and the pointers 16-byte granular
   const half_t* glu_gate;
   int64_t ldgate;
   const half_t* glu_up;

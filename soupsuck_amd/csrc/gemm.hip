@@ -852,6 +852,8 @@ extern "C" int ss_nf4_gemm_fwd_swiglu(const uint16_t* x, int64_t ldx, int64_t t,
   p.ldgate = ldgate;
   p.glu_out = reinterpret_cast<half_t*>(act);
   p.ldglu = ldact;
+  p.glu_vec = n % 8 == 0 && aligned16(c, ldc) && aligned16(gate, ldgate) &&
+              aligned16(act, ldact);
   p.glu_done = &done;
   rc = run_fwd<EPI_PLAIN>(p, workspace, workspace_bytes, (hipStream_t)stream);
   if (rc || done) return rc;
@@ -885,6 +887,8 @@ extern "C" int ss_nf4_gemm_dx_swiglu(const uint16_t* dy, int64_t lddy, int64_t t
   p.ldup = ldup;
   p.glu_out = reinterpret_cast<half_t*>(dup);
   p.ldglu = lddup;
+  p.glu_vec = k % 8 == 0 && aligned16(dgate, lddgate) && aligned16(gate, ldgate) &&
+              aligned16(up, ldup) && aligned16(dup, lddup);
   p.glu_done = &done;
   rc = run_dx<EPI_PLAIN>(p, n, k, workspace, workspace_bytes, (hipStream_t)stream);
   if (rc || done) return rc;

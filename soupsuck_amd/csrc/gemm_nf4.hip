@@ -306,7 +306,8 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmPara
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
   nf4_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
-  nt_epilogue<C, CT, EPI>(p, m0, n0, acc);
+  static_assert(EPI != EPI_GLU || GluStage<C>::kBytes <= Nf4Layout<C>::kSmem, "GLU stage");
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
 }
 
 // Configurations (same tiles, waves and stage depth as the dense kernel's

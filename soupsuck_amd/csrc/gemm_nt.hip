@@ -316,7 +316,8 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
   } else {
     nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
   }
-  nt_epilogue<C, CT, EPI>(p, m0, n0, acc);
+  static_assert(EPI != EPI_GLU || GluStage<C>::kBytes <= nt_smem_bytes<C, EPI>(), "GLU stage");
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
 }
 
 // Split-K reduction: out[row][col] = epilogue(sum over splits s = 0.. of

@@ -172,12 +172,118 @@ __device__ __forceinline__ void nt_glu_epilogue(const GemmParams& p, int64_t m0,
   }
 }
 
+// EPI_GLU epilogue through LDS, with 16-byte gate / up / output accesses.
+// For each wave row group q in turn, the waves of that group write their
+// values h = fp16(alpha acc + bias) into an LDS tile [WM][BN + 8]; then every
+// thread of the workgroup takes 8-column chunks of it (kGluBatch at a time:
+// gate / up / staged chunks first, then the activation and the stores).
+// Needs N, the leading dimensions and the base pointers 16-byte granular
+// (p.glu_vec) and the whole workgroup (it synchronises); the stage ring is
+// drained and free once the main loop has returned.
+template <class C>
+struct GluStage {
+  static constexpr int kPitch = C::BN + 8;  // halves per staged row (bank spread)
+  static constexpr int kChunksRow = C::BN / 8;
+  static constexpr int kPer = C::WM * kChunksRow / C::kThreads;
+  static constexpr int kBatch = kPer < 4 ? kPer : 4;
+  static constexpr int kBytes = C::WM * kPitch * 2;
+  static constexpr bool kOk = C::WM * kChunksRow % C::kThreads == 0 && kPer >= 1 && kPer <= 8 &&
+                              kPer % kBatch == 0;
+};
+
+template <class C>
+__device__ __forceinline__ void nt_glu_epilogue_lds(const GemmParams& p, int64_t m0, int64_t n0,
+                                                    const NtAcc<C>& acc, unsigned char* smem) {
+  using G = GluStage<C>;
+  half_t* stage = reinterpret_cast<half_t*>(smem);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+  wait_vm<0>();
+  __syncthreads();
+#pragma unroll 1
+  for (int q = 0; q < C::BM / C::WM; ++q) {
+    if (wm == q) {
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) {
+          const int col_l = wn * C::WN + j * 32 + lr;
+          const int64_t col = n0 + col_l;
+          const float b = p.bias && col < p.N ? (float)p.bias[col] : 0.0f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row_l = i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            stage[row_l * G::kPitch + col_l] = f32_to_f16(acc[i][j][r] * p.alpha + b);
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int k0 = 0; k0 < G::kPer; k0 += G::kBatch) {
+      half8 h[G::kBatch], g[G::kBatch], u[G::kBatch];
+      int64_t row[G::kBatch], col[G::kBatch];
+      bool in[G::kBatch];
+#pragma unroll
+      for (int k = 0; k < G::kBatch; ++k) {
+        const int c = tid + (k0 + k) * C::kThreads;
+        const int row_l = c / G::kChunksRow;
+        const int c8 = (c % G::kChunksRow) * 8;
+        row[k] = m0 + q * C::WM + row_l;
+        col[k] = n0 + c8;
+        in[k] = row[k] < p.M && col[k] < p.N;
+        h[k] = *reinterpret_cast<const half8*>(stage + row_l * G::kPitch + c8);
+        g[k] = in[k] ? *reinterpret_cast<const half8*>(p.glu_gate + row[k] * p.ldgate + col[k])
+                     : half8{};
+        u[k] = in[k] && p.glu == 2
+                   ? *reinterpret_cast<const half8*>(p.glu_up + row[k] * p.ldup + col[k])
+                   : half8{};
+      }
+#pragma unroll
+      for (int k = 0; k < G::kBatch; ++k) {
+        if (!in[k]) continue;
+        half8 o0, o1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const SwigluTerms t = swiglu_terms((float)g[k][e]);
+          const float v = (float)h[k][e];
+          if (p.glu == 1) {
+            o1[e] = f32_to_f16(t.act * v);
+          } else {
+            o0[e] = f32_to_f16((v * (float)u[k][e]) * swiglu_slope(t));
+            o1[e] = f32_to_f16(v * t.act);
+          }
+        }
+        half_t* c_out = reinterpret_cast<half_t*>(p.C) + row[k] * p.ldc + col[k];
+        if (p.glu == 2)
+          *reinterpret_cast<half8*>(c_out) = o0;
+        else if (p.glu_store_c)
+          *reinterpret_cast<half8*>(c_out) = h[k];
+        *reinterpret_cast<half8*>(p.glu_out + row[k] * p.ldglu + col[k]) = o1;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
 // 4][lane % 32] of each 32x32 block in register r.
+// `smem` (EPI_GLU only): the kernel's LDS, at least GluStage<C>::kBytes.
 template <class C, int CT, int EPI>
 __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
-                                            const NtAcc<C>& acc) {
+                                            const NtAcc<C>& acc, unsigned char* smem = nullptr) {
   if constexpr (EPI == EPI_GLU) {
+    if constexpr (GluStage<C>::kOk) {
+      if (p.glu_vec) {
+        nt_glu_epilogue_lds<C>(p, m0, n0, acc, smem);
+        return;
+      }
+    }
     nt_glu_epilogue<C>(p, m0, n0, acc);
     return;
   }
