@@ -99,6 +99,9 @@ struct GemmParams {
   int glu;
   int glu_store_c;
   int glu_vec;  // N, ldc / ldgate / ldup / ldglu and the pointers 16-byte granular
+  // fp16 output through the LDS-staged epilogue (16-byte stores): set by the
+  // NT / fused NF4 launchers when beta = 0 and N, ldc and C are 16-byte granular.
+  int c_vec;
   const half_t* glu_gate;
   int64_t ldgate;
   const half_t* glu_up;
@@ -239,6 +242,8 @@ __device__ __forceinline__ void epilogue_f16(const GemmParams& p, int64_t row, i
 // nt_partial_bytes(M, N, K) bytes.
 int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream, void* partials = nullptr,
             size_t partial_bytes = 0);
+// LDS-staged fp16 epilogue switch of the NT and fused NF4 launchers (default on).
+bool staged_epilogue_enabled();
 // fp32 split-K scratch that gemm_nt uses for an M x N x K product (0: no split).
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
 // Tile configuration (1..8 in gemm_nt.hip's list) and split-K plan of an

@@ -306,7 +306,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmPara
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
   nf4_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
-  static_assert(EPI != EPI_GLU || GluStage<C>::kBytes <= Nf4Layout<C>::kSmem, "GLU stage");
+  static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= Nf4Layout<C>::kSmem, "stage");
   nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
 }
 
@@ -400,6 +400,8 @@ int gemm_nf4_fwd(const GemmParams& p0, int epi, hipStream_t stream, void* partia
                  size_t partial_bytes) {
   if (!gemm_nf4_fwd_ok(p0, epi)) return SS_ERR_UNSUPPORTED;
   GemmParams p = p0;
+  p.c_vec = staged_epilogue_enabled() && !p.beta && p.N % 8 == 0 && p.ldc % 8 == 0 &&
+            reinterpret_cast<uintptr_t>(p.C) % 16 == 0;
   NtPlan plan = nf4_plan(p.M, p.N, p.K);
   const size_t need = (size_t)(plan.splits * p.M * p.N) * sizeof(float);
   if (plan.splits > 1 && (!partials || partial_bytes < need ||

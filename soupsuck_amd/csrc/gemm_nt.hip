@@ -316,7 +316,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
   } else {
     nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
   }
-  static_assert(EPI != EPI_GLU || GluStage<C>::kBytes <= nt_smem_bytes<C, EPI>(), "GLU stage");
+  static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= nt_smem_bytes<C, EPI>(), "stage");
   nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
 }
 
@@ -565,10 +565,22 @@ static bool pingpong_enabled() {
   return on;
 }
 
+// SS_NT_STAGED=0 keeps fp16 epilogues on direct 2-byte stores (A/B knob,
+// read once per process).
+bool staged_epilogue_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("SS_NT_STAGED");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* partials,
             size_t partial_bytes) {
   GemmParams p = p0;
   p.pingpong = pingpong_enabled();
+  p.c_vec = staged_epilogue_enabled() && ct == SS_F16 && !p.beta && p.N % 8 == 0 &&
+            p.ldc % 8 == 0 && aligned16(p.C);
   if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return SS_ERR_UNSUPPORTED;  // K % 64
   if (!aligned16(p.A) || !aligned16(p.B) || p.lda % 8 != 0 || p.ldb % 8 != 0)
     return SS_ERR_UNSUPPORTED;

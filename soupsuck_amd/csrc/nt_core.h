@@ -273,7 +273,97 @@ __device__ __forceinline__ void nt_glu_epilogue_lds(const GemmParams& p, int64_t
 
 // Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
 // 4][lane % 32] of each 32x32 block in register r.
-// `smem` (EPI_GLU only): the kernel's LDS, at least GluStage<C>::kBytes.
+// Rank-16 term of one 32x32 block on one v_mfma_f32_32x32x16_f16 (EPI_LORA /
+// EPI_RANK): A = Z rows (row lane % 32, ranks 8 (lane / 32) .. + 7), B =
+// (rank, column).
+template <int EPI>
+__device__ __forceinline__ float16v rank16_block(const GemmParams& p, int64_t row_base,
+                                                 int64_t col, int lr, int lh) {
+  const int64_t zr = row_base + lr;
+  const half8 zero = half8{};
+  const half8 za = zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
+  half8 zb = zero;
+  if (col < p.N) {
+    if constexpr (EPI == EPI_LORA) {
+      zb = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
+    }
+  }
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, float16v{}, 0, 0, 0);
+}
+
+// fp16 epilogue (plain / LoRA / rank-16, beta = 0) with the tile staged
+// through LDS: per wave row group, the waves write their rounded outputs
+// (the values and rounding order of nt_epilogue's direct stores) into
+// [WM][BN + 8], then the workgroup stores them as 16-byte row chunks -- one
+// store instruction per 1 KiB instead of per 128 B.  Needs N, ldc and C
+// 16-byte granular (p.c_vec) and the whole workgroup.
+template <class C, int EPI>
+__device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t m0, int64_t n0,
+                                                   const NtAcc<C>& acc, unsigned char* smem) {
+  using G = GluStage<C>;
+  half_t* stage = reinterpret_cast<half_t*>(smem);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const int lr = lane & 31;
+  const int lh = lane >> 5;
+  wait_vm<0>();
+  __syncthreads();
+#pragma unroll 1
+  for (int q = 0; q < C::BM / C::WM; ++q) {
+    if (wm == q) {
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) {
+          const int64_t row_base = m0 + wm * C::WM + i * 32;
+          const int col_l = wn * C::WN + j * 32 + lr;
+          const int64_t col = n0 + col_l;
+          float16v extra = float16v{};
+          if constexpr (EPI == EPI_LORA || EPI == EPI_RANK)
+            extra = rank16_block<EPI>(p, row_base, col, lr, lh);
+          const float b = p.bias && col < p.N ? (float)p.bias[col] : 0.0f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row_l = i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            half_t h;
+            if constexpr (EPI == EPI_LORA) {
+              const float y = (float)f32_to_f16(acc[i][j][r] * p.alpha + b);
+              const float lora = (float)f32_to_f16(extra[r]);
+              const float scaled = (float)f32_to_f16(lora * p.lscale);
+              h = f32_to_f16(y + scaled);
+            } else if constexpr (EPI == EPI_RANK) {
+              h = f32_to_f16(acc[i][j][r] + extra[r]);
+            } else {
+              h = f32_to_f16(acc[i][j][r] * p.alpha + b);
+            }
+            stage[row_l * G::kPitch + col_l] = h;
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < G::kPer; ++k) {
+      const int c = tid + k * C::kThreads;
+      const int row_l = c / G::kChunksRow;
+      const int c8 = (c % G::kChunksRow) * 8;
+      const int64_t row = m0 + q * C::WM + row_l;
+      const int64_t col = n0 + c8;
+      if (row < p.M && col < p.N)
+        *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(p.C) + row * p.ldc + col) =
+            *reinterpret_cast<const half8*>(stage + row_l * G::kPitch + c8);
+    }
+    __syncthreads();
+  }
+}
+
+// `smem`: the kernel's LDS, at least GluStage<C>::kBytes (staged epilogues).
 template <class C, int CT, int EPI>
 __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
                                             const NtAcc<C>& acc, unsigned char* smem = nullptr) {
@@ -286,6 +376,12 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
     }
     nt_glu_epilogue<C>(p, m0, n0, acc);
     return;
+  }
+  if constexpr (CT == SS_F16 && EPI != EPI_PARTIAL && GluStage<C>::kOk) {
+    if (p.c_vec && smem) {
+      nt_epilogue_staged<C, EPI>(p, m0, n0, acc, smem);
+      return;
+    }
   }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
