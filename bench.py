@@ -71,6 +71,9 @@ def parse():
                    help="only run one configs[1] projection entry point (DIR forward or "
                         "backward, weight [N,K]) --reps times at the bench's T and exit (for "
                         "rocprofv3 counter passes that attribute every kernel to one call)")
+    p.add_argument("--profile-mlp", action="store_true",
+                   help="only run the configs[1] layer's frozen NF4 MLP forward + backward "
+                        "(SwiGLU as its own kernels) --reps times at the bench's T and exit")
     p.add_argument("--reps", type=int, default=20)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
@@ -91,6 +94,30 @@ def copy_calibration(mib):
     torch.cuda.synchronize()
     assert torch.equal(dst, src)
     print(json.dumps({"copy_calibration_bytes_per_dispatch": n, "dispatches": 10}), flush=True)
+
+
+def profile_mlp(reps):
+    """Repeat the frozen NF4 MLP step (gate/up 8960x1536, down 1536x8960) of the layer."""
+    import torch
+
+    from soupsuck_amd import mlp as fmlp
+    from soupsuck_amd.bnb_compat import quantize_4bit
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    tokens, h, inter = sum(lengths_config1()), 1536, 8960
+    parts = []
+    for n, k in ((inter, h), (inter, h), (h, inter)):
+        packed, st = quantize_4bit((torch.randn((n, k), device=dev, generator=gen) * 0.02).half())
+        parts.append((packed, st, n, k))
+    x = torch.randn((tokens, h), device=dev, generator=gen).half()
+    g = torch.randn((tokens, h), device=dev, generator=gen).half()
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        _, gate, up = fmlp.mlp_forward_2d(x, parts, keep=True)
+        fmlp.mlp_backward_2d(g, parts, gate, up)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_mlp": True, "tokens": tokens, "reps": reps}), flush=True)
 
 
 def profile_call(spec, reps):
@@ -600,6 +627,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.profile_mlp:
+        profile_mlp(args.reps)
         return
     if args.profile_call:
         profile_call(args.profile_call, args.reps)
