@@ -421,6 +421,15 @@ def other_configs(torch, _lib):
 
         us = graph_us(torch, _lib, fwd, 32)
         out[f"configs2_add_rmsnorm_fwd_T{t}"] = hbm_point(us, t * row_fwd + 2 * h, copies)
+
+        def norm_fwd(i, stream):
+            r, _, _, yy, rstd = bufs[i % copies]
+            _lib.call("ss_rmsnorm_fwd", r.data_ptr(), f16, h, wn.data_ptr(), f16, 1,
+                      yy.data_ptr(), f16, rstd.data_ptr(), t, h, 1e-6, stream)
+
+        # Standalone RMSNorm (x in, y out: 4 H B per row + rstd + w).
+        out[f"rmsnorm_fwd_T{t}"] = hbm_point(graph_us(torch, _lib, norm_fwd, 32),
+                                             t * (4 * h + 4) + 2 * h, copies)
         # Backward reuses the buffers: r -> gs, d -> gy (inputs), and writes
         # dr, dd into two fresh planes per copy.
         grads = [(torch.empty_like(b[0]), torch.empty_like(b[0])) for b in bufs]

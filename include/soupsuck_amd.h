@@ -319,6 +319,17 @@ int ss_add_rmsnorm_bwd_dgamma(const void* s, int s_dtype, const void* w, int w_d
                               int dd_dtype, int half_products, float* partial, void* dw,
                               int dw_dtype, int64_t rows, int64_t h, void* stream);
 
+/* Standalone Qwen2 RMSNorm forward (no residual): rstd = rsqrt(mean(fp32(x)^2)
+ * + eps), y = w * cast_x(fp32(x) * rstd) in promote(x, w), or rounded to fp16
+ * when y_dtype is SS_F16 (the fused output cast).  x rows have stride x_row
+ * (elements, >= h), y is contiguous [rows, h], rstd fp32[rows].  The backward
+ * is ss_add_rmsnorm_bwd / ss_add_rmsnorm_bwd_dgamma with s = x (contiguous)
+ * and no residual gradient.  Replaces rmsnorm_forward_kernel
+ * (solution/kernels/rmsnorm.py:42-53,108-125). */
+int ss_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row, const void* w, int w_dtype,
+                   int64_t w_stride, void* y, int y_dtype, float* rstd, int64_t rows, int64_t h,
+                   float eps, void* stream);
+
 /* dgamma[c] = sum_rows gy * cast_s(s*rstd) (products rounded to fp16 when
  * half_products), two-stage and non-atomic: partial fp32[ceil(rows/32), h]
  * is caller-provided scratch.  Replaces rmsnorm_weight_partials_kernel /

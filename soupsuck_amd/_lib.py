@@ -84,6 +84,8 @@ SIGNATURES = {
     "ss_add_rmsnorm_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _c_void_p, _c_void_p, _int,
                            _i64, _i64, _c_void_p, _int, _i64, _i64, _c_void_p, _int, _c_void_p,
                            _int, _i64, _i64, _c_void_p],
+    "ss_rmsnorm_fwd": [_c_void_p, _int, _i64, _c_void_p, _int, _i64, _c_void_p, _int, _c_void_p,
+                       _i64, _i64, _f32, _c_void_p],
     "ss_add_rmsnorm_dgamma_waves": [_i64],
     "ss_add_rmsnorm_bwd_dgamma": [_c_void_p, _int, _c_void_p, _int, _i64, _c_void_p, _c_void_p,
                                   _int, _i64, _i64, _c_void_p, _int, _i64, _i64, _c_void_p, _int,

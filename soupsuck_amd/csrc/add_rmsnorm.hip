@@ -80,8 +80,11 @@ __device__ __forceinline__ void store8(void* p, int dt, int64_t off, int valid, 
   }
 }
 
+// d == nullptr: the standalone RMSNorm (s = r, read with row stride r_row,
+// not stored when s == nullptr).
 struct FwdArgs {
   const void* r; int rd;
+  int64_t r_row;
   const void* d; int dd;
   const void* w; int wd; int64_t w_stride;
   void* s; int sd;
@@ -110,16 +113,21 @@ __global__ __launch_bounds__(256) void add_rmsnorm_fwd_kernel(FwdArgs a) {
     const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
     const int valid = chunk_valid(a.h, col0);
     if (valid > 0) {
-      const F8 r = load8(a.r, a.rd, base + col0, valid, a.vec);
-      const F8 d = load8(a.d, a.dd, base + col0, valid, a.vec);
+      const F8 r = load8(a.r, a.rd, row * a.r_row + col0, valid, a.vec);
+      if (a.d) {
+        const F8 d = load8(a.d, a.dd, base + col0, valid, a.vec);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[c][j] = round_to(a.sd, r.v[j] + d.v[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[c][j] = r.v[j];
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float s = round_to(a.sd, r.v[j] + d.v[j]);
-        sv[c][j] = s;
-        const float sq = s * s;
+        const float sq = sv[c][j] * sv[c][j];
         ss += sq;
       }
-      store8(a.s, a.sd, base + col0, valid, sv[c], a.vec);
+      if (a.s) store8(a.s, a.sd, base + col0, valid, sv[c], a.vec);
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j) sv[c][j] = 0.0f;
@@ -389,9 +397,40 @@ extern "C" int ss_add_rmsnorm_fwd(const void* r, int r_dtype, const void* d, int
   }
   if (rows == 0) return SS_OK;
   SS_CHECK_ARG(r && d && w && s && y && rstd, "%s: null pointer", fn);
-  FwdArgs a{r, r_dtype, d, d_dtype, w, w_dtype, w_stride, s, s_dtype, y, y_dtype, rstd, rows,
+  FwdArgs a{r, r_dtype, h, d, d_dtype, w, w_dtype, w_stride, s, s_dtype, y, y_dtype, rstd, rows,
             h, eps, 0};
   a.vec = (h % 8 == 0) && al16(r) && al16(d) && al16(s) && al16(y) && (w_stride != 1 || al16(w));
+  const int nch = (int)cdiv(h, 512);
+  const dim3 grid((unsigned)cdiv(rows, 4));
+  hipStream_t st = (hipStream_t)stream;
+  SS_ROW_KERNEL_SWITCH(add_rmsnorm_fwd_kernel, nch, a, grid, st);
+  SS_CHECK_LAUNCH("add_rmsnorm_fwd_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row, const void* w,
+                              int w_dtype, int64_t w_stride, void* y, int y_dtype, float* rstd,
+                              int64_t rows, int64_t h, float eps, void* stream) {
+  const char* fn = "ss_rmsnorm_fwd";
+  SS_CHECK_ARG(rows >= 0 && h > 0, "%s: need rows >= 0 and h > 0", fn);
+  SS_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype) && valid_dtype(y_dtype),
+               "%s: dtype must be SS_F16 or SS_F32", fn);
+  SS_CHECK_ARG(y_dtype == promote(x_dtype, w_dtype) || y_dtype == SS_F16,
+               "%s: y dtype must be promote(x, w) or fp16", fn);
+  SS_CHECK_ARG(eps >= 0.0f, "%s: eps must be >= 0", fn);
+  SS_CHECK_ARG(x_row >= h, "%s: row stride %lld < h", fn, (long long)x_row);
+  if (h > 512 * kMaxChunks) {
+    ss::set_error("%s: h=%lld exceeds the register-resident row limit %d", fn, (long long)h,
+                  512 * kMaxChunks);
+    return SS_ERR_UNSUPPORTED;
+  }
+  if (rows == 0) return SS_OK;
+  SS_CHECK_ARG(x && w && y && rstd, "%s: null pointer", fn);
+  FwdArgs a{x, x_dtype, x_row, nullptr, x_dtype, w, w_dtype, w_stride, nullptr, x_dtype, y,
+            y_dtype, rstd, rows, h, eps, 0};
+  const int64_t xs = x_dtype == SS_F16 ? 2 : 4;
+  a.vec = (h % 8 == 0) && al16(x) && (x_row * xs) % 16 == 0 && al16(y) &&
+          (w_stride != 1 || al16(w));
   const int nch = (int)cdiv(h, 512);
   const dim3 grid((unsigned)cdiv(rows, 4));
   hipStream_t st = (hipStream_t)stream;

@@ -10,8 +10,10 @@ Targets:
   * ``transformers.models.qwen2.modeling_qwen2``: ``Qwen2DecoderLayer.forward``
     fuses the attention residual add with the post-attention RMSNorm
     (reference solution/decoder.py:54-89), and ``Qwen2MLP.forward`` runs frozen
-    NF4 MLPs through ``soupsuck_amd.mlp.fused_qwen2_mlp`` with the SwiGLU in
-    the projection epilogues (reference solution/mlp.py:597-612).
+    NF4 MLPs through ``soupsuck_amd.mlp.fused_qwen2_mlp`` (reference
+    solution/mlp.py:597-612), and ``Qwen2RMSNorm.forward`` (input and final
+    norms) runs ``kernels.rmsnorm.rms_norm`` with the eager dtype semantics
+    (reference solution/kernels/rmsnorm.py:159-188).
 Every wrapper carries ``_solution_fused_original`` (the reference's marker)
 and falls back to the original when ``SOUP_FUSED_DISABLE`` is set or the
 inputs are outside the supported contract.  No GPU work happens here.
@@ -128,11 +130,43 @@ def patch_qwen2_decoder(module=None):
     return True
 
 
+def patch_qwen2_rmsnorm(module=None):
+    """Route Qwen2RMSNorm.forward through the HIP RMSNorm (same dtype semantics as eager)."""
+    try:
+        module = module or importlib.import_module(_QWEN)
+    except (ImportError, AttributeError):
+        return False
+    cls = getattr(module, "Qwen2RMSNorm", None)
+    if not isinstance(cls, type):
+        return False
+    original = cls.forward
+    if hasattr(original, _MARKER):
+        return True
+
+    @wraps(original)
+    def forward(self, hidden_states):
+        weight = getattr(self, "weight", None)
+        if (not enabled() or type(self) is not cls or not _supported(hidden_states)
+                or not _supported(weight) or weight.ndim != 1
+                or weight.shape[0] != hidden_states.shape[-1]
+                or weight.device != hidden_states.device or self._forward_hooks
+                or self._forward_pre_hooks):
+            return original(self, hidden_states)
+        from .kernels.rmsnorm import rms_norm
+
+        return rms_norm(hidden_states, weight, self.variance_epsilon)
+
+    setattr(forward, _MARKER, original)
+    cls.forward = forward
+    return True
+
+
 def _register_module(name, module):
     if name == _QWEN:
         from .mlp import patch_qwen2_mlp_fused
 
         patch_qwen2_decoder(module)
+        patch_qwen2_rmsnorm(module)
         patch_qwen2_mlp_fused(module)
     elif name == _BNB_FUNCTIONAL:
         patch_bnb_dequant(module)
