@@ -517,6 +517,34 @@ def other_configs(torch, _lib):
                                                     5 * per, copies)
     del planes
 
+    # RoPE of the configs[1] layer's attention: q 12 heads, k 2 heads, head_dim
+    # 128 at T tokens, q / k as transposed [1, T, H, D] projection views, fp16
+    # cos / sin [1, T, 128].  Bytes: q, k read and written (4 B per element)
+    # plus cos and sin once.
+    hq, hk, hd = 12, 2, 128
+    qv = torch.randn((1, t, hq * hd), device=dev, generator=gen).half()
+    kv = torch.randn((1, t, hk * hd), device=dev, generator=gen).half()
+    cs = torch.randn((2, 1, t, hd), device=dev, generator=gen).half()
+    yq = torch.empty((1, hq, t, hd), device=dev, dtype=torch.float16)
+    yk = torch.empty((1, hk, t, hd), device=dev, dtype=torch.float16)
+    qst, kst = (t * hq * hd, hd, hq * hd), (t * hk * hd, hd, hk * hd)
+    cst = (t * hd, hd, t * hd, hd, 1)
+
+    def rope_fwd(i, stream):
+        _lib.call("ss_rope_fwd", qv.data_ptr(), f16, *qst, kv.data_ptr(), f16, *kst,
+                  cs[0].data_ptr(), cs[1].data_ptr(), f16, *cst, yq.data_ptr(), f16,
+                  yk.data_ptr(), f16, 1, hq, hk, t, hd // 2, stream)
+
+    def rope_bwd(i, stream):
+        _lib.call("ss_rope_bwd", qv.data_ptr(), f16, *qst, 1, kv.data_ptr(), f16, *kst, 1,
+                  cs[0].data_ptr(), cs[1].data_ptr(), f16, *cst, yq.data_ptr(), f16,
+                  yk.data_ptr(), f16, 1, hq, hk, t, hd // 2, stream)
+
+    moved = (hq + hk) * t * hd * 4 + 2 * t * hd * 2
+    out[f"rope_fwd_T{t}"] = hbm_point(graph_us(torch, _lib, rope_fwd, 64), moved, 1)
+    out[f"rope_bwd_T{t}"] = hbm_point(graph_us(torch, _lib, rope_bwd, 64), moved, 1)
+    del qv, kv, cs, yq, yk
+
     # The frozen NF4 MLP of the configs[1] layer (gate/up 8960x1536, down
     # 1536x8960) forward + input-gradient backward at the same T, with the
     # SwiGLU in the GEMM epilogues and as its own kernels between plain GEMMs

@@ -1,0 +1,128 @@
+// Joint q/k rotary position embedding, forward and input gradients.
+//
+// Rows are (batch, head, token) with the q heads first, then the k heads; one
+// wave handles one row, its lanes over the half width (lane c holds columns
+// c and c + half, looping when half > 64).  With x1 = x[c], x2 = x[c + half]:
+//   forward   y1 = R(x1 c1) + R(-x2 s1),  y2 = R(x2 c2) + R(x1 s2)
+//             R = rounding to the output dtype promote(x, cos), sums rounded
+//             on store (solution/kernels/rope.py:24-56);
+//   backward  d1 = R'(g1 c1) + R'(g2 s2),  d2 = R'(g2 c2) - R'(g1 s1)
+//             R' = rounding to the input's dtype (:59-98).
+// fp32 arithmetic, no contraction (-ffp-contract=off), so the results equal
+// the numpy restatement bit for bit.  Inputs take runtime strides (batch,
+// head, token; the last dimension stride is given for gradients and must be
+// 1 for q / k / cos / sin); cos / sin have 1 or B batches; outputs are
+// contiguous [B, H, S, D].  HBM-bound: 2 x 2 B per fp16 element of q / k
+// plus cos / sin (shared by all heads of a token, mostly cache hits).
+
+#include "common.h"
+#include "elementwise.h"
+
+namespace ss {
+namespace {
+
+struct RopeOperand {
+  const void* x;  // q / k (forward) or its output gradient (backward); null: skip
+  int xd;
+  int64_t sb, sh, st, sd;  // element strides: batch, head, token, last dim
+  void* y;
+  int yd;
+  int64_t heads;
+};
+
+struct RopeArgs {
+  RopeOperand q, k;
+  const void* c;
+  const void* s;
+  int cd;
+  int64_t cb, ct, sb, st;  // cos / sin strides (batch, token); last stride 1
+  int64_t c_batches;
+  int64_t batches, tokens, half;
+};
+
+template <bool BWD>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t heads = a.q.heads + a.k.heads;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.batches * heads * a.tokens) return;
+  const int64_t token = row % a.tokens;
+  const int64_t head = (row / a.tokens) % heads;
+  const int64_t batch = row / (heads * a.tokens);
+  const bool is_q = head < a.q.heads;
+  const RopeOperand& o = is_q ? a.q : a.k;
+  const int64_t h = is_q ? head : head - a.q.heads;
+  if (!o.x) return;
+  const int64_t cbatch = a.c_batches == 1 ? 0 : batch;
+  const int64_t coff = cbatch * a.cb + token * a.ct;
+  const int64_t soff = cbatch * a.sb + token * a.st;
+  const int64_t xoff = batch * o.sb + h * o.sh + token * o.st;
+  const int64_t yoff = ((batch * o.heads + h) * a.tokens + token) * (2 * a.half);
+  for (int64_t c = lane; c < a.half; c += 64) {
+    const float c1 = ld_elem(a.c, a.cd, coff + c), c2 = ld_elem(a.c, a.cd, coff + c + a.half);
+    const float s1 = ld_elem(a.s, a.cd, soff + c), s2 = ld_elem(a.s, a.cd, soff + c + a.half);
+    const float x1 = ld_elem(o.x, o.xd, xoff + c * o.sd);
+    const float x2 = ld_elem(o.x, o.xd, xoff + (c + a.half) * o.sd);
+    float lo, hi;
+    if (BWD) {
+      lo = round_to(o.yd, x1 * c1) + round_to(o.yd, x2 * s2);
+      hi = round_to(o.yd, x2 * c2) - round_to(o.yd, x1 * s1);
+    } else {
+      lo = round_to(o.yd, x1 * c1) + round_to(o.yd, -x2 * s1);
+      hi = round_to(o.yd, x2 * c2) + round_to(o.yd, x1 * s2);
+    }
+    st_elem(o.y, o.yd, yoff + c, lo);
+    st_elem(o.y, o.yd, yoff + c + a.half, hi);
+  }
+}
+
+int launch_rope(bool bwd, const RopeArgs& a, void* stream, const char* fn) {
+  SS_CHECK_ARG(a.batches >= 0 && a.tokens >= 0 && a.half > 0 && a.q.heads >= 0 &&
+                   a.k.heads >= 0 && (a.c_batches == 1 || a.c_batches == a.batches),
+               "%s: bad shape", fn);
+  SS_CHECK_ARG(valid_dtype(a.cd) && (!a.q.x || (valid_dtype(a.q.xd) && valid_dtype(a.q.yd))) &&
+                   (!a.k.x || (valid_dtype(a.k.xd) && valid_dtype(a.k.yd))),
+               "%s: dtype must be SS_F16 or SS_F32", fn);
+  const int64_t rows = a.batches * (a.q.heads + a.k.heads) * a.tokens;
+  if (rows == 0) return SS_OK;
+  SS_CHECK_ARG(a.c && a.s && (!a.q.x || a.q.y) && (!a.k.x || a.k.y), "%s: null pointer", fn);
+  SS_CHECK_ARG(cdiv(rows, 4) <= 0x7fffffff, "%s: too many rows", fn);
+  auto kern = bwd ? rope_kernel<true> : rope_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, (hipStream_t)stream, a);
+  SS_CHECK_LAUNCH(fn);
+  return SS_OK;
+}
+
+}  // namespace
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" int ss_rope_fwd(const void* q, int q_dtype, int64_t qb, int64_t qh, int64_t qt,
+                           const void* k, int k_dtype, int64_t kb, int64_t kh, int64_t kt,
+                           const void* cos, const void* sin, int cs_dtype, int64_t cb, int64_t ct,
+                           int64_t sb, int64_t st, int64_t c_batches, void* yq, int yq_dtype,
+                           void* yk, int yk_dtype, int64_t batches, int64_t qheads,
+                           int64_t kheads, int64_t tokens, int64_t half, void* stream) {
+  const char* fn = "ss_rope_fwd";
+  SS_CHECK_ARG(yq_dtype == promote(q_dtype, cs_dtype) && yk_dtype == promote(k_dtype, cs_dtype),
+               "%s: outputs must be promote(x, cos)", fn);
+  RopeArgs a{{q, q_dtype, qb, qh, qt, 1, yq, yq_dtype, qheads},
+             {k, k_dtype, kb, kh, kt, 1, yk, yk_dtype, kheads},
+             cos, sin, cs_dtype, cb, ct, sb, st, c_batches, batches, tokens, half};
+  return launch_rope(false, a, stream, fn);
+}
+
+extern "C" int ss_rope_bwd(const void* gq, int gq_dtype, int64_t qb, int64_t qh, int64_t qt,
+                           int64_t qd, const void* gk, int gk_dtype, int64_t kb, int64_t kh,
+                           int64_t kt, int64_t kd, const void* cos, const void* sin,
+                           int cs_dtype, int64_t cb, int64_t ct, int64_t sb, int64_t st,
+                           int64_t c_batches, void* dq, int dq_dtype, void* dk, int dk_dtype,
+                           int64_t batches, int64_t qheads, int64_t kheads, int64_t tokens,
+                           int64_t half, void* stream) {
+  const char* fn = "ss_rope_bwd";
+  RopeArgs a{{gq, gq_dtype, qb, qh, qt, qd, dq, dq_dtype, qheads},
+             {gk, gk_dtype, kb, kh, kt, kd, dk, dk_dtype, kheads},
+             cos, sin, cs_dtype, cb, ct, sb, st, c_batches, batches, tokens, half};
+  return launch_rope(true, a, stream, fn);
+}

@@ -13,7 +13,8 @@ Targets:
     NF4 MLPs through ``soupsuck_amd.mlp.fused_qwen2_mlp`` (reference
     solution/mlp.py:597-612), and ``Qwen2RMSNorm.forward`` (input and final
     norms) runs ``kernels.rmsnorm.rms_norm`` with the eager dtype semantics
-    (reference solution/kernels/rmsnorm.py:159-188).
+    (reference solution/kernels/rmsnorm.py:159-188); ``apply_rotary_pos_emb``
+    runs ``kernels.rope.fused_rope`` (reference solution/rope.py:55-80).
 Every wrapper carries ``_solution_fused_original`` (the reference's marker)
 and falls back to the original when ``SOUP_FUSED_DISABLE`` is set or the
 inputs are outside the supported contract.  No GPU work happens here.
@@ -168,6 +169,9 @@ def _register_module(name, module):
         patch_qwen2_decoder(module)
         patch_qwen2_rmsnorm(module)
         patch_qwen2_mlp_fused(module)
+        from .kernels.rope import patch_qwen2_rope
+
+        patch_qwen2_rope(module)
     elif name == _BNB_FUNCTIONAL:
         patch_bnb_dequant(module)
 
