@@ -14,6 +14,7 @@
 // 1 for q / k / cos / sin); cos / sin have 1 or B batches; outputs are
 // contiguous [B, H, S, D].  HBM-bound: 2 x 2 B per fp16 element of q / k
 // plus cos / sin (shared by all heads of a token, mostly cache hits).
+// Aligned layouts take the vector kernel (4 columns per thread).
 
 #include "common.h"
 #include "elementwise.h"
@@ -76,6 +77,90 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
 }
 
+__device__ __forceinline__ void load4(const void* p, int dt, int64_t off, float (&v)[4]) {
+  if (dt == SS_F16) {
+    const half4 h = *reinterpret_cast<const half4*>(static_cast<const half_t*>(p) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (float)h[e];
+  } else {
+    const float4v f = *reinterpret_cast<const float4v*>(static_cast<const float*>(p) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = f[e];
+  }
+}
+
+__device__ __forceinline__ void store4(void* p, int dt, int64_t off, const float (&v)[4]) {
+  if (dt == SS_F16) {
+    half4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = f32_to_f16(v[e]);
+    *reinterpret_cast<half4*>(static_cast<half_t*>(p) + off) = h;
+  } else {
+    float4v f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = v[e];
+    *reinterpret_cast<float4v*>(static_cast<float*>(p) + off) = f;
+  }
+}
+
+// Vector form: each thread takes 4 consecutive columns of one row's half
+// width (8- or 16-byte accesses), half / 4 threads per row, rows packed
+// across the workgroup.  Needs half % 4 == 0, unit last-dimension strides,
+// every other stride a multiple of 4 and 16-byte aligned bases (vec_ok).
+template <bool BWD>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
+  const int64_t quads = a.half / 4;
+  const int64_t heads = a.q.heads + a.k.heads;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / quads;
+  if (row >= a.batches * heads * a.tokens) return;
+  const int64_t c = (gid - row * quads) * 4;
+  const int64_t token = row % a.tokens;
+  const int64_t head = (row / a.tokens) % heads;
+  const int64_t batch = row / (heads * a.tokens);
+  const bool is_q = head < a.q.heads;
+  const RopeOperand& o = is_q ? a.q : a.k;
+  const int64_t h = is_q ? head : head - a.q.heads;
+  if (!o.x) return;
+  const int64_t cbatch = a.c_batches == 1 ? 0 : batch;
+  const int64_t coff = cbatch * a.cb + token * a.ct + c;
+  const int64_t soff = cbatch * a.sb + token * a.st + c;
+  const int64_t xoff = batch * o.sb + h * o.sh + token * o.st + c;
+  const int64_t yoff = ((batch * o.heads + h) * a.tokens + token) * (2 * a.half) + c;
+  float c1[4], c2[4], s1[4], s2[4], x1[4], x2[4], lo[4], hi[4];
+  load4(o.x, o.xd, xoff, x1);
+  load4(o.x, o.xd, xoff + a.half, x2);
+  load4(a.c, a.cd, coff, c1);
+  load4(a.c, a.cd, coff + a.half, c2);
+  load4(a.s, a.cd, soff, s1);
+  load4(a.s, a.cd, soff + a.half, s2);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (BWD) {
+      lo[e] = round_to(o.yd, x1[e] * c1[e]) + round_to(o.yd, x2[e] * s2[e]);
+      hi[e] = round_to(o.yd, x2[e] * c2[e]) - round_to(o.yd, x1[e] * s1[e]);
+    } else {
+      lo[e] = round_to(o.yd, x1[e] * c1[e]) + round_to(o.yd, -x2[e] * s1[e]);
+      hi[e] = round_to(o.yd, x2[e] * c2[e]) + round_to(o.yd, x1[e] * s2[e]);
+    }
+  }
+  store4(o.y, o.yd, yoff, lo);
+  store4(o.y, o.yd, yoff + a.half, hi);
+}
+
+bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+bool vec_ok(const RopeArgs& a) {
+  if (a.half % 4 || !al16(a.c) || !al16(a.s) || a.cb % 4 || a.ct % 4 || a.sb % 4 || a.st % 4)
+    return false;
+  for (const RopeOperand* o : {&a.q, &a.k}) {
+    if (!o->x) continue;
+    if (o->sd != 1 || !al16(o->x) || !al16(o->y) || o->sb % 4 || o->sh % 4 || o->st % 4)
+      return false;
+  }
+  return true;
+}
+
 int launch_rope(bool bwd, const RopeArgs& a, void* stream, const char* fn) {
   SS_CHECK_ARG(a.batches >= 0 && a.tokens >= 0 && a.half > 0 && a.q.heads >= 0 &&
                    a.k.heads >= 0 && (a.c_batches == 1 || a.c_batches == a.batches),
@@ -87,6 +172,13 @@ int launch_rope(bool bwd, const RopeArgs& a, void* stream, const char* fn) {
   if (rows == 0) return SS_OK;
   SS_CHECK_ARG(a.c && a.s && (!a.q.x || a.q.y) && (!a.k.x || a.k.y), "%s: null pointer", fn);
   SS_CHECK_ARG(cdiv(rows, 4) <= 0x7fffffff, "%s: too many rows", fn);
+  if (vec_ok(a) && cdiv(rows * (a.half / 4), 256) <= 0x7fffffff) {
+    auto kern = bwd ? rope_vec_kernel<true> : rope_vec_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(rows * (a.half / 4), 256)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+    SS_CHECK_LAUNCH(fn);
+    return SS_OK;
+  }
   auto kern = bwd ? rope_kernel<true> : rope_kernel<false>;
   hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, (hipStream_t)stream, a);
   SS_CHECK_LAUNCH(fn);
