@@ -15,10 +15,11 @@
 // The pass is HBM-bound: 6 bytes per fp16 element forward (g, u read, a
 // written), 10 backward (g, u, da read, dg, du written), against about 15
 // VALU operations per element.  Contiguous rows take the vector kernel: a
-// workgroup (grid x: row tiles, y: column tiles) covers 16 rows x 256
-// columns, each thread two 8-element chunks of one column group in rows r
-// and r + 8 (16-byte loads and stores for fp16, two for fp32), all loads
-// issued before the arithmetic.  Anything
+// workgroup (grid x: row tiles, y: column tiles) covers 8 rows x 256
+// columns, each thread one 8-element chunk (16-byte loads and stores for
+// fp16, two for fp32), all loads issued before the arithmetic.  Measured at
+// [990, 8960] fp16: 8-row tiles 10.2 / 20.4 us (forward / backward), 16-row
+// tiles (two chunks per thread) 11.4 / 23.2 us, 32-row tiles 11.5 / 26.6 us.  Anything
 // else (column strides, unaligned rows, widths not a multiple of 8) runs the
 // element-wise kernel over the same tiles.
 
@@ -30,7 +31,7 @@ namespace ss {
 namespace {
 
 constexpr int kCols = 256;       // columns per workgroup tile
-constexpr int kRows = 16;        // rows per workgroup tile
+constexpr int kRows = 8;         // rows per workgroup tile
 constexpr int kChunk = 8;        // elements per vector access
 
 struct Mat {

@@ -98,11 +98,11 @@ def _epilogue_fusion():
     """SS_MLP_GLU_EPILOGUE=1 applies the SwiGLU in the GEMM epilogues; the
     default runs it as its own HBM-bound kernels.  Measured on MI355X at the
     configs[1] shapes (T = 990): alone, the down dX with the activation in its
-    epilogue takes 70 us against 59 + 17 us for the product and the kernel,
-    and the up forward 74.5 against 63 + 11 us; inside the whole MLP step the
-    epilogue variant measured 414 us against 401 us, so the kernels stay the
-    default (every output tile reaches its epilogue at once, so the extra
-    gate / up traffic there overlaps no MFMA work)."""
+    epilogue takes 66-70 us against 54-59 + 17 us for the product and the
+    kernel; inside the whole MLP step the epilogue variant measured 398-414 us
+    against 386-401 us in the same runs, so the kernels stay the default
+    (every output tile reaches its epilogue at once, so the extra gate / up
+    traffic there overlaps no MFMA work)."""
     return os.environ.get("SS_MLP_GLU_EPILOGUE", "0") == "1"
 
 
