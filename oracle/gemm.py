@@ -13,6 +13,11 @@ accumulation order approximates.  The acceptance gate is the reference's
 preregistered one (experiments/reports/EXP-002.md:60-76):
 assert_close(rtol=2e-3, atol=2e-3) on the fp16 output plus relative L2 <= 1e-3.
 
+Beyond EXP-002's calibrated reductions (K <= 8960), ``no_worse_than_reference``
+compares the errors of a result and of the reference's own decode-then-dense
+path against the exact-weight product (the north star's "no worse than the
+reference's own error").
+
 Pins: the float64 product is numpy's matmul (a library routine); tests plant a
 transposed operand and a dropped bias in the oracle on tiny shapes and check
 that the gate rejects them, and compare against a brute-force triple loop.
@@ -23,6 +28,7 @@ import numpy as np
 RTOL = 2e-3
 ATOL = 2e-3
 REL_L2 = 1e-3
+SLACK = 1.25     # no_worse_than_reference: allowed ratio to the reference's own error
 
 
 def linear(x, w, bias=None):
@@ -52,6 +58,31 @@ def brute_force_linear(x, w, bias=None):
                 acc += x[i, kk] * w[j, kk]
             y[i, j] = acc + (0.0 if bias is None else float(bias[j]))
     return y
+
+
+def no_worse_than_reference(actual, exact, reference, slack=SLACK):
+    """Return (ok, ratio_max, ratio_l2): is ``actual`` as close to the exact-weight
+    product as the reference's own decode-then-dense result is?
+
+    ``exact`` is the float64 product with the unrounded weight NF4 * scale
+    (oracle.nf4.decode_exact); ``reference`` is what the reference computes: the
+    product of the fp16-decoded weight with the output rounded to fp16.  Both the
+    largest element error and the relative L2 error of ``actual`` against
+    ``exact`` may exceed the reference's by at most the factor ``slack``.  This is
+    the north star's "no worse than the reference's own error", for reductions
+    longer than EXP-002 calibrated its fixed 2e-3 element tolerance on (K <= 8960):
+    there the rounding of each decoded weight alone moves the decoded-weight
+    product by more than 2e-3 (the deviation grows as sqrt(K)).
+    """
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(exact, np.float64)
+    r = np.asarray(reference, np.float64)
+    if a.shape != e.shape or not np.all(np.isfinite(a)):
+        return False, float("inf"), float("inf")
+    denom = max(np.linalg.norm(e), 1e-300)
+    ra = np.abs(a - e).max(initial=0.0) / max(np.abs(r - e).max(initial=0.0), 1e-300)
+    rl = (np.linalg.norm(a - e) / denom) / max(np.linalg.norm(r - e) / denom, 1e-300)
+    return bool(ra <= slack and rl <= slack), float(ra), float(rl)
 
 
 def gate(actual, expected, rtol=RTOL, atol=ATOL, rel_l2=REL_L2):

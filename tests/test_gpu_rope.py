@@ -101,3 +101,56 @@ def test_rejects_unsupported(device):
     cos = torch.zeros((1, 4, 7), device=device, dtype=torch.float16)
     with pytest.raises(ValueError):
         fused_rope(q, q, cos, cos)
+
+
+# The element-wise kernel (rope_kernel): taken when half = D / 2 is not a
+# multiple of 4, when the upstream gradient's last stride is not 1, or when a
+# base address is not 16-byte aligned.  Same bit-exact bar.
+def test_scalar_path_head_dim_12(device):
+    gen = torch.Generator().manual_seed(21)
+    q = _proj(2, 37, 3, 12, torch.float16, device, gen).requires_grad_()
+    k = _proj(2, 37, 1, 12, torch.float32, device, gen).requires_grad_()
+    cos, sin = _angles(2, 37, 12, device, torch.float16)
+    yq, yk = fused_rope(q, k, cos, sin)
+    cn, sn = np16(cos), np16(sin)
+    _exact(yq, orope.rope_forward(np16(q), cn, sn))
+    _exact(yk, orope.rope_forward(np16(k), cn, sn))
+    gq = torch.randn(yq.shape, generator=gen).half().to(device)
+    gk = torch.randn(yk.shape, generator=gen).float().to(device)
+    torch.autograd.backward([yq, yk], [gq, gk])
+    _exact(q.grad, orope.rope_backward(np16(gq), cn, sn, np.float16))
+    _exact(k.grad, orope.rope_backward(np16(gk), cn, sn, np.float32))
+
+
+def test_scalar_path_expanded_gradient(device):
+    gen = torch.Generator().manual_seed(22)
+    q = _proj(1, 50, 12, 128, torch.float16, device, gen).requires_grad_()
+    k = _proj(1, 50, 2, 128, torch.float16, device, gen).requires_grad_()
+    cos, sin = _angles(1, 50, 128, device, torch.float16)
+    yq, yk = fused_rope(q, k, cos, sin)
+    gq = torch.randn((1, 12, 50, 1), generator=gen).half().to(device).expand(1, 12, 50, 128)
+    gk = torch.randn((1, 2, 50, 1), generator=gen).half().to(device).expand(1, 2, 50, 128)
+    assert gq.stride(-1) == 0
+    torch.autograd.backward([yq, yk], [gq, gk])
+    cn, sn = np16(cos), np16(sin)
+    _exact(q.grad, orope.rope_backward(np16(gq), cn, sn, np.float16))
+    _exact(k.grad, orope.rope_backward(np16(gk), cn, sn, np.float16))
+
+
+def test_scalar_path_unaligned_base(device):
+    gen = torch.Generator().manual_seed(23)
+    b, s, h, d = 1, 45, 12, 128
+    buf = torch.randn(b * s * h * d + 1, generator=gen).half().to(device)
+    q = buf[1:].view(b, s, h, d).transpose(1, 2).requires_grad_()
+    assert q.data_ptr() % 16 != 0
+    k = _proj(b, s, 2, d, torch.float16, device, gen).requires_grad_()
+    cos, sin = _angles(1, s, d, device, torch.float16)
+    yq, yk = fused_rope(q, k, cos, sin)
+    cn, sn = np16(cos), np16(sin)
+    _exact(yq, orope.rope_forward(np16(q), cn, sn))
+    _exact(yk, orope.rope_forward(np16(k), cn, sn))
+    gq = torch.randn(yq.shape, generator=gen).half().to(device)
+    gk = torch.randn(yk.shape, generator=gen).half().to(device)
+    torch.autograd.backward([yq, yk], [gq, gk])
+    _exact(q.grad, orope.rope_backward(np16(gq), cn, sn, np.float16))
+    _exact(k.grad, orope.rope_backward(np16(gk), cn, sn, np.float16))

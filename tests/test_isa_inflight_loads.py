@@ -12,8 +12,12 @@ This test compiles the sources to gfx950 assembly and follows the vector
 memory counter through each kernel in program order (s_waitcnt vmcnt(N)
 retires all but the newest N operations): no VALU or LDS instruction may read
 or write a destination register of an asm-issued load that is still
-outstanding.  The scan is linear (it does not follow branches), which is exact
-for the straight-line pipelines checked here.
+outstanding.  The scan is linear in layout order: it does not follow branches
+or loop back-edges.  It is paired with a rule the kernels keep: every register
+of an asm load ring is tied after the kernel's final vmcnt(0), so a load left
+in flight on a loop exit (a skipped guarded issue, a wave without work) keeps
+its registers allocated until that wait, and the code the scan checks between
+an issue and its wait is the code that runs between them.
 """
 
 import re
@@ -75,7 +79,8 @@ def inflight_hazards(asm, name):
 
 
 @pytest.mark.parametrize("source,kernel", [("gemm_nf4.hip", "gemm_nf4_kernel"),
-                                           ("nf4_stream.hip", "nf4_stream_fwd_kernel")])
+                                           ("nf4_stream.hip", "nf4_stream_fwd_kernel"),
+                                           ("nf4_stream_dx.hip", "nf4_stream_dx_kernel")])
 def test_no_register_reuse_under_inflight_asm_loads(tmp_path, source, kernel):
     out = tmp_path / (source + ".s")
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-Xclang",

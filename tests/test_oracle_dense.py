@@ -51,6 +51,46 @@ def test_gate_rejects_planted_mistakes():
     assert not gemm.gate(-good, good)[0]                                    # wrong sign
 
 
+def test_exact_weight_decode_rounds_to_the_fp16_decode():
+    from oracle import nf4
+
+    rng = np.random.default_rng(2)
+    state = nf4.quantize_nested((rng.standard_normal((40, 640)) * 0.02).astype(np.float16))
+    exact = state.decode_exact()
+    dec = state.decode()
+    np.testing.assert_array_equal(exact.astype(np.float32).astype(np.float16).view(np.uint16),
+                                  dec.view(np.uint16))
+    half_ulp = np.spacing(np.abs(dec)).astype(np.float64) / 2
+    assert np.all(np.abs(exact - dec.astype(np.float64)) <= half_ulp * (1 + 2 ** -10))
+
+
+def test_no_worse_gate_accepts_reference_and_rejects_planted_mistakes():
+    from oracle import nf4
+
+    rng = np.random.default_rng(3)
+    state = nf4.quantize_nested((rng.standard_normal((96, 4096)) * 0.02).astype(np.float16))
+    x = rng.standard_normal((24, 4096)).astype(np.float16)
+    exact = gemm.linear(x, state.decode_exact())
+    ref = gemm.linear(x, state.decode()).astype(np.float16)
+    assert gemm.no_worse_than_reference(ref, exact, ref)[0]
+    # post-scaled blocks (sum of x * fp16(NF4) per 64-block, times the scale): one
+    # rounding per weight like the reference, so within the slack
+    n = state.n
+    nib = nf4.unpack_nibbles(state.packed, n).reshape(96, 64, 64)
+    scale = nf4.blockwise_absmax(state.qabs, state.absmax2, state.code2, state.offset,
+                                 n // 64).astype(np.float64).reshape(96, 64)
+    v16 = nf4.NF4_VALUES.astype(np.float16).astype(np.float64)[nib]
+    post = np.einsum("tbk,nbk->tnb", x.astype(np.float64).reshape(24, 64, 64), v16)
+    post = (post * scale[None]).sum(-1).astype(np.float16)
+    assert gemm.no_worse_than_reference(post, exact, ref)[0]
+    dropped = gemm.linear(x[:, 64:], state.decode_exact()[:, 64:]).astype(np.float16)
+    assert not gemm.no_worse_than_reference(dropped, exact, ref)[0]       # one block dropped
+    coarse = exact.astype(np.float16).astype(np.float32)
+    coarse = (np.round(coarse * 64) / 64).astype(np.float16)
+    assert not gemm.no_worse_than_reference(coarse, exact, ref)[0]       # 6-bit output rounding
+    assert not gemm.no_worse_than_reference(-ref, exact, ref)[0]          # wrong sign
+
+
 # ------------------------------------------------------------------ lora ---
 
 def test_epilogue_rounded_product_cancels_to_zero():
