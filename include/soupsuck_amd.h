@@ -86,6 +86,21 @@ int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* pa
                     uint16_t* y, int64_t ldy, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ss_nf4_gemm_fwd without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * result and kernels as ss_nf4_gemm_fwd (bit-identical output); its scratch is
+ * a fixed 64 MiB device array per GPU, held until the process ends.  Shapes
+ * whose forward needs more scratch than that (T >= 256 with a large weight)
+ * are rejected with SS_ERR_INVALID_ARGUMENT; every T < 256 at the Qwen2.5
+ * 1.5B/7B projection shapes fits.  Nothing is allocated and no library routine
+ * that allocates is called.  Calls that overlap in time on one GPU share the
+ * scratch and race: issue them on one stream, or serialise them. */
+int ss_nf4_gemm_fwd_noalloc(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                            const uint8_t* qabs, const float* absmax2, const float* code2,
+                            const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                            uint16_t* y, int64_t ldy, void* stream);
+
 /* A8/A9 backward.  dx[t,k] = fp16(sum_n dy[t,n] * Wdec[n,k]).  Replaces
  * MatMul4Bit.backward's dequantize_4bit + torch.matmul(dY, W)
  * (solution/nf4_patch.py:62-87; tasks/RUNTIME_AUDIT.md:113) and

@@ -37,6 +37,9 @@ SIGNATURES = {
     "ss_nf4_gemm_fwd": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p,
                                                                    _c_void_p, _i64, _c_void_p,
                                                                    _size, _c_void_p],
+    "ss_nf4_gemm_fwd_noalloc": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64,
+                                                                            _c_void_p, _c_void_p,
+                                                                            _i64, _c_void_p],
     "ss_nf4_gemm_dx": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _i64,
                                                                   _int, _c_void_p, _size,
                                                                   _c_void_p],

@@ -25,6 +25,8 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "gemm.h"
 #include "soupsuck_amd.h"
 #include "rank16.h"
@@ -547,16 +549,36 @@ static size_t decoded_bytes(int64_t n, int64_t k) {
   return ((size_t)n * (size_t)k * sizeof(uint16_t) + 255) / 256 * 256;
 }
 
-extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
-  // From T rows on, decoding W once into fp16 (one 2.5 B/weight HBM pass)
-  // and running the dense MFMA GEMM beats decoding every W tile again for each
-  // of the ceil(T/BM) row tiles: in-loop decode costs about 1/(2*BM) VALU
-  // decodes per flop, more than the VALU can issue next to full-rate MFMA.
-  // SS_NF4_DECODE_FIRST_T overrides the crossover (tuning knob).
+// From T rows on, decoding W once into fp16 (one 2.5 B/weight HBM pass) and
+// running the dense MFMA GEMM beats decoding every W tile again for each of
+// the ceil(T/BM) row tiles: in-loop decode costs about 1/(2*BM) VALU decodes
+// per flop, more than the VALU can issue next to full-rate MFMA.
+// SS_NF4_DECODE_FIRST_T overrides the crossover (tuning knob).
+static int64_t decode_first_threshold() {
   static const int64_t threshold = [] {
     const char* e = getenv("SS_NF4_DECODE_FIRST_T");
     return e ? (int64_t)atoll(e) : (int64_t)256;
   }();
+  return threshold;
+}
+
+// Scratch the forward alone needs (the forward part of
+// ss_nf4_gemm_workspace_size).
+static size_t fwd_workspace_bytes(int64_t t, int64_t n, int64_t k) {
+  if (n <= 0 || k <= 0 || t <= 0) return 0;
+  if (t <= ss::kSkinnyMaxT) {
+    size_t fwd = ss::skinny_partial_bytes(t, n, k);
+    const size_t fwd_stream = ss::stream_partial_bytes(t, n, k);
+    if (fwd_stream > fwd) fwd = fwd_stream;
+    const size_t fwd_fused = ss::nf4_fused_partial_bytes(t, n, k);
+    return fwd_fused > fwd ? fwd_fused : fwd;
+  }
+  if (t < decode_first_threshold()) return ss::nf4_fused_partial_bytes(t, n, k);
+  return decoded_bytes(n, k) + ss::nt_partial_bytes(t, n, k);
+}
+
+extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
+  const int64_t threshold = decode_first_threshold();
   if (n <= 0 || k <= 0 || t <= 0) return 0;
   if (t <= ss::kSkinnyMaxT) {
     // Forward: skinny-kernel partials.  Backward: decode W^T once and run the
@@ -778,6 +800,81 @@ extern "C" int ss_nf4_gemm_fwd(const uint16_t* x, int64_t ldx, int64_t t, const 
   SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
   GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, y, ldy);
   return run_fwd<EPI_PLAIN>(p, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------ no-alloc forward ---
+// ss_nf4_gemm_fwd_noalloc runs ss_nf4_gemm_fwd's dispatch with its scratch in
+// a fixed device array instead of a caller workspace.  Every GPU the library
+// runs on holds its own copy of the array (64 MiB) until the process ends;
+// its address on the current device is looked up once per device with
+// hipGetSymbolAddress.  The forward's scratch holds split-K / stage-group
+// partial planes that each call writes in full before reading (and, at
+// T >= 256 for weights small enough, the decoded weight), so nothing in it
+// has to start at zero.  Calls that overlap in time on one GPU share the
+// array and race.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __align__(256) static unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_on_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    ss::set_error("%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+    return SS_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    ss::set_error("%s: device index %d outside 0..%d", fn, dev, kMaxDevices - 1);
+    return SS_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      ss::set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                    hipGetErrorString(e));
+      return SS_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SS_OK;
+}
+
+}  // namespace
+
+extern "C" int ss_nf4_gemm_fwd_noalloc(const uint16_t* x, int64_t ldx, int64_t t,
+                                       const uint8_t* packed, const uint8_t* qabs,
+                                       const float* absmax2, const float* code2,
+                                       const float* offset, int64_t n, int64_t k,
+                                       const uint16_t* bias, uint16_t* y, int64_t ldy,
+                                       void* stream) {
+  const char* fn = "ss_nf4_gemm_fwd_noalloc";
+  SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
+  int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
+  if (rc) return rc;
+  if (t == 0) return SS_OK;
+  SS_CHECK_ARG(x && y, "%s: null activation/output pointer", fn);
+  SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
+  const size_t need = fwd_workspace_bytes(t, n, k);
+  SS_CHECK_ARG(need <= kNoAllocScratchBytes,
+               "%s: T=%lld N=%lld K=%lld needs %zu bytes of scratch, more than the fixed "
+               "%zu-byte device scratch of this entry point; use ss_nf4_gemm_fwd with a "
+               "workspace of ss_nf4_gemm_workspace_size() bytes",
+               fn, (long long)t, (long long)n, (long long)k, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need) {
+    rc = scratch_on_current_device(fn, &ws);
+    if (rc) return rc;
+  }
+  GemmParams p = fwd_params(x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, y, ldy);
+  return run_fwd<EPI_PLAIN>(p, ws, need, (hipStream_t)stream);
 }
 
 extern "C" int ss_qlora_fwd(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
