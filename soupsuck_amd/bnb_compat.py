@@ -218,5 +218,47 @@ class Linear4bit(torch.nn.Linear):
         return out.to(inp_dtype)
 
 
-functional = SimpleNamespace(quantize_4bit=quantize_4bit, dequantize_4bit=dequantize_4bit)
+functional = SimpleNamespace(quantize_4bit=quantize_4bit, dequantize_4bit=dequantize_4bit,
+                             QuantState=QuantState)
 nn = SimpleNamespace(Params4bit=Params4bit, Linear4bit=Linear4bit)
+
+COMPAT_VERSION = "0.50.2+soupsuck_amd.compat"
+
+
+def register_as_bitsandbytes():
+    """Make ``import bitsandbytes`` (and ``.nn``, ``.functional``) resolve to this module.
+
+    For images without bitsandbytes (this ROCm build): PEFT and user code that
+    import bitsandbytes by name then get the NF4 surface above.  Returns False
+    and changes nothing when a real bitsandbytes is importable or a module of
+    that name is already loaded.  The version string is bitsandbytes' pinned
+    0.50.2 with a local tag, so version checks parse it and the routes of
+    soupsuck_amd.bnb_routes (built for the real 0.50.2 only) leave it alone.
+    """
+    import importlib.machinery
+    import importlib.util
+    import sys
+    from types import ModuleType
+
+    if "bitsandbytes" in sys.modules:
+        return False
+    try:
+        if importlib.util.find_spec("bitsandbytes") is not None:
+            return False
+    except (ImportError, ValueError):
+        return False
+    package = ModuleType("bitsandbytes")
+    package.__spec__ = importlib.machinery.ModuleSpec("bitsandbytes", None, is_package=True)
+    package.__path__ = []
+    package.__version__ = COMPAT_VERSION
+    package.matmul_4bit = matmul_4bit
+    children = {}
+    for name, ns in (("nn", nn), ("functional", functional)):
+        child = ModuleType(f"bitsandbytes.{name}")
+        child.__spec__ = importlib.machinery.ModuleSpec(f"bitsandbytes.{name}", None)
+        child.__dict__.update(vars(ns))
+        setattr(package, name, child)
+        children[f"bitsandbytes.{name}"] = child
+    sys.modules["bitsandbytes"] = package
+    sys.modules.update(children)
+    return True

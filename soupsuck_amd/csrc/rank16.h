@@ -131,12 +131,20 @@ __device__ __forceinline__ bool finish_splits(float (&vals)[VALS], float* __rest
   float* base = part + blk * splits * (VALS * 64);
 #pragma unroll
   for (int v = 0; v < VALS; ++v) store_dev(base + s * (VALS * 64) + v * 64 + lane, vals[v]);
-  // This wave's stores are complete before it counts itself.
+  // Ordering without cache maintenance: the compiler-only fences keep the
+  // device-scope stores above the count and the device-scope loads below it
+  // (the compiler may otherwise reorder relaxed accesses to different
+  // addresses); the wait makes the stores complete in memory before the
+  // count is issued, and the loads are issued only after the counted value
+  // has returned (they depend on it through the branch).  A release/acquire
+  // atomic would add whole-L2 writeback and invalidate instructions.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   int seen = 0;
   if (lane == 0)
     seen = __hip_atomic_fetch_add(counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   seen = __shfl(seen, 0, kWave);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (seen != (int)splits - 1) return false;
   float sum[VALS];
 #pragma unroll

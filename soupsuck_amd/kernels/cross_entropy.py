@@ -1,194 +1,232 @@
-"""Chunked fused linear cross-entropy without full-vocabulary logits (A17-A19).
+"""``fused_linear_cross_entropy``: chunked linear + cross-entropy without full logits (A17-A19).
 
-Mirrors the reference's solution/kernels/cross_entropy.py:133-241
-(``_FrozenLinearCrossEntropy`` / ``fused_linear_cross_entropy``):
-  * logits of each vocabulary chunk are fp16(h16 . w16^T) (MFMA GEMM,
-    ss_gemm_f16), and online statistics m, sum exp, sum exp*z, target logit
-    and first argmax are merged chunk by chunk (ss_ce_stats); outputs
-    lse, entropy and per-token loss (ss_ce_outputs);
-  * backward compacts the rows with a target (one nonzero synchronisation),
-    recomputes each chunk, forms dz = g (softmax - onehot) scaled per row by
-    1/gain, gain = max(|g|, 1e-30)/1024, rounds it to fp16
-    (ss_ce_derivative), accumulates dX in fp32 over chunks and undoes the gain
-    while scattering back to all rows (ss_ce_finalize_dx).
-Extension (``weight_grad=True``): the reference rejects a trainable head
-(cross_entropy.py:221-222); here the lm_head gradient dW = dz^T . h is also
-produced, from a second fp16 copy of dz scaled by one global gain
-max_r |g_r| / 1024 (a per-row gain cannot be factored out of a sum over rows).
+Interface of solution/kernels/cross_entropy.py:214-241 (arguments, the four
+returned tensors loss / entropy / first argmax / lse with only ``loss``
+differentiable, ValueError before launch) and its numerics (:1-43):
+
+  forward   per vocabulary chunk c: z = fp16(h16 . W_c16^T) on the MFMA GEMM
+            (ss_gemm_f16); the per-row online state (max m, sum e^(z-m), sum
+            e^(z-m) z, target logit) and the first argmax are merged chunk by
+            chunk (ss_ce_stats); lse = m + log s, loss = lse - z_target (0 for
+            ignored rows), entropy = lse - t/s (ss_ce_outputs);
+  backward  rows with a target only (one nonzero synchronisation); each chunk
+            is recomputed and dz = fp16((softmax - onehot) g / gain) with the
+            per-row gain max(|g|, 1e-30)/1024 (ss_ce_derivative); dX = dz . W_c
+            accumulated in fp32 over chunks, multiplied back by the gain and
+            scattered to all rows (ss_ce_finalize_dx).  Ignored rows get zero
+            gradient whatever the upstream value.
+
+Extension (``weight_grad=True``, asked for by BASELINE configs[3]): the
+reference only accepts a frozen head (ValueError "frozen"); here the head
+gradient dW_c = dz'^T . h is also produced, from a second fp16 copy dz' of the
+derivative scaled by one global gain max_r |g_r| / 1024 (a per-row gain cannot
+be factored out of a sum over rows).
+
+Layout for the MFMA engine: the dense NT kernel wants both operands contiguous
+along the reduced dimension, so dX = dz . W_c uses W_c^T [H, width] per chunk
+(ss_transpose_f16) and dW_c = dz'^T . h uses h^T [H, T'] (built once, T' =
+rows with a target padded to 64 with zero columns) and dz'^T per chunk.
 """
 
 import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
+from ..contract import FLOAT_DTYPES, Rule, enforce, on_one_cuda_device
 from .nf4_gemm import gemm_f16, transpose_f16
 
-
-def _chunk_size(n, h):
-    """Reference default (cross_entropy.py:125-130): <= 4096 and memory-capped, power of 2."""
-    limit = min(4096, (64 * 1024 ** 2) // (2 * max(n, 1)), (32 * 1024 ** 2) // (2 * h))
-    if limit < 1:
-        raise ValueError("A single vocabulary column exceeds the temporary memory budget")
-    return 1 << (limit.bit_length() - 1)
+MAX_CHUNK = 8192            # BASELINE configs[3]'s vocabulary chunk
+TILE_BUDGET = 64 << 20      # bytes of one fp16 [rows, chunk] logits tile
 
 
-def _rows(src, index, row_bytes_per_elem):
-    """Gather rows of a contiguous tensor by a device index (ss_unpad_gather)."""
-    count = index.numel()
-    out = torch.empty((count, *src.shape[1:]), device=src.device, dtype=src.dtype)
-    row_bytes = src[0].numel() * src.element_size() if src.ndim > 1 else src.element_size()
+def default_chunk(rows):
+    """Vocabulary chunk when the caller gives none: the widest multiple of 256,
+    at most MAX_CHUNK, whose fp16 logits tile fits TILE_BUDGET."""
+    fit = TILE_BUDGET // (2 * max(rows, 1))
+    return max(256, min(MAX_CHUNK, fit // 256 * 256))
+
+
+def _vocab_chunks(vocab, chunk):
+    for start in range(0, vocab, chunk):
+        yield start, min(chunk, vocab - start)
+
+
+def _head_rows(weight, start, width):
+    w = weight.narrow(0, start, width)
+    return w if (w.dtype == torch.float16 and w.is_contiguous()) else \
+        w.to(torch.float16).contiguous()
+
+
+def _gather_rows(src, index):
+    """src[index] for a contiguous tensor and a device int64 index (ss_unpad_gather)."""
+    out = torch.empty((index.numel(), *src.shape[1:]), device=src.device, dtype=src.dtype)
+    row_bytes = (src[0].numel() if src.ndim > 1 else 1) * src.element_size()
     _lib.call("ss_unpad_gather", src.data_ptr(), src.shape[0], out.data_ptr(), index.data_ptr(),
-              count, row_bytes, _lib.stream(src.device))
+              index.numel(), row_bytes, _lib.stream(src.device))
     return out
 
 
-def _chunk_weight(weight, start, chunk):
-    w = weight[start:start + chunk]
-    if w.dtype != torch.float16 or not w.is_contiguous():
-        w = w.to(torch.float16).contiguous()
-    return w
+def _forward(hidden16, weight, targets, ignore_index, chunk):
+    rows = hidden16.shape[0]
+    dev = hidden16.device
+    loss = torch.empty(rows, device=dev, dtype=torch.float32)
+    entropy = torch.empty(rows, device=dev, dtype=torch.float32)
+    lse = torch.empty(rows, device=dev, dtype=torch.float32)
+    best = torch.empty(rows, device=dev, dtype=torch.int64)
+    if rows == 0:
+        return loss, entropy, best, lse
+    stream = _lib.stream(dev)
+    online = torch.empty((rows, 4), device=dev, dtype=torch.float32)
+    tile = torch.empty((rows, min(chunk, weight.shape[0])), device=dev, dtype=torch.float16)
+    for start, width in _vocab_chunks(weight.shape[0], chunk):
+        logits = tile[:, :width]
+        gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True, out=logits)
+        _lib.call("ss_ce_stats", logits.data_ptr(), tile.stride(0), targets.data_ptr(),
+                  online.data_ptr(), best.data_ptr(), rows, width, start, ignore_index,
+                  int(start == 0), stream)
+    _lib.call("ss_ce_outputs", online.data_ptr(), targets.data_ptr(), loss.data_ptr(),
+              entropy.data_ptr(), lse.data_ptr(), rows, ignore_index, stream)
+    return loss, entropy, best, lse
 
 
-class _LinearCrossEntropy(torch.autograd.Function):
+class _Backward:
+    """Gradients of the summed loss w.r.t. hidden and (optionally) the head."""
+
+    def __init__(self, hidden16, weight, targets, lse, grad, ignore_index, chunk):
+        self.weight, self.ignore, self.chunk = weight, ignore_index, chunk
+        self.dev = hidden16.device
+        self.stream = _lib.stream(self.dev)
+        self.full_grad = grad
+        self.kept = torch.nonzero(targets != ignore_index, as_tuple=False).flatten()
+        self.count = self.kept.numel()
+        if self.count:
+            self.h = _gather_rows(hidden16, self.kept)
+            self.targets = _gather_rows(targets, self.kept)
+            self.lse = _gather_rows(lse, self.kept)
+            self.grad = _gather_rows(grad, self.kept)
+
+    def run(self, dx, dw):
+        width_max = min(self.chunk, self.weight.shape[0])
+        hdim = self.h.shape[1]
+        logits = torch.empty((self.count, width_max), device=self.dev, dtype=torch.float16)
+        dz = torch.empty_like(logits)
+        acc = torch.zeros((self.count, hdim), device=self.dev, dtype=torch.float32) \
+            if dx is not None else None
+        wt = torch.empty((hdim, width_max), device=self.dev, dtype=torch.float16) \
+            if dx is not None else None
+        head_gain = 1.0
+        if dw is not None:
+            head_gain = max(self.grad.abs().max().item(), 1e-30) / 1024.0
+            padded = -(-self.count // 64) * 64
+            ht = torch.zeros((hdim, padded), device=self.dev, dtype=torch.float16)
+            transpose_f16(self.h, out=ht[:, :self.count])
+            dz_head = torch.empty_like(logits)
+            dz_head_t = torch.zeros((width_max, padded), device=self.dev, dtype=torch.float16)
+        for start, width in _vocab_chunks(self.weight.shape[0], self.chunk):
+            w = _head_rows(self.weight, start, width)
+            z = logits[:, :width]
+            gemm_f16(self.h, w, b_trans=True, out=z)
+            d = dz.view(-1)[:self.count * width].view(self.count, width)
+            dh = dz_head.view(-1)[:self.count * width].view(self.count, width) \
+                if dw is not None else None
+            _lib.call("ss_ce_derivative", z.data_ptr(), logits.stride(0),
+                      self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
+                      d.data_ptr(), _lib.ptr(dh), float(head_gain), self.count, width, start,
+                      self.ignore, self.stream)
+            if acc is not None:
+                gemm_f16(d, transpose_f16(w, out=wt[:, :width]), b_trans=True, out=acc,
+                         accumulate=True, split_k=True)
+            if dw is not None:
+                transpose_f16(dh, out=dz_head_t[:width, :self.count])
+                rows_w = dw.narrow(0, start, width)
+                if rows_w.dtype in FLOAT_DTYPES:
+                    gemm_f16(dz_head_t[:width], ht, b_trans=True, out=rows_w,
+                             alpha=float(head_gain))
+                else:
+                    rows_w.copy_(gemm_f16(dz_head_t[:width], ht, b_trans=True,
+                                          out_dtype=torch.float32, alpha=float(head_gain)))
+        if acc is not None:
+            rows, hd = dx.shape
+            inverse = torch.empty(rows, device=self.dev, dtype=torch.int32)
+            _lib.call("ss_unpad_inverse", self.kept.data_ptr(), self.count, inverse.data_ptr(),
+                      rows, self.stream)
+            _lib.call("ss_ce_finalize_dx", acc.data_ptr(), self.count, self.full_grad.data_ptr(),
+                      inverse.data_ptr(), dx.data_ptr(), _lib.dtype_code(dx.dtype), rows, hd,
+                      self.stream)
+
+
+class LinearCrossEntropy(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, targets, ignore_index, chunk, weight_grad):
-        ctx.hidden_dtype = hidden.dtype
-        hidden = hidden.to(torch.float16).contiguous()
+        hidden16 = hidden.to(torch.float16).contiguous()
         targets = targets.contiguous()
-        n, h = hidden.shape
-        v = weight.shape[0]
-        chunk = chunk or _chunk_size(n, h)
-        loss = torch.empty(n, device=hidden.device, dtype=torch.float32)
-        entropy, lse = torch.empty_like(loss), torch.empty_like(loss)
-        best = torch.empty(n, device=hidden.device, dtype=torch.int64)
-        stream = _lib.stream(hidden.device)
-        if n:
-            state = torch.empty((n, 4), device=hidden.device, dtype=torch.float32)
-            z = torch.empty((n, min(chunk, v)), device=hidden.device, dtype=torch.float16)
-            for start in range(0, v, chunk):
-                w = _chunk_weight(weight, start, chunk)
-                width = w.shape[0]
-                zc = z[:, :width]
-                gemm_f16(hidden, w, b_trans=True, out=zc)
-                _lib.call("ss_ce_stats", zc.data_ptr(), z.stride(0), targets.data_ptr(),
-                          state.data_ptr(), best.data_ptr(), n, width, start, ignore_index,
-                          int(start == 0), stream)
-            _lib.call("ss_ce_outputs", state.data_ptr(), targets.data_ptr(), loss.data_ptr(),
-                      entropy.data_ptr(), lse.data_ptr(), n, ignore_index, stream)
-        ctx.save_for_backward(hidden, weight, targets, lse)
-        ctx.ignore_index, ctx.chunk, ctx.weight_grad = ignore_index, chunk, weight_grad
+        chunk = chunk or default_chunk(hidden16.shape[0])
+        loss, entropy, best, lse = _forward(hidden16, weight, targets, ignore_index, chunk)
+        ctx.save_for_backward(hidden16, weight, targets, lse)
+        ctx.setup = (hidden.dtype, ignore_index, chunk, weight_grad)
         ctx.mark_non_differentiable(entropy, best, lse)
         ctx.set_materialize_grads(False)
         return loss, entropy, best, lse
 
     @staticmethod
     @once_differentiable
-    def backward(ctx, grad_loss, _grad_entropy, _grad_best, _grad_lse):
-        hidden, weight, targets, lse = ctx.saved_tensors
-        need_x = ctx.needs_input_grad[0]
-        need_w = ctx.weight_grad and ctx.needs_input_grad[1]
-        if grad_loss is None or not (need_x or need_w):
-            return None, None, None, None, None, None
-        n, h = hidden.shape
-        v = weight.shape[0]
-        device = hidden.device
-        dx = torch.zeros((n, h), device=device, dtype=ctx.hidden_dtype) if need_x else None
-        dw = torch.zeros(weight.shape, device=device, dtype=weight.dtype) if need_w else None
-        if not n:
-            return dx, dw, None, None, None, None
-        valid_index = torch.nonzero(targets != ctx.ignore_index, as_tuple=False).flatten()
-        valid_n = valid_index.numel()
-        if not valid_n:
-            # Ignored rows have zero gradient regardless of a non-finite upstream.
-            return dx, dw, None, None, None, None
-        stream = _lib.stream(device)
-        grad = grad_loss.float().contiguous()
-        work_hidden = _rows(hidden, valid_index, 2)
-        work_targets = _rows(targets, valid_index, 8)
-        work_lse = _rows(lse, valid_index, 4)
-        work_grad = _rows(grad, valid_index, 4)
-        inverse = torch.empty(n, device=device, dtype=torch.int32)
-        _lib.call("ss_unpad_inverse", valid_index.data_ptr(), valid_n, inverse.data_ptr(), n,
-                  stream)
-        global_gain = 1.0
-        if need_w:
-            global_gain = max(work_grad.abs().max().item(), 1e-30) / 1024.0
-        acc = torch.zeros((valid_n, h), device=device, dtype=torch.float32) if need_x else None
-        width_max = min(ctx.chunk, v)
-        z = torch.empty((valid_n, width_max), device=device, dtype=torch.float16)
-        dz = torch.empty((valid_n, width_max), device=device, dtype=torch.float16)
-        dzg = torch.empty_like(dz) if need_w else None
-        # The chunk products go to the dense NT kernel, which wants both operands
-        # contiguous along the reduced dimension: dX = dz . W_c reduces over the
-        # chunk (W_c^T [H, width] per chunk), dW_c = dzg^T . h reduces over the
-        # valid rows (dzg^T [width, T'] and h^T [H, T'], T' = valid rows padded
-        # to 64 with zero columns, so K % 64 == 0).
-        wt = torch.empty((h, width_max), device=device, dtype=torch.float16) if need_x else None
-        if need_w:
-            t_pad = -(-valid_n // 64) * 64
-            ht = torch.zeros((h, t_pad), device=device, dtype=torch.float16)
-            transpose_f16(work_hidden, out=ht[:, :valid_n])
-            dzgt = torch.zeros((width_max, t_pad), device=device, dtype=torch.float16)
-        for start in range(0, v, ctx.chunk):
-            w = _chunk_weight(weight, start, ctx.chunk)
-            width = w.shape[0]
-            zc = z[:, :width]
-            gemm_f16(work_hidden, w, b_trans=True, out=zc)
-            dzc = dz.view(-1)[:valid_n * width].view(valid_n, width)
-            dzgc = dzg.view(-1)[:valid_n * width].view(valid_n, width) if need_w else None
-            _lib.call("ss_ce_derivative", zc.data_ptr(), z.stride(0), work_targets.data_ptr(),
-                      work_lse.data_ptr(), work_grad.data_ptr(), dzc.data_ptr(),
-                      _lib.ptr(dzgc), float(global_gain), valid_n, width, start,
-                      ctx.ignore_index, stream)
-            if need_x:
-                wtc = transpose_f16(w, out=wt[:, :width])
-                gemm_f16(dzc, wtc, b_trans=True, out=acc, accumulate=True, split_k=True)
-            if need_w:
-                dw_chunk = dw[start:start + width]
-                transpose_f16(dzgc, out=dzgt[:width, :valid_n])
-                dzgtc = dzgt[:width]
-                if dw.dtype == torch.float16 or dw.dtype == torch.float32:
-                    gemm_f16(dzgtc, ht, b_trans=True, out=dw_chunk, alpha=float(global_gain))
-                else:
-                    dw_chunk.copy_(gemm_f16(dzgtc, ht, b_trans=True, out_dtype=torch.float32,
-                                            alpha=float(global_gain)))
-        if need_x:
-            _lib.call("ss_ce_finalize_dx", acc.data_ptr(), valid_n, grad.data_ptr(),
-                      inverse.data_ptr(), dx.data_ptr(), _lib.dtype_code(dx.dtype), n, h, stream)
+    def backward(ctx, grad_loss, *_unused):
+        hidden_dtype, ignore_index, chunk, weight_grad = ctx.setup
+        want_x = ctx.needs_input_grad[0]
+        want_w = weight_grad and ctx.needs_input_grad[1]
+        nothing = (None,) * 6
+        if grad_loss is None or not (want_x or want_w):
+            return nothing
+        hidden16, weight, targets, lse = ctx.saved_tensors
+        dx = torch.zeros(hidden16.shape, device=hidden16.device, dtype=hidden_dtype) \
+            if want_x else None
+        dw = torch.zeros(weight.shape, device=weight.device, dtype=weight.dtype) \
+            if want_w else None
+        if hidden16.shape[0]:
+            grad = grad_loss.float().contiguous()
+            back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk)
+            if back.count:
+                back.run(dx, dw)
         return dx, dw, None, None, None, None
+
+
+CE_RULES = (
+    Rule("fused_linear_cross_entropy: a trainable weight needs weight_grad=True (the "
+         "reference requires a frozen weight)",
+         lambda a: a.weight_grad or not getattr(a.weight, "requires_grad", False)),
+    Rule("fused_linear_cross_entropy: expected hidden [N, H], weight [V, H], targets [N] with "
+         "V, H > 0",
+         lambda a: all(isinstance(t, torch.Tensor) for t in (a.hidden, a.weight, a.targets))
+         and a.hidden.ndim == 2 and a.weight.ndim == 2 and a.targets.ndim == 1
+         and a.hidden.shape[1] == a.weight.shape[1] and a.hidden.shape[0] == a.targets.shape[0]
+         and a.weight.shape[0] > 0 and a.weight.shape[1] > 0),
+    Rule("fused_linear_cross_entropy: hidden and weight must be fp16 or fp32, targets int64",
+         lambda a: a.hidden.dtype in FLOAT_DTYPES and a.weight.dtype in FLOAT_DTYPES
+         and a.targets.dtype == torch.int64),
+    Rule("fused_linear_cross_entropy: hidden, weight and targets must be CUDA tensors on one "
+         "device",
+         lambda a: on_one_cuda_device(a.hidden, a.weight, a.targets)),
+    Rule("fused_linear_cross_entropy: ignore_index must be an int",
+         lambda a: isinstance(a.ignore_index, int) and not isinstance(a.ignore_index, bool)),
+    Rule("fused_linear_cross_entropy: chunk must be None or a positive int",
+         lambda a: a.chunk is None or (isinstance(a.chunk, int) and a.chunk > 0)),
+)
 
 
 def fused_linear_cross_entropy(hidden, weight, targets, ignore_index=-100, *, chunk=None,
                                weight_grad=False):
-    """Return per-token loss, entropy, first argmax and lse (reference cross_entropy.py:214-241).
+    """Per-token (loss, entropy, first argmax, lse) of softmax(hidden . weight^T).
 
-    hidden[N,H] fp16/fp32, weight[V,H] fp16/fp32, targets[N] int64 (already
-    shifted), all on one CUDA device.  Only ``loss`` has an autograd edge.
-    ``weight_grad=True`` (extension) also differentiates w.r.t. a trainable
-    weight; otherwise a weight that requires grad is rejected like the reference.
+    hidden [N, H] and weight [V, H] fp16/fp32, targets [N] int64 (already
+    shifted), on one CUDA device.  Only ``loss`` carries a gradient.  A target
+    outside [0, V) other than ignore_index fails a device-side assertion (no
+    host synchronisation in the forward).
     """
-    if weight.requires_grad and not weight_grad:
-        raise ValueError("fused_linear_cross_entropy requires frozen weight")
-    if hidden.ndim != 2 or weight.ndim != 2 or targets.ndim != 1:
-        raise ValueError("Expected hidden[N,H], weight[V,H], targets[N]")
-    if hidden.shape[1] != weight.shape[1] or hidden.shape[0] != targets.shape[0]:
-        raise ValueError("Incompatible hidden, weight and targets shapes")
-    if weight.shape[0] == 0 or weight.shape[1] == 0:
-        raise ValueError("Vocabulary and hidden dimensions must be positive")
-    if (hidden.dtype not in (torch.float16, torch.float32)
-            or weight.dtype not in (torch.float16, torch.float32)):
-        raise ValueError("Expected fp16/fp32 hidden and weight")
-    if targets.dtype != torch.int64:
-        raise ValueError("Expected int64 targets")
-    if not hidden.is_cuda or weight.device != hidden.device or targets.device != hidden.device:
-        raise ValueError("Inputs must be on the same CUDA device")
-    if not isinstance(ignore_index, int):
-        raise ValueError("ignore_index must be an integer")
-    if chunk is not None and (not isinstance(chunk, int) or chunk <= 0):
-        raise ValueError("chunk must be a positive integer")
+    enforce(CE_RULES, hidden=hidden, weight=weight, targets=targets, ignore_index=ignore_index,
+            chunk=chunk, weight_grad=weight_grad)
     with torch.cuda.device(hidden.device):
-        torch._assert_async(((targets == ignore_index)
-                             | ((targets >= 0) & (targets < weight.shape[0]))).all(),
-                            "Target outside vocabulary")
-        return _LinearCrossEntropy.apply(hidden, weight, targets, ignore_index, chunk,
-                                         bool(weight_grad))
+        out_of_range = (targets != ignore_index) & ((targets < 0) | (targets >= weight.shape[0]))
+        torch._assert_async(torch.logical_not(out_of_range.any()),
+                            "fused_linear_cross_entropy: target outside the vocabulary")
+        return LinearCrossEntropy.apply(hidden, weight, targets, ignore_index, chunk,
+                                        bool(weight_grad))

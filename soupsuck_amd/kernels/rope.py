@@ -9,21 +9,15 @@ before the add (eager PyTorch's order), the backward rounds products to the
 input dtype.  Kernels: ss_rope_fwd / ss_rope_bwd.  Saves only cos and sin.
 """
 
-import importlib
-from functools import wraps
-from types import ModuleType
-
 import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
-from ..utils import enabled
 
-_MARKER = "_solution_fused_original"
 _DTYPES = (torch.float16, torch.float32)
 
 
-def _supported(q, k, cos, sin, unsqueeze_dim=1):
+def rope_supported(q, k, cos, sin, unsqueeze_dim=1):
     tensors = (q, k, cos, sin)
     if not all(isinstance(t, torch.Tensor) for t in tensors) or unsqueeze_dim != 1:
         return False
@@ -91,7 +85,7 @@ class _RoPE(torch.autograd.Function):
 
 def fused_rope(q, k, cos, sin):
     """Rotate q / k on the GPU; cos / sin are detached [1|B, S, D] (rope.py:146-152)."""
-    if not _supported(q, k, cos, sin):
+    if not rope_supported(q, k, cos, sin):
         raise ValueError("Expected CUDA q/k[B,H,S,even D] and detached cos/sin[1|B,S,D], "
                          "last stride 1")
     with torch.cuda.device(q.device):
@@ -100,26 +94,6 @@ def fused_rope(q, k, cos, sin):
 
 def patch_qwen2_rope(module=None):
     """Route modeling_qwen2.apply_rotary_pos_emb through fused_rope (idempotent)."""
-    if module is None:
-        try:
-            module = importlib.import_module("transformers.models.qwen2.modeling_qwen2")
-        except (ImportError, AttributeError):
-            return False
-    if not isinstance(module, ModuleType):
-        return False
-    original = getattr(module, "apply_rotary_pos_emb", None)
-    if not callable(original):
-        return False
-    if hasattr(original, _MARKER):
-        return True
+    from ..patch import ROPE_ROUTE, install_route
 
-    @wraps(original)
-    def apply_rotary_pos_emb(q, k, cos, sin, *args, **kwargs):
-        dim = kwargs.get("unsqueeze_dim", 1)
-        if args or not enabled() or not _supported(q, k, cos, sin, dim):
-            return original(q, k, cos, sin, *args, **kwargs)
-        return fused_rope(q, k, cos, sin)
-
-    setattr(apply_rotary_pos_emb, _MARKER, original)
-    module.apply_rotary_pos_emb = apply_rotary_pos_emb
-    return True
+    return install_route(ROPE_ROUTE, module)

@@ -50,12 +50,16 @@ _RANK_WORKSPACE = {}
 
 
 def _rank_workspace(nbytes, device):
-    """Zero-filled workspace of the rank-16 ops, one per device, grown on demand.
+    """Zero-filled workspace of the rank-16 ops, one per (device, stream), grown on demand.
 
     Its leading arrival counters must be zero when an op starts and the op
     leaves them zero, so one zero-filled buffer serves every call issued in
-    order on the device's stream (torch's current stream)."""
-    key = (device.type, device.index)
+    order on one stream.  Calls on different streams can overlap in time, so
+    each stream (torch's current stream at the call) gets its own buffer; a
+    buffer replaced by a larger one is released only after the work queued on
+    its stream (torch's caching allocator records the stream that used it)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, _lib.stream(device))
     ws = _RANK_WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)

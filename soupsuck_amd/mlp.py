@@ -1,7 +1,7 @@
 """Frozen Qwen2 MLP on NF4 projections with the SwiGLU fused into the GEMMs.
 
-Mirrors the reference's solution/mlp.py:500-612 (``_FrozenMLP``,
-``fused_qwen2_mlp``, ``patch_qwen2_mlp_fused``): down(silu(gate(x)) * up(x))
+Interface of the reference's solution/mlp.py:579-612 (``fused_qwen2_mlp``,
+``patch_qwen2_mlp_fused``) over its node's semantics (:500-576): down(silu(gate(x)) * up(x))
 for frozen bias-free NF4 Linear4bit projections, as one autograd node that
 keeps gate and up (fp16) for the backward, or only x with ``recompute=True``
 (gate and up are recomputed in the backward).  Kernels per direction:
@@ -28,10 +28,7 @@ reference's pinned-host offload pools (solution/mlp.py:105-359) are a memory
 policy outside this path; ``offload`` is accepted and ignored.
 """
 
-import importlib
 import os
-from functools import wraps
-from types import ModuleType
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -40,9 +37,6 @@ from . import _lib
 from .kernels.nf4 import _validate_state
 from .kernels.nf4_gemm import nf4_dx_2d, nf4_forward_2d
 from .kernels.swiglu import swiglu_fused_backward, swiglu_fused_forward
-from .utils import enabled
-
-_MARKER = "_solution_fused_original"
 
 
 def _nf4(module):
@@ -68,7 +62,8 @@ def _projections(mlp):
     return None if any(p is None for p in parts) else parts
 
 
-def _eligible(mlp, x):
+def eligible_mlp(mlp, x):
+    """Frozen bias-free NF4 gate/up/down of matching shapes on x's device, SiLU, CUDA fp16/fp32 x."""
     if not isinstance(x, torch.Tensor) or not x.is_cuda or x.dtype not in (torch.float16,
                                                                           torch.float32):
         return False
@@ -196,7 +191,7 @@ class _FrozenMLP(torch.autograd.Function):
 def fused_qwen2_mlp(mlp, x, recompute=None, offload=None):
     """Run an eligible frozen NF4 MLP; raise ValueError otherwise (solution/mlp.py:579-594)."""
     del offload  # pinned-host offload is a memory policy outside this path
-    if not _eligible(mlp, x):
+    if not eligible_mlp(mlp, x):
         raise ValueError("Expected frozen bias-free fp16 NF4 Linear4bit projections on CUDA")
     if recompute is None:
         recompute = os.environ.get("SOUP_MLP_RECOMPUTE") == "1"
@@ -211,28 +206,9 @@ def fused_qwen2_mlp(mlp, x, recompute=None, offload=None):
 
 def patch_qwen2_mlp_fused(module=None):
     """Route Qwen2MLP.forward through fused_qwen2_mlp for eligible modules (idempotent)."""
-    try:
-        module = module or importlib.import_module("transformers.models.qwen2.modeling_qwen2")
-    except (ImportError, AttributeError):
-        return False
-    if not isinstance(module, ModuleType):
-        return False
-    cls = getattr(module, "Qwen2MLP", None)
-    if not isinstance(cls, type) or not issubclass(cls, torch.nn.Module):
-        return False
-    original = cls.forward
-    if hasattr(original, _MARKER):
-        return True
+    from .patch import MLP_ROUTE, install_route
 
-    @wraps(original)
-    def forward(self, x):
-        if not enabled() or type(self) is not cls or not _eligible(self, x):
-            return original(self, x)
-        return fused_qwen2_mlp(self, x)
-
-    setattr(forward, _MARKER, original)
-    cls.forward = forward
-    return True
+    return install_route(MLP_ROUTE, module)
 
 
 def mlp_flops(t, hidden, inter):
@@ -240,5 +216,5 @@ def mlp_flops(t, hidden, inter):
     return 7 * 2 * t * hidden * inter
 
 
-__all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "gate_up_swiglu", "down_dx_swiglu",
+__all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "eligible_mlp", "gate_up_swiglu", "down_dx_swiglu",
            "mlp_forward_2d", "mlp_backward_2d", "mlp_flops"]

@@ -1,182 +1,270 @@
-"""Lazy, idempotent patch registration (reference solution/patch.py:441-487).
+"""Lazy, idempotent routing of the reference's patch surface (solution/patch.py:441-487).
 
-``install()`` patches target modules that are already imported and installs a
-``sys.meta_path`` finder that patches the others right after they are
-imported, so the order of ``apply()`` and the imports does not matter.
-Targets:
-  * ``bitsandbytes`` 0.50.2 (when present): ``functional.dequantize_4bit`` is
-    routed to the HIP NF4 decoder for nested NF4 states
-    (reference solution/nf4_patch.py:43-125); other states keep the original;
-  * ``transformers.models.qwen2.modeling_qwen2``: ``Qwen2DecoderLayer.forward``
-    fuses the attention residual add with the post-attention RMSNorm
-    (reference solution/decoder.py:54-89), and ``Qwen2MLP.forward`` runs frozen
-    NF4 MLPs through ``soupsuck_amd.mlp.fused_qwen2_mlp`` (reference
-    solution/mlp.py:597-612), and ``Qwen2RMSNorm.forward`` (input and final
-    norms) runs ``kernels.rmsnorm.rms_norm`` with the eager dtype semantics
-    (reference solution/kernels/rmsnorm.py:159-188); ``apply_rotary_pos_emb``
-    runs ``kernels.rope.fused_rope`` (reference solution/rope.py:55-80).
-Every wrapper carries ``_solution_fused_original`` (the reference's marker)
-and falls back to the original when ``SOUP_FUSED_DISABLE`` is set or the
-inputs are outside the supported contract.  No GPU work happens here.
+A *route* replaces one function or method of a third-party module by a
+version that sends supported calls to this package's HIP path and every other
+call to the original.  Routes are declared as data (``ROUTES``): the module
+name, the owning class (or None for a module attribute), the attribute, the
+builder that makes the replacement from the original, and the marker
+attribute that holds the original.  ``install()`` installs the routes of
+modules already imported and puts one ``sys.meta_path`` finder in front that
+installs the others as soon as their module is imported, so the order of
+``apply()`` and the imports does not matter.  No GPU work happens here.
+
+Routes (reference file of the behaviour each one keeps):
+  bitsandbytes 0.50.2 (solution/nf4_patch.py:43-125), in soupsuck_amd.bnb_routes:
+    functional.dequantize_4bit, backends.cuda.ops._dequantize_4bit_impl and
+    _dequant_linear_fallback, and matmul_4bit (the NF4 GEMM);
+  transformers Qwen2 (modeling_qwen2):
+    Qwen2DecoderLayer.forward  attention residual add + post-attention norm
+                               fused (solution/decoder.py:54-89);
+    Qwen2RMSNorm.forward       the HIP row norm (solution/patch.py:232-250);
+    Qwen2MLP.forward           the frozen NF4 MLP node (solution/mlp.py:597-612);
+    apply_rotary_pos_emb       the joint q/k RoPE (solution/rope.py:55-80);
+    Qwen2ForCausalLM.forward   the chunked fused CE head (solution/patch.py:167-229),
+                               in soupsuck_amd.head;
+  PEFT (solution/lora.py:135-166), in soupsuck_amd.peft_route:
+    tuners.lora.bnb.Linear4bit.forward  the fused QLoRA projection.
+Every replacement falls back to the original when SOUP_FUSED_DISABLE is set
+or a call is outside the supported contract, and carries the original under
+its marker (``_solution_fused_original``; the PEFT route uses
+``_solution_lora_4bit_original``, as the reference does).
 """
 
+import functools
 import importlib
 import sys
-from functools import wraps
 from importlib.abc import Loader, MetaPathFinder
 from importlib.machinery import PathFinder
+from types import ModuleType
+from typing import Callable, NamedTuple, Optional
 
 from .utils import enabled
 
-_MARKER = "_solution_fused_original"
-_QWEN = "transformers.models.qwen2.modeling_qwen2"
-_BNB_FUNCTIONAL = "bitsandbytes.functional"
-_TARGETS = (_QWEN, _BNB_FUNCTIONAL)
+MARKER = "_solution_fused_original"
+QWEN = "transformers.models.qwen2.modeling_qwen2"
 
 
-def _supported(t):
+class Route(NamedTuple):
+    module: str
+    owner: Optional[str]                 # class in ``module``; None for a module attribute
+    attr: str
+    build: Callable                      # build(original, module) -> replacement or None
+    marker: str = MARKER
+
+
+def _holder(route, module):
+    if route.owner is None:
+        return module
+    cls = getattr(module, route.owner, None)
+    return cls if isinstance(cls, type) else None
+
+
+def install_route(route, module=None):
+    """Install one route on ``module`` (imported if None); True when it is in place."""
+    if module is None:
+        try:
+            module = importlib.import_module(route.module)
+        except (ImportError, AttributeError):
+            return False
+    if not isinstance(module, ModuleType):
+        return False
+    holder = _holder(route, module)
+    original = getattr(holder, route.attr, None) if holder is not None else None
+    if not callable(original):
+        return False
+    if hasattr(original, route.marker):
+        return True
+    replacement = route.build(original, module)
+    if replacement is None:
+        return False
+    functools.update_wrapper(replacement, original)
+    setattr(replacement, route.marker, original)
+    setattr(holder, route.attr, replacement)
+    return True
+
+
+# ---------------------------------------------------------------- Qwen2 ---
+
+def _float_cuda(t):
     import torch
 
     return (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype in (torch.float16, torch.float32)
             and t.is_contiguous())
 
 
-def patch_bnb_dequant(functional=None):
-    """Route bnb 0.50.2 nested-NF4 dequantize_4bit to the HIP decoder; return success."""
-    try:
-        import torch
+def _hookless(module):
+    return not (module._forward_hooks or module._forward_pre_hooks)
 
-        bnb = importlib.import_module("bitsandbytes")
-        functional = functional or importlib.import_module(_BNB_FUNCTIONAL)
-    except (ImportError, AttributeError):
-        return False
-    if getattr(bnb, "__version__", None) != "0.50.2" or not callable(
-            getattr(functional, "dequantize_4bit", None)):
-        return False
-    original = functional.dequantize_4bit
-    if hasattr(original, _MARKER):
-        return True
 
-    @wraps(original)
-    def dequantize(A, quant_state=None, absmax=None, out=None, blocksize=None, quant_type="fp4"):
-        args = dict(quant_state=quant_state, absmax=absmax, out=out, blocksize=blocksize,
-                    quant_type=quant_type)
-        if not enabled() or not isinstance(A, torch.Tensor) or not A.is_cuda:
-            return original(A, **args)
-        from .kernels.nf4 import _validate_state, dequantize_nf4
+def _exact_class(module, name):
+    cls = getattr(module, name, None)
+    if not isinstance(cls, type) or cls.__module__ != module.__name__:
+        return None
+    return cls
 
-        try:
-            shape = _validate_state(A, quant_state, torch.float16)
-        except ValueError:
-            return original(A, **args)
-        if out is not None and (not isinstance(out, torch.Tensor) or tuple(out.shape) != shape
-                                or out.dtype != torch.float16 or out.device != A.device
-                                or not out.is_contiguous() or out.requires_grad):
-            return original(A, **args)
-        return dequantize_nf4(A, quant_state, out=out)
 
-    setattr(dequantize, _MARKER, original)
-    functional.dequantize_4bit = dequantize
-    return True
+# Qwen2DecoderLayer.forward's arguments after hidden_states, with their defaults.
+_DECODER_ARGS = (("attention_mask", None), ("position_ids", None), ("past_key_values", None),
+                 ("use_cache", False), ("position_embeddings", None))
+
+
+def _residual_norm(norm, norm_cls, residual, update):
+    """(residual + update, norm(residual + update)); one HIP pass when the norm qualifies."""
+    weight = getattr(norm, "weight", None)
+    if (type(norm) is norm_cls and _hookless(norm) and _float_cuda(update) and _float_cuda(weight)
+            and update.shape == residual.shape and weight.ndim == 1
+            and weight.numel() == residual.shape[-1]
+            and update.device == residual.device == weight.device):
+        from .kernels.add_rmsnorm import add_rms_norm
+
+        return add_rms_norm(residual, update, weight, norm.variance_epsilon)
+    total = residual + update
+    return total, norm(total)
+
+
+def _build_decoder(original, module):
+    cls, norm_cls = _exact_class(module, "Qwen2DecoderLayer"), _exact_class(module, "Qwen2RMSNorm")
+    if cls is None or norm_cls is None:
+        return None
+
+    def forward(self, hidden_states, *args, **kwargs):
+        if not enabled() or type(self) is not cls or not _float_cuda(hidden_states) \
+                or len(args) > len(_DECODER_ARGS):
+            return original(self, hidden_states, *args, **kwargs)
+        named = dict(zip((name for name, _ in _DECODER_ARGS), args))
+        if set(named) & set(kwargs):
+            return original(self, hidden_states, *args, **kwargs)
+        call = dict(_DECODER_ARGS)
+        call.update(named)
+        call.update(kwargs)
+        attended, _ = self.self_attn(hidden_states=self.input_layernorm(hidden_states), **call)
+        residual, normed = _residual_norm(self.post_attention_layernorm, norm_cls,
+                                          hidden_states, attended)
+        return residual + self.mlp(normed)
+
+    return forward
+
+
+def _build_rmsnorm(original, module):
+    cls = _exact_class(module, "Qwen2RMSNorm")
+    if cls is None:
+        return None
+
+    def forward(self, hidden_states):
+        weight = getattr(self, "weight", None)
+        if (enabled() and type(self) is cls and _hookless(self) and _float_cuda(hidden_states)
+                and _float_cuda(weight) and weight.ndim == 1
+                and weight.shape[0] == hidden_states.shape[-1]
+                and weight.device == hidden_states.device):
+            from .kernels.rmsnorm import rms_norm
+
+            return rms_norm(hidden_states, weight, self.variance_epsilon)
+        return original(self, hidden_states)
+
+    return forward
+
+
+def _build_mlp(original, module):
+    cls = _exact_class(module, "Qwen2MLP")
+    if cls is None:
+        return None
+    from .mlp import eligible_mlp, fused_qwen2_mlp
+
+    def forward(self, x):
+        if enabled() and type(self) is cls and eligible_mlp(self, x):
+            return fused_qwen2_mlp(self, x)
+        return original(self, x)
+
+    return forward
+
+
+def _build_rope(original, module):
+    from .kernels.rope import fused_rope, rope_supported
+
+    def apply_rotary_pos_emb(q, k, cos, sin, *args, **kwargs):
+        dim = kwargs.get("unsqueeze_dim", 1)
+        if args or not enabled() or not rope_supported(q, k, cos, sin, dim):
+            return original(q, k, cos, sin, *args, **kwargs)
+        return fused_rope(q, k, cos, sin)
+
+    return apply_rotary_pos_emb
+
+
+def _build_head(original, module):
+    from .head import build_causal_lm_forward
+
+    return build_causal_lm_forward(original, module)
+
+
+def _build_bnb(name):
+    def build(original, module):
+        from . import bnb_routes
+
+        return getattr(bnb_routes, name)(original, module)
+
+    return build
+
+
+def _build_peft(original, module):
+    from .peft_route import build_linear4bit_forward
+
+    return build_linear4bit_forward(original, module)
+
+
+DECODER_ROUTE = Route(QWEN, "Qwen2DecoderLayer", "forward", _build_decoder)
+RMSNORM_ROUTE = Route(QWEN, "Qwen2RMSNorm", "forward", _build_rmsnorm)
+MLP_ROUTE = Route(QWEN, "Qwen2MLP", "forward", _build_mlp)
+ROPE_ROUTE = Route(QWEN, None, "apply_rotary_pos_emb", _build_rope)
+HEAD_ROUTE = Route(QWEN, "Qwen2ForCausalLM", "forward", _build_head)
+PEFT_ROUTE = Route("peft.tuners.lora.bnb", "Linear4bit", "forward", _build_peft,
+                   "_solution_lora_4bit_original")
+BNB_ROUTES = (
+    Route("bitsandbytes.functional", None, "dequantize_4bit", _build_bnb("build_dequantize")),
+    Route("bitsandbytes.backends.cuda.ops", None, "_dequantize_4bit_impl",
+          _build_bnb("build_backend_decode")),
+    Route("bitsandbytes.backends.cuda.ops", None, "_dequant_linear_fallback",
+          _build_bnb("build_linear_fallback")),
+    Route("bitsandbytes", None, "matmul_4bit", _build_bnb("build_matmul")),
+)
+ROUTES = (DECODER_ROUTE, RMSNORM_ROUTE, MLP_ROUTE, ROPE_ROUTE, HEAD_ROUTE, PEFT_ROUTE) + BNB_ROUTES
+TARGETS = tuple(sorted({r.module for r in ROUTES}))
 
 
 def patch_qwen2_decoder(module=None):
-    """Fuse residual add + post-attention RMSNorm in Qwen2DecoderLayer.forward."""
-    try:
-        import torch
-
-        module = module or importlib.import_module(_QWEN)
-    except (ImportError, AttributeError):
-        return False
-    cls = getattr(module, "Qwen2DecoderLayer", None)
-    norm_cls = getattr(module, "Qwen2RMSNorm", None)
-    if not isinstance(cls, type) or not isinstance(norm_cls, type):
-        return False
-    original = cls.forward
-    if hasattr(original, _MARKER):
-        return True
-
-    @wraps(original)
-    def forward(self, hidden_states, attention_mask=None, position_ids=None,
-                past_key_values=None, use_cache=False, position_embeddings=None, **kwargs):
-        if not enabled() or type(self) is not cls or not _supported(hidden_states):
-            return original(self, hidden_states, attention_mask=attention_mask,
-                            position_ids=position_ids, past_key_values=past_key_values,
-                            use_cache=use_cache, position_embeddings=position_embeddings,
-                            **kwargs)
-        residual = hidden_states
-        hidden_states = self.input_layernorm(hidden_states)
-        hidden_states, _ = self.self_attn(
-            hidden_states=hidden_states, attention_mask=attention_mask,
-            position_ids=position_ids, past_key_values=past_key_values, use_cache=use_cache,
-            position_embeddings=position_embeddings, **kwargs)
-        norm = self.post_attention_layernorm
-        if (type(norm) is norm_cls and _supported(hidden_states) and _supported(norm.weight)
-                and hidden_states.shape == residual.shape
-                and hidden_states.device == residual.device == norm.weight.device
-                and norm.weight.ndim == 1 and norm.weight.numel() == residual.shape[-1]
-                and not norm._forward_hooks and not norm._forward_pre_hooks):
-            from .kernels.add_rmsnorm import add_rms_norm
-
-            residual, hidden_states = add_rms_norm(residual, hidden_states, norm.weight,
-                                                   norm.variance_epsilon)
-        else:
-            residual = residual + hidden_states
-            hidden_states = norm(residual)
-        hidden_states = self.mlp(hidden_states)
-        return residual + hidden_states
-
-    setattr(forward, _MARKER, original)
-    cls.forward = forward
-    return True
+    return install_route(DECODER_ROUTE, module)
 
 
 def patch_qwen2_rmsnorm(module=None):
-    """Route Qwen2RMSNorm.forward through the HIP RMSNorm (same dtype semantics as eager)."""
-    try:
-        module = module or importlib.import_module(_QWEN)
-    except (ImportError, AttributeError):
-        return False
-    cls = getattr(module, "Qwen2RMSNorm", None)
-    if not isinstance(cls, type):
-        return False
-    original = cls.forward
-    if hasattr(original, _MARKER):
-        return True
-
-    @wraps(original)
-    def forward(self, hidden_states):
-        weight = getattr(self, "weight", None)
-        if (not enabled() or type(self) is not cls or not _supported(hidden_states)
-                or not _supported(weight) or weight.ndim != 1
-                or weight.shape[0] != hidden_states.shape[-1]
-                or weight.device != hidden_states.device or self._forward_hooks
-                or self._forward_pre_hooks):
-            return original(self, hidden_states)
-        from .kernels.rmsnorm import rms_norm
-
-        return rms_norm(hidden_states, weight, self.variance_epsilon)
-
-    setattr(forward, _MARKER, original)
-    cls.forward = forward
-    return True
+    return install_route(RMSNORM_ROUTE, module)
 
 
-def _register_module(name, module):
-    if name == _QWEN:
-        from .mlp import patch_qwen2_mlp_fused
-
-        patch_qwen2_decoder(module)
-        patch_qwen2_rmsnorm(module)
-        patch_qwen2_mlp_fused(module)
-        from .kernels.rope import patch_qwen2_rope
-
-        patch_qwen2_rope(module)
-    elif name == _BNB_FUNCTIONAL:
-        patch_bnb_dequant(module)
+def patch_qwen2_head(module=None):
+    return install_route(HEAD_ROUTE, module)
 
 
-class _PatchLoader(Loader):
+def patch_peft_linear4bit(module=None):
+    return install_route(PEFT_ROUTE, module)
+
+
+def patch_bnb(modules=None):
+    """Install the bitsandbytes routes; ``modules`` maps module names to (fake) modules."""
+    modules = modules or {}
+    return [install_route(r, modules.get(r.module)) for r in BNB_ROUTES]
+
+
+def routes_for(module):
+    """Install the routes of ``module`` and of its loaded submodules (called right after
+    it is imported: a package's submodules may load while the package itself is still
+    initialising, before the attributes a builder checks, such as __version__, exist)."""
+    name = module.__name__
+    for route in ROUTES:
+        if route.module == name:
+            install_route(route, module)
+        elif route.module.startswith(name + ".") and route.module in sys.modules:
+            install_route(route, sys.modules[route.module])
+
+
+class _RoutingLoader(Loader):
     def __init__(self, loader):
         self.loader = loader
 
@@ -185,27 +273,27 @@ class _PatchLoader(Loader):
 
     def exec_module(self, module):
         self.loader.exec_module(module)
-        _register_module(module.__name__, module)
+        routes_for(module)
 
 
-class _PatchFinder(MetaPathFinder):
+class _RoutingFinder(MetaPathFinder):
     _solution_patch_finder = True
 
     def find_spec(self, fullname, path, target=None):
-        if fullname not in _TARGETS:
+        if fullname not in TARGETS:
             return None
         spec = PathFinder.find_spec(fullname, path)
         if spec is None or spec.loader is None:
             return None
-        spec.loader = _PatchLoader(spec.loader)
+        spec.loader = _RoutingLoader(spec.loader)
         return spec
 
 
 def install():
-    """Idempotent: one finder in sys.meta_path; already-imported targets patched now."""
+    """Idempotent: one finder on sys.meta_path; routes of imported targets installed now."""
     if not any(getattr(f, "_solution_patch_finder", False) for f in sys.meta_path):
-        sys.meta_path.insert(0, _PatchFinder())
-    for name in _TARGETS:
+        sys.meta_path.insert(0, _RoutingFinder())
+    for name in TARGETS:
         module = sys.modules.get(name)
         if module is not None:
-            _register_module(name, module)
+            routes_for(module)

@@ -1,8 +1,9 @@
 """Right-padding removal: packed gather / zero-filling scatter with autograd (A16).
 
-Mirrors the reference's solution/unpad.py:51-72 (right_padding_lengths),
-:149-161 (_pack / _scatter) and :184-199 (row-major indices built on the
-device without a host-to-device copy).  The row copies are the HIP kernels
+Interface of the reference's solution/unpad.py: right_padding_lengths
+(:51-72), packing into [1, T, ...] and scattering back with zero padding rows
+(:149-161), and row-major indices of the real tokens built on the device
+without a host-to-device copy (:184-199).  The row copies are the HIP kernels
 ss_unpad_gather / ss_unpad_scatter (bit-exact); the scatter's zero rows and
 copies are one pass, and each op's backward is the other op.
 """
@@ -15,39 +16,37 @@ from . import _lib
 
 
 def right_padding_lengths(rows):
-    """Validate binary nonempty right-padded rows; pure Python (reference unpad.py:51-72)."""
-    if not rows or not rows[0]:
+    """Real-token count of each right-padded mask row, or None if the mask is not one.
+
+    ``rows`` is a sequence of equally long rows of 0/1 values (host data, e.g.
+    a mask's ``tolist()``); a row qualifies when it is ones followed by zeros
+    with at least one one.  Same accept/reject rule as the reference
+    (solution/unpad.py:51-72); no device work.
+    """
+    if not rows or not len(rows[0]):
         return None
-    width, lengths = len(rows[0]), []
+    width = len(rows[0])
+    lengths = []
     for row in rows:
-        if len(row) != width:
+        values = list(row)
+        if len(values) != width or any(v not in (0, 1) for v in values):
             return None
-        count, padding = 0, False
-        for value in row:
-            if value not in (0, 1):
-                return None
-            if value == 0:
-                padding = True
-            elif padding:
-                return None
-            else:
-                count += 1
-        if not count:
+        ones = int(sum(values))
+        if ones == 0 or values != [1] * ones + [0] * (width - ones):
             return None
-        lengths.append(count)
+        lengths.append(ones)
     return tuple(lengths)
 
 
 def indices_from_lengths(lengths, sequence, device):
-    """Row-major packed indices row*S + t (t < length), built on the device."""
-    indices = torch.arange(sum(lengths), device=device, dtype=torch.long)
-    start = 0
-    for row, length in enumerate(lengths):
-        offset = row * sequence - start
-        if offset:
-            indices.narrow(0, start, length).add_(offset)
-        start += length
-    return indices
+    """int64 indices row * sequence + t (t < length) of the real tokens, row-major.
+
+    Built from per-row ``arange`` launches on the device, so no host-to-device
+    copy (and no synchronisation) happens.
+    """
+    parts = [torch.arange(row * sequence, row * sequence + n, device=device, dtype=torch.long)
+             for row, n in enumerate(lengths)]
+    return torch.cat(parts) if parts else torch.empty(0, device=device, dtype=torch.long)
 
 
 @dataclass

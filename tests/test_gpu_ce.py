@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import cross_entropy as oce
-from soupsuck_amd.kernels.cross_entropy import fused_linear_cross_entropy
+from soupsuck_amd.kernels.cross_entropy import default_chunk, fused_linear_cross_entropy
 from tests.gpu_util import np16, rel_norm
 
 pytestmark = pytest.mark.gpu
@@ -49,7 +49,7 @@ def test_matches_oracle(device, n, h, v, ignored, scale, chunk, weight_grad):
     yt = torch.from_numpy(y).to(device)
     loss, entropy, best, lse = fused_linear_cross_entropy(xt, wt, yt, chunk=chunk,
                                                           weight_grad=weight_grad)
-    rl, re, rb, rlse = oce.forward(x, w, y, chunk=chunk or 4096)
+    rl, re, rb, rlse = oce.forward(x, w, y, chunk=chunk or default_chunk(n))
     for a, e in ((loss, rl), (entropy, re), (lse, rlse)):
         assert a.dtype == torch.float32
         np.testing.assert_allclose(np16(a), e, rtol=2e-3, atol=2e-3)

@@ -142,9 +142,37 @@ def test_rank_ops_deterministic_and_leave_counters_zero(device):
         assert torch.equal(lora.project16(a, w, True, 2.0), first_p)
         assert torch.equal(lora.grad16(z, a, True, 2.0), first_g)
     torch.cuda.synchronize()
-    ws = lora._RANK_WORKSPACE[(device.type, device.index if device.index is not None else 0)]
+    ws = lora._RANK_WORKSPACE[(device.index if device.index is not None else 0,
+                               torch.cuda.current_stream(device).cuda_stream)]
     counters = ws[:256 * 1024].view(torch.int32)  # the fixed counter area
     assert int(torch.count_nonzero(counters)) == 0
+
+
+def test_rank_ops_on_concurrent_streams(device):
+    """Rank-16 ops queued on two side streams at once (each stream has its own
+    counter workspace) give the single-stream results, and every workspace's
+    counters are zero afterwards."""
+    from soupsuck_amd import lora
+
+    rng = np.random.default_rng(13)
+    inputs = [torch.from_numpy(rng.standard_normal((990, 8960)).astype(np.float16)).to(device)
+              for _ in range(2)]
+    w = torch.from_numpy((rng.standard_normal((8960, 16)) * 0.1).astype(np.float16)).to(device)
+    z = torch.from_numpy((rng.standard_normal((990, 16)) * 0.3).astype(np.float16)).to(device)
+    ref = [(lora.project16(a, w, True, 2.0), lora.grad16(z, a, True, 2.0)) for a in inputs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device) for _ in inputs]
+    results = [[], []]
+    for _ in range(4):
+        for i, (a, st) in enumerate(zip(inputs, streams)):
+            with torch.cuda.stream(st):
+                results[i].append((lora.project16(a, w, True, 2.0), lora.grad16(z, a, True, 2.0)))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for p, g in results[i]:
+            assert torch.equal(p, ref[i][0]) and torch.equal(g, ref[i][1])
+    for key, ws in lora._RANK_WORKSPACE.items():
+        assert int(torch.count_nonzero(ws[:256 * 1024].view(torch.int32))) == 0, key
 
 
 def test_general_path_matches_fused_and_dropout_runs(device):

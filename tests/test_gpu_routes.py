@@ -1,0 +1,184 @@
+"""GPU tests of the routes: each routed call must reach the HIP entry points and agree
+with the original (eager) code it replaces.
+
+  * PEFT ``Linear4bit.forward`` (reference solution/lora.py:135-163): a PEFT-shaped
+    layer over bnb_compat's Linear4bit reaches ss_qlora_forward / ss_qlora_backward;
+    output within the EXP-002 gate of the original forward, gradients (x, A, B)
+    within relative L2 1e-2;
+  * ``Qwen2ForCausalLM.forward`` (solution/patch.py:167-229): loss of the fused
+    head vs the eager head within 1e-3 relative, with padding labels and with a
+    ``num_items_in_batch`` denominator; the final-norm weight gradient within
+    relative L2 1e-2; no logits materialised;
+  * ``Qwen2DecoderLayer.forward`` (solution/decoder.py:54-89): the fused residual
+    add + norm vs the original layer within fp16 tolerance;
+  * ``bitsandbytes.matmul_4bit`` (fake bitsandbytes 0.50.2 module): routed output
+    bit-identical to nf4_matmul.
+PEFT and bitsandbytes are not installed, so their modules are stand-ins
+(ModuleType objects holding a class / function of the same name and signature).
+"""
+
+import sys
+from types import ModuleType
+
+import pytest
+import torch
+
+from soupsuck_amd import _lib, patch
+from soupsuck_amd.bnb_compat import Linear4bit, quantize_4bit
+from soupsuck_amd.kernels.nf4_gemm import nf4_matmul
+
+pytestmark = pytest.mark.gpu
+
+
+class _Recorder:
+    def __init__(self, names):
+        self.names, self.calls = names, []
+
+    def __enter__(self):
+        for n in self.names:
+            _lib.hooks[n] = (lambda name, args: self.calls.append(name), lambda name, args: None)
+        return self
+
+    def __exit__(self, *exc):
+        for n in self.names:
+            _lib.hooks.pop(n, None)
+
+
+def _rel(a, b):
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _fake_peft_module():
+    module = ModuleType("peft.tuners.lora.bnb")
+
+    class Linear4bit(torch.nn.Module):
+        """The attributes and eager forward of PEFT's bnb LoRA layer (peft 0.20.0)."""
+
+        def __init__(self, base, r, alpha):
+            super().__init__()
+            self.base_layer = base
+            k, n = base.in_features, base.out_features
+            self.lora_A = torch.nn.ModuleDict({"default": torch.nn.Linear(k, r, bias=False)})
+            self.lora_B = torch.nn.ModuleDict({"default": torch.nn.Linear(r, n, bias=False)})
+            self.lora_dropout = torch.nn.ModuleDict({"default": torch.nn.Identity()})
+            self.scaling = {"default": alpha / r}
+            self.active_adapters = ["default"]
+            self.disable_adapters = self.merged = False
+            self.use_dora, self.lora_variant, self.lora_bias = {}, {}, {}
+
+        def forward(self, x, *args, **kwargs):
+            result = self.base_layer(x)
+            a, b = self.lora_A["default"], self.lora_B["default"]
+            lora = b(a(self.lora_dropout["default"](x.to(a.weight.dtype))))
+            return result + (lora * self.scaling["default"]).to(result.dtype)
+
+    module.Linear4bit = Linear4bit
+    return module
+
+
+def test_peft_linear4bit_reaches_the_fused_projection(device):
+    module = _fake_peft_module()
+    assert patch.install_route(patch.PEFT_ROUTE, module)
+    torch.manual_seed(0)
+    k, n, t = 1536, 256, 300
+    base = Linear4bit(k, n, bias=True, compute_dtype=torch.float16)
+    with torch.no_grad():
+        base.weight.data.normal_(0, 0.02)
+        base.bias.normal_(0, 0.02)
+    base = base.to(device)
+    layer = module.Linear4bit(base, 16, 32).to(device).half()
+    with torch.no_grad():
+        layer.lora_B["default"].weight.normal_(0, 0.01)
+    x = torch.randn(2, t // 2, k, device=device, dtype=torch.float16, requires_grad=True)
+    g = torch.randn(2, t // 2, n, device=device, dtype=torch.float16)
+    with _Recorder(["ss_qlora_forward", "ss_qlora_backward"]) as rec:
+        out = layer(x)
+        out.backward(g)
+    assert rec.calls == ["ss_qlora_forward", "ss_qlora_backward"]
+    routed = (x.grad.clone(), layer.lora_A["default"].weight.grad.clone(),
+              layer.lora_B["default"].weight.grad.clone())
+    x.grad = None
+    layer.zero_grad()
+    original = getattr(module.Linear4bit.forward, "_solution_lora_4bit_original")
+    eager = original(layer, x)
+    eager.backward(g)
+    torch.testing.assert_close(out, eager, rtol=2e-3, atol=2e-3)
+    eager_grads = (x.grad, layer.lora_A["default"].weight.grad,
+                   layer.lora_B["default"].weight.grad)
+    for name, got, ref in zip(("dX", "dA", "dB"), routed, eager_grads):
+        assert _rel(got, ref) < 1e-2, name
+
+
+def _tiny_causal_lm(device, dtype):
+    from transformers import Qwen2Config
+    from transformers.models.qwen2 import modeling_qwen2 as qwen
+
+    cfg = Qwen2Config(hidden_size=128, intermediate_size=256, num_attention_heads=4,
+                      num_key_value_heads=2, num_hidden_layers=2, vocab_size=1000,
+                      tie_word_embeddings=True)
+    torch.manual_seed(1)
+    return qwen, qwen.Qwen2ForCausalLM(cfg).to(device=device, dtype=dtype)
+
+
+@pytest.mark.parametrize("num_items", [None, 37])
+def test_causal_lm_head_route_matches_eager(device, num_items):
+    qwen, model = _tiny_causal_lm(device, torch.float32)
+    model.model.embed_tokens.weight.requires_grad_(False)   # frozen tied head (QLoRA)
+    assert patch.install_route(patch.HEAD_ROUTE, qwen)
+    ids = torch.randint(0, 1000, (3, 40), device=device)
+    labels = ids.clone()
+    labels[0, 30:] = -100
+    labels[2, 10:] = -100
+    kwargs = {} if num_items is None else {"num_items_in_batch": num_items}
+    with _Recorder(["ss_ce_stats", "ss_ce_derivative"]) as rec:
+        out = model(input_ids=ids, labels=labels, **kwargs)
+        out.loss.backward()
+    assert out.logits is None and "ss_ce_stats" in rec.calls and "ss_ce_derivative" in rec.calls
+    routed_grad = model.model.norm.weight.grad.clone()
+    model.zero_grad()
+    original = getattr(qwen.Qwen2ForCausalLM.forward, patch.MARKER)
+    ref = original(model, input_ids=ids, labels=labels, **kwargs)
+    ref.loss.backward()
+    assert abs(out.loss.item() - ref.loss.item()) <= 1e-3 * abs(ref.loss.item())
+    assert _rel(routed_grad, model.model.norm.weight.grad) < 1e-2
+    step = model._soupsuck_head_step
+    assert step.token_loss.shape == labels.shape
+    assert int(step.labelled) == int((labels[:, 1:] != -100).sum())
+
+
+def test_decoder_route_matches_original_layer(device):
+    from transformers import Qwen2Config
+    from transformers.models.qwen2 import modeling_qwen2 as qwen
+
+    assert patch.install_route(patch.DECODER_ROUTE, qwen)
+    cfg = Qwen2Config(hidden_size=256, intermediate_size=512, num_attention_heads=4,
+                      num_key_value_heads=2, num_hidden_layers=1, vocab_size=64)
+    torch.manual_seed(2)
+    layer = qwen.Qwen2DecoderLayer(cfg, 0).to(device=device, dtype=torch.float16)
+    h = torch.randn(2, 33, 256, device=device, dtype=torch.float16)
+    emb = qwen.Qwen2RotaryEmbedding(cfg).to(device)(h, torch.arange(33, device=device)[None])
+    with _Recorder(["ss_add_rmsnorm_fwd"]) as rec:
+        got = layer(h, position_embeddings=emb)
+    assert rec.calls == ["ss_add_rmsnorm_fwd"]
+    original = getattr(qwen.Qwen2DecoderLayer.forward, patch.MARKER)
+    torch.testing.assert_close(got, original(layer, h, position_embeddings=emb),
+                               rtol=2e-3, atol=2e-3)
+
+
+def test_bnb_matmul_route_runs_the_nf4_gemm(device, monkeypatch):
+    fake = ModuleType("bitsandbytes")
+    fake.__version__ = "0.50.2"
+
+    def matmul_4bit(A, B, quant_state, out=None, bias=None):
+        raise AssertionError("the original must not run for a supported call")
+
+    fake.matmul_4bit = matmul_4bit
+    monkeypatch.setitem(sys.modules, "bitsandbytes", fake)
+    assert patch.install_route(patch.BNB_ROUTES[3], fake)
+    w = (torch.randn(640, 1536, device=device) * 0.02).half()
+    packed, state = quantize_4bit(w)
+    x = torch.randn(2, 70, 1536, device=device, dtype=torch.float16)
+    bias = (torch.randn(640, device=device) * 0.1).half()
+    got = fake.matmul_4bit(x, packed.t(), state, bias=bias)
+    assert torch.equal(got, nf4_matmul(x, packed, state, bias=bias))
