@@ -74,6 +74,13 @@ def parse():
     p.add_argument("--profile-mlp", action="store_true",
                    help="only run the configs[1] layer's frozen NF4 MLP forward + backward "
                         "(SwiGLU as its own kernels) --reps times at the bench's T and exit")
+    p.add_argument("--profile-sweep", default="", metavar="NAME:T:MODE",
+                   help="only run one configs[4] point (NAME in q_o, k_v, gate_up, down; MODE "
+                        "fwd or dx) --reps times, rotating weight copies as the sweep does, "
+                        "and exit (for rocprofv3 kernel-trace and counter passes)")
+    p.add_argument("--profile-ce", action="store_true",
+                   help="only run the configs[3] fused CE forward + backward --reps times and "
+                        "exit (for a rocprofv3 kernel trace)")
     p.add_argument("--reps", type=int, default=20)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
@@ -246,6 +253,46 @@ SWEEP_SHAPES = [("q_o", 3584, 3584), ("k_v", 512, 3584), ("gate_up", 18944, 3584
 SWEEP_T = [1, 16, 128, 2048, 16384]
 
 
+def sweep_weight(torch, name, n, k, gen, dev):
+    """Quantized weight of one configs[4] shape and enough copies of its codes and
+    block scales (> 300 MB in total) that rotating over them reads HBM, not the
+    256 MB last-level cache."""
+    from soupsuck_amd.bnb_compat import quantize_4bit
+
+    w = (torch.randn((n, k), device=dev, generator=gen) * 0.02).half()
+    packed, st = quantize_4bit(w)
+    del w
+    wbytes = n * k // 2 + n * k // 64 + 4 * ((n * k // 64 + 255) // 256)
+    copies = max(1, -(-300_000_000 // wbytes))
+    states = [(packed.clone(), st.absmax.clone()) for _ in range(copies)]
+    rest = (st.state2.absmax.data_ptr(), st.state2.code.data_ptr(), st.offset.data_ptr())
+    return {"states": states, "rest": rest, "copies": copies, "wbytes": wbytes, "keep": st}
+
+
+def sweep_call(torch, _lib, weight, n, k, t, mode, gen, dev):
+    """call(i, stream) of one configs[4] point (weight copy i % copies) and its buffers."""
+    lib = _lib.load()
+    size = lib.ss_nf4_gemm_workspace_size(t, n, k)
+    ws = torch.empty(max(size, 16), device=dev, dtype=torch.uint8)
+    a = torch.randn((t, n if mode == "dx" else k), device=dev, generator=gen).half()
+    o = torch.empty((t, k if mode == "dx" else n), device=dev, dtype=torch.float16)
+    states, rest, copies = weight["states"], weight["rest"], weight["copies"]
+
+    def call(i, stream):
+        pk, am = states[i % copies]
+        if mode == "dx":
+            _lib.call("ss_nf4_gemm_dx", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
+                      am.data_ptr(), *rest, n, k, o.data_ptr(), o.stride(0), 0,
+                      ws.data_ptr(), size, stream)
+        else:
+            _lib.call("ss_nf4_gemm_fwd", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
+                      am.data_ptr(), *rest, n, k, None, o.data_ptr(), o.stride(0),
+                      ws.data_ptr(), size, stream)
+
+    call.buffers = (ws, a, o)
+    return call
+
+
 def sweep(torch, _lib):
     """NF4 forward and dX at every configs[4] shape and T through the C ABI.
 
@@ -255,43 +302,19 @@ def sweep(torch, _lib):
     from HBM.  Algorithmic bytes: packed codes + qabs + absmax2 + the fp16
     activation read and output written; flops 2*T*N*K.  roofline_frac =
     max(bytes / 8 TB/s, flops / 2.5 PFLOP/s) / measured time."""
-    from soupsuck_amd.bnb_compat import quantize_4bit
-
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
     out = {}
-    lib = _lib.load()
     for name, n, k in SWEEP_SHAPES:
-        w = (torch.randn((n, k), device=dev, generator=gen) * 0.02).half()
-        packed, st = quantize_4bit(w)
-        del w
-        wbytes = n * k // 2 + n * k // 64 + 4 * ((n * k // 64 + 255) // 256)
-        copies = max(1, -(-300_000_000 // wbytes))
-        states = [(packed.clone(), st.absmax.clone()) for _ in range(copies)]
-        rest = (st.state2.absmax.data_ptr(), st.state2.code.data_ptr(), st.offset.data_ptr())
+        weight = sweep_weight(torch, name, n, k, gen, dev)
         for t in SWEEP_T:
-            size = lib.ss_nf4_gemm_workspace_size(t, n, k)
-            ws = torch.empty(max(size, 16), device=dev, dtype=torch.uint8)
             for mode in ("fwd", "dx"):
-                a = torch.randn((t, n if mode == "dx" else k), device=dev, generator=gen).half()
-                o = torch.empty((t, k if mode == "dx" else n), device=dev, dtype=torch.float16)
-
-                def call(i, stream):
-                    pk, am = states[i % copies]
-                    if mode == "dx":
-                        _lib.call("ss_nf4_gemm_dx", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
-                                  am.data_ptr(), *rest, n, k, o.data_ptr(), o.stride(0), 0,
-                                  ws.data_ptr(), size, stream)
-                    else:
-                        _lib.call("ss_nf4_gemm_fwd", a.data_ptr(), a.stride(0), t, pk.data_ptr(),
-                                  am.data_ptr(), *rest, n, k, None, o.data_ptr(), o.stride(0),
-                                  ws.data_ptr(), size, stream)
-
+                call = sweep_call(torch, _lib, weight, n, k, t, mode, gen, dev)
                 flops = 2.0 * t * n * k
                 reps = max(4, min(64, int(2e10 / max(flops, 1.0))))
                 us = graph_us(torch, _lib, call, reps)
-                moved = wbytes + 2 * t * (n + k)
+                moved = weight["wbytes"] + 2 * t * (n + k)
                 bound_us = max(moved / PEAK_HBM_GBS / 1e3, flops / PEAK_FP16_TFLOPS / 1e6)
                 out[f"{name} T={t} {mode}"] = {
                     "N": n, "K": k, "us": round(us, 2), "GB/s": round(moved / us / 1e3, 1),
@@ -299,11 +322,65 @@ def sweep(torch, _lib):
                     "bound": "hbm" if moved / PEAK_HBM_GBS / 1e3 >= flops / PEAK_FP16_TFLOPS / 1e6
                     else "mfma",
                     "roofline_frac": round(bound_us / us, 4)}
-                del a, o
-            del ws
-        del states, packed, st
+                del call
+        del weight
         torch.cuda.empty_cache()
+    out["vendor_ceiling"] = vendor_ceiling(torch)
     return out
+
+
+def vendor_ceiling(torch):
+    """Same-box reference point: torch.matmul (hipBLASLt) on fp16 operands already
+    in HBM, at 8192^3 and at the configs[4] T=16384 gate/up and down products
+    (X [T, K] . W^T with W [N, K] row-major).  Average of 10 calls between HIP
+    events after 3 warm-ups; a probe of what the vendor GEMM reaches on this
+    board, not a target."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(3)
+    res = {}
+    for label, m, n, k in (("8192^3", 8192, 8192, 8192),
+                           ("gate_up T=16384 (16384x18944x3584)", 16384, 18944, 3584),
+                           ("down T=16384 (16384x3584x18944)", 16384, 3584, 18944)):
+        a = torch.randn((m, k), device=dev, generator=gen).half()
+        w = torch.randn((n, k), device=dev, generator=gen).half()
+        c = torch.empty((m, n), device=dev, dtype=torch.float16)
+        for _ in range(3):
+            torch.matmul(a, w.t(), out=c)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            torch.matmul(a, w.t(), out=c)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) / 10 * 1e3
+        tf = 2.0 * m * n * k / us / 1e6
+        res[label] = {"us": round(us, 1), "TFLOP/s": round(tf, 1),
+                      "frac_of_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+        del a, w, c
+    torch.cuda.empty_cache()
+    return res
+
+
+def profile_sweep(spec, reps):
+    """Repeat one configs[4] point (eager calls through the C ABI), rotating copies."""
+    import torch
+
+    from soupsuck_amd import _lib
+
+    name, t, mode = spec.split(":")
+    t = int(t)
+    n, k = next((n, k) for nm, n, k in SWEEP_SHAPES if nm == name)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    weight = sweep_weight(torch, name, n, k, gen, dev)
+    call = sweep_call(torch, _lib, weight, n, k, t, mode, gen, dev)
+    stream = _lib.stream(dev)
+    torch.cuda.synchronize()
+    for i in range(reps):
+        call(i, stream)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_sweep": spec, "N": n, "K": k, "reps": reps,
+                      "weight_copies": weight["copies"]}), flush=True)
 
 
 def graph_us(torch, _lib, call, reps):
@@ -349,12 +426,11 @@ def other_configs(torch, _lib):
       gather       T rows read + T rows written (4 H B per token);
       scatter      T rows read + B*S rows written + the int32 inverse map.
     CE is timed whole through fused_linear_cross_entropy
-    (forward, then backward with the lm_head gradient), host clock around
-    synchronized calls, median of 5; flops 2 T V H forward and 3 x 2 T_valid V H
+    (forward, then backward with the lm_head gradient), HIP events on the
+    stream around each, median of 5; flops 2 T V H forward and 3 x 2 T_valid V H
     backward (recomputed logits, dX, dW)."""
     from soupsuck_amd import unpad
     from soupsuck_amd.bnb_compat import quantize_4bit
-    from soupsuck_amd.kernels.cross_entropy import fused_linear_cross_entropy
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -578,31 +654,23 @@ def other_configs(torch, _lib):
     del parts, xm, gm
 
     # chunked fused linear CE, hidden [826, 1536], tied head [151936, 1536].
-    t, v = 826, 151936
-    hidden = torch.randn((t, h), device=dev, generator=gen).half()
-    head = (torch.randn((v, h), device=dev, generator=gen) * 0.02).half()
-    labels = torch.randint(0, v, (t,), device=dev, generator=gen)
-    ignored = torch.rand(t, device=dev, generator=gen) < 0.365
-    labels[ignored] = -100
-    valid = int((labels != -100).sum().item())
-    hd = hidden.clone().requires_grad_()
-    hw = head.clone().requires_grad_()
+    hd, hw, labels, valid = ce_inputs(torch, gen, dev)
+    t, v = hd.shape[0], hw.shape[0]
     fwd_ms, tot_ms = [], []
     for rep in range(6):
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         hd.grad = None
         hw.grad = None
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        loss, _, _, _ = fused_linear_cross_entropy(hd, hw, labels, chunk=8192, weight_grad=True)
-        mean = loss.sum() / valid
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
+        e0.record()
+        mean = ce_forward(hd, hw, labels, valid)
+        e1.record()
         mean.backward()
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
+        e2.record()
+        e2.synchronize()
         if rep:
-            fwd_ms.append(1e3 * (t1 - t0))
-            tot_ms.append(1e3 * (t2 - t0))
+            fwd_ms.append(e0.elapsed_time(e1))
+            tot_ms.append(e0.elapsed_time(e2))
     fwd = statistics.median(fwd_ms)
     tot = statistics.median(tot_ms)
     f_fwd = 2.0 * t * v * h
@@ -614,11 +682,61 @@ def other_configs(torch, _lib):
         "fwd_bwd_TFLOP/s": round((f_fwd + f_bwd) / tot / 1e9, 1),
         "bound": "mfma",
         "roofline_frac": round((f_fwd + f_bwd) / PEAK_FP16_TFLOPS / 1e9 / tot, 4),
-        "timing": "host clock around synchronized calls (includes the backward's two host "
-                  "syncs), median of 5 after 1 warm-up"}
-    del hidden, head, hd, hw
+        "timing": "HIP events on the stream (GPU clock) around the forward and the backward, "
+                  "median of 5 after 1 warm-up; the backward reads the head-gradient gain "
+                  "max|g|/1024 on the host once (its idle gap is inside the time)"}
+    del hd, hw
     torch.cuda.empty_cache()
     return out
+
+
+def ce_inputs(torch, gen, dev):
+    """hidden [826, 1536] ~ N(0,1), tied head [151936, 1536] ~ N(0, 0.02),
+    labels uniform over the vocabulary with 36.5 % set to -100 (both trainable)."""
+    t, v, h = 826, 151936, 1536
+    hidden = torch.randn((t, h), device=dev, generator=gen).half()
+    head = (torch.randn((v, h), device=dev, generator=gen) * 0.02).half()
+    labels = torch.randint(0, v, (t,), device=dev, generator=gen)
+    ignored = torch.rand(t, device=dev, generator=gen) < 0.365
+    labels[ignored] = -100
+    valid = int((labels != -100).sum().item())
+    return hidden.requires_grad_(), head.requires_grad_(), labels, valid
+
+
+def ce_forward(hidden, head, labels, valid):
+    from soupsuck_amd.kernels.cross_entropy import fused_linear_cross_entropy
+
+    loss, _, _, _ = fused_linear_cross_entropy(hidden, head, labels, chunk=8192, weight_grad=True)
+    return loss.sum() / valid
+
+
+def profile_ce(reps):
+    """Repeat the configs[3] fused CE forward + backward (with the head gradient)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    hd, hw, labels, valid = ce_inputs(torch, gen, dev)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        hd.grad = None
+        hw.grad = None
+        ce_forward(hd, hw, labels, valid).backward()
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_ce": True, "tokens": hd.shape[0], "valid": valid, "reps": reps}),
+          flush=True)
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(layer, xs, gs, budget_s):
@@ -670,6 +788,12 @@ def main():
         return
     if args.profile_call:
         profile_call(args.profile_call, args.reps)
+        return
+    if args.profile_sweep:
+        profile_sweep(args.profile_sweep, args.reps)
+        return
+    if args.profile_ce:
+        profile_ce(args.reps)
         return
 
     import torch
@@ -777,7 +901,7 @@ def main():
     if not args.no_cpu_baseline:
         med, reps, threads = cpu_baseline(layer, xs, gs, args.cpu_seconds)
         cpu = {"value": round(flops / med / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-               "kind": "port",
+               "kind": "port", "cpu_model": cpu_model(),
                "sample": (f"{reps} full configs[1] steps (7 projections fwd+bwd, T={tokens}) of "
                           f"oracle/baseline.py: A2 decode + fp32 BLAS GEMMs; median "
                           f"{med * 1e3:.1f} ms/step")}

@@ -9,7 +9,8 @@ differentiable, ValueError before launch) and its numerics (:1-43):
             e^(z-m) z, target logit) and the first argmax are merged chunk by
             chunk (ss_ce_stats); lse = m + log s, loss = lse - z_target (0 for
             ignored rows), entropy = lse - t/s (ss_ce_outputs);
-  backward  rows with a target only (one nonzero synchronisation); each chunk
+  backward  rows with a target only (found in the forward: a stable sort and a
+            count copied to pinned memory early, so no stall); each chunk
             is recomputed and dz = fp16((softmax - onehot) g / gain) with the
             per-row gain max(|g|, 1e-30)/1024 (ss_ce_derivative); dX = dz . W_c
             accumulated in fp32 over chunks, multiplied back by the gain and
@@ -89,15 +90,36 @@ def _forward(hidden16, weight, targets, ignore_index, chunk):
     return loss, entropy, best, lse
 
 
+class _KeptRows:
+    """Rows with a target, found in the forward without a host synchronisation.
+
+    A stable sort puts the labelled rows first (in row order); their count is
+    copied to pinned host memory as soon as it is computed, ahead of the
+    forward's GEMMs, so by the time the backward needs it the copy has long
+    completed and reading it does not stall the device."""
+
+    def __init__(self, targets, ignore_index):
+        kept = targets != ignore_index
+        self.order = torch.argsort((~kept).to(torch.int8), stable=True)
+        self.count_host = torch.empty((), dtype=torch.int64, pin_memory=True)
+        self.count_host.copy_(kept.sum(), non_blocking=True)
+        self.ready = torch.cuda.Event()
+        self.ready.record()
+
+    def indices(self):
+        self.ready.synchronize()
+        return self.order[:int(self.count_host)]
+
+
 class _Backward:
     """Gradients of the summed loss w.r.t. hidden and (optionally) the head."""
 
-    def __init__(self, hidden16, weight, targets, lse, grad, ignore_index, chunk):
+    def __init__(self, hidden16, weight, targets, lse, grad, ignore_index, chunk, kept):
         self.weight, self.ignore, self.chunk = weight, ignore_index, chunk
         self.dev = hidden16.device
         self.stream = _lib.stream(self.dev)
         self.full_grad = grad
-        self.kept = torch.nonzero(targets != ignore_index, as_tuple=False).flatten()
+        self.kept = kept.indices()
         self.count = self.kept.numel()
         if self.count:
             self.h = _gather_rows(hidden16, self.kept)
@@ -161,6 +183,7 @@ class LinearCrossEntropy(torch.autograd.Function):
         hidden16 = hidden.to(torch.float16).contiguous()
         targets = targets.contiguous()
         chunk = chunk or default_chunk(hidden16.shape[0])
+        ctx.kept = _KeptRows(targets, ignore_index) if hidden16.shape[0] else None
         loss, entropy, best, lse = _forward(hidden16, weight, targets, ignore_index, chunk)
         ctx.save_for_backward(hidden16, weight, targets, lse)
         ctx.setup = (hidden.dtype, ignore_index, chunk, weight_grad)
@@ -184,7 +207,7 @@ class LinearCrossEntropy(torch.autograd.Function):
             if want_w else None
         if hidden16.shape[0]:
             grad = grad_loss.float().contiguous()
-            back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk)
+            back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk, ctx.kept)
             if back.count:
                 back.run(dx, dw)
         return dx, dw, None, None, None, None
