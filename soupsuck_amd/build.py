@@ -32,13 +32,22 @@ def sources():
     return sorted(str(p) for p in CSRC.glob("*.hip"))
 
 
-def build(verbose=False, jobs=None):
-    """Compile all sources to objects in parallel, then link the shared library."""
-    objdir = PACKAGE / "_build"
-    objdir.mkdir(exist_ok=True)
+def build(verbose=False, jobs=None, address_sanitizer=False):
+    """Compile all sources to objects in parallel, then link the shared library.
+
+    address_sanitizer=True builds a copy with AddressSanitizer in the host code
+    only (the device code is compiled as usual), for CPU runs of the C ABI's
+    argument checks and host arithmetic, into _build/asan/libsoupsuck_amd.so;
+    the GPU library is untouched.
+    """
+    objdir = PACKAGE / "_build" / ("asan" if address_sanitizer else "")
+    objdir.mkdir(parents=True, exist_ok=True)
     common = [hipcc(), f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
               "-ffp-contract=off", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
               "-Wall", "-Wno-unused-function", "-I", str(PACKAGE.parent / "include")]
+    sanitize = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+    if address_sanitizer:
+        common = common + ["-g"] + sanitize
     procs = []
     objects = []
     for src in sources():
@@ -61,14 +70,33 @@ def build(verbose=False, jobs=None):
     if failed:
         msg = "\n".join(f"--- {src}\n{text}" for src, text in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
-    tmp = str(LIBRARY) + ".tmp"
+    target = objdir / LIBRARY.name if address_sanitizer else LIBRARY
+    tmp = str(target) + ".tmp"
     link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objects
+    if address_sanitizer:
+        link += sanitize
     res = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stdout.decode(errors="replace"))
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, target)
+    return target
+
+
+def built_library(address_sanitizer=False):
+    """The library, built first if it is missing or older than a source or header."""
+    target = (PACKAGE / "_build" / "asan" / LIBRARY.name) if address_sanitizer else LIBRARY
+    inputs = [Path(p) for p in sources()] + list(CSRC.glob("*.h")) + \
+        list((PACKAGE.parent / "include").glob("*.h"))
+    if not target.exists() or target.stat().st_mtime < max(p.stat().st_mtime for p in inputs):
+        return build(address_sanitizer=address_sanitizer)
+    return target
+
+
+def asan_runtime():
+    """Path of the compiler's AddressSanitizer runtime (to preload into a host process)."""
+    found = sorted(Path("/opt/rocm/llvm/lib/clang").glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return found[-1] if found else None
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, address_sanitizer="--asan" in sys.argv))

@@ -30,6 +30,7 @@
 #include "gemm.h"
 #include "soupsuck_amd.h"
 #include "rank16.h"
+#include "tuning.h"
 
 namespace ss {
 
@@ -447,13 +448,7 @@ using TileSmall = Tile<64, 64, 64, 32, 32>;
 using TileWide = Tile<256, 128, 64, 128, 64>;
 using TileTall = Tile<128, 256, 64, 64, 128>;
 
-static int remap_setting() {
-  static int v = [] {
-    const char* e = getenv("SS_GEMM_REMAP");
-    return e ? atoi(e) : 1;
-  }();
-  return v;
-}
+static int remap_setting() { return SS_TUNE_GEMM_REMAP; }
 
 template <class T, int OPA, int OPB, int CT, int EPI>
 static int launch(const GemmParams& p0, hipStream_t stream, const char* name) {
@@ -477,17 +472,11 @@ static int launch(const GemmParams& p0, hipStream_t stream, const char* name) {
 
 // Tile choice: 128x128 when it still gives every CU a workgroup, else 64x64.
 // The 256x128 / 128x256 tiles (one wave per SIMD) measured slower than
-// 128x128 at every Qwen shape, so only SS_GEMM_TILE (1..4 = 64x64, 128x128,
-// 256x128, 128x256) selects them; it is a tuning knob read once per process.
+// 128x128 at every Qwen shape, so only SS_TUNE_GEMM_TILE (1..4 = 64x64,
+// 128x128, 256x128, 128x256; a build-time constant) selects them.
 enum TileId { TILE_AUTO = 0, TILE_SMALL = 1, TILE_BIG = 2, TILE_WIDE = 3, TILE_TALL = 4 };
 
-static int tile_override() {
-  static int v = [] {
-    const char* e = getenv("SS_GEMM_TILE");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
+static int tile_override() { return SS_TUNE_GEMM_TILE; }
 
 static int pick_tile(int64_t m, int64_t n) {
   const int forced = tile_override();
@@ -496,15 +485,8 @@ static int pick_tile(int64_t m, int64_t n) {
   return TILE_SMALL;
 }
 
-// SS_GEMM_NT=0 keeps dense NT products on the register-staged kernel (A/B
-// comparison knob, read once per process).
-static bool nt_enabled() {
-  static const bool v = [] {
-    const char* e = getenv("SS_GEMM_NT");
-    return !(e && atoi(e) == 0);
-  }();
-  return v;
-}
+// SS_TUNE_GEMM_NT = 0 keeps dense NT products on the register-staged kernel.
+static bool nt_enabled() { return SS_TUNE_GEMM_NT != 0; }
 
 template <int OPA, int OPB, int CT, int EPI = EPI_PLAIN>
 static int dispatch(const GemmParams& p, hipStream_t stream, const char* name,
@@ -553,14 +535,8 @@ static size_t decoded_bytes(int64_t n, int64_t k) {
 // running the dense MFMA GEMM beats decoding every W tile again for each of
 // the ceil(T/BM) row tiles: in-loop decode costs about 1/(2*BM) VALU decodes
 // per flop, more than the VALU can issue next to full-rate MFMA.
-// SS_NF4_DECODE_FIRST_T overrides the crossover (tuning knob).
-static int64_t decode_first_threshold() {
-  static const int64_t threshold = [] {
-    const char* e = getenv("SS_NF4_DECODE_FIRST_T");
-    return e ? (int64_t)atoll(e) : (int64_t)256;
-  }();
-  return threshold;
-}
+// SS_TUNE_NF4_DECODE_FIRST_T sets the crossover.
+static int64_t decode_first_threshold() { return SS_TUNE_NF4_DECODE_FIRST_T; }
 
 // Scratch the forward alone needs (the forward part of
 // ss_nf4_gemm_workspace_size).
@@ -621,32 +597,10 @@ static int check_nf4(const char* fn, const uint8_t* packed, const uint8_t* qabs,
 
 namespace ss {
 
-// SS_NF4_STREAM=0 turns the streaming small-T kernels off (A/B timing knob).
-static bool stream_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("SS_NF4_STREAM");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
-
-// SS_NF4_FUSED=0 turns the fused NF4 GEMM off (decode-first instead; A/B knob).
-static bool nf4_fused_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("SS_NF4_FUSED");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
-
-// SS_NF4_FUSED=2 takes the fused NF4 GEMM wherever it applies (A/B knob).
-static bool nf4_fused_forced() {
-  static const bool on = [] {
-    const char* e = getenv("SS_NF4_FUSED");
-    return e && e[0] == '2';
-  }();
-  return on;
-}
+// Build-time switches of the small-T and fused paths (tuning.h).
+static bool stream_enabled() { return SS_TUNE_NF4_STREAM != 0; }
+static bool nf4_fused_enabled() { return SS_TUNE_NF4_FUSED != 0; }
+static bool nf4_fused_forced() { return SS_TUNE_NF4_FUSED == 2; }
 
 // Decode-first path with the decode fused into the preparation launch of the
 // QLoRA step (rank-16 jobs + decode in one launch): T above the skinny range,

@@ -20,6 +20,7 @@
 // (vmcnt(0)) before every LDS read, draining the pipeline; the waits are
 // explicit instead.
 
+#include "tuning.h"
 #include <stdlib.h>
 
 #include "nt_core.h"
@@ -500,17 +501,11 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 //   long K with few 128x128 tiles: 128x128 split over k so that about 512
 //   workgroups run (each split at least 1024 k);
 //   128x128 while it gives half the CUs a tile; else 64x64.
-// SS_NT_TILE (1..8, the configurations above in order) and SS_NT_SPLITS
-// override the choice (tuning knobs read once per process).
+// SS_TUNE_NT_TILE (1..8, the configurations above in order) and
+// SS_TUNE_NT_SPLITS override the choice (build-time constants, tuning.h).
 NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
-  static const int forced = [] {
-    const char* e = getenv("SS_NT_TILE");
-    return e ? atoi(e) : 0;
-  }();
-  static const int forced_splits = [] {
-    const char* e = getenv("SS_NT_SPLITS");
-    return e ? atoi(e) : 0;
-  }();
+  constexpr int forced = SS_TUNE_NT_TILE;
+  constexpr int forced_splits = SS_TUNE_NT_SPLITS;
   NtPlan plan{1, 1, k};
   const int64_t t256 = cdiv(m, 256) * cdiv(n, 256);
   const int64_t t128 = cdiv(m, 128) * cdiv(n, 128);
@@ -555,25 +550,12 @@ size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k) {
   return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
 }
 
-// SS_NT_PINGPONG=0 keeps the 8-wave configurations on the lockstep main loop
-// (A/B knob, read once per process).
-static bool pingpong_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("SS_NT_PINGPONG");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
+// SS_TUNE_NT_PINGPONG = 0 keeps the 8-wave configurations on the lockstep
+// main loop (tuning.h).
+static bool pingpong_enabled() { return SS_TUNE_NT_PINGPONG != 0; }
 
-// SS_NT_STAGED=0 keeps fp16 epilogues on direct 2-byte stores (A/B knob,
-// read once per process).
-bool staged_epilogue_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("SS_NT_STAGED");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
+// SS_TUNE_NT_STAGED = 0 keeps fp16 epilogues on direct 2-byte stores.
+bool staged_epilogue_enabled() { return SS_TUNE_NT_STAGED != 0; }
 
 int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* partials,
             size_t partial_bytes) {

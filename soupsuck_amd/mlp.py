@@ -16,8 +16,8 @@ keeps gate and up (fp16) for the backward, or only x with ``recompute=True``
                                                   second accumulating in fp32)
 
 The activation in the GEMM epilogue (the ``*_swiglu`` entry points,
-SS_MLP_GLU_EPILOGUE=1) gives bit-identical results; it is off by default
-because it measured slower (see ``_epilogue_fusion``).
+``fuse=True``) gives bit-identical results; it is off by default
+because it measured slower (see ``GLU_IN_EPILOGUE``).
 
 Numerics follow the reference's node (bnb fp16 projections, the fp32 SwiGLU
 tile engine of solution/kernels/swiglu_fused.py): every projection output is
@@ -89,16 +89,15 @@ def _state_args(packed, state):
             state.state2.code.data_ptr(), state.offset.data_ptr())
 
 
-def _epilogue_fusion():
-    """SS_MLP_GLU_EPILOGUE=1 applies the SwiGLU in the GEMM epilogues; the
-    default runs it as its own HBM-bound kernels.  Measured on MI355X at the
-    configs[1] shapes (T = 990): alone, the down dX with the activation in its
-    epilogue takes 66-70 us against 54-59 + 17 us for the product and the
-    kernel; inside the whole MLP step the epilogue variant measured 398-414 us
-    against 386-401 us in the same runs, so the kernels stay the default
-    (every output tile reaches its epilogue at once, so the extra gate / up
-    traffic there overlaps no MFMA work)."""
-    return os.environ.get("SS_MLP_GLU_EPILOGUE", "0") == "1"
+# Where the SwiGLU runs by default: its own HBM-bound kernels (False) or the
+# GEMM epilogues (True; bit-identical).  Measured on MI355X at the configs[1]
+# shapes (T = 990): alone, the down dX with the activation in its epilogue takes
+# 66-70 us against 54-59 + 17 us for the product and the kernel; inside the
+# whole MLP step the epilogue variant measured 398-414 us against 386-401 us in
+# the same runs (every output tile reaches its epilogue at once, so the extra
+# gate / up traffic there overlaps no MFMA work).  Callers choose per call with
+# ``fuse=``.
+GLU_IN_EPILOGUE = False
 
 
 def gate_up_swiglu(x2d, gate_proj, up_proj, keep=True, fuse=None):
@@ -107,7 +106,7 @@ def gate_up_swiglu(x2d, gate_proj, up_proj, keep=True, fuse=None):
     packed_u, state_u, _, _ = up_proj
     t = x2d.shape[0]
     gate = nf4_forward_2d(x2d, packed_g, state_g, n, k)
-    if not (_epilogue_fusion() if fuse is None else fuse):
+    if not (GLU_IN_EPILOGUE if fuse is None else fuse):
         up = nf4_forward_2d(x2d, packed_u, state_u, n, k)
         act = swiglu_fused_forward(gate, up)
         return (gate if keep else None), (up if keep else None), act
@@ -126,7 +125,7 @@ def down_dx_swiglu(dy2d, down_proj, gate, up, fuse=None):
     """(dgate, dup) from dact = dy2d . Wd, fp16 [T, I]."""
     packed, state, n, k = down_proj
     t = dy2d.shape[0]
-    if not (_epilogue_fusion() if fuse is None else fuse):
+    if not (GLU_IN_EPILOGUE if fuse is None else fuse):
         return swiglu_fused_backward(gate, up, nf4_dx_2d(dy2d, packed, state, n, k))
     dgate = torch.empty((t, k), device=dy2d.device, dtype=torch.float16)
     dup = torch.empty_like(dgate)

@@ -93,7 +93,9 @@ def _dense(proj):
 def test_fused_mlp_matches_fp32_module(device, monkeypatch, epilogue, recompute, dtype, shape):
     print(f"case mlp epilogue={epilogue} recompute={recompute} dtype={dtype} shape={shape}",
           flush=True)
-    monkeypatch.setenv("SS_MLP_GLU_EPILOGUE", epilogue)
+    from soupsuck_amd import mlp as fmlp
+
+    monkeypatch.setattr(fmlp, "GLU_IN_EPILOGUE", epilogue == "1")
     torch.manual_seed(777)
     mlp = _MLP(128, 320).to(device)
     x = torch.randn(shape, device=device, dtype=dtype, requires_grad=True)
