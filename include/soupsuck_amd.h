@@ -426,6 +426,35 @@ int ss_ce_finalize_dx(const float* acc, int64_t valid_n, const float* grad,
                       const int32_t* inverse, void* out, int out_dtype, int64_t n, int64_t h,
                       void* stream);
 
+/* ------------------------------------------- causal attention, packed rows ---
+ * Rows of the packed token axis are given by cu_seqlens (int32 [rows + 1] on
+ * the device, cu[0] = 0, cu[rows] = total, nondecreasing); a query attends to
+ * the keys of its own row at positions <= its own, softmax(scale q.k), GQA
+ * (kv head = q head / (hq / hk)).  Replaces the per-row SDPA loop over a
+ * packed batch (solution/unpad.py:359-410).  q [T, hq, 128], k / v
+ * [T, hk, 128], o [T, hq, 128], fp16, each given as (base, token stride, head
+ * stride) in elements with a unit last stride; bases 16-byte aligned, strides
+ * multiples of 8.  max_len >= the longest row.  lse2 fp32 [hq, T] receives
+ * m + log2(sum) of the base-2 scaled scores.  head_dim must be 128. */
+int ss_attn_varlen_fwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                       int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                       int64_t v_head, const int32_t* cu_seqlens, int rows, int max_len,
+                       int64_t total, int hq, int hk, int head_dim, float scale, void* o,
+                       int64_t o_tok, int64_t o_head, float* lse2, void* stream);
+
+/* Backward of ss_attn_varlen_fwd: dq [T, hq, 128], dk / dv [T, hk, 128] fp16
+ * (fully written), from q, k, v, the forward's o and lse2 and the upstream
+ * dout.  delta: fp32 [hq, T] scratch (rowsum(dout . o), written here).
+ * Deterministic: dk / dv are summed over the GQA group in registers. */
+int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                       int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                       int64_t v_head, const void* o, int64_t o_tok, int64_t o_head,
+                       const void* dout, int64_t do_tok, int64_t do_head, const float* lse2,
+                       const int32_t* cu_seqlens, int rows, int max_len, int64_t total, int hq,
+                       int hk, int head_dim, float scale, void* dq, int64_t dq_tok,
+                       int64_t dq_head, void* dk, int64_t dk_tok, int64_t dk_head, void* dv,
+                       int64_t dv_tok, int64_t dv_head, float* delta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -108,6 +108,12 @@ SIGNATURES = {
     "ss_ce_outputs": [_c_void_p] * 5 + [_i64, _i64, _c_void_p],
     "ss_ce_derivative": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                          _f32, _i64, _i64, _i64, _i64, _c_void_p],
+    "ss_attn_varlen_fwd": [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _int, _int, _i64, _int,
+                                                           _int, _int, _f32, _c_void_p, _i64,
+                                                           _i64, _c_void_p, _c_void_p],
+    "ss_attn_varlen_bwd": [_c_void_p, _i64, _i64] * 5 + [_c_void_p, _c_void_p, _int, _int, _i64,
+                                                           _int, _int, _int, _f32]
+                          + [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _c_void_p],
     "ss_ce_finalize_dx": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
                           _c_void_p],
 }

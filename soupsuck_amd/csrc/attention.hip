@@ -1,0 +1,456 @@
+// Causal attention over packed rows (varlen), forward and backward, head_dim 128.
+//
+// Replaces the reference's per-row SDPA loop over a packed batch
+// (solution/unpad.py:359-410: each real row of length L attends causally to
+// itself only; GQA by repeating the KV heads; scale 1/sqrt(head_dim)).  Rows
+// are given by cu_seqlens (int32 [rows + 1], offsets into the packed token
+// axis); a query attends to the keys of its own row at positions <= its own.
+//
+// Layout (HBM): q [T, Hq, 128], k / v [T, Hk, 128] with any token and head
+// strides (unit last stride), o [T, Hq, 128] likewise, fp16; lse2 fp32 [Hq, T]
+// holds m + log2(l) of the base-2 scaled scores (the backward's softmax
+// statistic).  Scores are s = (q . k) * scale in fp32 (MFMA accumulate),
+// softmax in fp32 with an online maximum, P rounded to fp16 for the P.V MFMA,
+// O accumulated in fp32 and rounded once.
+//
+// MFMA: v_mfma_f32_16x16x16_f16.  Its accumulator layout (lane l holds rows
+// 4 (l / 16) + i of column l % 16) is the B-operand layout of the next product
+// (k = 4 (l / 16) + i, column l % 16), so the score tile S^T = K . Q^T becomes
+// the B operand P^T of O^T += V^T . P^T in registers, with no shuffle.  Each
+// wave owns 16 queries (forward, dQ) or 16 keys (dK / dV); 4 waves per
+// workgroup share the LDS tiles of the other operand.
+//
+// Backward: a dQ kernel per (row, 64 queries, q head), which also writes
+// delta = rowsum(dO . O); then a dK / dV kernel per (row, 64 keys, kv head)
+// that loops over the GQA group's q heads and the causal query tiles, so dK
+// and dV are summed in registers (no atomics, deterministic).
+#include "common.h"
+
+namespace ss {
+namespace {
+
+constexpr int kD = 128;        // head dimension
+constexpr int kBlk = 64;       // queries / keys per workgroup (4 waves x 16)
+constexpr int kLdRow = kD + 8; // padded LDS row of a [token][d] tile (halfs, 16-byte rows)
+constexpr int kLdT = 64 + 4;   // padded LDS row of a [d][token] tile (halfs)
+constexpr int kLdTq = 16 + 4;  // padded LDS row of a [d][16 queries] tile (halfs)
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+  const half_t* q; int64_t q_tok, q_head;
+  const half_t* k; int64_t k_tok, k_head;
+  const half_t* v; int64_t v_tok, v_head;
+  const half_t* o; int64_t o_tok, o_head;     // forward output / backward input
+  const half_t* dout; int64_t do_tok, do_head;
+  half_t* out; int64_t out_tok, out_head;     // forward O, or backward dQ
+  half_t* dk; int64_t dk_tok, dk_head;
+  half_t* dv; int64_t dv_tok, dv_head;
+  float* lse2;      // [hq][total]
+  float* delta;     // [hq][total]
+  const int* cu;    // [rows + 1]
+  int64_t total;
+  int hq, hk;
+  float scale;      // softmax scale (1/sqrt(128) for Qwen2)
+};
+
+__device__ __forceinline__ float4v mfma16(half4 a, half4 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half4 ld4(const half_t* p) { return *reinterpret_cast<const half4*>(p); }
+__device__ __forceinline__ half8 ld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+
+__device__ __forceinline__ float xor_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+__device__ __forceinline__ float xor_sum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+}
+
+// Cooperative load of 64 token rows [t0, t0 + 64) of one head into LDS as a
+// row-major tile (and, when `tr` is given, its transpose [d][token]); rows
+// past the row end re-read the last row (their results are masked).
+__device__ __forceinline__ void load_rows64(const half_t* base, int64_t tok, int start, int len,
+                                            int t0, half_t (*rows)[kLdRow],
+                                            half_t (*tr)[kLdT]) {
+  for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
+    const int r = c >> 4, ch = c & 15;
+    const int t = min(t0 + r, len - 1);
+    const half8 v = ld8(base + (int64_t)(start + t) * tok + ch * 8);
+    *reinterpret_cast<half8*>(&rows[r][ch * 8]) = v;
+    if (tr) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tr[ch * 8 + j][r] = v[j];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ forward
+
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+  const int row = blockIdx.z, h = blockIdx.y;
+  const int start = a.cu[row], len = a.cu[row + 1] - start;
+  const int q0 = blockIdx.x * kBlk;
+  if (q0 >= len) return;
+  const int kvh = h / (a.hq / a.hk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int myq = q0 + wave * 16 + col;  // the query of this lane's column
+  const float sl2 = a.scale * kLog2e;
+
+  __shared__ __align__(16) half_t sK[kBlk][kLdRow];
+  __shared__ __align__(16) half_t sVt[kD][kLdT];
+
+  half4 qf[8];  // B operand of S^T = K . Q^T: Q[myq][16 ks + 4 grp + j]
+  {
+    const half_t* qp = a.q + (int64_t)(start + min(myq, len - 1)) * a.q_tok + (int64_t)h * a.q_head;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld4(qp + ks * 16 + grp * 4);
+  }
+  float4v acc[8];  // O^T tiles: [d = 16 dt + 4 grp + i][q = myq]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+
+  const int kend = min(len, q0 + kBlk);  // causal: keys beyond the block's last query unused
+  const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
+  const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
+  for (int kb = 0; kb < kend; kb += kBlk) {
+    __syncthreads();
+    load_rows64(kbase, a.k_tok, start, len, kb, sK, nullptr);
+    // V block transposed into LDS: sVt[d][key].
+    for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
+      const int r = c >> 4, ch = c & 15;
+      const half8 v = ld8(vbase + (int64_t)(start + min(kb + r, len - 1)) * a.v_tok + ch * 8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sVt[ch * 8 + j][r] = v[j];
+    }
+    __syncthreads();
+    float4v s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        s[kt] = mfma16(ld4(&sK[kt * 16 + col][ks * 16 + grp * 4]), qf[ks], s[kt]);
+    }
+    // s[kt][i] = S^T[key = kb + 16 kt + 4 grp + i][q = myq]; base-2 scaled, masked.
+    float mx = m;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + kt * 16 + grp * 4 + i;
+        const float x = (key <= myq && key < len) ? s[kt][i] * sl2 : -INFINITY;
+        s[kt][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = xor_max(mx);
+    const float alpha = exp2f(m - mx);
+    float rs = 0.f;
+    half4 p[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = exp2f(s[kt][i] - mx);
+        rs += e;
+        p[kt][i] = f32_to_f16(e);
+      }
+    rs = xor_sum(rs);
+    l = l * alpha + rs;
+    m = mx;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      acc[dt] *= alpha;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        acc[dt] = mfma16(ld4(&sVt[dt * 16 + col][kt * 16 + grp * 4]), p[kt], acc[dt]);
+    }
+  }
+  if (myq < len) {
+    const float inv = 1.0f / l;
+    half_t* op = a.out + (int64_t)(start + myq) * a.out_tok + (int64_t)h * a.out_head;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      half4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = f32_to_f16(acc[dt][i] * inv);
+      *reinterpret_cast<half4*>(op + dt * 16 + grp * 4) = v;
+    }
+    if (grp == 0) a.lse2[(int64_t)h * a.total + start + myq] = m + __log2f(l);
+  }
+}
+
+// --------------------------------------------------------------- backward dQ
+
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
+  const int row = blockIdx.z, h = blockIdx.y;
+  const int start = a.cu[row], len = a.cu[row + 1] - start;
+  const int q0 = blockIdx.x * kBlk;
+  if (q0 >= len) return;
+  const int kvh = h / (a.hq / a.hk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int q0w = q0 + wave * 16;
+  const int myq = q0w + col;
+  const int qc = min(myq, len - 1);
+  const float sl2 = a.scale * kLog2e;
+
+  __shared__ __align__(16) half_t sK[kBlk][kLdRow];
+  __shared__ __align__(16) half_t sKt[kD][kLdT];
+  __shared__ __align__(16) half_t sV[kBlk][kLdRow];
+
+  half4 qf[8], df[8];  // Q[myq][16 ks + 4 grp + j], dO[myq][...]
+  float dsum = 0.f;    // this lane's part of rowsum(dO . O)
+  {
+    const half_t* qp = a.q + (int64_t)(start + qc) * a.q_tok + (int64_t)h * a.q_head;
+    const half_t* dp = a.dout + (int64_t)(start + qc) * a.do_tok + (int64_t)h * a.do_head;
+    const half_t* op = a.o + (int64_t)(start + qc) * a.o_tok + (int64_t)h * a.o_head;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      qf[ks] = ld4(qp + ks * 16 + grp * 4);
+      df[ks] = ld4(dp + ks * 16 + grp * 4);
+      const half4 ov = ld4(op + ks * 16 + grp * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dsum += (float)df[ks][j] * (float)ov[j];
+    }
+  }
+  const float delta = xor_sum(dsum);
+  const float lse = a.lse2[(int64_t)h * a.total + start + qc];
+  if (myq < len && grp == 0) a.delta[(int64_t)h * a.total + start + myq] = delta;
+
+  float4v dq[8];  // dQ tiles: [q = q0w + 4 grp + i][d = 16 dt + col]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) dq[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  const int kend = min(len, q0 + kBlk);
+  const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
+  const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
+  for (int kb = 0; kb < kend; kb += kBlk) {
+    __syncthreads();
+    load_rows64(kbase, a.k_tok, start, len, kb, sK, sKt);
+    load_rows64(vbase, a.v_tok, start, len, kb, sV, nullptr);
+    __syncthreads();
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        s = mfma16(ld4(&sK[kt * 16 + col][ks * 16 + grp * 4]), qf[ks], s);   // S^T
+        dp = mfma16(ld4(&sV[kt * 16 + col][ks * 16 + grp * 4]), df[ks], dp); // dP^T
+      }
+      half4 ds;  // dS^T[key = kb + 16 kt + 4 grp + i][q = myq] = A of dS (rows q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + kt * 16 + grp * 4 + i;
+        const float p = (key <= myq && key < len) ? exp2f(s[i] * sl2 - lse) : 0.f;
+        ds[i] = f32_to_f16(p * (dp[i] - delta));
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        dq[dt] = mfma16(ds, ld4(&sKt[dt * 16 + col][kt * 16 + grp * 4]), dq[dt]);
+    }
+  }
+  half_t* base = a.out + (int64_t)h * a.out_head;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = q0w + grp * 4 + i;
+    if (q < len) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        base[(int64_t)(start + q) * a.out_tok + dt * 16 + col] = f32_to_f16(dq[dt][i] * a.scale);
+    }
+  }
+}
+
+// ------------------------------------------------------------ backward dK/dV
+
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+  const int row = blockIdx.z, kvh = blockIdx.y;
+  const int start = a.cu[row], len = a.cu[row + 1] - start;
+  const int k0 = blockIdx.x * kBlk;
+  if (k0 >= len) return;
+  const int group = a.hq / a.hk;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int col = lane & 15, grp = lane >> 4;
+  const int k0w = k0 + wave * 16;
+  const int mykey = k0w + col;
+  const int kc = min(mykey, len - 1);
+  const float sl2 = a.scale * kLog2e;
+
+  __shared__ __align__(16) half_t sQ[16][kLdRow];
+  __shared__ __align__(16) half_t sQt[kD][kLdTq];
+  __shared__ __align__(16) half_t sO[16][kLdRow];    // dO rows
+  __shared__ __align__(16) half_t sOt[kD][kLdTq];    // dO transposed
+  __shared__ float sL[16], sDl[16];    // lse2 and delta of the tile's queries
+
+  half4 kf[8], vf[8];  // K[mykey][16 ks + 4 grp + j], V[mykey][...]
+  {
+    const half_t* kp = a.k + (int64_t)(start + kc) * a.k_tok + (int64_t)kvh * a.k_head;
+    const half_t* vp = a.v + (int64_t)(start + kc) * a.v_tok + (int64_t)kvh * a.v_head;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      kf[ks] = ld4(kp + ks * 16 + grp * 4);
+      vf[ks] = ld4(vp + ks * 16 + grp * 4);
+    }
+  }
+  float4v dk[8], dv[8];  // [key = k0w + 4 grp + i][d = 16 dt + col]
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    dk[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+    dv[dt] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int hh = 0; hh < group; ++hh) {
+    const int h = kvh * group + hh;
+    const half_t* qbase = a.q + (int64_t)h * a.q_head;
+    const half_t* dbase = a.dout + (int64_t)h * a.do_head;
+    for (int qt = k0; qt < len; qt += 16) {
+      __syncthreads();
+      // Query tile [qt, qt + 16): Q and dO rows and transposes, lse2, delta.
+      {
+        const int c = threadIdx.x;  // 256 threads: 16 rows x 16 chunks of 8
+        const int r = c >> 4, ch = c & 15;
+        const int t = min(qt + r, len - 1);
+        const half8 qv = ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
+        const half8 dvv = ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
+        *reinterpret_cast<half8*>(&sQ[r][ch * 8]) = qv;
+        *reinterpret_cast<half8*>(&sO[r][ch * 8]) = dvv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sQt[ch * 8 + j][r] = qv[j];
+          sOt[ch * 8 + j][r] = dvv[j];
+        }
+        if (c < 16) {
+          sL[c] = a.lse2[(int64_t)h * a.total + start + min(qt + c, len - 1)];
+          sDl[c] = a.delta[(int64_t)h * a.total + start + min(qt + c, len - 1)];
+        }
+      }
+      __syncthreads();
+      float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        s = mfma16(ld4(&sQ[col][ks * 16 + grp * 4]), kf[ks], s);   // S[q][key]
+        dp = mfma16(ld4(&sO[col][ks * 16 + grp * 4]), vf[ks], dp); // dP[q][key]
+      }
+      half4 p16, ds16;  // P^T / dS^T as A operands: [key = mykey][q = qt + 4 grp + i]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = qt + grp * 4 + i;
+        const float p = (mykey <= q && q < len && mykey < len)
+                            ? exp2f(s[i] * sl2 - sL[grp * 4 + i]) : 0.f;
+        p16[i] = f32_to_f16(p);
+        ds16[i] = f32_to_f16(p * (dp[i] - sDl[grp * 4 + i]));
+      }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        dv[dt] = mfma16(p16, ld4(&sOt[dt * 16 + col][grp * 4]), dv[dt]);
+        dk[dt] = mfma16(ds16, ld4(&sQt[dt * 16 + col][grp * 4]), dk[dt]);
+      }
+    }
+  }
+  half_t* kb = a.dk + (int64_t)kvh * a.dk_head;
+  half_t* vb = a.dv + (int64_t)kvh * a.dv_head;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = k0w + grp * 4 + i;
+    if (key < len) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        kb[(int64_t)(start + key) * a.dk_tok + dt * 16 + col] = f32_to_f16(dk[dt][i] * a.scale);
+        vb[(int64_t)(start + key) * a.dv_tok + dt * 16 + col] = f32_to_f16(dv[dt][i]);
+      }
+    }
+  }
+}
+
+bool al8(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int check_common(const char* fn, int rows, int max_len, int hq, int hk, int head_dim,
+                 int64_t total, const int* cu) {
+  SS_CHECK_ARG(rows >= 0 && max_len >= 0 && total >= 0, "%s: negative sizes", fn);
+  SS_CHECK_ARG(head_dim == kD, "%s: head_dim %d unsupported (only %d)", fn, head_dim, kD);
+  SS_CHECK_ARG(hq > 0 && hk > 0 && hq % hk == 0, "%s: hq=%d must be a positive multiple of hk=%d",
+               fn, hq, hk);
+  SS_CHECK_ARG(rows <= 65535 && hq <= 65535, "%s: rows / heads exceed the grid", fn);
+  SS_CHECK_ARG(rows == 0 || cu, "%s: null cu_seqlens", fn);
+  return SS_OK;
+}
+
+// Token / head strides (elements) of a tensor must keep every 16-byte load aligned.
+bool strides_ok(const void* p, int64_t tok, int64_t head) {
+  return p && al8(p) && tok % 8 == 0 && head % 8 == 0;
+}
+
+}  // namespace
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" int ss_attn_varlen_fwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                                  int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                                  int64_t v_head, const int* cu_seqlens, int rows, int max_len,
+                                  int64_t total, int hq, int hk, int head_dim, float scale,
+                                  void* o, int64_t o_tok, int64_t o_head, float* lse2,
+                                  void* stream) {
+  const char* fn = "ss_attn_varlen_fwd";
+  int rc = check_common(fn, rows, max_len, hq, hk, head_dim, total, cu_seqlens);
+  if (rc) return rc;
+  if (rows == 0 || max_len == 0) return SS_OK;
+  SS_CHECK_ARG(strides_ok(q, q_tok, q_head) && strides_ok(k, k_tok, k_head) &&
+                   strides_ok(v, v_tok, v_head) && strides_ok(o, o_tok, o_head) && lse2,
+               "%s: q/k/v/o need 16-byte aligned bases and strides that are multiples of 8", fn);
+  AttnArgs a{};
+  a.q = (const half_t*)q; a.q_tok = q_tok; a.q_head = q_head;
+  a.k = (const half_t*)k; a.k_tok = k_tok; a.k_head = k_head;
+  a.v = (const half_t*)v; a.v_tok = v_tok; a.v_head = v_head;
+  a.out = (half_t*)o; a.out_tok = o_tok; a.out_head = o_head;
+  a.lse2 = lse2; a.cu = cu_seqlens; a.total = total; a.hq = hq; a.hk = hk; a.scale = scale;
+  const dim3 grid((unsigned)cdiv(max_len, kBlk), (unsigned)hq, (unsigned)rows);
+  hipLaunchKernelGGL(attn_fwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+  SS_CHECK_LAUNCH("attn_fwd_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                                  int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                                  int64_t v_head, const void* o, int64_t o_tok, int64_t o_head,
+                                  const void* dout, int64_t do_tok, int64_t do_head,
+                                  const float* lse2, const int* cu_seqlens, int rows, int max_len,
+                                  int64_t total, int hq, int hk, int head_dim, float scale,
+                                  void* dq, int64_t dq_tok, int64_t dq_head, void* dk,
+                                  int64_t dk_tok, int64_t dk_head, void* dv, int64_t dv_tok,
+                                  int64_t dv_head, float* delta, void* stream) {
+  const char* fn = "ss_attn_varlen_bwd";
+  int rc = check_common(fn, rows, max_len, hq, hk, head_dim, total, cu_seqlens);
+  if (rc) return rc;
+  if (rows == 0 || max_len == 0) return SS_OK;
+  SS_CHECK_ARG(strides_ok(q, q_tok, q_head) && strides_ok(k, k_tok, k_head) &&
+                   strides_ok(v, v_tok, v_head) && strides_ok(o, o_tok, o_head) &&
+                   strides_ok(dout, do_tok, do_head) && dq && dk && dv && lse2 && delta,
+               "%s: q/k/v/o/dO need 16-byte aligned bases and strides that are multiples of 8",
+               fn);
+  AttnArgs a{};
+  a.q = (const half_t*)q; a.q_tok = q_tok; a.q_head = q_head;
+  a.k = (const half_t*)k; a.k_tok = k_tok; a.k_head = k_head;
+  a.v = (const half_t*)v; a.v_tok = v_tok; a.v_head = v_head;
+  a.o = (const half_t*)o; a.o_tok = o_tok; a.o_head = o_head;
+  a.dout = (const half_t*)dout; a.do_tok = do_tok; a.do_head = do_head;
+  a.out = (half_t*)dq; a.out_tok = dq_tok; a.out_head = dq_head;
+  a.dk = (half_t*)dk; a.dk_tok = dk_tok; a.dk_head = dk_head;
+  a.dv = (half_t*)dv; a.dv_tok = dv_tok; a.dv_head = dv_head;
+  a.lse2 = const_cast<float*>(lse2); a.delta = delta;
+  a.cu = cu_seqlens; a.total = total; a.hq = hq; a.hk = hk; a.scale = scale;
+  const unsigned blocks = (unsigned)cdiv(max_len, kBlk);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(blocks, (unsigned)hq, (unsigned)rows), dim3(256), 0,
+                     st, a);
+  SS_CHECK_LAUNCH("attn_bwd_dq_kernel");
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(blocks, (unsigned)hk, (unsigned)rows), dim3(256),
+                     0, st, a);
+  SS_CHECK_LAUNCH("attn_bwd_dkdv_kernel");
+  return SS_OK;
+}
