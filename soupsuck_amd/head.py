@@ -19,7 +19,10 @@
 ``build_causal_lm_forward`` routes ``Qwen2ForCausalLM.forward`` (reference
 solution/patch.py:167-229) to it when labels are given and the head is a
 plain bias-free Linear on the hidden states' device; the model's logits are
-then never materialised (``logits`` is None in the output).
+then never materialised (``logits`` is None in the output).  When the model
+route packed the batch (soupsuck_amd.unpad_route, which also checks that the
+labels are -100 at every padding position), the head reads the packed hidden
+states it published and runs on the real rows only.
 """
 
 from dataclasses import dataclass
@@ -129,12 +132,19 @@ def build_causal_lm_forward(original, module):
             return original(self, labels=labels, logits_to_keep=logits_to_keep, **model_args)
         num_items = kwargs.pop("num_items_in_batch", None)
         model_args.pop("num_items_in_batch", None)
-        outputs = self.model(**model_args)
+        from .unpad_route import HEAD_LABELS, take_packed_head
+
+        token = HEAD_LABELS.set((labels, attention_mask))
+        try:
+            outputs = self.model(**model_args)
+        finally:
+            HEAD_LABELS.reset(token)
         hidden = outputs.last_hidden_state
+        packed = take_packed_head(self.model, hidden)
         if (isinstance(hidden, torch.Tensor) and hidden.shape[:2] == labels.shape
                 and hidden.dtype in (torch.float16, torch.float32)
                 and _head_weight_ok(self.lm_head, hidden)):
-            loss, step = fused_head(hidden, self.lm_head.weight, labels, num_items)
+            loss, step = fused_head(hidden, self.lm_head.weight, labels, num_items, packed=packed)
             self._soupsuck_head_step = step
             logits = None
         else:

@@ -22,6 +22,9 @@ Routes (reference file of the behaviour each one keeps):
     apply_rotary_pos_emb       the joint q/k RoPE (solution/rope.py:55-80);
     Qwen2ForCausalLM.forward   the chunked fused CE head (solution/patch.py:167-229),
                                in soupsuck_amd.head;
+    Qwen2Model.forward,        right-padded batches packed to their real tokens,
+    Qwen2Attention.forward     causal attention within each row in one launch
+                               (solution/unpad.py:359-450), in soupsuck_amd.unpad_route;
   PEFT (solution/lora.py:135-166), in soupsuck_amd.peft_route:
     tuners.lora.bnb.Linear4bit.forward  the fused QLoRA projection.
 Every replacement falls back to the original when SOUP_FUSED_DISABLE is set
@@ -196,6 +199,18 @@ def _build_head(original, module):
     return build_causal_lm_forward(original, module)
 
 
+def _build_model(original, module):
+    from .unpad_route import build_model_forward
+
+    return build_model_forward(original, module)
+
+
+def _build_attention(original, module):
+    from .unpad_route import build_attention_forward
+
+    return build_attention_forward(original, module)
+
+
 def _build_bnb(name):
     def build(original, module):
         from . import bnb_routes
@@ -216,6 +231,8 @@ RMSNORM_ROUTE = Route(QWEN, "Qwen2RMSNorm", "forward", _build_rmsnorm)
 MLP_ROUTE = Route(QWEN, "Qwen2MLP", "forward", _build_mlp)
 ROPE_ROUTE = Route(QWEN, None, "apply_rotary_pos_emb", _build_rope)
 HEAD_ROUTE = Route(QWEN, "Qwen2ForCausalLM", "forward", _build_head)
+MODEL_ROUTE = Route(QWEN, "Qwen2Model", "forward", _build_model)
+ATTENTION_ROUTE = Route(QWEN, "Qwen2Attention", "forward", _build_attention)
 PEFT_ROUTE = Route("peft.tuners.lora.bnb", "Linear4bit", "forward", _build_peft,
                    "_solution_lora_4bit_original")
 BNB_ROUTES = (
@@ -226,7 +243,8 @@ BNB_ROUTES = (
           _build_bnb("build_linear_fallback")),
     Route("bitsandbytes", None, "matmul_4bit", _build_bnb("build_matmul")),
 )
-ROUTES = (DECODER_ROUTE, RMSNORM_ROUTE, MLP_ROUTE, ROPE_ROUTE, HEAD_ROUTE, PEFT_ROUTE) + BNB_ROUTES
+ROUTES = (DECODER_ROUTE, RMSNORM_ROUTE, MLP_ROUTE, ROPE_ROUTE, HEAD_ROUTE, MODEL_ROUTE,
+          ATTENTION_ROUTE, PEFT_ROUTE) + BNB_ROUTES
 TARGETS = tuple(sorted({r.module for r in ROUTES}))
 
 
@@ -240,6 +258,10 @@ def patch_qwen2_rmsnorm(module=None):
 
 def patch_qwen2_head(module=None):
     return install_route(HEAD_ROUTE, module)
+
+
+def patch_qwen2_unpad(module=None):
+    return [install_route(MODEL_ROUTE, module), install_route(ATTENTION_ROUTE, module)]
 
 
 def patch_peft_linear4bit(module=None):

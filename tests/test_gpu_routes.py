@@ -12,7 +12,10 @@ with the original (eager) code it replaces.
   * ``Qwen2DecoderLayer.forward`` (solution/decoder.py:54-89): the fused residual
     add + norm vs the original layer within fp16 tolerance;
   * ``bitsandbytes.matmul_4bit`` (fake bitsandbytes 0.50.2 module): routed output
-    bit-identical to nf4_matmul.
+    bit-identical to nf4_matmul;
+  * ``Qwen2Model`` / ``Qwen2Attention`` (solution/unpad.py:359-450): a right-padded
+    fp16 batch runs packed (gather, packed causal attention, fused head on the real
+    rows) and matches the original padded forward (SDPA with the mask).
 PEFT and bitsandbytes are not installed, so their modules are stand-ins
 (ModuleType objects holding a class / function of the same name and signature).
 """
@@ -182,3 +185,48 @@ def test_bnb_matmul_route_runs_the_nf4_gemm(device, monkeypatch):
     bias = (torch.randn(640, device=device) * 0.1).half()
     got = fake.matmul_4bit(x, packed.t(), state, bias=bias)
     assert torch.equal(got, nf4_matmul(x, packed, state, bias=bias))
+
+
+def test_unpadded_model_matches_padded_eager(device, monkeypatch):
+    """Qwen2ForCausalLM on a right-padded fp16 batch: the packed path (Qwen2Model and
+    Qwen2Attention routes, packed causal attention kernels, fused head on the real
+    rows) against the original padded forward (SOUP_FUSED_DISABLE=1, SDPA with the
+    padding mask): loss within 5e-3 relative, gradients within relative L2 5e-2."""
+    from transformers import Qwen2Config
+    from transformers.models.qwen2 import modeling_qwen2 as qwen
+
+    for route in (patch.MODEL_ROUTE, patch.ATTENTION_ROUTE, patch.HEAD_ROUTE):
+        assert patch.install_route(route, qwen)
+    cfg = Qwen2Config(hidden_size=256, intermediate_size=512, num_attention_heads=2,
+                      num_key_value_heads=1, num_hidden_layers=2, vocab_size=1000,
+                      use_cache=False, attn_implementation="sdpa")
+    torch.manual_seed(5)
+    model = qwen.Qwen2ForCausalLM(cfg).to(device=device, dtype=torch.float16).train()
+    lengths = [37, 12, 50]
+    b, s = len(lengths), max(lengths)
+    ids = torch.randint(0, 1000, (b, s), device=device)
+    mask = torch.zeros((b, s), device=device, dtype=torch.long)
+    for r, n in enumerate(lengths):
+        mask[r, :n] = 1
+    labels = ids.masked_fill(mask == 0, -100)
+
+    def run():
+        model.zero_grad()
+        out = model(input_ids=ids, attention_mask=mask, labels=labels)
+        out.loss.backward()
+        grads = [p.grad.detach().float().clone() for p in (
+            model.model.layers[0].self_attn.q_proj.weight,
+            model.model.layers[1].self_attn.v_proj.weight,
+            model.model.layers[1].mlp.down_proj.weight)]
+        return out.loss.detach().float(), grads
+
+    with _Recorder(["ss_attn_varlen_fwd", "ss_attn_varlen_bwd", "ss_unpad_gather",
+                    "ss_ce_stats"]) as rec:
+        loss, grads = run()
+    assert rec.calls.count("ss_attn_varlen_fwd") == 2 and "ss_attn_varlen_bwd" in rec.calls
+    assert "ss_unpad_gather" in rec.calls and "ss_ce_stats" in rec.calls
+    monkeypatch.setenv("SOUP_FUSED_DISABLE", "1")
+    ref_loss, ref_grads = run()
+    assert abs(loss.item() - ref_loss.item()) <= 5e-3 * abs(ref_loss.item())
+    for got, ref in zip(grads, ref_grads):
+        assert _rel(got, ref) < 5e-2
