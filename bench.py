@@ -21,6 +21,9 @@ roofline   = the dominant NF4 entry point's achieved TFLOP/s (algorithmic
              against the MI355X dense fp16 MFMA peak
 cpu_baseline = the oracle's "dequantize then fp32 BLAS matmul" port of the
              same step (oracle/baseline.py) timed on this host's cores
+full_decoder_layer = the whole decoder layer (norms, seven QLoRA projections, RoPE,
+             packed causal attention, SwiGLU, residual adds) fwd+bwd on the same
+             batch, HIP-graph replay (the north star's full-layer time)
 other_configs = configs[0] (gate dequant GB/s, GEMM T=1024 TFLOP/s), configs[2]
              (add-RMSNorm fwd/bwd/bwd+dgamma and unpad gather/scatter GB/s),
              configs[3] (fused chunked CE fwd+bwd ms and TFLOP/s), and the
@@ -690,6 +693,54 @@ def other_configs(torch, _lib):
     return out
 
 
+def full_layer(torch, lengths, steps, warmup):
+    """The whole Qwen2.5-1.5B decoder layer (soupsuck_amd.layer.DecoderLayer: norms,
+    seven QLoRA projections, RoPE, packed causal attention, SwiGLU, residual adds)
+    forward + backward on the configs[1] batch: eager, then one HIP-graph capture
+    replayed ``steps`` times between HIP events."""
+    from soupsuck_amd.layer import DecoderLayer
+
+    dev = torch.device("cuda:0")
+    layer = DecoderLayer(dev, lengths)
+    t = sum(lengths)
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    h = torch.randn((t, 1536), generator=gen).half().to(dev).requires_grad_()
+    g = (torch.randn((t, 1536), generator=gen) * 0.05).half().to(dev)
+    for _ in range(warmup):
+        layer.step(h, g)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer.step(h, g)
+    torch.cuda.synchronize()
+    eager_ms = 1e3 * (time.perf_counter() - t0) / steps
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            layer.step(h, g)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        layer.step(h, g)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = layer.flops()
+    return {"workload": "Qwen2.5-1.5B decoder layer fwd+bwd (RMSNorm, q/k/v/o/gate/up/down "
+                        "QLoRA r=16, RoPE, packed causal attention 12/2 heads, SwiGLU, residuals)",
+            "tokens": t, "ms": round(ms, 4), "eager_ms": round(eager_ms, 4),
+            "TFLOP/s": round(flops / ms / 1e9, 1), "gflop": round(flops / 1e9, 2),
+            "timing": f"HIP-graph replay x{steps} between HIP events"}
+
+
 def ce_inputs(torch, gen, dev):
     """hidden [826, 1536] ~ N(0,1), tied head [151936, 1536] ~ N(0, 0.02),
     labels uniform over the vocabulary with 36.5 % set to -100 (both trainable)."""
@@ -894,6 +945,7 @@ def main():
                 "timing": (f"HIP events on the launch stream around each call, {args.timing_steps}"
                            " eager steps each queued behind a GPU spin (calls run back to back)")}
 
+    full = full_layer(torch, lengths, args.steps, args.warmup)
     sweep_res = None if args.no_sweep else sweep(torch, _lib)
     others = None if args.no_other_configs else other_configs(torch, _lib)
 
@@ -917,6 +969,7 @@ def main():
                    "tokens": tokens, "lengths": lengths, "hidden": 1536,
                    "intermediate": 8960, "kv_out": 256, "lora_rank": 16},
         "layer_fwd_bwd_ms": round(ms_per_step, 4),
+        "full_decoder_layer": full,
         "step_mode": mode,
         "eager_ms_per_step": round(eager_ms, 4),
         "graph_error": graph_error,

@@ -97,3 +97,74 @@ class QLoRALayer:
             nk = p.n * p.k
             total += nk // 2 + -(-nk // 64) + 4 * -(-nk // 16384) + 1024 + 4
         return total
+
+
+class DecoderLayer:
+    """A whole Qwen2.5-1.5B decoder layer on a packed batch, every op on this package's
+    kernels: RMSNorm -> q/k/v QLoRA projections -> joint q/k RoPE -> causal attention
+    within each packed row -> o projection -> residual add + RMSNorm -> gate/up
+    projections -> SwiGLU -> down projection -> residual add.  Forward then backward
+    of the whole layer from an upstream gradient (the north star's full-layer time).
+    The seven projections are ``QLoRALayer``'s; norm weights ~ 1 + N(0, 0.1) fp16;
+    RoPE angles are Qwen2's (theta 1e6) at each token's position within its row."""
+
+    def __init__(self, device, lengths, hidden=1536, intermediate=8960, kv=256, heads=12,
+                 kv_heads=2, seed=0):
+        from .kernels.attention import row_offsets
+
+        self.proj = QLoRALayer(device, hidden, intermediate, kv, seed=seed)
+        gen = torch.Generator(device="cpu").manual_seed(seed + 7)
+        self.norm_in = (1 + 0.1 * torch.randn(hidden, generator=gen)).half().to(device)
+        self.norm_post = (1 + 0.1 * torch.randn(hidden, generator=gen)).half().to(device)
+        self.lengths = [int(n) for n in lengths]
+        self.heads, self.kv_heads, self.head_dim = heads, kv_heads, hidden // heads
+        self.cu = row_offsets(self.lengths, device)
+        pos = torch.cat([torch.arange(n, dtype=torch.float64) for n in self.lengths])
+        inv = 1.0 / (1_000_000 ** (torch.arange(0, self.head_dim, 2, dtype=torch.float64)
+                                    / self.head_dim))
+        ang = pos[:, None] * inv[None, :]
+        emb = torch.cat([ang, ang], dim=-1)
+        self.cos = emb.cos()[None].half().to(device)
+        self.sin = emb.sin()[None].half().to(device)
+
+    def forward(self, h):
+        from .kernels.add_rmsnorm import add_rms_norm
+        from .kernels.attention import packed_causal_attention
+        from .kernels.rmsnorm import rms_norm
+        from .kernels.rope import fused_rope
+        from .kernels.swiglu import swiglu
+
+        p = {q.name: q for q in self.proj.projections}
+        s = self.proj.scaling
+        t, d = h.shape[0], self.head_dim
+
+        def run(name, x):
+            q = p[name]
+            return qlora_projection(x, q.lora_a, q.lora_b, q.packed, q.state, q.bias, s)
+
+        x = rms_norm(h, self.norm_in, 1e-6)
+        q = run("q_proj", x).view(1, t, self.heads, d).transpose(1, 2)
+        k = run("k_proj", x).view(1, t, self.kv_heads, d).transpose(1, 2)
+        v = run("v_proj", x).view(1, t, self.kv_heads, d).transpose(1, 2)
+        q, k = fused_rope(q, k, self.cos, self.sin)
+        attn = packed_causal_attention(q, k, v, self.lengths, d ** -0.5, cu_seqlens=self.cu)
+        o = run("o_proj", attn.view(t, self.heads * d))
+        residual, x2 = add_rms_norm(h, o, self.norm_post, 1e-6)
+        act = swiglu(run("gate_proj", x2), run("up_proj", x2))
+        return residual + run("down_proj", act)
+
+    def step(self, h, g):
+        for q in self.proj.projections:
+            q.lora_a.grad = None
+            q.lora_b.grad = None
+        h.grad = None
+        out = self.forward(h)
+        out.backward(g)
+        return out
+
+    def flops(self):
+        """Projection flops (QLoRALayer.flops) + attention: 2 products forward and 4
+        backward of 2 * head_dim flops per causal (query, key) pair per q head."""
+        t = sum(self.lengths)
+        pairs = sum(n * (n + 1) // 2 for n in self.lengths)
+        return self.proj.flops(t) + 6 * 2 * self.head_dim * pairs * self.heads
