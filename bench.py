@@ -81,6 +81,9 @@ def parse():
                    help="only run one configs[4] point (NAME in q_o, k_v, gate_up, down; MODE "
                         "fwd or dx) --reps times, rotating weight copies as the sweep does, "
                         "and exit (for rocprofv3 kernel-trace and counter passes)")
+    p.add_argument("--profile-layer", action="store_true",
+                   help="only run the full decoder layer (layer.DecoderLayer) forward + backward "
+                        "--reps times on the configs[1] batch and exit (for a kernel trace)")
     p.add_argument("--profile-ce", action="store_true",
                    help="only run the configs[3] fused CE forward + backward --reps times and "
                         "exit (for a rocprofv3 kernel trace)")
@@ -741,6 +744,25 @@ def full_layer(torch, lengths, steps, warmup):
             "timing": f"HIP-graph replay x{steps} between HIP events"}
 
 
+def profile_layer(reps):
+    """Repeat the full decoder layer's forward + backward (eager) on the configs[1] batch."""
+    import torch
+
+    from soupsuck_amd.layer import DecoderLayer
+
+    dev = torch.device("cuda:0")
+    lengths = lengths_config1()
+    layer = DecoderLayer(dev, lengths)
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    h = torch.randn((sum(lengths), 1536), generator=gen).half().to(dev).requires_grad_()
+    g = (torch.randn((sum(lengths), 1536), generator=gen) * 0.05).half().to(dev)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        layer.step(h, g)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_layer": True, "tokens": sum(lengths), "reps": reps}), flush=True)
+
+
 def ce_inputs(torch, gen, dev):
     """hidden [826, 1536] ~ N(0,1), tied head [151936, 1536] ~ N(0, 0.02),
     labels uniform over the vocabulary with 36.5 % set to -100 (both trainable)."""
@@ -845,6 +867,9 @@ def main():
         return
     if args.profile_ce:
         profile_ce(args.reps)
+        return
+    if args.profile_layer:
+        profile_layer(args.reps)
         return
 
     import torch

@@ -442,10 +442,16 @@ int ss_attn_varlen_fwd(const void* q, int64_t q_tok, int64_t q_head, const void*
                        int64_t total, int hq, int hk, int head_dim, float scale, void* o,
                        int64_t o_tok, int64_t o_head, float* lse2, void* stream);
 
+/* Scratch bytes of ss_attn_varlen_bwd: rowsum(dout . o) per (q head, token)
+ * and, with GQA (hq > hk), the q heads' fp32 dK / dV partial planes. */
+size_t ss_attn_varlen_bwd_workspace_size(int hq, int hk, int64_t total);
+
 /* Backward of ss_attn_varlen_fwd: dq [T, hq, 128], dk / dv [T, hk, 128] fp16
- * (fully written), from q, k, v, the forward's o and lse2 and the upstream
- * dout.  delta: fp32 [hq, T] scratch (rowsum(dout . o), written here).
- * Deterministic: dk / dv are summed over the GQA group in registers. */
+ * (fully written; same base / stride rules as the inputs), from q, k, v, the
+ * forward's o and lse2 and the upstream dout.  workspace: at least
+ * ss_attn_varlen_bwd_workspace_size() bytes, 16-byte aligned, fully written
+ * before it is read.  Deterministic: the GQA group's partials are added in
+ * head order. */
 int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
                        int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
                        int64_t v_head, const void* o, int64_t o_tok, int64_t o_head,
@@ -453,7 +459,8 @@ int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void*
                        const int32_t* cu_seqlens, int rows, int max_len, int64_t total, int hq,
                        int hk, int head_dim, float scale, void* dq, int64_t dq_tok,
                        int64_t dq_head, void* dk, int64_t dk_tok, int64_t dk_head, void* dv,
-                       int64_t dv_tok, int64_t dv_head, float* delta, void* stream);
+                       int64_t dv_tok, int64_t dv_head, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -113,13 +113,15 @@ SIGNATURES = {
                                                            _i64, _c_void_p, _c_void_p],
     "ss_attn_varlen_bwd": [_c_void_p, _i64, _i64] * 5 + [_c_void_p, _c_void_p, _int, _int, _i64,
                                                            _int, _int, _int, _f32]
-                          + [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _c_void_p],
+                          + [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _size, _c_void_p],
+    "ss_attn_varlen_bwd_workspace_size": [_int, _int, _i64],
     "ss_ce_finalize_dx": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
                           _c_void_p],
 }
 _RESTYPES = {"ss_last_error": ctypes.c_char_p, "ss_nf4_gemm_workspace_size": _size,
              "ss_lora_workspace_size": _size, "ss_qlora_rank_workspace_size": _size,
-             "ss_gemm_f16_workspace_size": _size, "ss_add_rmsnorm_dgamma_waves": _i64}
+             "ss_gemm_f16_workspace_size": _size, "ss_add_rmsnorm_dgamma_waves": _i64,
+             "ss_attn_varlen_bwd_workspace_size": _size}
 
 _lock = threading.Lock()
 _lib = None

@@ -21,9 +21,9 @@
 // workgroup share the LDS tiles of the other operand.
 //
 // Backward: a dQ kernel per (row, 64 queries, q head), which also writes
-// delta = rowsum(dO . O); then a dK / dV kernel per (row, 64 keys, kv head)
-// that loops over the GQA group's q heads and the causal query tiles, so dK
-// and dV are summed in registers (no atomics, deterministic).
+// delta = rowsum(dO . O); then a dK / dV kernel per (row, 64 keys, q head)
+// over the causal query tiles; with GQA each q head writes fp32 partials that
+// a reduce kernel adds in head order (no atomics, deterministic).
 #include "common.h"
 
 namespace ss {
@@ -33,7 +33,6 @@ constexpr int kD = 128;        // head dimension
 constexpr int kBlk = 64;       // queries / keys per workgroup (4 waves x 16)
 constexpr int kLdRow = kD + 8; // padded LDS row of a [token][d] tile (halfs, 16-byte rows)
 constexpr int kLdT = 64 + 4;   // padded LDS row of a [d][token] tile (halfs)
-constexpr int kLdTq = 16 + 4;  // padded LDS row of a [d][16 queries] tile (halfs)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -268,12 +267,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------ backward dK/dV
 
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
-  const int row = blockIdx.z, kvh = blockIdx.y;
+constexpr int kQt = 32;           // queries per LDS tile of the dK / dV kernel
+constexpr int kLdTq = kQt + 4;    // padded LDS row of a [d][query] tile (halfs)
+
+// One workgroup per (row, 64 keys, q head): 4 waves of 16 keys walk the row's
+// causal query tiles.  With GQA (hq > hk) the q heads of a group write fp32
+// partial dK / dV planes that attn_bwd_reduce_kernel adds in head order;
+// without it dK / dV are written directly.
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* part_k,
+                                                            float* part_v) {
+  const int row = blockIdx.z, h = blockIdx.y;
   const int start = a.cu[row], len = a.cu[row + 1] - start;
   const int k0 = blockIdx.x * kBlk;
   if (k0 >= len) return;
-  const int group = a.hq / a.hk;
+  const int kvh = h / (a.hq / a.hk);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int col = lane & 15, grp = lane >> 4;
   const int k0w = k0 + wave * 16;
@@ -281,11 +288,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int kc = min(mykey, len - 1);
   const float sl2 = a.scale * kLog2e;
 
-  __shared__ __align__(16) half_t sQ[16][kLdRow];
+  __shared__ __align__(16) half_t sQ[kQt][kLdRow];
   __shared__ __align__(16) half_t sQt[kD][kLdTq];
-  __shared__ __align__(16) half_t sO[16][kLdRow];    // dO rows
-  __shared__ __align__(16) half_t sOt[kD][kLdTq];    // dO transposed
-  __shared__ float sL[16], sDl[16];    // lse2 and delta of the tile's queries
+  __shared__ __align__(16) half_t sO[kQt][kLdRow];    // dO rows
+  __shared__ __align__(16) half_t sOt[kD][kLdTq];     // dO transposed
+  __shared__ float sL[kQt], sDl[kQt];                 // lse2 and delta of the tile's queries
 
   half4 kf[8], vf[8];  // K[mykey][16 ks + 4 grp + j], V[mykey][...]
   {
@@ -304,67 +311,105 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     dv[dt] = float4v{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int hh = 0; hh < group; ++hh) {
-    const int h = kvh * group + hh;
-    const half_t* qbase = a.q + (int64_t)h * a.q_head;
-    const half_t* dbase = a.dout + (int64_t)h * a.do_head;
-    for (int qt = k0; qt < len; qt += 16) {
-      __syncthreads();
-      // Query tile [qt, qt + 16): Q and dO rows and transposes, lse2, delta.
-      {
-        const int c = threadIdx.x;  // 256 threads: 16 rows x 16 chunks of 8
-        const int r = c >> 4, ch = c & 15;
-        const int t = min(qt + r, len - 1);
-        const half8 qv = ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
-        const half8 dvv = ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
-        *reinterpret_cast<half8*>(&sQ[r][ch * 8]) = qv;
-        *reinterpret_cast<half8*>(&sO[r][ch * 8]) = dvv;
+  const half_t* qbase = a.q + (int64_t)h * a.q_head;
+  const half_t* dbase = a.dout + (int64_t)h * a.do_head;
+  for (int qt = k0; qt < len; qt += kQt) {
+    __syncthreads();
+    // Query tile [qt, qt + 32): Q and dO rows and transposes, lse2, delta.
+    for (int c = threadIdx.x; c < kQt * (kD / 8); c += 256) {
+      const int r = c >> 4, ch = c & 15;
+      const int t = min(qt + r, len - 1);
+      const half8 qv = ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
+      const half8 dvv = ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
+      *reinterpret_cast<half8*>(&sQ[r][ch * 8]) = qv;
+      *reinterpret_cast<half8*>(&sO[r][ch * 8]) = dvv;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          sQt[ch * 8 + j][r] = qv[j];
-          sOt[ch * 8 + j][r] = dvv[j];
-        }
-        if (c < 16) {
-          sL[c] = a.lse2[(int64_t)h * a.total + start + min(qt + c, len - 1)];
-          sDl[c] = a.delta[(int64_t)h * a.total + start + min(qt + c, len - 1)];
-        }
+      for (int j = 0; j < 8; ++j) {
+        sQt[ch * 8 + j][r] = qv[j];
+        sOt[ch * 8 + j][r] = dvv[j];
       }
-      __syncthreads();
+    }
+    if (threadIdx.x < kQt) {
+      const int64_t idx = (int64_t)h * a.total + start + min(qt + (int)threadIdx.x, len - 1);
+      sL[threadIdx.x] = a.lse2[idx];
+      sDl[threadIdx.x] = a.delta[idx];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sub = 0; sub < kQt / 16; ++sub) {
       float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        s = mfma16(ld4(&sQ[col][ks * 16 + grp * 4]), kf[ks], s);   // S[q][key]
-        dp = mfma16(ld4(&sO[col][ks * 16 + grp * 4]), vf[ks], dp); // dP[q][key]
+        s = mfma16(ld4(&sQ[sub * 16 + col][ks * 16 + grp * 4]), kf[ks], s);   // S[q][key]
+        dp = mfma16(ld4(&sO[sub * 16 + col][ks * 16 + grp * 4]), vf[ks], dp); // dP[q][key]
       }
-      half4 p16, ds16;  // P^T / dS^T as A operands: [key = mykey][q = qt + 4 grp + i]
+      half4 p16, ds16;  // P^T / dS^T as A operands: [key = mykey][q = qt + 16 sub + 4 grp + i]
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int q = qt + grp * 4 + i;
+        const int ql = sub * 16 + grp * 4 + i;
+        const int q = qt + ql;
         const float p = (mykey <= q && q < len && mykey < len)
-                            ? exp2f(s[i] * sl2 - sL[grp * 4 + i]) : 0.f;
+                            ? exp2f(s[i] * sl2 - sL[ql]) : 0.f;
         p16[i] = f32_to_f16(p);
-        ds16[i] = f32_to_f16(p * (dp[i] - sDl[grp * 4 + i]));
+        ds16[i] = f32_to_f16(p * (dp[i] - sDl[ql]));
       }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        dv[dt] = mfma16(p16, ld4(&sOt[dt * 16 + col][grp * 4]), dv[dt]);
-        dk[dt] = mfma16(ds16, ld4(&sQt[dt * 16 + col][grp * 4]), dk[dt]);
+        dv[dt] = mfma16(p16, ld4(&sOt[dt * 16 + col][sub * 16 + grp * 4]), dv[dt]);
+        dk[dt] = mfma16(ds16, ld4(&sQt[dt * 16 + col][sub * 16 + grp * 4]), dk[dt]);
       }
     }
   }
-  half_t* kb = a.dk + (int64_t)kvh * a.dk_head;
-  half_t* vb = a.dv + (int64_t)kvh * a.dv_head;
+  const bool direct = a.hq == a.hk;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = k0w + grp * 4 + i;
-    if (key < len) {
+    if (key >= len) continue;
+    if (direct) {
+      half_t* kb = a.dk + (int64_t)kvh * a.dk_head + (int64_t)(start + key) * a.dk_tok;
+      half_t* vb = a.dv + (int64_t)kvh * a.dv_head + (int64_t)(start + key) * a.dv_tok;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        kb[(int64_t)(start + key) * a.dk_tok + dt * 16 + col] = f32_to_f16(dk[dt][i] * a.scale);
-        vb[(int64_t)(start + key) * a.dv_tok + dt * 16 + col] = f32_to_f16(dv[dt][i]);
+        kb[dt * 16 + col] = f32_to_f16(dk[dt][i] * a.scale);
+        vb[dt * 16 + col] = f32_to_f16(dv[dt][i]);
+      }
+    } else {
+      float* kp = part_k + ((int64_t)h * a.total + start + key) * kD;
+      float* vp = part_v + ((int64_t)h * a.total + start + key) * kD;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        kp[dt * 16 + col] = dk[dt][i];
+        vp[dt * 16 + col] = dv[dt][i];
       }
     }
   }
+}
+
+// dK / dV of a GQA group: the q heads' fp32 partials added in head order
+// (deterministic), dK scaled; four consecutive d per thread.
+__global__ __launch_bounds__(256) void attn_bwd_reduce_kernel(AttnArgs a, const float* part_k,
+                                                              const float* part_v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (token, kv head, d / 4)
+  const int64_t per_tok = (int64_t)a.hk * (kD / 4);
+  if (i >= a.total * per_tok) return;
+  const int64_t t = i / per_tok;
+  const int kvh = (int)((i % per_tok) / (kD / 4));
+  const int d = (int)(i % (kD / 4)) * 4;
+  const int group = a.hq / a.hk;
+  float4v sk = float4v{0.f, 0.f, 0.f, 0.f}, sv = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int hh = 0; hh < group; ++hh) {
+    const int64_t off = ((int64_t)(kvh * group + hh) * a.total + t) * kD + d;
+    sk += *reinterpret_cast<const float4v*>(part_k + off);
+    sv += *reinterpret_cast<const float4v*>(part_v + off);
+  }
+  half4 ok, ov;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ok[j] = f32_to_f16(sk[j] * a.scale);
+    ov[j] = f32_to_f16(sv[j]);
+  }
+  *reinterpret_cast<half4*>(a.dk + t * a.dk_tok + (int64_t)kvh * a.dk_head + d) = ok;
+  *reinterpret_cast<half4*>(a.dv + t * a.dv_tok + (int64_t)kvh * a.dv_head + d) = ov;
 }
 
 bool al8(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -415,6 +460,15 @@ extern "C" int ss_attn_varlen_fwd(const void* q, int64_t q_tok, int64_t q_head, 
   return SS_OK;
 }
 
+static size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+extern "C" size_t ss_attn_varlen_bwd_workspace_size(int hq, int hk, int64_t total) {
+  if (hq <= 0 || hk <= 0 || total <= 0) return 0;
+  const size_t delta = round256((size_t)hq * total * sizeof(float));
+  const size_t part = hq == hk ? 0 : round256((size_t)hq * total * kD * sizeof(float));
+  return delta + 2 * part;
+}
+
 extern "C" int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void* k,
                                   int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
                                   int64_t v_head, const void* o, int64_t o_tok, int64_t o_head,
@@ -423,16 +477,22 @@ extern "C" int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, 
                                   int64_t total, int hq, int hk, int head_dim, float scale,
                                   void* dq, int64_t dq_tok, int64_t dq_head, void* dk,
                                   int64_t dk_tok, int64_t dk_head, void* dv, int64_t dv_tok,
-                                  int64_t dv_head, float* delta, void* stream) {
+                                  int64_t dv_head, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
   const char* fn = "ss_attn_varlen_bwd";
   int rc = check_common(fn, rows, max_len, hq, hk, head_dim, total, cu_seqlens);
   if (rc) return rc;
   if (rows == 0 || max_len == 0) return SS_OK;
   SS_CHECK_ARG(strides_ok(q, q_tok, q_head) && strides_ok(k, k_tok, k_head) &&
                    strides_ok(v, v_tok, v_head) && strides_ok(o, o_tok, o_head) &&
-                   strides_ok(dout, do_tok, do_head) && dq && dk && dv && lse2 && delta,
-               "%s: q/k/v/o/dO need 16-byte aligned bases and strides that are multiples of 8",
-               fn);
+                   strides_ok(dout, do_tok, do_head) && strides_ok(dq, dq_tok, dq_head) &&
+                   strides_ok(dk, dk_tok, dk_head) && strides_ok(dv, dv_tok, dv_head) && lse2,
+               "%s: q/k/v/o/dO/dq/dk/dv need 16-byte aligned bases and strides that are "
+               "multiples of 8", fn);
+  const size_t need = ss_attn_varlen_bwd_workspace_size(hq, hk, total);
+  SS_CHECK_ARG(workspace && workspace_bytes >= need && al8(workspace),
+               "%s: workspace of %zu bytes (16-byte aligned) needed, %zu given", fn, need,
+               workspace_bytes);
   AttnArgs a{};
   a.q = (const half_t*)q; a.q_tok = q_tok; a.q_head = q_head;
   a.k = (const half_t*)k; a.k_tok = k_tok; a.k_head = k_head;
@@ -442,15 +502,26 @@ extern "C" int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, 
   a.out = (half_t*)dq; a.out_tok = dq_tok; a.out_head = dq_head;
   a.dk = (half_t*)dk; a.dk_tok = dk_tok; a.dk_head = dk_head;
   a.dv = (half_t*)dv; a.dv_tok = dv_tok; a.dv_head = dv_head;
-  a.lse2 = const_cast<float*>(lse2); a.delta = delta;
+  a.lse2 = const_cast<float*>(lse2);
+  a.delta = static_cast<float*>(workspace);
   a.cu = cu_seqlens; a.total = total; a.hq = hq; a.hk = hk; a.scale = scale;
+  char* base = static_cast<char*>(workspace) + round256((size_t)hq * total * sizeof(float));
+  const size_t part = round256((size_t)hq * total * kD * sizeof(float));
+  float* part_k = hq == hk ? nullptr : reinterpret_cast<float*>(base);
+  float* part_v = hq == hk ? nullptr : reinterpret_cast<float*>(base + part);
   const unsigned blocks = (unsigned)cdiv(max_len, kBlk);
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(attn_bwd_dq_kernel, dim3(blocks, (unsigned)hq, (unsigned)rows), dim3(256), 0,
                      st, a);
   SS_CHECK_LAUNCH("attn_bwd_dq_kernel");
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(blocks, (unsigned)hk, (unsigned)rows), dim3(256),
-                     0, st, a);
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(blocks, (unsigned)hq, (unsigned)rows), dim3(256),
+                     0, st, a, part_k, part_v);
   SS_CHECK_LAUNCH("attn_bwd_dkdv_kernel");
+  if (hq != hk) {
+    const int64_t work = total * hk * (kD / 4);
+    hipLaunchKernelGGL(attn_bwd_reduce_kernel, dim3((unsigned)cdiv(work, 256)), dim3(256), 0, st,
+                       a, part_k, part_v);
+    SS_CHECK_LAUNCH("attn_bwd_reduce_kernel");
+  }
   return SS_OK;
 }

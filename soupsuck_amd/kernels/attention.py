@@ -4,8 +4,8 @@ Semantics of the reference's packed attention (solution/unpad.py:359-410): the
 rows of a packed batch lie back to back on the token axis and each attends
 causally to itself only, softmax(scale q.k) with GQA.  Here one launch covers
 every row and head (ss_attn_varlen_fwd; backward ss_attn_varlen_bwd: dQ, then
-dK / dV summed over the GQA group in registers), instead of one SDPA call
-per row.  fp16 in and out, fp32 softmax statistics.
+dK / dV per q head, the GQA group's partials added in head order), instead of
+one SDPA call per row.  fp16 in and out, fp32 softmax statistics.
 
 Inputs follow Qwen2Attention's layout: q [1, Hq, T, 128], k / v [1, Hk, T, 128]
 (any head / token strides with a unit last stride, e.g. the transposed
@@ -29,11 +29,6 @@ def row_offsets(lengths, device):
         cu.append(cu[-1] + int(n))
     host = torch.tensor(cu, dtype=torch.int32).pin_memory()
     return host.to(device, non_blocking=True)
-
-
-def _view(t):
-    """(tensor, token stride, head stride) of a [1, H, T, D] tensor."""
-    return t, t.stride(2), t.stride(1)
 
 
 def _aligned(t):
@@ -73,7 +68,8 @@ class PackedCausalAttention(torch.autograd.Function):
         dq = torch.empty((1, total, hq, d), device=q.device, dtype=torch.float16)
         dk = torch.empty((1, total, hk, d), device=q.device, dtype=torch.float16)
         dv = torch.empty((1, total, hk, d), device=q.device, dtype=torch.float16)
-        delta = torch.empty((hq, total), device=q.device, dtype=torch.float32)
+        size = _lib.load().ss_attn_varlen_bwd_workspace_size(hq, hk, total)
+        ws = torch.empty(max(size, 16), device=q.device, dtype=torch.uint8)
         dqv, dkv, dvv = dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2)
         _lib.call("ss_attn_varlen_bwd", q.data_ptr(), q.stride(2), q.stride(1), k.data_ptr(),
                   k.stride(2), k.stride(1), v.data_ptr(), v.stride(2), v.stride(1),
@@ -81,7 +77,7 @@ class PackedCausalAttention(torch.autograd.Function):
                   gv.stride(1), lse2.data_ptr(), cu.data_ptr(), cu.numel() - 1, max_len, total,
                   hq, hk, d, scale, dq.data_ptr(), dqv.stride(2), dqv.stride(1), dk.data_ptr(),
                   dkv.stride(2), dkv.stride(1), dv.data_ptr(), dvv.stride(2), dvv.stride(1),
-                  delta.data_ptr(), _lib.stream(q.device))
+                  ws.data_ptr(), size, _lib.stream(q.device))
         return dqv, dkv, dvv, None, None, None
 
 
