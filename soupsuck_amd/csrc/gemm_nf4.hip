@@ -377,17 +377,13 @@ bool gemm_nf4_fwd_ok(const GemmParams& p, int epi) {
 // graph, one call at a time, weights rotated through HBM for the 7B shapes):
 //   T in (128, 256] (one or two 128-row tiles): fused ahead at every shape
 //     (7B gate 18944 x 3584 at T = 256: 88 vs 103 us; 1.5B gate: 34 vs 44);
-//   larger T: ahead for 64x64 tiles (990 x 1536 x 1536: 23.4 vs 25.2 us) and
-//     for 256x256 tiles with at most 4 M tiles (990 x 8960 x 1536: 61.9 vs
-//     66.1), behind for 128x128 tiles (990 x 1536 x 8960: 73.7 vs 66.5) and
-//     8 M tiles of 256 (2048 x 18944 x 3584: 392 vs 360).
+//   larger T: behind once the decode runs at the stand-alone decoder's rate
+//     (990 x 1536 x 1536: 25.0 vs 24.2 us; 990 x 8960 x 1536: 62.8 vs 56.1;
+//     2048 x 18944 x 3584: 392 vs 360).
 // T <= 128 stays on the streaming / skinny kernels (7B gate at T = 33: 32 vs
 // 48 us fused).
 bool gemm_nf4_fwd_preferred(const GemmParams& p) {
-  if (p.M <= kSkinnyMaxT) return false;
-  if (p.M <= 256) return true;
-  const NtPlan plan = nf4_plan(p.M, p.N, p.K);
-  return plan.cfg == 1 || (plan.cfg == 8 && cdiv(p.M, 256) <= 4);
+  return p.M > kSkinnyMaxT && p.M <= 256;
 }
 
 size_t nf4_fused_partial_bytes(int64_t m, int64_t n, int64_t k) {

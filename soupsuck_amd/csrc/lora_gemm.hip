@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kRankMaxWaves * 64) void rank_grad_kernel(RankGradA
 }
 
 constexpr int cmax(int a, int b) { return a > b ? a : b; }
-constexpr int kPrepSmem = cmax(cmax(kRankGradSmem, kRankProjSmem), cmax(kDecodeSmem, kDecodeT2Smem));
+constexpr int kPrepSmem = cmax(cmax(kRankGradSmem, kRankProjSmem), cmax(cmax(kDecodeSmem, kDecodeT2Smem), kDecodeRowsSmem));
 
 // The wide transposed decode tile (64 n x 128 k) applies to cols % 128 == 0
 // and 16-byte aligned codes.
@@ -53,10 +53,15 @@ static bool wide_t(const Nf4View& w, int64_t cols) {
 
 // Blocks [0, proj_blocks): project (mblocks x splits, block-major); then
 // grad blocks; then decode blocks (row-major decode: grid-stride over
-// dec_blocks; transposed decode: one 64 x 128 tile each, 64 x 64 when the
-// columns are not a multiple of 128).
+// dec_blocks, eight code dwords in flight per lane; transposed decode: one
+// 64 x 128 tile each, 64 x 64 when the columns are not a multiple of 128).
+// With vector grad loads (VG) at most 168 VGPRs, so that three workgroups
+// share a CU (the LDS allows three).  The decode blocks inherit the rank blocks' footprint: with one
+// code dword in flight per lane they ran at half the stand-alone decoder's
+// rate (gate 8960 x 1536: prep 19.8 us against 10.9 us for the decode
+// alone); with eight, the launch costs about what its longer job costs.
 template <bool VP, bool VG>
-__global__ __launch_bounds__(256) void qlora_prep_kernel(PrepJobs pj) {
+__global__ __launch_bounds__(256, VG ? 3 : 2) void qlora_prep_kernel(PrepJobs pj) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[kPrepSmem];
   int64_t b = blockIdx.x;
   if (b < pj.proj_blocks) {
@@ -73,9 +78,10 @@ __global__ __launch_bounds__(256) void qlora_prep_kernel(PrepJobs pj) {
   b -= pj.grad_blocks;
   const Nf4View& w = pj.dec_w;
   if (pj.dec_kind == kDecodeRows) {
-    decode_vec_block<true>(reinterpret_cast<const uint32_t*>(w.packed), w.qabs, nullptr,
-                           w.absmax2, w.code2, w.offset, reinterpret_cast<half8*>(pj.dec_out),
-                           pj.dec_rows * pj.dec_cols / 8, b, pj.dec_blocks, smem);
+    decode_rows_block<true, 8>(reinterpret_cast<const uint32_t*>(w.packed), w.qabs, nullptr,
+                               w.absmax2, w.code2, w.offset,
+                               reinterpret_cast<half8*>(pj.dec_out),
+                               pj.dec_rows * pj.dec_cols / 8, b, pj.dec_blocks, smem);
   } else if (pj.dec_cols % 128 == 0 && reinterpret_cast<uintptr_t>(w.packed) % 16 == 0) {
     decode_t2_block(w.packed, w.qabs, w.absmax2, w.code2, w.offset, pj.dec_out, pj.dec_rows,
                     pj.dec_cols, b, smem);
@@ -136,8 +142,8 @@ int launch_prep(PrepJobs& pj, bool vp, bool vg, hipStream_t stream) {
   int64_t dec = 0;
   if (pj.dec_kind == kDecodeRows) {
     const int64_t groups = pj.dec_rows * pj.dec_cols / 8;
-    const int64_t cap = 256 * 8;
-    pj.dec_blocks = cdiv(groups, 256) < cap ? cdiv(groups, 256) : cap;
+    const int64_t cap = 4096;
+    pj.dec_blocks = cdiv(groups, 8 * 256) < cap ? cdiv(groups, 8 * 256) : cap;
     dec = pj.dec_blocks;
   } else if (pj.dec_kind == kDecodeTransposed) {
     pj.dec_blocks = cdiv(pj.dec_rows, 64) *
@@ -146,6 +152,9 @@ int launch_prep(PrepJobs& pj, bool vp, bool vg, hipStream_t stream) {
   }
   const int64_t blocks = pj.proj_blocks + pj.grad_blocks + dec;
   if (blocks == 0) return SS_OK;
+  // Without grad blocks the grad variant is irrelevant; the vector one has
+  // the smaller register footprint.
+  if (pj.grad_blocks == 0) vg = true;
   auto kern = vp ? (vg ? qlora_prep_kernel<true, true> : qlora_prep_kernel<true, false>)
                  : (vg ? qlora_prep_kernel<false, true> : qlora_prep_kernel<false, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, pj);

@@ -3,27 +3,27 @@
 // Reference: solution/kernels/nf4.py:41-59 (nf4_decode_kernel), formula at
 // :7-10.  HBM-bound: 0.5 B read + 2 B written per element (+1/64 B qabs).
 //
-// Vector path: each lane decodes 8 consecutive elements per step -- one
-// packed dword (4 bytes) in, one 16-byte fp16 store out -- so a wave moves
-// 256 B of nibbles and writes 1 KiB contiguous per step.  The 16-entry NF4
-// table sits in LDS; 16 floats occupy 16 distinct banks, so any per-lane
-// lookup pattern is conflict-free.  8 consecutive elements always share one
-// 64-block (8 divides 64), so each step needs a single scale.
+// Vector path (decode_rows_block): each lane decodes 8 consecutive elements
+// per group -- one packed dword (4 bytes) in, one 16-byte fp16 store out --
+// with U groups per lane in flight, so a wave moves U x 256 B of nibbles and
+// writes 1 KiB contiguous per store.  The NF4 and code2 tables sit in LDS.
+// 8 consecutive elements always share one 64-block (8 divides 64), so each
+// group needs a single scale.
 // Generic path: one element per lane, any alignment / tail.
 
 #include "decode_blocks.h"
 
 namespace ss {
 
-template <bool NESTED>
+template <bool NESTED, int U>
 __global__ __launch_bounds__(256) void nf4_dequant_vec_kernel(
     const uint32_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ absmax, const float* __restrict__ absmax2,
     const float* __restrict__ code2, const float* __restrict__ offset_ptr,
     half8* __restrict__ out, int64_t groups) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[64];
-  decode_vec_block<NESTED>(packed, qabs, absmax, absmax2, code2, offset_ptr, out, groups,
-                           blockIdx.x, gridDim.x, smem);
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kDecodeRowsSmem];
+  decode_rows_block<NESTED, U>(packed, qabs, absmax, absmax2, code2, offset_ptr, out, groups,
+                               blockIdx.x, gridDim.x, smem);
 }
 
 template <bool NESTED>
@@ -81,9 +81,15 @@ static int launch_dequant(const uint8_t* packed, const uint8_t* qabs, const floa
   if (aligned) {
     const int64_t groups = n / 8;
     if (groups > 0) {
-      hipLaunchKernelGGL(nf4_dequant_vec_kernel<NESTED>, dim3(grid_for(groups, 256)), dim3(256), 0,
-                         stream, reinterpret_cast<const uint32_t*>(packed), qabs, absmax, absmax2,
-                         code2, offset, reinterpret_cast<half8*>(o), groups);
+      // 8 groups per lane and step from 2^20 groups (8M elements) on, else 2;
+      // at most 4096 workgroups, grid-stride beyond.
+      const bool wide = groups >= ((int64_t)1 << 20);
+      const int64_t per_block = (wide ? 8 : 2) * 256;
+      const int64_t blocks = cdiv(groups, per_block) < 4096 ? cdiv(groups, per_block) : 4096;
+      auto kern = wide ? nf4_dequant_vec_kernel<NESTED, 8> : nf4_dequant_vec_kernel<NESTED, 2>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         reinterpret_cast<const uint32_t*>(packed), qabs, absmax, absmax2, code2,
+                         offset, reinterpret_cast<half8*>(o), groups);
       SS_CHECK_LAUNCH("nf4_dequant_vec_kernel");
     }
     done = groups * 8;
