@@ -462,6 +462,15 @@ int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void*
                        int64_t dv_tok, int64_t dv_head, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* --------------------------------------- lossless fp16 table storage (f4) ---
+ * dst[i] = fp16_rne(src[i]) for i < n, and *flag = 1 if any element does not
+ * round-trip exactly ((float)dst[i] != src[i]; NaN never does).  *flag is
+ * only ever set, never cleared: the caller zeroes it first and reads it
+ * after the stream reaches this call.  Replaces the chunked copy-and-compare
+ * of solution/embedding.py:51-64 (_lossless_candidate) with one pass.
+ * Any alignment (16-byte aligned src / dst take the vector path). */
+int ss_f32_to_f16_exact(const float* src, uint16_t* dst, int64_t n, int* flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,10 @@ Routes (reference file of the behaviour each one keeps):
     Qwen2Attention.forward     causal attention within each row in one launch
                                (solution/unpad.py:359-450), in soupsuck_amd.unpad_route;
   PEFT (solution/lora.py:135-166), in soupsuck_amd.peft_route:
-    tuners.lora.bnb.Linear4bit.forward  the fused QLoRA projection.
+    tuners.lora.bnb.Linear4bit.forward  the fused QLoRA projection;
+  Soup (solution/embedding.py:146-169), in soupsuck_amd.embedding:
+    trainer.sft.SFTTrainerWrapper._setup_transformers  lossless fp16 storage of the
+                               tied embedding / lm_head after the original setup.
 Every replacement falls back to the original when SOUP_FUSED_DISABLE is set
 or a call is outside the supported contract, and carries the original under
 its marker (``_solution_fused_original``; the PEFT route uses
@@ -220,6 +223,12 @@ def _build_bnb(name):
     return build
 
 
+def _build_soup_setup(original, module):
+    from .embedding import build_soup_setup
+
+    return build_soup_setup(original, module)
+
+
 def _build_peft(original, module):
     from .peft_route import build_linear4bit_forward
 
@@ -235,6 +244,8 @@ MODEL_ROUTE = Route(QWEN, "Qwen2Model", "forward", _build_model)
 ATTENTION_ROUTE = Route(QWEN, "Qwen2Attention", "forward", _build_attention)
 PEFT_ROUTE = Route("peft.tuners.lora.bnb", "Linear4bit", "forward", _build_peft,
                    "_solution_lora_4bit_original")
+SOUP_SETUP_ROUTE = Route("soup_cli.trainer.sft", "SFTTrainerWrapper", "_setup_transformers",
+                         _build_soup_setup)
 BNB_ROUTES = (
     Route("bitsandbytes.functional", None, "dequantize_4bit", _build_bnb("build_dequantize")),
     Route("bitsandbytes.backends.cuda.ops", None, "_dequantize_4bit_impl",
@@ -244,7 +255,7 @@ BNB_ROUTES = (
     Route("bitsandbytes", None, "matmul_4bit", _build_bnb("build_matmul")),
 )
 ROUTES = (DECODER_ROUTE, RMSNORM_ROUTE, MLP_ROUTE, ROPE_ROUTE, HEAD_ROUTE, MODEL_ROUTE,
-          ATTENTION_ROUTE, PEFT_ROUTE) + BNB_ROUTES
+          ATTENTION_ROUTE, PEFT_ROUTE, SOUP_SETUP_ROUTE) + BNB_ROUTES
 TARGETS = tuple(sorted({r.module for r in ROUTES}))
 
 
