@@ -20,6 +20,7 @@ Only the format on the reference's hot path is implemented: NF4, blocksize
 Anything else raises NotImplementedError -- there is no CPU path.
 """
 
+import json
 from types import SimpleNamespace
 
 import torch
@@ -53,8 +54,38 @@ def dynamic_map_signed():
 _DYNAMIC = None
 
 
+def pack_dict_to_tensor(items):
+    """The non-tensor items of a serialized QuantState as one uint8 tensor: the UTF-8
+    bytes of ``json.dumps(items)`` (bitsandbytes' checkpoint format)."""
+    return torch.tensor(list(json.dumps(items).encode("utf-8")), dtype=torch.uint8)
+
+
+def unpack_tensor_to_dict(t):
+    return json.loads(bytes(t.detach().cpu().numpy()).decode("utf-8"))
+
+
+_QS_KEYS = ("absmax", "quant_map", "nested_absmax", "nested_quant_map", "quant_state",
+            "quant_type", "blocksize", "dtype", "shape", "nested_blocksize", "nested_dtype",
+            "nested_offset")
+
+
+def _dtype_name(dtype):
+    return str(dtype).split(".")[-1]
+
+
 class QuantState:
-    """NF4 quantization state with bitsandbytes' attribute names."""
+    """NF4 quantization state with bitsandbytes' attribute names and checkpoint format.
+
+    ``as_dict(packed=True)`` gives the tensors a ``Linear4bit`` state dict carries
+    next to its packed weight -- absmax (uint8 block codes), quant_map (NF4
+    table), nested_absmax / nested_quant_map (second-level statistics) and
+    ``quant_state.bitsandbytes__nf4``, the JSON of the remaining fields packed
+    into uint8 -- so safetensors checkpoints of bitsandbytes 0.50.2 and of this
+    package load into each other; ``from_dict`` reads either form back.
+    """
+
+    valid_quant_types = ("fp4", "nf4")
+    valid_qs_type_keys = tuple(f"bitsandbytes__{q}" for q in valid_quant_types)
 
     def __init__(self, absmax, shape=None, code=None, blocksize=None, quant_type=None,
                  dtype=None, offset=None, state2=None):
@@ -74,6 +105,57 @@ class QuantState:
             self.state2.absmax = self.state2.absmax.to(device)
             self.state2.code = self.state2.code.to(device)
         return self
+
+    def as_dict(self, packed=False):
+        items = {"quant_type": self.quant_type, "absmax": self.absmax,
+                 "blocksize": self.blocksize, "quant_map": self.code,
+                 "dtype": _dtype_name(self.dtype), "shape": tuple(self.shape)}
+        if self.nested:
+            items.update({"nested_absmax": self.state2.absmax,
+                          "nested_blocksize": self.state2.blocksize,
+                          # its own storage: safetensors drops tensors that share one
+                          "nested_quant_map": self.state2.code.clone(),
+                          "nested_dtype": _dtype_name(self.state2.dtype),
+                          "nested_offset": float(self.offset.reshape(-1)[0].item())})
+        if not packed:
+            return items
+        out = {k: v for k, v in items.items() if isinstance(v, torch.Tensor)}
+        rest = {k: v for k, v in items.items() if not isinstance(v, torch.Tensor)}
+        out["quant_state.bitsandbytes__" + self.quant_type] = pack_dict_to_tensor(rest)
+        return out
+
+    @classmethod
+    def from_dict(cls, qs_dict, device):
+        """A QuantState from ``as_dict()`` output (packed or not; key prefixes allowed)."""
+        qs_dict = dict(qs_dict)
+        packed_keys = [k for k, v in qs_dict.items()
+                       if "quant_state" in k and isinstance(v, torch.Tensor)]
+        if not packed_keys and "quant_type" not in qs_dict:
+            raise ValueError("expected packed or unpacked quant_state items, found neither")
+        if packed_keys:
+            if len(packed_keys) != 1 or packed_keys[0].split(".")[-1] not in \
+                    cls.valid_qs_type_keys:
+                raise ValueError(f"expected exactly one quant_state item ending in one of "
+                                 f"{cls.valid_qs_type_keys}, found {packed_keys}")
+            qs_dict.update(unpack_tensor_to_dict(qs_dict.pop(packed_keys[0])))
+        qs_dict = {k.split(".")[-1]: v for k, v in qs_dict.items()}
+        unknown = set(qs_dict) - set(_QS_KEYS)
+        if unknown:
+            raise ValueError(f"unknown quant_state items {sorted(unknown)}")
+        device = torch.device(device)
+        offset = state2 = None
+        if "nested_absmax" in qs_dict:
+            offset = torch.tensor(float(qs_dict["nested_offset"]), device=device)
+            state2 = cls(absmax=qs_dict["nested_absmax"].to(device),
+                         blocksize=qs_dict["nested_blocksize"],
+                         code=qs_dict["nested_quant_map"].to(device),
+                         dtype=getattr(torch, qs_dict["nested_dtype"]))
+        shape = qs_dict["shape"]
+        return cls(quant_type=qs_dict["quant_type"], absmax=qs_dict["absmax"].to(device),
+                   blocksize=qs_dict["blocksize"], code=qs_dict["quant_map"].to(device),
+                   dtype=getattr(torch, qs_dict["dtype"]),
+                   shape=torch.Size(shape) if shape is not None else None,
+                   offset=offset, state2=state2)
 
 
 def quantize_4bit(A, absmax=None, out=None, blocksize=64, compress_statistics=True,
@@ -101,8 +183,7 @@ def quantize_4bit(A, absmax=None, out=None, blocksize=64, compress_statistics=Tr
         _lib.call("ss_nf4_quantize", flat.data_ptr(), _lib.dtype_code(flat.dtype), n,
                   packed.data_ptr(), qabs.data_ptr(), absmax2.data_ptr(), code2.data_ptr(),
                   offset.data_ptr(), scratch.data_ptr(), _lib.stream(device))
-    state2 = SimpleNamespace(absmax=absmax2, code=code2, blocksize=256, dtype=torch.float32,
-                             nested=False)
+    state2 = QuantState(absmax2, code=code2, blocksize=256, dtype=torch.float32)
     nf4_code = torch.tensor(_nf4_table(), dtype=torch.float32, device=device)
     shape = tuple(A.shape) if A.ndim == 2 else (1, n)
     state = QuantState(qabs, shape=shape, code=nf4_code, blocksize=64, quant_type="nf4",
@@ -146,6 +227,18 @@ class Params4bit(torch.nn.Parameter):
         self.quant_state = quant_state
         self.blocksize, self.compress_statistics = blocksize, compress_statistics
         self.quant_type, self.quant_storage = quant_type, quant_storage
+        return self
+
+    @classmethod
+    def from_prequantized(cls, data, quantized_stats, requires_grad=False, device="cuda",
+                          module=None, **_):
+        """A quantized weight from a checkpoint: packed codes + ``QuantState.as_dict`` items."""
+        state = QuantState.from_dict(quantized_stats, device=device)
+        self = cls(data.to(device), requires_grad=requires_grad, quant_state=state,
+                   blocksize=state.blocksize, compress_statistics=state.nested,
+                   quant_type=state.quant_type, quant_storage=data.dtype)
+        if module is not None:
+            module.quant_state = state
         return self
 
     def _quantize(self, device):
@@ -204,6 +297,38 @@ class Linear4bit(torch.nn.Linear):
                 raise NotImplementedError("moving a quantized Linear4bit between GPUs")
         return result
 
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        state = getattr(self.weight, "quant_state", None)
+        if state is not None:
+            for key, value in state.as_dict(packed=True).items():
+                destination[prefix + "weight." + key] = value if keep_vars else value.detach()
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        stats_prefix = prefix + "weight."
+        stats = {k[len(stats_prefix):]: v for k, v in state_dict.items()
+                 if k.startswith(stats_prefix)}
+        packed = state_dict.get(prefix + "weight")
+        if not stats or packed is None:
+            super()._load_from_state_dict(state_dict, prefix, local_metadata, strict,
+                                          missing_keys, unexpected_keys, error_msgs)
+            return
+        current = self.weight
+        if packed.is_cuda:
+            device = packed.device
+        elif current.is_cuda:
+            device = current.device
+        else:
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.weight = Params4bit.from_prequantized(packed, stats, device=device, module=self)
+        rest = {k: v for k, v in state_dict.items()
+                if k.startswith(prefix) and k != prefix + "weight" and not k.startswith(stats_prefix)}
+        before = len(missing_keys)
+        super()._load_from_state_dict(rest, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+        missing_keys[before:] = [k for k in missing_keys[before:] if k != prefix + "weight"]
+
     def forward(self, x):
         state = getattr(self.weight, "quant_state", None)
         if state is None:
@@ -219,7 +344,8 @@ class Linear4bit(torch.nn.Linear):
 
 
 functional = SimpleNamespace(quantize_4bit=quantize_4bit, dequantize_4bit=dequantize_4bit,
-                             QuantState=QuantState)
+                             QuantState=QuantState, pack_dict_to_tensor=pack_dict_to_tensor,
+                             unpack_tensor_to_dict=unpack_tensor_to_dict)
 nn = SimpleNamespace(Params4bit=Params4bit, Linear4bit=Linear4bit)
 
 COMPAT_VERSION = "0.50.2+soupsuck_amd.compat"
