@@ -128,15 +128,21 @@ def build_causal_lm_forward(original, module):
         model_args = dict(input_ids=input_ids, attention_mask=attention_mask,
                           position_ids=position_ids, past_key_values=past_key_values,
                           inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
-        if type(self) is not cls or not _call_ok(labels, logits_to_keep, kwargs):
-            return original(self, labels=labels, logits_to_keep=logits_to_keep, **model_args)
+        from .norm_scope import final_norm_half_ready, half_norm_scope
+
+        exact = type(self) is cls
+        owner = self.model.norm if exact and final_norm_half_ready(self, kwargs) else None
+        if not exact or not _call_ok(labels, logits_to_keep, kwargs):
+            with half_norm_scope(owner):
+                return original(self, labels=labels, logits_to_keep=logits_to_keep, **model_args)
         num_items = kwargs.pop("num_items_in_batch", None)
         model_args.pop("num_items_in_batch", None)
         from .unpad_route import HEAD_LABELS, take_packed_head
 
         token = HEAD_LABELS.set((labels, attention_mask))
         try:
-            outputs = self.model(**model_args)
+            with half_norm_scope(owner):
+                outputs = self.model(**model_args)
         finally:
             HEAD_LABELS.reset(token)
         hidden = outputs.last_hidden_state

@@ -16,8 +16,10 @@ Routes (reference file of the behaviour each one keeps):
     _dequant_linear_fallback, and matmul_4bit (the NF4 GEMM);
   transformers Qwen2 (modeling_qwen2):
     Qwen2DecoderLayer.forward  attention residual add + post-attention norm
-                               fused (solution/decoder.py:54-89);
-    Qwen2RMSNorm.forward       the HIP row norm (solution/patch.py:232-250);
+                               fused (solution/decoder.py:54-89), with the fp16
+                               norm-output scopes of soupsuck_amd.norm_scope;
+    Qwen2RMSNorm.forward       the HIP row norm, fp16 output for the scoped owner
+                               (solution/patch.py:35-125,232-250);
     Qwen2MLP.forward           the frozen NF4 MLP node (solution/mlp.py:597-612);
     apply_rotary_pos_emb       the joint q/k RoPE (solution/rope.py:55-80);
     Qwen2ForCausalLM.forward   the chunked fused CE head (solution/patch.py:167-229),
@@ -114,16 +116,20 @@ _DECODER_ARGS = (("attention_mask", None), ("position_ids", None), ("past_key_va
                  ("use_cache", False), ("position_embeddings", None))
 
 
-def _residual_norm(norm, norm_cls, residual, update):
-    """(residual + update, norm(residual + update)); one HIP pass when the norm qualifies."""
+def _residual_norm(norm, norm_cls, residual, update, half=False):
+    """(residual + update, norm(residual + update)); one HIP pass when the norm qualifies,
+    with an fp16 norm output when ``half`` (the layer's MLP consumes it as fp16)."""
     weight = getattr(norm, "weight", None)
     if (type(norm) is norm_cls and _hookless(norm) and _float_cuda(update) and _float_cuda(weight)
             and update.shape == residual.shape and weight.ndim == 1
             and weight.numel() == residual.shape[-1]
             and update.device == residual.device == weight.device):
+        import torch
+
         from .kernels.add_rmsnorm import add_rms_norm
 
-        return add_rms_norm(residual, update, weight, norm.variance_epsilon)
+        return add_rms_norm(residual, update, weight, norm.variance_epsilon,
+                            torch.float16 if half else None)
     total = residual + update
     return total, norm(total)
 
@@ -143,9 +149,16 @@ def _build_decoder(original, module):
         call = dict(_DECODER_ARGS)
         call.update(named)
         call.update(kwargs)
-        attended, _ = self.self_attn(hidden_states=self.input_layernorm(hidden_states), **call)
+        from .norm_scope import half_norm_scope, input_norm_half_ready, post_norm_half_ready
+
+        owner = self.input_layernorm if input_norm_half_ready(self, hidden_states, kwargs) \
+            else None
+        with half_norm_scope(owner):
+            normed = self.input_layernorm(hidden_states)
+        attended, _ = self.self_attn(hidden_states=normed, **call)
         residual, normed = _residual_norm(self.post_attention_layernorm, norm_cls,
-                                          hidden_states, attended)
+                                          hidden_states, attended,
+                                          post_norm_half_ready(self, hidden_states))
         return residual + self.mlp(normed)
 
     return forward
@@ -162,9 +175,13 @@ def _build_rmsnorm(original, module):
                 and _float_cuda(weight) and weight.ndim == 1
                 and weight.shape[0] == hidden_states.shape[-1]
                 and weight.device == hidden_states.device):
-            from .kernels.rmsnorm import rms_norm
+            import torch
 
-            return rms_norm(hidden_states, weight, self.variance_epsilon)
+            from .kernels.rmsnorm import rms_norm
+            from .norm_scope import owns_half_output
+
+            half = torch.float16 if owns_half_output(self) else None
+            return rms_norm(hidden_states, weight, self.variance_epsilon, half)
         return original(self, hidden_states)
 
     return forward

@@ -71,13 +71,16 @@ def _nf4_base(base):
     return packed, state, bias
 
 
-def routed_call(layer, x, args, kwargs):
-    """The arguments of qlora_projection for an eligible call, else None."""
+def routed_call(layer, x, args, kwargs, as_fp16=False):
+    """The arguments of qlora_projection for an eligible call, else None.
+
+    as_fp16: judge the call as if x were the contiguous fp16 tensor it is about
+    to become (an owner deciding to produce x in fp16 asks this first)."""
     if not enabled() or args or any(k not in _ALLOWED_KWARGS or kwargs[k] is not None
                                     for k in kwargs):
         return None
-    if not (isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float16
-            and x.is_contiguous() and x.ndim >= 1):
+    if not (isinstance(x, torch.Tensor) and x.is_cuda and x.ndim >= 1
+            and (as_fp16 or (x.dtype == torch.float16 and x.is_contiguous()))):
         return None
     if layer.disable_adapters or layer.merged or len(layer.active_adapters) != 1:
         return None
@@ -113,6 +116,26 @@ def routed_call(layer, x, args, kwargs):
     p = float(drop.p) if isinstance(drop, torch.nn.Dropout) else 0.0
     return dict(x=x, lora_a=a.weight, lora_b=b.weight, packed=packed, state=state, bias=bias,
                 scaling=float(scaling), dropout_p=p, training=bool(drop.training))
+
+
+def fp16_ingress_ready(layer, x):
+    """True when the routed PEFT forward would take ``layer``'s input x as fp16
+    (reference solution/lora.py:104-127): an exact, hook-free PEFT Linear4bit whose
+    class carries this route, over an fp16-compute NF4 base, eligible for an fp16 x."""
+    import sys
+
+    from .norm_scope import _nf4_linear
+    from .patch import PEFT_ROUTE
+
+    cls = getattr(sys.modules.get(PEFT_ROUTE.module), PEFT_ROUTE.owner, None)
+    if (not isinstance(cls, type) or type(layer) is not cls
+            or not hasattr(cls.forward, PEFT_ROUTE.marker) or not _hookless(layer)):
+        return False
+    base = getattr(layer, "base_layer", None)
+    if (base is None or not _nf4_linear(base) or base.compute_dtype != torch.float16
+            or not base.compute_type_is_set or not _hookless(base)):
+        return False
+    return routed_call(layer, x, (), {}, as_fp16=True) is not None
 
 
 def packed_k(nf4):
