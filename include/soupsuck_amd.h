@@ -181,6 +181,43 @@ int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t
                       uint16_t* db, void* workspace, size_t workspace_bytes,
                       void* rank_workspace, size_t rank_workspace_bytes, void* stream);
 
+/* The same two steps with LoRA dropout p in (0, 1) on the LoRA input
+ * (reference solution/lora.py:1-40,151-163: PEFT's Dropout on an fp32 copy of
+ * X feeding lora_A only).  The mask is a function of (seed, element index of
+ * X [t, k]) -- Philox4x32-10, defined in ss_dropout_mask below -- recomputed
+ * wherever an element is used, never stored; forward and backward must get
+ * the same seed and p.  With Xd = fp16(keep ? fp32(x) * fp32(1 / (1 - p)) : 0):
+ * forward:  z = fp16(Xd . lora_a^T); y as ss_qlora_forward;
+ * backward: dz, db as ss_qlora_backward; da = fp16(dz^T . Xd);
+ *           dx = fp16(fp16(dy . Wdec) + (keep ? fp16(fp32(fp16(dz . lora_a))
+ *                * fp32(1 / (1 - p))) : 0)).
+ * K % 8 == 0; the backward also needs 16-byte aligned x, dx and lora_a rows
+ * (SS_ERR_UNSUPPORTED otherwise). */
+int ss_qlora_forward_dropout(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                             const uint8_t* qabs, const float* absmax2, const float* code2,
+                             const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                             const uint16_t* lora_a, const uint16_t* lora_b, float scale,
+                             uint64_t seed, float p, uint16_t* z, uint16_t* y, int64_t ldy,
+                             void* workspace, size_t workspace_bytes, void* rank_workspace,
+                             size_t rank_workspace_bytes, void* stream);
+int ss_qlora_backward_dropout(const uint16_t* dy, int64_t lddy, int64_t t, const uint8_t* packed,
+                              const uint8_t* qabs, const float* absmax2, const float* code2,
+                              const float* offset, int64_t n, int64_t k, const uint16_t* x,
+                              int64_t ldx, const uint16_t* z, const uint16_t* lora_a,
+                              const uint16_t* lora_b, float scale, uint64_t seed, float p,
+                              uint16_t* dx, int64_t lddx, uint16_t* dz, uint16_t* da,
+                              uint16_t* db, void* workspace, size_t workspace_bytes,
+                              void* rank_workspace, size_t rank_workspace_bytes, void* stream);
+
+/* The dropout mask of an X [rows, cols] for (seed, p): out[e] = 1 if element
+ * e = row * cols + col is kept, else 0 (uint8 [rows * cols]).  Definition:
+ * key = (seed mod 2^32, seed div 2^32), counter = (e div 4 mod 2^32,
+ * e div 4 div 2^32, 0, 0), u = word (e mod 4) of Philox4x32-10(counter, key)
+ * (Salmon et al., SC'11), keep = u < floor((1 - p) * 2^32).  The fused
+ * dropout entry points use exactly these bits.  p in (0, 1). */
+int ss_dropout_mask(uint64_t seed, float p, int64_t rows, int64_t cols, uint8_t* out,
+                    void* stream);
+
 /* ------------------------------------------------ rank-16 LoRA products ---
  * HBM-bound skinny GEMMs of the LoRA branch (reference solution/lora.py:161,
  * solution/lora_pair.py:52-65), fp32 accumulation, one fp16 rounding.

@@ -23,6 +23,7 @@ ERR_UNSUPPORTED = -3
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
 _int = ctypes.c_int
 _f32 = ctypes.c_float
 _size = ctypes.c_size_t
@@ -56,6 +57,15 @@ SIGNATURES = {
     "ss_qlora_backward": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p, _i64]
                          + [_c_void_p] * 3 + [_f32, _c_void_p, _i64] + [_c_void_p] * 3
                          + [_c_void_p, _size, _c_void_p, _size, _c_void_p],
+    "ss_qlora_forward_dropout": [_c_void_p, _i64, _i64] + [_c_void_p] * 5 + [_i64, _i64]
+                                + [_c_void_p] * 3 + [_f32, _u64, _f32, _c_void_p, _c_void_p,
+                                                      _i64, _c_void_p, _size, _c_void_p, _size,
+                                                      _c_void_p],
+    "ss_qlora_backward_dropout": [_c_void_p, _i64, _i64] + [_c_void_p] * 5
+                                 + [_i64, _i64, _c_void_p, _i64] + [_c_void_p] * 3
+                                 + [_f32, _u64, _f32, _c_void_p, _i64] + [_c_void_p] * 3
+                                 + [_c_void_p, _size, _c_void_p, _size, _c_void_p],
+    "ss_dropout_mask": [_u64, _f32, _i64, _i64, _c_void_p, _c_void_p],
     "ss_qlora_rank_workspace_size": [_i64, _i64, _i64],
     "ss_lora_workspace_size": [_i64, _i64],
     "ss_lora_project": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _int, _int, _f32,

@@ -4,6 +4,7 @@
 
 #include "common.h"
 #include "swiglu.h"
+#include "philox.h"
 
 namespace ss {
 
@@ -44,6 +45,7 @@ struct RankProjectArgs {
   half_t* out;
   float* part;
   int* counters;
+  DropoutArgs drop;  // A' = dropout(A) (rows x k, row-major element index) when drop.on
 };
 
 struct RankGradArgs {
@@ -57,6 +59,7 @@ struct RankGradArgs {
   half_t* out;
   float* part;
   int* counters;
+  DropoutArgs drop;  // Q' = dropout(Q) (t x n, row-major element index) when drop.on
 };
 
 struct GemmParams {

@@ -975,14 +975,17 @@ extern "C" size_t ss_qlora_rank_workspace_size(int64_t t, int64_t n, int64_t k) 
   return m > da ? m : da;
 }
 
-extern "C" int ss_qlora_forward(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
-                                const uint8_t* qabs, const float* absmax2, const float* code2,
-                                const float* offset, int64_t n, int64_t k, const uint16_t* bias,
-                                const uint16_t* lora_a, const uint16_t* lora_b, float scale,
-                                uint16_t* z, uint16_t* y, int64_t ldy, void* workspace,
-                                size_t workspace_bytes, void* rank_workspace,
-                                size_t rank_workspace_bytes, void* stream) {
-  const char* fn = "ss_qlora_forward";
+namespace ss {
+
+// Body of ss_qlora_forward[_dropout]: drop == nullptr for the dropout-free
+// projection, else Z = fp16(fp16(drop(X)) . A^T) with the call's mask.
+static int qlora_forward(const char* fn, const uint16_t* x, int64_t ldx, int64_t t,
+                         const uint8_t* packed, const uint8_t* qabs, const float* absmax2,
+                         const float* code2, const float* offset, int64_t n, int64_t k,
+                         const uint16_t* bias, const uint16_t* lora_a, const uint16_t* lora_b,
+                         float scale, uint16_t* z, uint16_t* y, int64_t ldy, void* workspace,
+                         size_t workspace_bytes, void* rank_workspace,
+                         size_t rank_workspace_bytes, const DropoutArgs* drop, void* stream) {
   SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
   int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
   if (rc) return rc;
@@ -1002,21 +1005,23 @@ extern "C" int ss_qlora_forward(const uint16_t* x, int64_t ldx, int64_t t, const
   // Z = fp16(X . A^T): the rank-16 job the LoRA epilogue reads.
   pj.proj_blocks = rank_project_setup(pj.proj, x, ldx, t, k, lora_a, k, 0, 1.0f, z,
                                       rank_workspace, rank_workspace_bytes, t, vp);
+  if (drop) pj.proj.drop = *drop;
   pj.grad_blocks = 0;
   pj.dec_kind = kDecodeNone;
   return run_fwd<EPI_LORA>(p, workspace, workspace_bytes, (hipStream_t)stream, &pj, vp, vg);
 }
 
-extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
-                                 const uint8_t* packed, const uint8_t* qabs,
-                                 const float* absmax2, const float* code2, const float* offset,
-                                 int64_t n, int64_t k, const uint16_t* x, int64_t ldx,
-                                 const uint16_t* z, const uint16_t* lora_a,
-                                 const uint16_t* lora_b, float scale, uint16_t* dx, int64_t lddx,
-                                 uint16_t* dz, uint16_t* da, uint16_t* db, void* workspace,
-                                 size_t workspace_bytes, void* rank_workspace,
-                                 size_t rank_workspace_bytes, void* stream) {
-  const char* fn = "ss_qlora_backward";
+// Body of ss_qlora_backward[_dropout].  With dropout the dX GEMM runs without
+// the rank-16 term, and one tail launch then computes dA from the masked X
+// and adds the masked fp16(dZ . A) to dX.
+static int qlora_backward(const char* fn, const uint16_t* dy, int64_t lddy, int64_t t,
+                          const uint8_t* packed, const uint8_t* qabs, const float* absmax2,
+                          const float* code2, const float* offset, int64_t n, int64_t k,
+                          const uint16_t* x, int64_t ldx, const uint16_t* z,
+                          const uint16_t* lora_a, const uint16_t* lora_b, float scale,
+                          uint16_t* dx, int64_t lddx, uint16_t* dz, uint16_t* da, uint16_t* db,
+                          void* workspace, size_t workspace_bytes, void* rank_workspace,
+                          size_t rank_workspace_bytes, const DropoutArgs* drop, void* stream) {
   SS_CHECK_ARG(t >= 0, "%s: t=%lld must be >= 0", fn, (long long)t);
   int rc = check_nf4(fn, packed, qabs, absmax2, code2, offset, n, k);
   if (rc) return rc;
@@ -1030,6 +1035,16 @@ extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
   SS_CHECK_ARG(dy && dx && dz && x && z, "%s: null pointer", fn);
   SS_CHECK_ARG(lddy >= n && lddx >= k && ldx >= k, "%s: leading dimensions too small", fn);
   SS_CHECK_ARG(reinterpret_cast<uintptr_t>(dz) % 16 == 0, "%s: dZ must be 16-byte aligned", fn);
+  if (drop) {
+    auto al = [](const void* q, int64_t ld) {
+      return reinterpret_cast<uintptr_t>(q) % 16 == 0 && ld % 8 == 0;
+    };
+    if (!(al(x, ldx) && al(dx, lddx) && al(lora_a, k) && k % 8 == 0)) {
+      ss::set_error("%s: the dropout path needs 16-byte aligned X, dX and lora_A rows and "
+                    "K %% 8 == 0", fn);
+      return SS_ERR_UNSUPPORTED;
+    }
+  }
   hipStream_t s = (hipStream_t)stream;
   PrepJobs pj{};
   bool vp = false, vg = false;
@@ -1040,6 +1055,17 @@ extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
   pj.grad_blocks = rank_grad_setup(pj.grad, z, 16, dy, lddy, t, n, scale, 1, db, rank_workspace,
                                    rank_workspace_bytes, t, vg);
   pj.dec_kind = kDecodeNone;
+  if (drop) {
+    GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx,
+                             0);
+    rc = run_dx<EPI_PLAIN>(p, n, k, workspace, workspace_bytes, s, &pj, vp, vg);
+    if (rc) return rc;
+    return launch_dropout_tail(reinterpret_cast<const half_t*>(dz),
+                               reinterpret_cast<const half_t*>(x), ldx,
+                               reinterpret_cast<const half_t*>(lora_a), t, k,
+                               reinterpret_cast<half_t*>(dx), lddx, reinterpret_cast<half_t*>(da),
+                               *drop, rank_workspace, rank_workspace_bytes, s);
+  }
   GemmParams p = dx_params(dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, dx, lddx, 0);
   p.lz = reinterpret_cast<const half_t*>(dz);
   p.lb = reinterpret_cast<const half_t*>(lora_a);
@@ -1059,6 +1085,79 @@ extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
   if (rc || da_ran) return rc;
   return ss_lora_grad(dz, 16, x, ldx, t, k, 0, 1.0f, 0, da, rank_workspace, rank_workspace_bytes,
                       stream);
+}
+
+static int check_dropout(const char* fn, float p) {
+  SS_CHECK_ARG(p > 0.0f && p < 1.0f, "%s: dropout p=%g must be in (0, 1)", fn, (double)p);
+  return SS_OK;
+}
+
+}  // namespace ss
+
+extern "C" int ss_qlora_forward(const uint16_t* x, int64_t ldx, int64_t t, const uint8_t* packed,
+                                const uint8_t* qabs, const float* absmax2, const float* code2,
+                                const float* offset, int64_t n, int64_t k, const uint16_t* bias,
+                                const uint16_t* lora_a, const uint16_t* lora_b, float scale,
+                                uint16_t* z, uint16_t* y, int64_t ldy, void* workspace,
+                                size_t workspace_bytes, void* rank_workspace,
+                                size_t rank_workspace_bytes, void* stream) {
+  return qlora_forward("ss_qlora_forward", x, ldx, t, packed, qabs, absmax2, code2, offset, n, k,
+                       bias, lora_a, lora_b, scale, z, y, ldy, workspace, workspace_bytes,
+                       rank_workspace, rank_workspace_bytes, nullptr, stream);
+}
+
+extern "C" int ss_qlora_forward_dropout(const uint16_t* x, int64_t ldx, int64_t t,
+                                        const uint8_t* packed, const uint8_t* qabs,
+                                        const float* absmax2, const float* code2,
+                                        const float* offset, int64_t n, int64_t k,
+                                        const uint16_t* bias, const uint16_t* lora_a,
+                                        const uint16_t* lora_b, float scale, uint64_t seed,
+                                        float p, uint16_t* z, uint16_t* y, int64_t ldy,
+                                        void* workspace, size_t workspace_bytes,
+                                        void* rank_workspace, size_t rank_workspace_bytes,
+                                        void* stream) {
+  const char* fn = "ss_qlora_forward_dropout";
+  const int rc = check_dropout(fn, p);
+  if (rc) return rc;
+  SS_CHECK_ARG(k % 8 == 0, "%s: K=%lld must be a multiple of 8", fn, (long long)k);
+  const DropoutArgs drop = dropout_args(seed, p);
+  return qlora_forward(fn, x, ldx, t, packed, qabs, absmax2, code2, offset, n, k, bias, lora_a,
+                       lora_b, scale, z, y, ldy, workspace, workspace_bytes, rank_workspace,
+                       rank_workspace_bytes, &drop, stream);
+}
+
+extern "C" int ss_qlora_backward(const uint16_t* dy, int64_t lddy, int64_t t,
+                                 const uint8_t* packed, const uint8_t* qabs,
+                                 const float* absmax2, const float* code2, const float* offset,
+                                 int64_t n, int64_t k, const uint16_t* x, int64_t ldx,
+                                 const uint16_t* z, const uint16_t* lora_a,
+                                 const uint16_t* lora_b, float scale, uint16_t* dx, int64_t lddx,
+                                 uint16_t* dz, uint16_t* da, uint16_t* db, void* workspace,
+                                 size_t workspace_bytes, void* rank_workspace,
+                                 size_t rank_workspace_bytes, void* stream) {
+  return qlora_backward("ss_qlora_backward", dy, lddy, t, packed, qabs, absmax2, code2, offset, n,
+                        k, x, ldx, z, lora_a, lora_b, scale, dx, lddx, dz, da, db, workspace,
+                        workspace_bytes, rank_workspace, rank_workspace_bytes, nullptr, stream);
+}
+
+extern "C" int ss_qlora_backward_dropout(const uint16_t* dy, int64_t lddy, int64_t t,
+                                         const uint8_t* packed, const uint8_t* qabs,
+                                         const float* absmax2, const float* code2,
+                                         const float* offset, int64_t n, int64_t k,
+                                         const uint16_t* x, int64_t ldx, const uint16_t* z,
+                                         const uint16_t* lora_a, const uint16_t* lora_b,
+                                         float scale, uint64_t seed, float p, uint16_t* dx,
+                                         int64_t lddx, uint16_t* dz, uint16_t* da, uint16_t* db,
+                                         void* workspace, size_t workspace_bytes,
+                                         void* rank_workspace, size_t rank_workspace_bytes,
+                                         void* stream) {
+  const char* fn = "ss_qlora_backward_dropout";
+  const int rc = check_dropout(fn, p);
+  if (rc) return rc;
+  const DropoutArgs drop = dropout_args(seed, p);
+  return qlora_backward(fn, dy, lddy, t, packed, qabs, absmax2, code2, offset, n, k, x, ldx, z,
+                        lora_a, lora_b, scale, dx, lddx, dz, da, db, workspace, workspace_bytes,
+                        rank_workspace, rank_workspace_bytes, &drop, stream);
 }
 
 static int gemm_f16_impl(const char* fn, int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,

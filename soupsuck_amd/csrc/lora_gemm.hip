@@ -60,13 +60,13 @@ static bool wide_t(const Nf4View& w, int64_t cols) {
 // code dword in flight per lane they ran at half the stand-alone decoder's
 // rate (gate 8960 x 1536: prep 19.8 us against 10.9 us for the decode
 // alone); with eight, the launch costs about what its longer job costs.
-template <bool VP, bool VG>
-__global__ __launch_bounds__(256, VG ? 3 : 2) void qlora_prep_kernel(PrepJobs pj) {
+template <bool VP, bool VG, bool DROP>
+__global__ __launch_bounds__(256, VG && !DROP ? 3 : 2) void qlora_prep_kernel(PrepJobs pj) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[kPrepSmem];
   int64_t b = blockIdx.x;
   if (b < pj.proj_blocks) {
     const int64_t mblocks = cdiv(pj.proj.m, 16);
-    rank_project_block<VP>(pj.proj, b % mblocks, b / mblocks, smem);
+    rank_project_block<VP, DROP>(pj.proj, b % mblocks, b / mblocks, smem);
     return;
   }
   b -= pj.proj_blocks;
@@ -111,6 +111,7 @@ int64_t rank_project_setup(RankProjectArgs& g, const void* a, int64_t lda, int64
   g.out = reinterpret_cast<half_t*>(out);
   g.counters = reinterpret_cast<int*>(ws);
   g.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  g.drop = DropoutArgs{0, 0, 1.0f, 0};
   // Vector loads need 16-byte aligned rows of both operands and K % 8 == 0.
   vec = al16(a, lda) && al16(w, ldw) && k % 8 == 0;
   return mblocks * plan.splits;
@@ -132,6 +133,7 @@ int64_t rank_grad_setup(RankGradArgs& g, const void* p, int64_t ldp, const void*
   g.transpose = transpose;
   g.out = reinterpret_cast<half_t*>(out);
   g.counters = reinterpret_cast<int*>(ws) + kCounters / 2;
+  g.drop = DropoutArgs{0, 0, 1.0f, 0};
   g.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes + proj_part);
   // Vector loads need 16-byte aligned rows of P and Q and N % 8 == 0.
   vec = al16(q, ldq) && al16(p, ldp) && n % 8 == 0;
@@ -155,8 +157,16 @@ int launch_prep(PrepJobs& pj, bool vp, bool vg, hipStream_t stream) {
   // Without grad blocks the grad variant is irrelevant; the vector one has
   // the smaller register footprint.
   if (pj.grad_blocks == 0) vg = true;
-  auto kern = vp ? (vg ? qlora_prep_kernel<true, true> : qlora_prep_kernel<true, false>)
-                 : (vg ? qlora_prep_kernel<false, true> : qlora_prep_kernel<false, false>);
+  // The forward's Z of the dropout path masks X (the only job that does).
+  if (pj.proj.drop.on) {
+    auto kern = vp ? qlora_prep_kernel<true, true, true> : qlora_prep_kernel<false, true, true>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, pj);
+    SS_CHECK_LAUNCH("qlora_prep_kernel");
+    return SS_OK;
+  }
+  auto kern = vp ? (vg ? qlora_prep_kernel<true, true, false> : qlora_prep_kernel<true, false, false>)
+                 : (vg ? qlora_prep_kernel<false, true, false>
+                       : qlora_prep_kernel<false, false, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, pj);
   SS_CHECK_LAUNCH("qlora_prep_kernel");
   return SS_OK;

@@ -10,7 +10,9 @@
 // rank_grad_block: C[16, N] = P[T, 16]^T . Q'[T, N], Q' = Q or fp16(Q * q_scale),
 //   stored [16][N] or [N][16]; one (64-column block, T split).
 // Both run on blocks of 64 * waves threads (waves past 4 only join the
-// barriers) with `smem` of at least kRankProjSmem / kRankGradSmem bytes.  A split's waves stream one chunk each
+// barriers) with `smem` of at least kRankProjSmem / kRankGradSmem bytes.
+// DROP: A' (project) / Q' (grad) additionally pass through the LoRA dropout
+// mask of g.drop (philox.h), for Z and dA of the dropout path.  A split's waves stream one chunk each
 // (one memory round trip), add their sums through LDS, and the splits of an
 // output block are added by the last workgroup to arrive (finish_splits).
 #pragma once
@@ -62,12 +64,13 @@ __device__ __forceinline__ int qtile_index(int n, int t) {
 
 // One 256-k chunk [kbeg, kend) of a 16-row block: acc += A'[rows, chunk] . W(chunk, :),
 // with W(k, r) staged in the wave's LDS tile as tile[r][k - kbeg].
-template <bool VEC>
+template <bool VEC, bool DROP>
 __device__ __forceinline__ void project_chunk(const half_t* __restrict__ a, int64_t lda,
                                               int64_t m, const half_t* __restrict__ w,
                                               int64_t ldw, int w_kr, float a_scale, int64_t row,
                                               int lane, int64_t kbeg, int64_t kend, half_t* tile,
-                                              float4v (&acc)[2]) {
+                                              float4v (&acc)[2], const DropoutArgs& drop,
+                                              int64_t cols) {
   const int r = lane & 15;
   const int kq = (lane >> 4) * 8;
   half8 av[8];
@@ -98,10 +101,24 @@ __device__ __forceinline__ void project_chunk(const half_t* __restrict__ a, int6
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_s_waitcnt(0);
   // fp16(a * 1.0) == a for every fp16 value, so "no scaling" is a_scale = 1.
+  if constexpr (DROP) {
+    // Dropout of A (the LoRA input X): the keep bits of the lane's 8
+    // consecutive elements (row, k .. k + 7); rows past m and columns past
+    // kend hold zeros and are never stored, so their bits do not matter.
 #pragma unroll
-  for (int st = 0; st < 8; ++st)
+    for (int st = 0; st < 8; ++st) {
+      const int64_t k = kbeg + st * 32 + kq;
+      const uint32_t bits = row < m && k < kend ? keep8(drop, row * cols + k) : 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) av[st][i] = f32_to_f16((float)av[st][i] * a_scale);
+      for (int i = 0; i < 8; ++i)
+        av[st][i] = f32_to_f16(dropped(drop, (float)av[st][i] * a_scale, (bits >> i) & 1u));
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) av[st][i] = f32_to_f16((float)av[st][i] * a_scale);
+  }
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
     const half8 bv = *reinterpret_cast<const half8*>(tile + r * kProjLd + st * 32 + kq);
@@ -163,12 +180,12 @@ __device__ __forceinline__ bool finish_splits(float (&vals)[VALS], float* __rest
 
 // One 64-t chunk [t0, tend) of a 64-column block at n0: acc[c] += P[chunk, :]^T .
 // Q'[chunk, n0 + 16c .. +15], Q transposed through the wave's LDS tile.
-template <bool VEC>
+template <bool VEC, bool DROP>
 __device__ __forceinline__ void grad_chunk(const half_t* __restrict__ p, int64_t ldp,
                                            const half_t* __restrict__ q, int64_t ldq, int64_t n,
                                            float q_scale, int64_t n0, int lane, int64_t t0,
                                            int64_t tend, half_t* tile, half_t* ptile,
-                                           float4v (&acc)[4]) {
+                                           float4v (&acc)[4], const DropoutArgs& drop) {
   const int r = lane & 15;
   const int kq = (lane >> 4) * 8;
   // Q tile [64 t x 64 n]: 8 rows of 8 lanes per pass, 16 bytes per lane.
@@ -183,10 +200,16 @@ __device__ __forceinline__ void grad_chunk(const half_t* __restrict__ p, int64_t
   for (int it = 0; it < 8; ++it) {
     const int tl = it * 8 + (lane >> 3);
     const int nl = (lane & 7) * 8;
+    // Dropout of Q (the LoRA input X for dA): keep bits of the lane's 8
+    // consecutive elements; out-of-range ones are zeros that no sum uses.
+    const int64_t t = t0 + tl;
+    uint32_t bits = 0xffu;
+    if constexpr (DROP) bits = t < tend && n0 + nl < n ? keep8(drop, t * n + n0 + nl) : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       // fp16(q * 1.0) == q for every fp16 value, so "no scaling" is q_scale = 1.
-      tile[qtile_index(nl + i, tl)] = f32_to_f16((float)v[it][i] * q_scale);
+      const float qv = (float)v[it][i] * q_scale;
+      tile[qtile_index(nl + i, tl)] = f32_to_f16(DROP ? dropped(drop, qv, (bits >> i) & 1u) : qv);
     }
   }
 #pragma unroll
@@ -215,7 +238,7 @@ constexpr int kRankGradSmem = kRankMaxWaves * (64 * 64 + kRank * kGradLd) * 2;
 
 // Split s of 16-row block mb: the 256-k chunks [s * cps, (s + 1) * cps);
 // wave w takes chunks w, w + waves, ... of it.  out row stride 16.
-template <bool VEC>
+template <bool VEC, bool DROP = false>
 __device__ __forceinline__ void rank_project_block(const RankProjectArgs& g, int64_t mb,
                                                    int64_t s, unsigned char* smem) {
   half_t (*sw)[kRank * kProjLd] = reinterpret_cast<half_t (*)[kRank * kProjLd]>(smem);
@@ -232,8 +255,8 @@ __device__ __forceinline__ void rank_project_block(const RankProjectArgs& g, int
   for (int64_t kbeg = kb + (int64_t)wave * kProjChunk; wave < waves && kbeg < ke;
        kbeg += (int64_t)waves * kProjChunk) {
     const int64_t kend = kbeg + kProjChunk < ke ? kbeg + kProjChunk : ke;
-    project_chunk<VEC>(g.a, g.lda, g.m, g.w, g.ldw, g.w_kr, g.a_scale, row, lane, kbeg, kend,
-                       sw[wave], acc);
+    project_chunk<VEC, DROP>(g.a, g.lda, g.m, g.w, g.ldw, g.w_kr, g.a_scale, row, lane, kbeg,
+                             kend, sw[wave], acc, g.drop, g.k);
   }
   // The per-wave tiles are dead once every wave has passed this barrier;
   // their first 4 KiB hold the waves' 16x16 sums.
@@ -255,7 +278,7 @@ __device__ __forceinline__ void rank_project_block(const RankProjectArgs& g, int
 
 // Split s of 64-column block nb: the 64-t chunks [s * cps, (s + 1) * cps);
 // wave w takes chunks w, w + waves, ... of it.
-template <bool VEC>
+template <bool VEC, bool DROP = false>
 __device__ __forceinline__ void rank_grad_block(const RankGradArgs& g, int64_t nb, int64_t s,
                                                 unsigned char* smem) {
   half_t (*sq)[64 * 64] = reinterpret_cast<half_t (*)[64 * 64]>(smem);
@@ -275,8 +298,8 @@ __device__ __forceinline__ void rank_grad_block(const RankGradArgs& g, int64_t n
   for (int64_t t0 = tb + (int64_t)wave * kGradChunk; wave < waves && t0 < te;
        t0 += (int64_t)waves * kGradChunk) {
     const int64_t tend = t0 + kGradChunk < te ? t0 + kGradChunk : te;
-    grad_chunk<VEC>(g.p, g.ldp, g.q, g.ldq, g.n, g.q_scale, n0, lane, t0, tend, sq[wave],
-                    sp[wave], acc);
+    grad_chunk<VEC, DROP>(g.p, g.ldp, g.q, g.ldq, g.n, g.q_scale, n0, lane, t0, tend,
+                          sq[wave], sp[wave], acc, g.drop);
   }
   // The Q tiles are dead once every wave has passed this barrier; their first
   // 16 KiB hold the waves' 16x64 sums.
@@ -376,5 +399,20 @@ int64_t rank_project_setup(RankProjectArgs& g, const void* a, int64_t lda, int64
 int64_t rank_grad_setup(RankGradArgs& g, const void* p, int64_t ldp, const void* q, int64_t ldq,
                         int64_t t, int64_t n, float q_scale, int transpose, void* out, void* ws,
                         size_t ws_bytes, int64_t rows, bool& vec);
+
+}  // namespace ss
+
+namespace ss {
+
+// LoRA dropout (dropout.hip): the kernels' view of (seed, p), and the
+// backward's tail launch -- dA = fp16(dZ^T . fp16(drop(X))) and the masked
+// rank-16 term added to dX (which the dX GEMM computed without it).  The tail
+// needs 16-byte aligned dZ, X, A and dX rows and k % 8 == 0
+// (SS_ERR_UNSUPPORTED otherwise, before any launch).
+DropoutArgs dropout_args(uint64_t seed, float p);
+int launch_dropout_tail(const half_t* dz, const half_t* x, int64_t ldx, const half_t* lora_a,
+                        int64_t t, int64_t k, half_t* dx, int64_t lddx, half_t* da,
+                        const DropoutArgs& drop, void* rank_ws, size_t rank_ws_bytes,
+                        hipStream_t stream);
 
 }  // namespace ss

@@ -10,16 +10,22 @@ Backward (reference solution/lora_pair.py:34-65 order, fp16 after each GEMM):
     dL = fp16(fp16(g) * s)                              ss_lora_epilogue_bwd
     dZ = fp16(dL . B),  dB = fp16(dL^T . Z),  dA = fp16(dZ^T . drop(X))
     dX = fp16(g . Wdec + mask * (dZ . A))               ss_nf4_gemm_dx, ss_gemm_f16
-The frozen base contributes no weight gradient.  Dropout (p > 0) uses torch's
-native dropout on an fp32 copy of X, as the reference keeps PEFT's own
-Dropout module and RNG (solution/lora.py:1-40); p = 0 skips it.
+The frozen base contributes no weight gradient.
 
-Fast path (rank 16, no active dropout, K % 64 == 0): two entry points per
-projection -- forward ss_qlora_forward (Z, then the NF4 GEMM with the LoRA
-add in its epilogue; Z runs in one launch with the NF4 decode); backward
-ss_qlora_backward (dZ from fp16(g*s) and dB in one launch with the
-transposed decode, the dX GEMM g.W + dZ.A in one accumulator, then dA).
-Otherwise each GEMM and the epilogue run as separate kernels.
+Fast path (rank 16, K % 64 == 0): two entry points per projection -- forward
+ss_qlora_forward (Z, then the NF4 GEMM with the LoRA add in its epilogue; Z
+runs in one launch with the NF4 decode); backward ss_qlora_backward (dZ from
+fp16(g*s) and dB in one launch with the transposed decode, the dX GEMM
+g.W + dZ.A in one accumulator, then dA).  With active dropout (p > 0,
+training) the same steps run as ss_qlora_forward_dropout /
+ss_qlora_backward_dropout: the keep mask of X is a counter-based (Philox)
+function of a per-call seed drawn from torch's CPU generator, recomputed by
+every kernel that reads X and never stored.  Its bits therefore differ from
+those PEFT's own Dropout would draw from torch's CUDA RNG (same keep
+probability and scaling, fp32(x) * fp32(1 / (1 - p)), as the reference's fp32
+dropout; solution/lora.py:1-40).
+Otherwise each GEMM and the epilogue run as separate kernels (torch's native
+dropout on an fp32 copy of X for p > 0).
 """
 
 import math
@@ -145,6 +151,65 @@ class _QLoRAFused(torch.autograd.Function):
                 None, None, None, None)
 
 
+def dropout_seed():
+    """A 64-bit seed for one dropout call, drawn from torch's default CPU generator (so
+    torch.manual_seed makes the masks reproducible)."""
+    return int(torch.empty((), dtype=torch.int64).random_().item())
+
+
+class _QLoRAFusedDropout(torch.autograd.Function):
+    """Rank-16 projection with LoRA dropout p > 0 on the fused entry points
+    (ss_qlora_forward_dropout / ss_qlora_backward_dropout): the keep mask is a
+    Philox function of (seed, element of X), drawn again wherever it is used,
+    so only the 8-byte seed is saved for the backward."""
+
+    @staticmethod
+    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling, dropout_p, seed):
+        n, k = state.shape
+        t = x.numel() // k
+        x2d = x.reshape(t, k)
+        a16 = lora_a.to(torch.float16).contiguous()
+        b16 = lora_b.to(torch.float16).contiguous()
+        z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
+        y = torch.empty((t, n), device=x.device, dtype=torch.float16)
+        ws, size = _gemm_ws(t, n, k, x.device)
+        rws = _qlora_rank_ws(t, n, k, x.device)
+        _lib.call("ss_qlora_forward_dropout", x2d.data_ptr(), x2d.stride(0), t,
+                  *_nf4_args(packed, state), n, k, _lib.ptr(bias), a16.data_ptr(),
+                  b16.data_ptr(), float(scaling), seed, float(dropout_p), z.data_ptr(),
+                  y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
+                  _lib.stream(x.device))
+        ctx.save_for_backward(x2d, z, a16, b16, packed)
+        ctx.state, ctx.scaling, ctx.dropout = state, float(scaling), (seed, float(dropout_p))
+        ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
+        return y.reshape(*x.shape[:-1], n)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad):
+        x2d, z, a16, b16, packed = ctx.saved_tensors
+        state = ctx.state
+        n, k = state.shape
+        t = x2d.shape[0]
+        seed, p = ctx.dropout
+        g = grad.reshape(t, n).to(torch.float16).contiguous()
+        dev = g.device
+        dz = torch.empty((t, 16), device=dev, dtype=torch.float16)
+        db = torch.empty((n, 16), device=dev, dtype=torch.float16)
+        da = torch.empty((16, k), device=dev, dtype=torch.float16)
+        dx = torch.empty((t, k), device=dev, dtype=torch.float16)
+        ws, size = _gemm_ws(t, n, k, dev)
+        rws = _qlora_rank_ws(t, n, k, dev)
+        _lib.call("ss_qlora_backward_dropout", g.data_ptr(), g.stride(0), t,
+                  *_nf4_args(packed, state), n, k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(),
+                  a16.data_ptr(), b16.data_ptr(), ctx.scaling, seed, p, dx.data_ptr(),
+                  dx.stride(0), dz.data_ptr(), da.data_ptr(), db.data_ptr(), _lib.ptr(ws), size,
+                  rws.data_ptr(), rws.numel(), _lib.stream(dev))
+        x_dtype, a_dtype, b_dtype = ctx.dtypes
+        return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
+                None, None, None, None, None, None)
+
+
 class _QLoRAProjection(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling, dropout_p, training):
@@ -218,10 +283,13 @@ def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, d
         raise ValueError("scaling must be finite")
     if not 0.0 <= dropout_p < 1.0:
         raise ValueError("dropout_p must be in [0, 1)")
-    fused = (lora_a.shape[0] == 16 and (dropout_p == 0.0 or not training) and k % 64 == 0
-             and packed.data_ptr() % 16 == 0)
+    fused = lora_a.shape[0] == 16 and k % 64 == 0 and packed.data_ptr() % 16 == 0
+    active = dropout_p > 0.0 and training
     with torch.cuda.device(x.device):
-        if fused:
+        if fused and not active:
             return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling))
+        if fused and x.data_ptr() % 16 == 0:
+            return _QLoRAFusedDropout.apply(x, lora_a, lora_b, packed, state, bias,
+                                            float(scaling), float(dropout_p), dropout_seed())
         return _QLoRAProjection.apply(x, lora_a, lora_b, packed, state, bias, float(scaling),
                                       float(dropout_p), bool(training))

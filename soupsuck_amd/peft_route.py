@@ -20,8 +20,10 @@ Eligibility (everything else runs PEFT's original forward):
   * the base layer a frozen nested-NF4 ``Linear4bit`` (fp16 or unset compute
     dtype) with a frozen bias or none, and no hooks or per-instance forward
     on any of the modules involved.
-Dropout with p > 0 in training runs torch's dropout on an fp32 copy of x (the
-reference's choice, solution/lora.py:1-40) and the unfused kernels.
+Dropout with p > 0 in training runs fused too (soupsuck_amd.lora: a Philox
+mask recomputed by the kernels from a per-call seed; the keep probability and
+the fp32 scaling are the reference's, solution/lora.py:1-40, the bits are not
+those of torch's CUDA RNG).
 """
 
 import math
