@@ -85,12 +85,15 @@ struct GemmParams {
   int64_t k_split;  // k elements per split (a multiple of 64)
   int fold_rank;    // EPI_PARTIAL: split 0 adds the rank-16 term lz . lb (EPI_RANK layout)
   int pingpong;     // 8-wave NT configurations: ping-pong main loop (set by gemm_nt)
-  // Optional rank-16 grad riding on the dense NT launch: tail_blocks extra
-  // workgroups (unsplit launches, after the GEMM tiles) each run one block
-  // of `tail` (rank_grad_block, vector loads).  tail_ran (host side) is set
-  // when a launch took the tail.
+  // Optional rank-16 grads riding on the dense NT launch (unsplit) or on its
+  // split-K reduce: tail_blocks + tail2_blocks extra workgroups each run one
+  // block of `tail`, then of `tail2` (rank_grad_block, vector loads).  The
+  // two write disjoint counter and exchange areas.  tail_ran (host side) is
+  // set when a launch took the tails.
   RankGradArgs tail;
   int64_t tail_blocks;
+  RankGradArgs tail2;
+  int64_t tail2_blocks;
   int* tail_ran;
   // Gated (SwiGLU) store of an fp16, beta = 0 output (glu_apply): glu = 1
   // forward, the product is `up` -- act = silu(gate) up goes to glu_out and

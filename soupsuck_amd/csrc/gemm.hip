@@ -969,7 +969,8 @@ extern "C" int ss_qlora_dx(const uint16_t* dy, int64_t lddy, int64_t t, const ui
 
 extern "C" size_t ss_qlora_rank_workspace_size(int64_t t, int64_t n, int64_t k) {
   const size_t fwd = ss_lora_workspace_size(t, 0);
-  const size_t bwd = ss_lora_workspace_size(t, n);
+  // The backward's dB and dA exchange areas follow dZ's, one after the other.
+  const size_t bwd = ss_lora_workspace_size(t, n) + ss::rank_grad_part_bytes(k);
   const size_t da = ss_lora_workspace_size(0, k);
   size_t m = fwd > bwd ? fwd : bwd;
   return m > da ? m : da;
@@ -1071,18 +1072,39 @@ static int qlora_backward(const char* fn, const uint16_t* dy, int64_t lddy, int6
   p.lb = reinterpret_cast<const half_t*>(lora_a);
   p.ldlb = k;
   // dA = fp16(dZ^T . X) needs dZ from the preparation launch, as the dX GEMM
-  // does: its workgroups ride on the dense dX launch when that path runs
-  // (vector loads), else it is launched on its own afterwards.
-  bool vda = false;
+  // does; dB has no consumer in this call.  dA rides on the dense dX launch
+  // (or on its split-K reduce) when that path runs with vector loads, else it
+  // is launched on its own afterwards.  dB joins it on an unsplit dX launch,
+  // in disjoint exchange areas (dB after dZ's, dA after dB's) and counter
+  // ranges, where both fill CUs the GEMM leaves idle instead of lengthening
+  // the preparation launch (measured at T = 990: k / v backward 18.0 -> 14.8
+  // us, q / o 32 -> 30); next to a split-K reduce it gained nothing (the
+  // reduce grew by what the preparation launch lost), so there it stays in
+  // the preparation launch.
+  bool vda = false, vdb = false;
   int da_ran = 0;
+  RankGradArgs dbg;
+  const int64_t db_blocks = rank_grad_setup(dbg, z, 16, dy, lddy, t, n, scale, 1, db,
+                                            rank_workspace, rank_workspace_bytes, t, vdb);
   const int64_t da_blocks = rank_grad_setup(p.tail, dz, 16, x, ldx, t, k, 1.0f, 0, da,
-                                            rank_workspace, rank_workspace_bytes, 0, vda);
+                                            rank_workspace, rank_workspace_bytes, t, vda,
+                                            rank_grad_part_bytes(n), kCounters / 4);
   if (vda) {
     p.tail_blocks = da_blocks;
     p.tail_ran = &da_ran;
+    if (vdb && nt_plan(t, k, n).splits == 1) {
+      p.tail2 = dbg;
+      p.tail2_blocks = db_blocks;
+      pj.grad_blocks = 0;
+    }
   }
   rc = run_dx<EPI_RANK>(p, n, k, workspace, workspace_bytes, s, &pj, vp, vg);
   if (rc || da_ran) return rc;
+  if (p.tail2_blocks) {
+    rc = ss_lora_grad(z, 16, dy, lddy, t, n, 1, scale, 1, db, rank_workspace,
+                      rank_workspace_bytes, stream);
+    if (rc) return rc;
+  }
   return ss_lora_grad(dz, 16, x, ldx, t, k, 0, 1.0f, 0, da, rank_workspace, rank_workspace_bytes,
                       stream);
 }

@@ -287,12 +287,10 @@ constexpr int nt_smem_bytes() {
 template <class C, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[nt_smem_bytes<C, EPI>()];
-  const int64_t tiles = gridDim.x - p.tail_blocks;
+  const int64_t tiles = gridDim.x - p.tail_blocks - p.tail2_blocks;
   if constexpr (EPI == EPI_RANK) {
     if ((int64_t)blockIdx.x >= tiles) {
-      const int64_t b = blockIdx.x - tiles;
-      const int64_t nblocks = cdiv(p.tail.n, 64);
-      rank_grad_block<true>(p.tail, b % nblocks, b / nblocks, smem);
+      run_tail_block(p, blockIdx.x - tiles, smem);
       return;
     }
   }
@@ -325,20 +323,20 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
 // part[s][row][col]), four columns per thread.  The epilogues are those of the
 // GEMM kernel with the same rounding order; the rank-16 terms are summed in
 // fp32 in rank order.
-// TAIL: the first p.tail_blocks workgroups run the rank-16 grad p.tail
-// (rank_grad_block, vector loads) instead, overlapping the reduce: used for
-// split-K dX products, whose dA would otherwise need a launch of its own.
+// TAIL: the first p.tail_blocks + p.tail2_blocks workgroups run the rank-16
+// grads p.tail / p.tail2 (run_tail_block, vector loads) instead, overlapping
+// the reduce: used for split-K dX products, whose dA and dB would otherwise
+// need launches of their own.
 template <int CT, int EPI, bool TAIL = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits) {
   int64_t block = blockIdx.x;
   if constexpr (TAIL) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kRankGradSmem];
-    if (block < p.tail_blocks) {
-      const int64_t nblocks = cdiv(p.tail.n, 64);
-      rank_grad_block<true>(p.tail, block % nblocks, block / nblocks, smem);
+    if (block < p.tail_blocks + p.tail2_blocks) {
+      run_tail_block(p, block, smem);
       return;
     }
-    block -= p.tail_blocks;
+    block -= p.tail_blocks + p.tail2_blocks;
   }
   const int64_t groups = cdiv(p.N, 4);
   const int64_t g = block * 256 + threadIdx.x;
@@ -458,7 +456,8 @@ using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 Ki
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
-  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN) + p.tail_blocks),
+  const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN) + p.tail_blocks +
+                             p.tail2_blocks),
                   (unsigned)splits);
   hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
   SS_CHECK_LAUNCH("gemm_nt_kernel");
@@ -483,7 +482,7 @@ int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream
 template <int CT, int EPI, bool TAIL = false>
 int reduce_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
   const int64_t threads = p.M * cdiv(p.N, 4);
-  const int64_t blocks = cdiv(threads, 256) + (TAIL ? p.tail_blocks : 0);
+  const int64_t blocks = cdiv(threads, 256) + (TAIL ? p.tail_blocks + p.tail2_blocks : 0);
   hipLaunchKernelGGL((splitk_reduce_kernel<CT, EPI, TAIL>), dim3((unsigned)blocks), dim3(256), 0,
                      stream, p, (int)splits);
   SS_CHECK_LAUNCH("splitk_reduce_kernel");
@@ -585,26 +584,28 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
   // / v backward 6-11 us faster).  On the split-K launches of the long-K dX it
   // slowed the GEMM more than a launch of its own costs; there it leads the
   // reduce launch instead.
-  if (epi != EPI_RANK) p.tail_blocks = 0;
-  if (p.tail_blocks > 0 && p.tail_ran) *p.tail_ran = 1;
+  if (epi != EPI_RANK) p.tail_blocks = p.tail2_blocks = 0;
+  if (p.tail_blocks + p.tail2_blocks > 0 && p.tail_ran) *p.tail_ran = 1;
   if (plan.splits > 1) {
     p.part = reinterpret_cast<float*>(partials);
     p.k_split = plan.k_split;
     // The rank-16 update is folded into split 0's partial (the reduce then
     // only sums: its lora_A column loads dominated its load count).
     p.fold_rank = epi == EPI_RANK;
-    const int64_t tail = p.tail_blocks;
-    p.tail_blocks = 0;
+    const int64_t tail = p.tail_blocks, tail2 = p.tail2_blocks;
+    p.tail_blocks = p.tail2_blocks = 0;
     const int rc = dispatch_nt<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);
     if (rc) return rc;
     p.tail_blocks = tail;
+    p.tail2_blocks = tail2;
     if (ct == SS_F32) return reduce_nt<SS_F32, EPI_PLAIN>(p, plan.splits, stream);
     if (epi == EPI_LORA) return reduce_nt<SS_F16, EPI_LORA>(p, plan.splits, stream);
     if (epi == EPI_RANK) {
       GemmParams q = p;
       q.alpha = 1.0f;
       q.bias = nullptr;
-      if (q.tail_blocks > 0) return reduce_nt<SS_F16, EPI_PLAIN, true>(q, plan.splits, stream);
+      if (q.tail_blocks + q.tail2_blocks > 0)
+        return reduce_nt<SS_F16, EPI_PLAIN, true>(q, plan.splits, stream);
       return reduce_nt<SS_F16, EPI_PLAIN>(q, plan.splits, stream);
     }
     if (p.glu) return reduce_nt<SS_F16, EPI_GLU>(p, plan.splits, stream);

@@ -119,11 +119,12 @@ int64_t rank_project_setup(RankProjectArgs& g, const void* a, int64_t lda, int64
 
 int64_t rank_grad_setup(RankGradArgs& g, const void* p, int64_t ldp, const void* q, int64_t ldq,
                         int64_t t, int64_t n, float q_scale, int transpose, void* out, void* ws,
-                        size_t ws_bytes, int64_t rows, bool& vec) {
+                        size_t ws_bytes, int64_t rows, bool& vec, size_t part_offset,
+                        int64_t counter_offset) {
   const int64_t nblocks = cdiv(n, 64);
-  const size_t proj_part = rows > 0 ? rank_project_part_bytes(rows) : 0;
+  const size_t proj_part = (rows > 0 ? rank_project_part_bytes(rows) : 0) + part_offset;
   const bool can_split = ws && ws_bytes >= kCounterBytes + proj_part + rank_grad_part_bytes(n) &&
-                         nblocks <= kCounters / 2;
+                         counter_offset + nblocks <= kCounters / 2;
   const RankPlan plan = rank_plan(t, kGradChunk, can_split);
   g.p = reinterpret_cast<const half_t*>(p);
   g.ldp = ldp;
@@ -132,7 +133,7 @@ int64_t rank_grad_setup(RankGradArgs& g, const void* p, int64_t ldp, const void*
   g.cps = plan.cps; g.splits = plan.splits;
   g.transpose = transpose;
   g.out = reinterpret_cast<half_t*>(out);
-  g.counters = reinterpret_cast<int*>(ws) + kCounters / 2;
+  g.counters = reinterpret_cast<int*>(ws) + kCounters / 2 + counter_offset;
   g.drop = DropoutArgs{0, 0, 1.0f, 0};
   g.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes + proj_part);
   // Vector loads need 16-byte aligned rows of P and Q and N % 8 == 0.

@@ -334,6 +334,17 @@ __device__ __forceinline__ void rank_grad_block(const RankGradArgs& g, int64_t n
   }
 }
 
+// Tail block b (0 <= b < p.tail_blocks + p.tail2_blocks) of a GEMM launch:
+// a block of p.tail, then of p.tail2.
+__device__ __forceinline__ void run_tail_block(const GemmParams& p, int64_t b,
+                                               unsigned char* smem) {
+  const bool first = b < p.tail_blocks;
+  const RankGradArgs& g = first ? p.tail : p.tail2;
+  if (!first) b -= p.tail_blocks;
+  const int64_t nblocks = cdiv(g.n, 64);
+  rank_grad_block<true>(g, b % nblocks, b / nblocks, smem);
+}
+
 // Host plans and workspace layout of the rank-16 products.
 //
 // Rank workspace (zero-filled once by its owner): kCounterBytes of arrival
@@ -396,9 +407,13 @@ int launch_prep(PrepJobs& pj, bool vp, bool vg, hipStream_t stream);
 int64_t rank_project_setup(RankProjectArgs& g, const void* a, int64_t lda, int64_t m, int64_t k,
                            const void* w, int64_t ldw, int w_kr, float a_scale, void* out,
                            void* ws, size_t ws_bytes, int64_t rows, bool& vec);
+// part_offset / counter_offset: extra bytes before the grad's exchange area
+// and extra grad counters to skip, so that two grads of one launch (the
+// backward's dB and dA tails) use disjoint areas.
 int64_t rank_grad_setup(RankGradArgs& g, const void* p, int64_t ldp, const void* q, int64_t ldq,
                         int64_t t, int64_t n, float q_scale, int transpose, void* out, void* ws,
-                        size_t ws_bytes, int64_t rows, bool& vec);
+                        size_t ws_bytes, int64_t rows, bool& vec, size_t part_offset = 0,
+                        int64_t counter_offset = 0);
 
 }  // namespace ss
 
