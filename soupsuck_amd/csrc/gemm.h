@@ -23,8 +23,8 @@ struct Nf4View {
 // forward out = fp16(fp16(acc + bias) + fp16(fp16(Z . B^T) * s)) with Z
 // [M,16] and B = lora_B [N,16]; and a rank-16 update out = fp16(acc + dZ . A)
 // with dZ [M,16] and A = lora_A [16, N] (row stride ldlb).
-// EPI_PARTIAL (split-K, dense NT kernel only): the raw fp32 accumulator of
-// split blockIdx.y is stored to part[split][M][N]; a reduce kernel sums the
+// EPI_PARTIAL (split-K): the raw fp32 accumulator of a workgroup's split
+// (split_tile) is stored to part[split][M][N]; a reduce kernel sums the
 // splits in order and applies the requested epilogue.
 // EPI_GLU (dense NT, fused NF4, split-K reduce): the plain value passed
 // through glu_apply; entry points request it with EPI_PLAIN and p.glu set, the
@@ -125,6 +125,20 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t p, int64_t n) {
   const int64_t q = n / kXcd, r = n % kXcd;
   const int64_t x = p % kXcd, local = p / kXcd;
   return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + local;
+}
+
+// (tile, split) of a split-K workgroup of a (tiles, splits) grid.  The pairs
+// are numbered split-major and, with remap, every XCD owns a contiguous range
+// of them: the workgroups that share an L2 then read one K slice of A and B
+// instead of every XCD reading the same rows of every slice (a row-major
+// remap of blockIdx.x alone gives each XCD all M tiles of its N columns in
+// every split, so A is fetched once per XCD).
+__device__ __forceinline__ void split_tile(bool remap, int64_t tiles, int64_t& tile,
+                                           int64_t& split) {
+  const int64_t w = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const int64_t l = remap ? xcd_remap(w, tiles * gridDim.y) : w;
+  split = l / tiles;
+  tile = l - split * tiles;
 }
 
 // LDS DMA (gfx950 global_load_lds_*).  One wave-wide dwordx4 DMA: lane i's

@@ -292,12 +292,16 @@ template <class C, int CD, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4Layout<C>::kSmem];
   const int64_t tiles = gridDim.x;
-  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
+  int64_t tile, split = 0;
+  if constexpr (EPI == EPI_PARTIAL)
+    split_tile(p.remap, tiles, tile, split);
+  else
+    tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
   int64_t m0, n0;
   tile_origin<C>(p, tile, m0, n0);
   int64_t kbeg = 0, klen = p.K;
   if constexpr (EPI == EPI_PARTIAL) {
-    kbeg = (int64_t)blockIdx.y * p.k_split;
+    kbeg = split * p.k_split;
     klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
   }
   NtAcc<C> acc;
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmPara
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
   nf4_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
   static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= Nf4Layout<C>::kSmem, "stage");
-  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem, split);
 }
 
 // Configurations (same tiles, waves and stage depth as the dense kernel's

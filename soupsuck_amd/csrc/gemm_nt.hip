@@ -280,8 +280,8 @@ constexpr int nt_smem_bytes() {
 }
 
 // Data-parallel / split-K kernel: workgroup = one output tile (blockIdx.x,
-// XCD-remapped) and one k split (blockIdx.y; EPI_PARTIAL stores its fp32
-// accumulator to split plane blockIdx.y).  Workgroups past the tiles run the
+// XCD-remapped) or, split over K, one (tile, split) pair (split_tile;
+// EPI_PARTIAL stores its fp32 accumulator to split plane `split`).  Workgroups past the tiles run the
 // optional rank-16 grad tail (p.tail; rank-16 epilogue, unsplit launches)
 // after the GEMM tiles, filling CUs the GEMM leaves idle.
 template <class C, int CT, int EPI>
@@ -294,12 +294,16 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
       return;
     }
   }
-  const int64_t tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
+  int64_t tile, split = 0;
+  if constexpr (EPI == EPI_PARTIAL)
+    split_tile(p.remap, tiles, tile, split);
+  else
+    tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
   int64_t m0, n0;
   tile_origin<C>(p, tile, m0, n0);
   int64_t kbeg = 0, klen = p.K;
   if constexpr (EPI == EPI_PARTIAL) {
-    kbeg = (int64_t)blockIdx.y * p.k_split;
+    kbeg = split * p.k_split;
     klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
   }
   NtAcc<C> acc;
@@ -316,7 +320,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
     nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
   }
   static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= nt_smem_bytes<C, EPI>(), "stage");
-  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem);
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem, split);
 }
 
 // Split-K reduction: out[row][col] = epilogue(sum over splits s = 0.. of

@@ -366,7 +366,8 @@ __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t 
 // `smem`: the kernel's LDS, at least GluStage<C>::kBytes (staged epilogues).
 template <class C, int CT, int EPI>
 __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int64_t n0,
-                                            const NtAcc<C>& acc, unsigned char* smem = nullptr) {
+                                            const NtAcc<C>& acc, unsigned char* smem = nullptr,
+                                            int64_t split = 0) {
   if constexpr (EPI == EPI_GLU) {
     if constexpr (GluStage<C>::kOk) {
       if (p.glu_vec) {
@@ -399,7 +400,7 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
         // Split 0 of a rank-16 (dX) product adds dZ . A to its partial, so the
         // reduce is a plain sum (fold_rank; same MFMA as the unsplit epilogue).
         float16v extra = float16v{};
-        if (p.fold_rank && blockIdx.y == 0) {
+        if (p.fold_rank && split == 0) {
           const int64_t zr = row_base + lr;
           const half8 zero = half8{};
           const half8 za =
@@ -412,7 +413,7 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
           extra = __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, extra, 0, 0, 0);
         }
         if (col >= p.N) continue;
-        float* part = p.part + (int64_t)blockIdx.y * p.M * p.N;
+        float* part = p.part + split * p.M * p.N;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
