@@ -348,55 +348,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
   const int64_t row = g / groups;
   const int64_t c0 = (g % groups) * 4;
   const int64_t plane = p.M * p.N;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.N % 4 == 0) {
-    for (int s = 0; s < splits; ++s) {
-      const float4v t = *reinterpret_cast<const float4v*>(p.part + s * plane + row * p.N + c0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += t[e];
-    }
-  } else {
-    for (int s = 0; s < splits; ++s)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (c0 + e < p.N) v[e] += p.part[s * plane + row * p.N + c0 + e];
-  }
-  // Rank-16 operands with 16-byte (Z, lora_B rows) and 8-byte (four lora_A
-  // columns) loads where aligned; the products are summed in rank order as in
-  // the GEMM epilogue.
-  float z[16];
+  // Every load of the thread -- the epilogue's operands (Z row, lora_B rows or
+  // lora_A columns, bias, gate / up) and then up to eight partials -- is
+  // issued before the first add, so the thread waits for memory once.
+  // Rank-16 operands use 16-byte (Z, lora_B rows) and 8-byte (four lora_A
+  // columns) loads where aligned.
+  half8 z8[2];
   if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
     const half_t* zr = p.lz + row * 16;
     if (reinterpret_cast<uintptr_t>(p.lz) % 16 == 0) {
-      const half8 z0 = *reinterpret_cast<const half8*>(zr);
-      const half8 z1 = *reinterpret_cast<const half8*>(zr + 8);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        z[r] = (float)z0[r];
-        z[8 + r] = (float)z1[r];
-      }
+      z8[0] = *reinterpret_cast<const half8*>(zr);
+      z8[1] = *reinterpret_cast<const half8*>(zr + 8);
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) z[r] = (float)zr[r];
+      for (int r = 0; r < 16; ++r) z8[r / 8][r % 8] = zr[r];
     }
   }
-  float a4[16][4];  // EPI_RANK: lora_A[r][c0 .. c0 + 3]
+  half4 a4[16];  // EPI_RANK: lora_A[r][c0 .. c0 + 3]
   if constexpr (EPI == EPI_RANK) {
     if (c0 + 4 <= p.N && p.ldlb % 4 == 0 && reinterpret_cast<uintptr_t>(p.lb) % 8 == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const half4 v4 = *reinterpret_cast<const half4*>(p.lb + r * p.ldlb + c0);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a4[r][e] = (float)v4[e];
-      }
+      for (int r = 0; r < 16; ++r) a4[r] = *reinterpret_cast<const half4*>(p.lb + r * p.ldlb + c0);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          a4[r][e] = c0 + e < p.N ? (float)p.lb[r * p.ldlb + c0 + e] : 0.0f;
+        for (int e = 0; e < 4; ++e) a4[r][e] = c0 + e < p.N ? p.lb[r * p.ldlb + c0 + e] : (half_t)0;
     }
   }
+  half8 b8[4][2];  // EPI_LORA: lora_B rows of the four columns
+  if constexpr (EPI == EPI_LORA) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t col = c0 + e < p.N ? c0 + e : p.N - 1;
+      const half_t* br = p.lb + col * 16;
+      if (reinterpret_cast<uintptr_t>(p.lb) % 16 == 0) {
+        b8[e][0] = *reinterpret_cast<const half8*>(br);
+        b8[e][1] = *reinterpret_cast<const half8*>(br + 8);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) b8[e][r / 8][r % 8] = br[r];
+      }
+    }
+  }
+  float bias[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bias[e] = p.bias && c0 + e < p.N ? (float)p.bias[c0 + e] : 0.0f;
   half_t gg[4], uu[4];  // EPI_GLU: gate / up of the four columns, loaded before any store
   if constexpr (EPI == EPI_GLU) {
 #pragma unroll
@@ -406,44 +403,57 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
       uu[e] = in && p.glu == 2 ? p.glu_up[row * p.ldup + c0 + e] : (half_t)0;
     }
   }
+  // Sum of the splits in split order.
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p.N % 4 == 0) {
+    constexpr int kAhead = 8;
+    float4v t[kAhead];
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s)
+      if (s < splits) t[s] = *reinterpret_cast<const float4v*>(p.part + s * plane + row * p.N + c0);
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s)
+      if (s < splits)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += t[s][e];
+    for (int s = kAhead; s < splits; ++s) {
+      const float4v u = *reinterpret_cast<const float4v*>(p.part + s * plane + row * p.N + c0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += u[e];
+    }
+  } else {
+    for (int s = 0; s < splits; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < p.N) v[e] += p.part[s * plane + row * p.N + c0 + e];
+  }
+  float z[16];
+  if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) z[r] = (float)z8[r / 8][r % 8];
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t col = c0 + e;
     if (col >= p.N) break;
     const int64_t idx = row * p.ldc + col;
     if constexpr (EPI == EPI_LORA) {
-      float bl[16];
-      const half_t* br = p.lb + col * 16;
-      if (reinterpret_cast<uintptr_t>(p.lb) % 16 == 0) {
-        const half8 b0 = *reinterpret_cast<const half8*>(br);
-        const half8 b1 = *reinterpret_cast<const half8*>(br + 8);
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          bl[r] = (float)b0[r];
-          bl[8 + r] = (float)b1[r];
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) bl[r] = (float)br[r];
-      }
       float l = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) l += z[r] * bl[r];
-      const float b = p.bias ? (float)p.bias[col] : 0.0f;
-      const float y = (float)f32_to_f16(v[e] * p.alpha + b);
+      for (int r = 0; r < 16; ++r) l += z[r] * (float)b8[e][r / 8][r % 8];
+      const float y = (float)f32_to_f16(v[e] * p.alpha + bias[e]);
       const float scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
       reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
     } else if constexpr (EPI == EPI_RANK) {
       float l = 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) l += z[r] * a4[r][e];
+      for (int r = 0; r < 16; ++r) l += z[r] * (float)a4[r][e];
       store_c<CT>(p.C, idx, v[e] + l, p.beta);
     } else {
-      const float b = p.bias ? (float)p.bias[col] : 0.0f;
       if constexpr (EPI == EPI_GLU)
-        glu_apply(p, row, col, idx, v[e] * p.alpha + b, gg[e], uu[e]);
+        glu_apply(p, row, col, idx, v[e] * p.alpha + bias[e], gg[e], uu[e]);
       else
-        store_c<CT>(p.C, idx, v[e] * p.alpha + b, p.beta);
+        store_c<CT>(p.C, idx, v[e] * p.alpha + bias[e], p.beta);
     }
   }
 }

@@ -273,25 +273,52 @@ __device__ __forceinline__ void nt_glu_epilogue_lds(const GemmParams& p, int64_t
 
 // Epilogue of one output tile.  Lane holds D[8 (r / 4) + 4 (lane / 32) + r %
 // 4][lane % 32] of each 32x32 block in register r.
-// Rank-16 term of one 32x32 block on one v_mfma_f32_32x32x16_f16 (EPI_LORA /
-// EPI_RANK): A = Z rows (row lane % 32, ranks 8 (lane / 32) .. + 7), B =
-// (rank, column).
-template <int EPI>
-__device__ __forceinline__ float16v rank16_block(const GemmParams& p, int64_t row_base,
-                                                 int64_t col, int lr, int lh) {
-  const int64_t zr = row_base + lr;
-  const half8 zero = half8{};
-  const half8 za = zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
-  half8 zb = zero;
-  if (col < p.N) {
-    if constexpr (EPI == EPI_LORA) {
-      zb = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
-    } else {
+// Rank-16 term of a 32x32 block on one v_mfma_f32_32x32x16_f16 (EPI_LORA,
+// EPI_RANK, or folded into a split-K partial): A = Z rows (row lane % 32,
+// ranks 8 (lane / 32) .. + 7), B = (rank, column) -- a lora_B row ([N, 16],
+// one 16-byte load; VEC_B) or a lora_A column ([16, ldlb], eight 2-byte
+// loads).  A wave loads the operands of all its FM x FN blocks (and their
+// bias) before it finishes any block, so it waits for them once instead of
+// once per block.
+template <class C, bool VEC_B>
+struct RankOps {
+  half8 za[C::FM];
+  half8 zb[C::FN];
+  __device__ __forceinline__ void load(const GemmParams& p, int64_t m0, int64_t n0, int wm, int wn,
+                                       int lr, int lh) {
+    const half8 zero = half8{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
+    for (int i = 0; i < C::FM; ++i) {
+      const int64_t zr = m0 + wm * C::WM + i * 32 + lr;
+      za[i] = zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
+    }
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int64_t col = n0 + wn * C::WN + j * 32 + lr;
+      zb[j] = zero;
+      if (col < p.N) {
+        if constexpr (VEC_B) {
+          zb[j] = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) zb[j][e] = p.lb[(8 * lh + e) * p.ldlb + col];
+        }
+      }
     }
   }
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, float16v{}, 0, 0, 0);
+  __device__ __forceinline__ float16v block(int i, int j) const {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(za[i], zb[j], float16v{}, 0, 0, 0);
+  }
+};
+
+template <class C>
+__device__ __forceinline__ void load_bias(const GemmParams& p, int64_t n0, int wn, int lr,
+                                          float (&bias)[C::FN]) {
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    const int64_t col = n0 + wn * C::WN + j * 32 + lr;
+    bias[j] = p.bias && col < p.N ? (float)p.bias[col] : 0.0f;
+  }
 }
 
 // fp16 epilogue (plain / LoRA / rank-16, beta = 0) with the tile staged
@@ -312,6 +339,11 @@ __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t 
   const int wn = wave % C::kWavesN;
   const int lr = lane & 31;
   const int lh = lane >> 5;
+  constexpr bool kRank = EPI == EPI_LORA || EPI == EPI_RANK;
+  RankOps<C, EPI == EPI_LORA> ops;
+  if constexpr (kRank) ops.load(p, m0, n0, wm, wn, lr, lh);
+  float bias[C::FN];
+  load_bias<C>(p, n0, wn, lr, bias);
   wait_vm<0>();
   __syncthreads();
 #pragma unroll 1
@@ -321,13 +353,10 @@ __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t 
       for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) {
-          const int64_t row_base = m0 + wm * C::WM + i * 32;
           const int col_l = wn * C::WN + j * 32 + lr;
-          const int64_t col = n0 + col_l;
           float16v extra = float16v{};
-          if constexpr (EPI == EPI_LORA || EPI == EPI_RANK)
-            extra = rank16_block<EPI>(p, row_base, col, lr, lh);
-          const float b = p.bias && col < p.N ? (float)p.bias[col] : 0.0f;
+          if constexpr (kRank) extra = ops.block(i, j);
+          const float b = bias[j];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int row_l = i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -390,6 +419,14 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
   const int wn = wave % C::kWavesN;
   const int lr = lane & 31;  // column within a 32x32 block
   const int lh = lane >> 5;
+  // Split 0 of a rank-16 (dX) product adds dZ . A to its partial, so the
+  // reduce is a plain sum (fold_rank; same MFMA as the unsplit epilogue).
+  const bool rank = EPI == EPI_LORA || EPI == EPI_RANK ||
+                    (EPI == EPI_PARTIAL && p.fold_rank && split == 0);
+  RankOps<C, EPI == EPI_LORA> ops;
+  if (rank) ops.load(p, m0, n0, wm, wn, lr, lh);
+  float bias[C::FN];
+  if constexpr (EPI != EPI_PARTIAL) load_bias<C>(p, n0, wn, lr, bias);
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
@@ -397,21 +434,8 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
       const int64_t row_base = m0 + wm * C::WM + i * 32;
       const int64_t col = n0 + wn * C::WN + j * 32 + lr;
       if constexpr (EPI == EPI_PARTIAL) {
-        // Split 0 of a rank-16 (dX) product adds dZ . A to its partial, so the
-        // reduce is a plain sum (fold_rank; same MFMA as the unsplit epilogue).
         float16v extra = float16v{};
-        if (p.fold_rank && split == 0) {
-          const int64_t zr = row_base + lr;
-          const half8 zero = half8{};
-          const half8 za =
-              zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
-          half8 zb = zero;
-          if (col < p.N) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
-          }
-          extra = __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, extra, 0, 0, 0);
-        }
+        if (rank) extra = ops.block(i, j);
         if (col >= p.N) continue;
         float* part = p.part + split * p.M * p.N;
 #pragma unroll
@@ -422,25 +446,9 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
         continue;
       }
       float16v extra = float16v{};
-      if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
-        // Rank-16 term of this block on one v_mfma_f32_32x32x16_f16:
-        // A = Z rows (row lane%32, ranks 8 (lane/32)..+7), B = (rank, column).
-        const int64_t zr = row_base + lr;
-        const half8 zero = half8{};
-        const half8 za = zr < p.M ? *reinterpret_cast<const half8*>(p.lz + zr * 16 + 8 * lh) : zero;
-        half8 zb = zero;
-        if (col < p.N) {
-          if constexpr (EPI == EPI_LORA) {
-            zb = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) zb[e] = p.lb[(8 * lh + e) * p.ldlb + col];
-          }
-        }
-        extra = __builtin_amdgcn_mfma_f32_32x32x16_f16(za, zb, extra, 0, 0, 0);
-      }
+      if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) extra = ops.block(i, j);
       if (col >= p.N) continue;
-      const float b = p.bias ? (float)p.bias[col] : 0.0f;
+      const float b = bias[j];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
