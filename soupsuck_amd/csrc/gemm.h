@@ -84,6 +84,10 @@ struct GemmParams {
   float* part;      // split-K partials [splits][M][N] fp32 (EPI_PARTIAL)
   int64_t k_split;  // k elements per split (a multiple of 64)
   int fold_rank;    // EPI_PARTIAL: split 0 adds the rank-16 term lz . lb (EPI_RANK layout)
+  // EPI_PARTIAL of an EPI_LORA product: split 0 also stores the rounded LoRA
+  // term fp16(fp16(lz . lb^T) * lscale) here ([M][N]), which the reduce adds
+  // instead of recomputing it from lora_B rows.
+  half_t* lora_plane;
   int pingpong;     // 8-wave NT configurations: ping-pong main loop (set by gemm_nt)
   // Optional rank-16 grads riding on the dense NT launch (unsplit) or on its
   // split-K reduce: tail_blocks + tail2_blocks extra workgroups each run one
@@ -264,9 +268,10 @@ int gemm_nt(const GemmParams& p, int ct, int epi, hipStream_t stream, void* part
             size_t partial_bytes = 0);
 // LDS-staged fp16 epilogue switch of the NT and fused NF4 launchers (default on).
 bool staged_epilogue_enabled();
-// fp32 split-K scratch that gemm_nt uses for an M x N x K product (0: no split).
+// Split-K scratch that gemm_nt uses for an M x N x K product (0: no split):
+// the fp32 partial planes and an fp16 plane for a LoRA forward's rank term.
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
-// Tile configuration (1..8 in gemm_nt.hip's list) and split-K plan of an
+// Tile configuration (1..9 in gemm_nt.hip's list) and split-K plan of an
 // M x N x K product on the NT kernels.
 struct NtPlan {
   int cfg;

@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
   // Rank-16 operands use 16-byte (Z, lora_B rows) and 8-byte (four lora_A
   // columns) loads where aligned.
   half8 z8[2];
-  if constexpr (EPI == EPI_LORA || EPI == EPI_RANK) {
+  if (EPI == EPI_RANK || (EPI == EPI_LORA && !p.lora_plane)) {
     const half_t* zr = p.lz + row * 16;
     if (reinterpret_cast<uintptr_t>(p.lz) % 16 == 0) {
       z8[0] = *reinterpret_cast<const half8*>(zr);
@@ -376,10 +376,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
         for (int e = 0; e < 4; ++e) a4[r][e] = c0 + e < p.N ? p.lb[r * p.ldlb + c0 + e] : (half_t)0;
     }
   }
-  half8 b8[4][2];  // EPI_LORA: lora_B rows of the four columns
+  half8 b8[4][2];  // EPI_LORA: lora_B rows of the four columns (no lora_plane)
+  half_t lp[4];    // EPI_LORA: the rounded LoRA terms (lora_plane)
   if constexpr (EPI == EPI_LORA) {
+    if (p.lora_plane) {
+      const half_t* src = p.lora_plane + row * p.N + c0;
+      if (p.N % 4 == 0) {
+        const half4 v4 = *reinterpret_cast<const half4*>(src);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) lp[e] = v4[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lp[e] = c0 + e < p.N ? src[e] : (half_t)0;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4 && !p.lora_plane; ++e) {
       const int64_t col = c0 + e < p.N ? c0 + e : p.N - 1;
       const half_t* br = p.lb + col * 16;
       if (reinterpret_cast<uintptr_t>(p.lb) % 16 == 0) {
@@ -438,11 +450,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
     if (col >= p.N) break;
     const int64_t idx = row * p.ldc + col;
     if constexpr (EPI == EPI_LORA) {
-      float l = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) l += z[r] * (float)b8[e][r / 8][r % 8];
       const float y = (float)f32_to_f16(v[e] * p.alpha + bias[e]);
-      const float scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
+      float scaled;
+      if (p.lora_plane) {
+        scaled = (float)lp[e];
+      } else {
+        float l = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) l += z[r] * (float)b8[e][r / 8][r % 8];
+        scaled = (float)f32_to_f16((float)f32_to_f16(l) * p.lscale);
+      }
       reinterpret_cast<half_t*>(p.C)[idx] = f32_to_f16(y + scaled);
     } else if constexpr (EPI == EPI_RANK) {
       float l = 0.0f;
@@ -467,6 +484,7 @@ using NtWide8 = NtCfg<256, 128, 4, 2, 64, 2, 2>;    // 8 waves of 64x64, 96 KiB 
 using NtBig8s = NtCfg<256, 256, 2, 4, 32, 3, 2>;    // 8 waves of 128x64, 96 KiB LDS
 using NtMid64 = NtCfg<128, 128, 2, 2, 64, 2, 2>;    // 4 waves of 64x64, 64 KiB LDS
 using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 KiB LDS
+using NtWide8s4 = NtCfg<256, 128, 4, 2, 32, 4, 1>;  // 8 waves of 64x64, 96 KiB LDS
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
@@ -482,6 +500,7 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
 template <int CT, int EPI>
 int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
   switch (cfg) {
+    case 9: return launch_nt<NtWide8s4, CT, EPI>(p, splits, stream);
     case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
     case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
     case 6: return launch_nt<NtBig8s, CT, EPI>(p, splits, stream);
@@ -511,10 +530,11 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 // Configuration and split-K plan for an M x N x K product.
 //   256x256 (8 waves, 4-stage ring) once it gives at least half the CUs a
 //   tile;
-//   long K with few 128x128 tiles: 128x128 split over k so that about 512
-//   workgroups run (each split at least 1024 k);
+//   long K with few 128x128 tiles: split over k (each split at least 1024
+//   k), 256x128 tiles with about one workgroup per CU where M fills 256-row
+//   tiles, else 128x128 with about 512 workgroups;
 //   128x128 while it gives half the CUs a tile; else 64x64.
-// SS_TUNE_NT_TILE (1..8, the configurations above in order) and
+// SS_TUNE_NT_TILE (1..9, the configurations above in order) and
 // SS_TUNE_NT_SPLITS override the choice (build-time constants, tuning.h).
 NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   constexpr int forced = SS_TUNE_NT_TILE;
@@ -529,6 +549,17 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     int64_t s = 512 / t128;
     if (s > k / 1024) s = k / 1024;
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
+    // 256x128 tiles (8 waves) when M fills 256-row tiles as well as 128-row
+    // ones and a split of about one workgroup per CU still gives 192 or more
+    // workgroups (990 x 1536 x 8960: 44 us against 50 us for 128x128).
+    const int64_t tw = cdiv(m, 256) * cdiv(n, 128);
+    int64_t sw = 256 / tw;
+    if (sw > k / 1024) sw = k / 1024;
+    sw = sw < 1 ? 1 : (sw > 8 ? 8 : sw);
+    if (cdiv(m, 256) * 2 == cdiv(m, 128) && tw * sw >= 192) {
+      plan.cfg = 9;
+      plan.splits = sw;
+    }
   } else if (t128 >= 128) {
     plan.cfg = 2;
   } else if (t128 < 64 && k >= 1024) {
@@ -539,7 +570,7 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     if (s > k / 384) s = k / 384;
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   }
-  if (forced >= 1 && forced <= 8) plan.cfg = forced;
+  if (forced >= 1 && forced <= 9) plan.cfg = forced;
   if (forced_splits >= 1) plan.splits = forced_splits;
   plan.k_split = cdiv(cdiv(k, plan.splits), 64) * 64;
   plan.splits = cdiv(k, plan.k_split);
@@ -557,10 +588,19 @@ int splitk_reduce(const GemmParams& p, int splits, int ct, int epi, hipStream_t 
   return reduce_nt<SS_F16, EPI_PLAIN>(p, splits, stream);
 }
 
+// Split-K scratch: the fp32 partial planes, then (256-byte aligned) the fp16
+// LoRA plane of a split LoRA forward.
+static size_t nt_plane_offset(int64_t m, int64_t n, int64_t splits) {
+  return ((size_t)(splits * m * n) * sizeof(float) + 255) / 256 * 256;
+}
+static size_t nt_split_bytes(int64_t m, int64_t n, int64_t splits) {
+  return nt_plane_offset(m, n, splits) + (size_t)(m * n) * sizeof(half_t);
+}
+
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || k % 64 != 0) return 0;
   const NtPlan plan = nt_plan(m, n, k);
-  return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
+  return plan.splits > 1 ? nt_split_bytes(m, n, plan.splits) : 0;
 }
 
 // SS_TUNE_NT_PINGPONG = 0 keeps the 8-wave configurations on the lockstep
@@ -587,7 +627,7 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
     return SS_ERR_UNSUPPORTED;
   if (ct != SS_F16 && epi != EPI_PLAIN) return SS_ERR_UNSUPPORTED;
   NtPlan plan = nt_plan(p.M, p.N, p.K);
-  const size_t need = (size_t)(plan.splits * p.M * p.N) * sizeof(float);
+  const size_t need = nt_split_bytes(p.M, p.N, plan.splits);
   if (plan.splits > 1 && (!partials || partial_bytes < need ||
                           reinterpret_cast<uintptr_t>(partials) % 16 != 0)) {
     plan.splits = 1;
@@ -604,8 +644,15 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
     p.part = reinterpret_cast<float*>(partials);
     p.k_split = plan.k_split;
     // The rank-16 update is folded into split 0's partial (the reduce then
-    // only sums: its lora_A column loads dominated its load count).
+    // only sums: its lora_A column loads dominated its load count); the
+    // forward's rounded LoRA term goes from split 0 to a plane of its own
+    // (its lora_B row loads doubled the reduce's load count: 990 x 1536 x
+    // 8960 reduce 11.7 us against 6.9 us without the LoRA term).
     p.fold_rank = epi == EPI_RANK;
+    p.lora_plane = epi == EPI_LORA
+                       ? reinterpret_cast<half_t*>(static_cast<char*>(partials) +
+                                                   nt_plane_offset(p.M, p.N, plan.splits))
+                       : nullptr;
     const int64_t tail = p.tail_blocks, tail2 = p.tail2_blocks;
     p.tail_blocks = p.tail2_blocks = 0;
     const int rc = dispatch_nt<SS_F32, EPI_PARTIAL>(p, plan.cfg, plan.splits, stream);

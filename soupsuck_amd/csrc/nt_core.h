@@ -276,16 +276,16 @@ __device__ __forceinline__ void nt_glu_epilogue_lds(const GemmParams& p, int64_t
 // Rank-16 term of a 32x32 block on one v_mfma_f32_32x32x16_f16 (EPI_LORA,
 // EPI_RANK, or folded into a split-K partial): A = Z rows (row lane % 32,
 // ranks 8 (lane / 32) .. + 7), B = (rank, column) -- a lora_B row ([N, 16],
-// one 16-byte load; VEC_B) or a lora_A column ([16, ldlb], eight 2-byte
+// one 16-byte load; vec_b) or a lora_A column ([16, ldlb], eight 2-byte
 // loads).  A wave loads the operands of all its FM x FN blocks (and their
 // bias) before it finishes any block, so it waits for them once instead of
 // once per block.
-template <class C, bool VEC_B>
+template <class C>
 struct RankOps {
   half8 za[C::FM];
   half8 zb[C::FN];
   __device__ __forceinline__ void load(const GemmParams& p, int64_t m0, int64_t n0, int wm, int wn,
-                                       int lr, int lh) {
+                                       int lr, int lh, bool vec_b) {
     const half8 zero = half8{};
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) {
@@ -297,7 +297,7 @@ struct RankOps {
       const int64_t col = n0 + wn * C::WN + j * 32 + lr;
       zb[j] = zero;
       if (col < p.N) {
-        if constexpr (VEC_B) {
+        if (vec_b) {
           zb[j] = *reinterpret_cast<const half8*>(p.lb + col * 16 + 8 * lh);
         } else {
 #pragma unroll
@@ -340,8 +340,8 @@ __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t 
   const int lr = lane & 31;
   const int lh = lane >> 5;
   constexpr bool kRank = EPI == EPI_LORA || EPI == EPI_RANK;
-  RankOps<C, EPI == EPI_LORA> ops;
-  if constexpr (kRank) ops.load(p, m0, n0, wm, wn, lr, lh);
+  RankOps<C> ops;
+  if constexpr (kRank) ops.load(p, m0, n0, wm, wn, lr, lh, EPI == EPI_LORA);
   float bias[C::FN];
   load_bias<C>(p, n0, wn, lr, bias);
   wait_vm<0>();
@@ -420,11 +420,13 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
   const int lr = lane & 31;  // column within a 32x32 block
   const int lh = lane >> 5;
   // Split 0 of a rank-16 (dX) product adds dZ . A to its partial, so the
-  // reduce is a plain sum (fold_rank; same MFMA as the unsplit epilogue).
+  // reduce is a plain sum (fold_rank); split 0 of a LoRA forward stores the
+  // rounded LoRA term to lora_plane.  Same MFMA as the unsplit epilogue.
+  const bool lora_plane = EPI == EPI_PARTIAL && p.lora_plane && split == 0;
   const bool rank = EPI == EPI_LORA || EPI == EPI_RANK ||
-                    (EPI == EPI_PARTIAL && p.fold_rank && split == 0);
-  RankOps<C, EPI == EPI_LORA> ops;
-  if (rank) ops.load(p, m0, n0, wm, wn, lr, lh);
+                    (EPI == EPI_PARTIAL && p.fold_rank && split == 0) || lora_plane;
+  RankOps<C> ops;
+  if (rank) ops.load(p, m0, n0, wm, wn, lr, lh, EPI == EPI_LORA || lora_plane);
   float bias[C::FN];
   if constexpr (EPI != EPI_PARTIAL) load_bias<C>(p, n0, wn, lr, bias);
 #pragma unroll
@@ -438,6 +440,17 @@ __device__ __forceinline__ void nt_epilogue(const GemmParams& p, int64_t m0, int
         if (rank) extra = ops.block(i, j);
         if (col >= p.N) continue;
         float* part = p.part + split * p.M * p.N;
+        if (lora_plane) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (row >= p.M) continue;
+            part[row * p.N + col] = acc[i][j][r];
+            p.lora_plane[row * p.N + col] =
+                f32_to_f16((float)f32_to_f16(extra[r]) * p.lscale);
+          }
+          continue;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t row = row_base + 8 * (r >> 2) + 4 * lh + (r & 3);
