@@ -68,6 +68,7 @@ constexpr int kStBiasOff = kStSlotOff + kStSlotRegion;
 constexpr int kStLzOff = kStBiasOff + kStMaxRange * 2;
 constexpr int kStLbOff = kStLzOff + kStreamMaxT * 32;
 constexpr int kStSmemBytes = kStLbOff + 3072;       // lora_B rows: three 1 KiB DMAs
+constexpr int64_t kStSmallBytes = (int64_t)8 << 20;  // small weight: codes bytes
 static_assert(kStSmemBytes <= 160 * 1024, "LDS");
 
 // Stage / wave plan.  mt = 0 when the kernel does not apply.
@@ -425,6 +426,11 @@ StreamPlan stream_plan(int64_t t, int64_t n, int64_t k) {
   int64_t g_fill = cdiv(cus, n_ranges);
   if (g_fill > s) g_fill = s;
   if (g_fill > g) g = g_fill;
+  // A small weight (at most 8 MiB of codes) is latency-bound, not
+  // bandwidth-bound: every stage in one workgroup, so the epilogue runs in
+  // the kernel and no partial planes or reduce launch follow (7B k/v at T =
+  // 1: 10.8 -> 7.0 us, q/o: 9.8 -> 7.6 us, although fewer CUs stream it).
+  if (n * (k / 2) <= kStSmallBytes && s <= max_waves) g = 1;
   plan.sg = cdiv(s, g);
   plan.groups = cdiv(s, plan.sg);
   plan.waves = (int)plan.sg;

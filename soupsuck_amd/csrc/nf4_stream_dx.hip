@@ -285,7 +285,12 @@ __global__ __launch_bounds__(kDxWaves * kWave) void nf4_stream_dx_kernel(GemmPar
       float v = 0.f;
       for (int q = 0; q < nw; ++q) v += s_red[(cl * nw + q) * t * 16 + m * 16 + c];
       const int64_t col = cs * kDxCols + 16 * (ca + cl) + (c ^ 1);
-      prm.part[grp * plane + m * nc + col] = v;
+      if (prm.part) {
+        prm.part[grp * plane + m * nc + col] = v;
+      } else {  // one row range: the plain epilogue here (no reduce launch)
+        const float b = prm.bias ? (float)prm.bias[col] : 0.0f;
+        store_c<SS_F16>(prm.C, m * prm.ldc + col, v * prm.alpha + b, prm.beta);
+      }
     }
   }
 }
@@ -347,9 +352,14 @@ int nf4_stream_dx(const GemmParams& p0, int epi, void* partials, size_t partial_
     return SS_ERR_UNSUPPORTED;
   GemmParams p = p0;
   p.part = reinterpret_cast<float*>(partials);
+  // One row range and the plain epilogue: the kernel stores dX itself.
+  const bool direct = plan.groups == 1 && epi == EPI_PLAIN;
+  if (direct) p.part = nullptr;
   hipLaunchKernelGGL(nf4_stream_dx_kernel, dim3((unsigned)plan.col_stages, (unsigned)plan.groups),
                      dim3(kDxWaves * kWave), 0, stream, p, plan.group_rows);
   SS_CHECK_LAUNCH("nf4_stream_dx_kernel");
+  if (direct) return SS_OK;
+  p.part = reinterpret_cast<float*>(partials);
   return splitk_reduce(p, (int)plan.groups, SS_F16, epi, stream);
 }
 
