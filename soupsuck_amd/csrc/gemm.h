@@ -271,7 +271,7 @@ bool staged_epilogue_enabled();
 // Split-K scratch that gemm_nt uses for an M x N x K product (0: no split):
 // the fp32 partial planes and an fp16 plane for a LoRA forward's rank term.
 size_t nt_partial_bytes(int64_t m, int64_t n, int64_t k);
-// Tile configuration (1..9 in gemm_nt.hip's list) and split-K plan of an
+// Tile configuration (1..10 in gemm_nt.hip's list) and split-K plan of an
 // M x N x K product on the NT kernels.
 struct NtPlan {
   int cfg;

@@ -485,6 +485,7 @@ using NtBig8s = NtCfg<256, 256, 2, 4, 32, 3, 2>;    // 8 waves of 128x64, 96 KiB
 using NtMid64 = NtCfg<128, 128, 2, 2, 64, 2, 2>;    // 4 waves of 64x64, 64 KiB LDS
 using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 KiB LDS
 using NtWide8s4 = NtCfg<256, 128, 4, 2, 32, 4, 1>;  // 8 waves of 64x64, 96 KiB LDS
+using NtTall8s4 = NtCfg<128, 256, 2, 4, 32, 4, 1>;  // 8 waves of 64x64, 96 KiB LDS
 
 template <class C, int CT, int EPI>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
@@ -500,6 +501,7 @@ int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
 template <int CT, int EPI>
 int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
   switch (cfg) {
+    case 10: return launch_nt<NtTall8s4, CT, EPI>(p, splits, stream);
     case 9: return launch_nt<NtWide8s4, CT, EPI>(p, splits, stream);
     case 8: return launch_nt<NtBig8s4, CT, EPI>(p, splits, stream);
     case 7: return launch_nt<NtMid64, CT, EPI>(p, splits, stream);
@@ -533,8 +535,10 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 //   long K with few 128x128 tiles: split over k (each split at least 1024
 //   k), 256x128 tiles with about one workgroup per CU where M fills 256-row
 //   tiles, else 128x128 with about 512 workgroups;
+//   96..127 tiles of 256x256: 128x256 tiles, or 256x256 split in two for
+//   a long K;
 //   128x128 while it gives half the CUs a tile; else 64x64.
-// SS_TUNE_NT_TILE (1..9, the configurations above in order) and
+// SS_TUNE_NT_TILE (1..10, the cases of dispatch_nt) and
 // SS_TUNE_NT_SPLITS override the choice (build-time constants, tuning.h).
 NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   constexpr int forced = SS_TUNE_NT_TILE;
@@ -560,6 +564,18 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
       plan.cfg = 9;
       plan.splits = sw;
     }
+  } else if (t256 >= 96) {
+    // 96..127 tiles of 256x256 (e.g. 2048 x 3584 at T = 2048): half-height
+    // 128x256 tiles (8 waves) fill the CUs better than 256x256 (60.8 vs
+    // 67.3 us at 2048 x 3584 x 3584, 128x128: 70.6 us); with a long K,
+    // 256x256 split in two (2048 x 3584 x 18944: 263 vs 295 us for
+    // 128x256, 354 us for 128x128).
+    if (k >= 8192) {
+      plan.cfg = 8;
+      plan.splits = 2;
+    } else {
+      plan.cfg = 10;
+    }
   } else if (t128 >= 128) {
     plan.cfg = 2;
   } else if (t128 < 64 && k >= 1024) {
@@ -570,7 +586,7 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     if (s > k / 384) s = k / 384;
     plan.splits = s < 1 ? 1 : (s > 8 ? 8 : s);
   }
-  if (forced >= 1 && forced <= 9) plan.cfg = forced;
+  if (forced >= 1 && forced <= 10) plan.cfg = forced;
   if (forced_splits >= 1) plan.splits = forced_splits;
   plan.k_split = cdiv(cdiv(k, plan.splits), 64) * 64;
   plan.splits = cdiv(k, plan.k_split);

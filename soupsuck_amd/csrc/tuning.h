@@ -32,7 +32,7 @@
 #ifndef SS_TUNE_NF4_FUSED
 #define SS_TUNE_NF4_FUSED 1
 #endif
-// NT kernel configuration (0 automatic, 1..9) and split count (0 automatic).
+// NT kernel configuration (0 automatic, 1..10) and split count (0 automatic).
 #ifndef SS_TUNE_NT_TILE
 #define SS_TUNE_NT_TILE 0
 #endif
