@@ -530,13 +530,14 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 }  // namespace
 
 // Configuration and split-K plan for an M x N x K product.
+//   128x256 (8 waves) when 96 or more 256x256 tiles would run but the
+//   128x256 tiles still fit one wave on the CUs (K < 8192);
 //   256x256 (8 waves, 4-stage ring) once it gives at least half the CUs a
 //   tile;
 //   long K with few 128x128 tiles: split over k (each split at least 1024
 //   k), 256x128 tiles with about one workgroup per CU where M fills 256-row
 //   tiles, else 128x128 with about 512 workgroups;
-//   96..127 tiles of 256x256: 128x256 tiles, or 256x256 split in two for
-//   a long K;
+//   96..127 tiles of 256x256 and a long K: 256x256 split in two;
 //   128x128 while it gives half the CUs a tile; else 64x64.
 // SS_TUNE_NT_TILE (1..10, the cases of dispatch_nt) and
 // SS_TUNE_NT_SPLITS override the choice (build-time constants, tuning.h).
@@ -546,7 +547,14 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
   NtPlan plan{1, 1, k};
   const int64_t t256 = cdiv(m, 256) * cdiv(n, 256);
   const int64_t t128 = cdiv(m, 128) * cdiv(n, 128);
-  if (t256 >= 128) {
+  const int64_t t10 = cdiv(m, 128) * cdiv(n, 256);  // 128x256 tiles
+  if (t256 >= 96 && t10 <= 256 && k < 8192) {
+    // 96 or more tiles of 256x256, but one wave of 128x256 tiles (8 waves):
+    // the half-height tiles fill the CUs better and pad M less (2048 x 3584
+    // x 3584: 60.8 vs 67.3 us for 256x256, 70.6 us for 128x128; the
+    // cross-entropy chunk 826 x 8192 x 1536: 31.5 vs 37.7 us).
+    plan.cfg = 10;
+  } else if (t256 >= 128) {
     plan.cfg = 8;
   } else if (k >= 2048 && t128 < 256) {
     plan.cfg = 2;
@@ -565,17 +573,11 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
       plan.splits = sw;
     }
   } else if (t256 >= 96) {
-    // 96..127 tiles of 256x256 (e.g. 2048 x 3584 at T = 2048): half-height
-    // 128x256 tiles (8 waves) fill the CUs better than 256x256 (60.8 vs
-    // 67.3 us at 2048 x 3584 x 3584, 128x128: 70.6 us); with a long K,
-    // 256x256 split in two (2048 x 3584 x 18944: 263 vs 295 us for
-    // 128x256, 354 us for 128x128).
-    if (k >= 8192) {
-      plan.cfg = 8;
-      plan.splits = 2;
-    } else {
-      plan.cfg = 10;
-    }
+    // 96..127 tiles of 256x256 with a long K (k >= 8192 here): 256x256 split
+    // in two (2048 x 3584 x 18944: 263 vs 295 us for 128x256, 354 us for
+    // 128x128).
+    plan.cfg = 8;
+    plan.splits = 2;
   } else if (t128 >= 128) {
     plan.cfg = 2;
   } else if (t128 < 64 && k >= 1024) {
