@@ -52,7 +52,11 @@ def test_epilogue_rounded_product_cancels(device):
                                         (37, 8960, 1536, False), (64, 1536, 8960, False),
                                         (300, 256, 1536, True), (990, 8960, 1536, False),
                                         (990, 1536, 8960, False), (2048, 8960, 256, True),
-                                        (16, 8960, 1536, True), (29, 1000, 3584, False)])
+                                        (16, 8960, 1536, True), (29, 1000, 3584, False),
+                                        # 592 tiles of 256x256 in the forward (LoRA
+                                        # epilogue) and in the dX product (rank-16)
+                                        (2048, 18944, 128, True),
+                                        (2048, 128, 18944, False)])
 def test_qlora_projection_matches_oracle(device, t, n, k, bias):
     rng = np.random.default_rng(t + n)
     state = onf4.quantize_nested(random_weight(n, k, seed=3))
