@@ -34,7 +34,7 @@ sweep_configs4 = configs[4]: NF4 forward and dX at the Qwen2.5-7B projection
              shapes, T in {1, 16, 128, 2048, 16384}, each point timed from HBM
              (GB/s, TFLOP/s, fraction of its HBM or MFMA roofline)
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-graph]
-       [--no-sweep] [--no-other-configs]
+       [--no-sweep] [--no-full-layer] [--no-other-configs]
 """
 
 import argparse
@@ -67,6 +67,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-sweep", action="store_true",
                    help="skip the configs[4] NF4 GEMM sweep (7B shapes, T in {1,16,128,2048,16384})")
+    p.add_argument("--no-full-layer", action="store_true",
+                   help="skip the whole-decoder-layer timing (full_decoder_layer: null)")
     p.add_argument("--no-other-configs", action="store_true",
                    help="skip configs[0], configs[2] and configs[3] (dequant, GEMM T=1024, "
                         "add-RMSNorm, unpad, fused CE)")
@@ -970,7 +972,7 @@ def main():
                 "timing": (f"HIP events on the launch stream around each call, {args.timing_steps}"
                            " eager steps each queued behind a GPU spin (calls run back to back)")}
 
-    full = full_layer(torch, lengths, args.steps, args.warmup)
+    full = None if args.no_full_layer else full_layer(torch, lengths, args.steps, args.warmup)
     sweep_res = None if args.no_sweep else sweep(torch, _lib)
     others = None if args.no_other_configs else other_configs(torch, _lib)
 
