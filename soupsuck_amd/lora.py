@@ -53,6 +53,7 @@ def _gemm_ws(t, n, k, device):
 
 
 _RANK_WORKSPACE = {}
+_RETIRED_WORKSPACES = []
 
 
 def _rank_workspace(nbytes, device):
@@ -61,14 +62,19 @@ def _rank_workspace(nbytes, device):
     Its leading arrival counters must be zero when an op starts and the op
     leaves them zero, so one zero-filled buffer serves every call issued in
     order on one stream.  Calls on different streams can overlap in time, so
-    each stream (torch's current stream at the call) gets its own buffer; a
-    buffer replaced by a larger one is released only after the work queued on
-    its stream (torch's caching allocator records the stream that used it)."""
+    each stream (torch's current stream at the call) gets its own buffer.  A
+    buffer replaced by a larger one is kept alive, not released: a HIP graph
+    captured on that stream still addresses it, and its replays must find
+    the counters it left at zero, not whatever a later tensor wrote there.
+    Growth at least doubles the size, so few buffers are ever retired."""
     index = device.index if device.index is not None else torch.cuda.current_device()
     key = (index, _lib.stream(device))
     ws = _RANK_WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)
+        grown = 2 * ws.numel() if ws is not None else 0
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
+        ws = torch.zeros(max(int(nbytes), 1 << 16, grown), dtype=torch.uint8, device=device)
         _RANK_WORKSPACE[key] = ws
     return ws
 

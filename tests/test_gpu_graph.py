@@ -62,3 +62,42 @@ def test_graph_replay_matches_eager(device):
             assert torch.equal(a, b), f"replay {replay}: gradient {i} differs"
         noise = noise @ noise.t() / 512.0   # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_graph_replay_after_rank_workspace_growth(device):
+    """A graph captured on a stream keeps addressing the rank-16 workspace it
+    was captured with.  A larger eager step on the same stream then grows that
+    stream's workspace; the old buffer must stay allocated (its counters at
+    zero) so that replays, after fresh allocations that could reuse freed
+    memory, still reproduce the eager step bit for bit."""
+    layer = QLoRALayer(device, seed=3)
+    small_x, small_g = layer.inputs(128, device, seed=5)
+    big_x, big_g = layer.inputs(2048, device, seed=6)
+
+    def step(xs, gs):
+        for p in layer.projections:
+            p.lora_a.grad = None
+            p.lora_b.grad = None
+        for x in xs:
+            x.grad = None
+        return layer.step(xs, gs)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = [o.detach().clone() for o in step(small_x, small_g)]
+        step(small_x, small_g)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        graph_out = step(small_x, small_g)
+    with torch.cuda.stream(s):
+        step(big_x, big_g)   # grows the stream's rank-16 workspace
+    torch.cuda.synchronize()
+    scribble = [torch.full((1 << 22,), 255, dtype=torch.uint8, device=device) for _ in range(8)]
+    for replay in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(graph_out, eager)):
+            assert torch.equal(a, b), f"replay {replay}: output {i} differs"
+    del scribble
