@@ -28,6 +28,7 @@ Otherwise each GEMM and the epilogue run as separate kernels (torch's native
 dropout on an fp32 copy of X for p > 0).
 """
 
+import contextlib
 import math
 
 import torch
@@ -47,8 +48,28 @@ def _nf4_args(packed, state):
             state.state2.code.data_ptr(), state.offset.data_ptr())
 
 
+def _on_device(device):
+    """torch.cuda.device(device), or nothing when it is already the current device."""
+    if device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
+
+
+_SIZES = {}
+
+
+def _size_of(query, t, n, k, device):
+    """Workspace size from the library (a pure function of the shape and the
+    device's CU count), asked once per (query, shape, device)."""
+    key = (query, t, n, k, device.index)
+    size = _SIZES.get(key)
+    if size is None:
+        size = _SIZES[key] = int(getattr(_lib.load(), query)(t, n, k))
+    return size
+
+
 def _gemm_ws(t, n, k, device):
-    size = _lib.load().ss_nf4_gemm_workspace_size(t, n, k)
+    size = _size_of("ss_nf4_gemm_workspace_size", t, n, k, device)
     return (_workspace(size, device), size) if size else (None, 0)
 
 
@@ -56,7 +77,7 @@ _RANK_WORKSPACE = {}
 _RETIRED_WORKSPACES = []
 
 
-def _rank_workspace(nbytes, device):
+def _rank_workspace(nbytes, device, stream=None):
     """Zero-filled workspace of the rank-16 ops, one per (device, stream), grown on demand.
 
     Its leading arrival counters must be zero when an op starts and the op
@@ -66,9 +87,10 @@ def _rank_workspace(nbytes, device):
     buffer replaced by a larger one is kept alive, not released: a HIP graph
     captured on that stream still addresses it, and its replays must find
     the counters it left at zero, not whatever a later tensor wrote there.
-    Growth at least doubles the size, so few buffers are ever retired."""
+    Growth at least doubles the size, so few buffers are ever retired.
+    ``stream``: the raw stream handle when the caller already has it."""
     index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, _lib.stream(device))
+    key = (index, stream if stream is not None else _lib.stream(device))
     ws = _RANK_WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
         grown = 2 * ws.numel() if ws is not None else 0
@@ -103,8 +125,9 @@ def grad16(p2d, q2d, transpose, scale=None):
     return out
 
 
-def _qlora_rank_ws(t, n, k, device):
-    return _rank_workspace(_lib.load().ss_qlora_rank_workspace_size(t, n, k), device)
+def _qlora_rank_ws(t, n, k, device, stream):
+    return _rank_workspace(_size_of("ss_qlora_rank_workspace_size", t, n, k, device), device,
+                           stream)
 
 
 class _QLoRAFused(torch.autograd.Function):
@@ -121,12 +144,13 @@ class _QLoRAFused(torch.autograd.Function):
         b16 = lora_b.to(torch.float16).contiguous()
         z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
         y = torch.empty((t, n), device=x.device, dtype=torch.float16)
+        stream = _lib.stream(x.device)
         ws, size = _gemm_ws(t, n, k, x.device)
-        rws = _qlora_rank_ws(t, n, k, x.device)
+        rws = _qlora_rank_ws(t, n, k, x.device, stream)
         _lib.call("ss_qlora_forward", x2d.data_ptr(), x2d.stride(0), t, *_nf4_args(packed, state),
                   n, k, _lib.ptr(bias), a16.data_ptr(), b16.data_ptr(), float(scaling),
                   z.data_ptr(), y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(),
-                  rws.numel(), _lib.stream(x.device))
+                  rws.numel(), stream)
         ctx.save_for_backward(x2d, z, a16, b16, packed)
         ctx.state, ctx.scaling = state, float(scaling)
         ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
@@ -145,13 +169,14 @@ class _QLoRAFused(torch.autograd.Function):
         db = torch.empty((n, 16), device=dev, dtype=torch.float16)   # fp16(fp16(g*s)^T . Z)
         da = torch.empty((16, k), device=dev, dtype=torch.float16)   # fp16(dZ^T . X)
         dx = torch.empty((t, k), device=dev, dtype=torch.float16)
+        stream = _lib.stream(dev)
         ws, size = _gemm_ws(t, n, k, dev)
-        rws = _qlora_rank_ws(t, n, k, dev)
+        rws = _qlora_rank_ws(t, n, k, dev, stream)
         _lib.call("ss_qlora_backward", g.data_ptr(), g.stride(0), t, *_nf4_args(packed, state), n,
                   k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(), a16.data_ptr(), b16.data_ptr(),
                   ctx.scaling, dx.data_ptr(), dx.stride(0), dz.data_ptr(), da.data_ptr(),
                   db.data_ptr(), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
-                  _lib.stream(dev))
+                  stream)
         x_dtype, a_dtype, b_dtype = ctx.dtypes
         return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
                 None, None, None, None)
@@ -178,13 +203,14 @@ class _QLoRAFusedDropout(torch.autograd.Function):
         b16 = lora_b.to(torch.float16).contiguous()
         z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
         y = torch.empty((t, n), device=x.device, dtype=torch.float16)
+        stream = _lib.stream(x.device)
         ws, size = _gemm_ws(t, n, k, x.device)
-        rws = _qlora_rank_ws(t, n, k, x.device)
+        rws = _qlora_rank_ws(t, n, k, x.device, stream)
         _lib.call("ss_qlora_forward_dropout", x2d.data_ptr(), x2d.stride(0), t,
                   *_nf4_args(packed, state), n, k, _lib.ptr(bias), a16.data_ptr(),
                   b16.data_ptr(), float(scaling), seed, float(dropout_p), z.data_ptr(),
                   y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
-                  _lib.stream(x.device))
+                  stream)
         ctx.save_for_backward(x2d, z, a16, b16, packed)
         ctx.state, ctx.scaling, ctx.dropout = state, float(scaling), (seed, float(dropout_p))
         ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
@@ -204,13 +230,14 @@ class _QLoRAFusedDropout(torch.autograd.Function):
         db = torch.empty((n, 16), device=dev, dtype=torch.float16)
         da = torch.empty((16, k), device=dev, dtype=torch.float16)
         dx = torch.empty((t, k), device=dev, dtype=torch.float16)
+        stream = _lib.stream(dev)
         ws, size = _gemm_ws(t, n, k, dev)
-        rws = _qlora_rank_ws(t, n, k, dev)
+        rws = _qlora_rank_ws(t, n, k, dev, stream)
         _lib.call("ss_qlora_backward_dropout", g.data_ptr(), g.stride(0), t,
                   *_nf4_args(packed, state), n, k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(),
                   a16.data_ptr(), b16.data_ptr(), ctx.scaling, seed, p, dx.data_ptr(),
                   dx.stride(0), dz.data_ptr(), da.data_ptr(), db.data_ptr(), _lib.ptr(ws), size,
-                  rws.data_ptr(), rws.numel(), _lib.stream(dev))
+                  rws.data_ptr(), rws.numel(), stream)
         x_dtype, a_dtype, b_dtype = ctx.dtypes
         return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
                 None, None, None, None, None, None)
@@ -291,7 +318,7 @@ def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, d
         raise ValueError("dropout_p must be in [0, 1)")
     fused = lora_a.shape[0] == 16 and k % 64 == 0 and packed.data_ptr() % 16 == 0
     active = dropout_p > 0.0 and training
-    with torch.cuda.device(x.device):
+    with _on_device(x.device):
         if fused and not active:
             return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling))
         if fused and x.data_ptr() % 16 == 0:
