@@ -20,21 +20,45 @@ __device__ __forceinline__ float block_scale(const uint8_t* __restrict__ qabs,
   }
 }
 
+// Both NF4 values of a code byte e in one 8-byte LDS read: pair[e] =
+// {NF4[e >> 4], NF4[e & 15]}.  Against a 16-entry table this halves the LDS
+// reads and drops the nibble split from the decode.
+constexpr int kPairBytes = 256 * 8;
+
+__device__ __forceinline__ const float2* load_pairs(unsigned char* smem) {
+  float2* pair = reinterpret_cast<float2*>(smem);
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) pair[i] = float2{kNF4[i >> 4], kNF4[i & 15]};
+  return pair;
+}
+
+// v[at + i] = fp16(NF4[c_i] * scale) for the 8 codes c_i of word: element 2j
+// is the high nibble of byte j, element 2j + 1 its low nibble.
+template <class V>
+__device__ __forceinline__ void decode_word(const float2* __restrict__ pair, uint32_t word,
+                                            float scale, V& v, int at) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const float2 pr = pair[(word >> (8 * b)) & 0xffu];
+    v[at + 2 * b] = f32_to_f16(pr.x * scale);
+    v[at + 2 * b + 1] = f32_to_f16(pr.y * scale);
+  }
+}
+
 constexpr int kDecodeTLd = 64 + 8;
-// LDS of a decode block: the 16-entry code table, then (transposed decode)
-// a [64 k][64 + 8 n] fp16 tile.
-constexpr int kDecodeSmem = 64 + 64 * kDecodeTLd * 2;
+// LDS of a decode block: the code-pair table, then (transposed decode) a
+// [64 k][64 + 8 n] fp16 tile.
+constexpr int kDecodeSmem = kPairBytes + 64 * kDecodeTLd * 2;
 
 // Row-major decode: 8 elements (one dword of codes) per lane and group.  A
 // wave covers U * 64 consecutive groups per step -- U coalesced dword loads
 // per lane (with their qabs / absmax2 loads) issued before any arithmetic,
 // then U 16-byte stores, each wave-wide store 1 KiB contiguous -- and the
-// waves of the grid stride over the groups.  The 16-entry NF4 table and the
+// waves of the grid stride over the groups.  The code-pair table and the
 // 256-entry code2 table sit in LDS, so the scale costs no dependent global
 // load.  U = 8 keeps 2 KiB of codes in flight per wave (large weights), U = 2
 // gives more waves to small ones (measured on MI355X: 18944 x 3584 in 32.3 us,
 // 5.3 TB/s, against 42.4 us with one group per lane and step).
-constexpr int kDecodeRowsSmem = (16 + 256) * 4;
+constexpr int kDecodeRowsSmem = kPairBytes + 256 * 4;
 
 template <bool NESTED, int U>
 __device__ __forceinline__ void decode_rows_block(
@@ -42,9 +66,8 @@ __device__ __forceinline__ void decode_rows_block(
     const float* __restrict__ absmax, const float* __restrict__ absmax2,
     const float* __restrict__ code2, const float* __restrict__ offset_ptr,
     half8* __restrict__ out, int64_t groups, int64_t vb, int64_t nblocks, unsigned char* smem) {
-  float* lut = reinterpret_cast<float*>(smem);
-  float* c2 = lut + 16;
-  for (int i = threadIdx.x; i < 16; i += blockDim.x) lut[i] = kNF4[i];
+  const float2* pair = load_pairs(smem);
+  float* c2 = reinterpret_cast<float*>(smem + kPairBytes);
   if constexpr (NESTED)
     for (int i = threadIdx.x; i < 256; i += blockDim.x) c2[i] = code2[i];
   __syncthreads();
@@ -79,12 +102,7 @@ __device__ __forceinline__ void decode_rows_block(
         scale = product + offset;
       }
       half8 v;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (word[j] >> (8 * b)) & 0xffu;
-        v[2 * b] = f32_to_f16(lut[byte >> 4] * scale);
-        v[2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
-      }
+      decode_word(pair, word[j], scale, v, 0);
       if (g < groups) out[g] = v;
     }
   }
@@ -99,9 +117,8 @@ __device__ __forceinline__ void decode_t_block(
     const float* __restrict__ offset_ptr, half_t* __restrict__ out, int64_t rows, int64_t cols,
     int64_t vb, unsigned char* smem) {
   constexpr int LD = kDecodeTLd;
-  float* lut = reinterpret_cast<float*>(smem);
-  half_t* tile = reinterpret_cast<half_t*>(smem + 64);  // [k][n]
-  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
+  const float2* pair = load_pairs(smem);
+  half_t* tile = reinterpret_cast<half_t*>(smem + kPairBytes);  // [k][n]
   __syncthreads();
   const float offset = offset_ptr[0];
   const int64_t ntiles = cdiv(rows, 64);
@@ -118,12 +135,7 @@ __device__ __forceinline__ void decode_t_block(
     const uint32_t words[2] = {w.x, w.y};
 #pragma unroll
     for (int wi = 0; wi < 2; ++wi)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
-        vals[8 * wi + 2 * b] = f32_to_f16(lut[byte >> 4] * scale);
-        vals[8 * wi + 2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
-      }
+      decode_word(pair, words[wi], scale, vals, 8 * wi);
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j) vals[j] = (half_t)0.0f;
@@ -152,9 +164,9 @@ __device__ __forceinline__ void decode_t_block(
 }
 
 constexpr int kDecodeT2Ld = 64 + 8;
-// LDS of the wide transposed decode: the code table, then a [128 k][64 + 8 n]
-// fp16 tile.
-constexpr int kDecodeT2Smem = 64 + 128 * kDecodeT2Ld * 2;
+// LDS of the wide transposed decode: the code-pair table, then a
+// [128 k][64 + 8 n] fp16 tile.
+constexpr int kDecodeT2Smem = kPairBytes + 128 * kDecodeT2Ld * 2;
 
 // Tile vb of the transposed decode with 64 n x 128 k tiles (cols % 128 ==
 // 0): thread (part = tid / 64, row = tid % 64) decodes 32 consecutive columns
@@ -168,9 +180,8 @@ __device__ __forceinline__ void decode_t2_block(
     const float* __restrict__ offset_ptr, half_t* __restrict__ out, int64_t rows, int64_t cols,
     int64_t vb, unsigned char* smem) {
   constexpr int LD = kDecodeT2Ld;
-  float* lut = reinterpret_cast<float*>(smem);
-  half_t* tile = reinterpret_cast<half_t*>(smem + 64);  // [k][n]
-  if (threadIdx.x < 16) lut[threadIdx.x] = kNF4[threadIdx.x];
+  const float2* pair = load_pairs(smem);
+  half_t* tile = reinterpret_cast<half_t*>(smem + kPairBytes);  // [k][n]
   __syncthreads();
   const float offset = offset_ptr[0];
   const int64_t ntiles = cdiv(rows, 64);
@@ -186,12 +197,7 @@ __device__ __forceinline__ void decode_t2_block(
     const float scale = nested_scale(qabs, absmax2, code2, offset, e >> 6);
 #pragma unroll
     for (int wi = 0; wi < 4; ++wi)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (w[wi] >> (8 * b)) & 0xffu;
-        vals[8 * wi + 2 * b] = f32_to_f16(lut[byte >> 4] * scale);
-        vals[8 * wi + 2 * b + 1] = f32_to_f16(lut[byte & 15u] * scale);
-      }
+      decode_word(pair, w[wi], scale, vals, 8 * wi);
   } else {
 #pragma unroll
     for (int j = 0; j < 32; ++j) vals[j] = (half_t)0.0f;

@@ -20,9 +20,11 @@
 // one weight row (TPR = 16 / DPT threads per row): they come with the row's
 // qabs byte and absmax2 entry as plain vector loads into a register ring
 // issued D stages ahead (D >= STAGES, the A tile ring's depth), in the same
-// per-iteration pattern as the A tile DMAs, so one vmcnt wait covers both.  The thread decodes them (16-entry fp32 code table
-// and the 256-entry code2 table in LDS) and writes 2 * DPT fp16 values into
-// a double-buffered B tile with the dense kernel's BK = 32 layout.
+// per-iteration pattern as the A tile DMAs, so one vmcnt wait covers both.
+// The thread decodes them (the 256-entry table of NF4 value pairs, one read
+// per code byte, and the 256-entry code2 table in LDS) and writes 2 * DPT
+// fp16 values into a double-buffered B tile with the dense kernel's BK = 32
+// layout.
 //
 // Loop, iteration kt: read the fragments of stage kt; wait for stage kt + 1;
 // decode stage kt + 1 into the other B tile, its arithmetic interleaved with
@@ -32,6 +34,7 @@
 // and B tile kt % 2); refill the A slot with stage kt + STAGES and the
 // register slot with the codes of stage kt + D.
 
+#include "decode_blocks.h"
 #include "nt_core.h"
 
 namespace ss {
@@ -71,7 +74,7 @@ struct Nf4Layout {
   static constexpr int kTileB = C::BN * 64;
   static constexpr int kOffB = C::STAGES * kTileA;
   static constexpr int kOffLut = kOffB + 2 * kTileB;
-  static constexpr int kOffCode2 = kOffLut + 64;
+  static constexpr int kOffCode2 = kOffLut + kPairBytes;
   static constexpr int kSmem = kOffCode2 + 1024;
   static constexpr int kOps = C::kDmaA + 3;  // vector-memory ops per stage and wave
   static_assert(kSmem <= 160 * 1024, "LDS");
@@ -92,11 +95,10 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
   const int wm = wave / C::kWavesN;
   const int wn = wave % C::kWavesN;
   const Nf4View& w = p.w;
-  float* const lut = reinterpret_cast<float*>(smem + L::kOffLut);
   float* const code2 = reinterpret_cast<float*>(smem + L::kOffCode2);
 
   // Tables first, with tracked loads, before any untracked load is issued.
-  if (tid < 16) lut[tid] = kNF4[tid];
+  const float2* const pair = load_pairs(smem + L::kOffLut);
   for (int i = tid; i < 256; i += C::kThreads) code2[i] = w.code2[i];
   float offset = w.offset[0];
   tie(offset);
@@ -154,11 +156,9 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
       half8 v;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (word >> (8 * b)) & 0xffu;
-        const float hi = lut[byte >> 4] * scale;
-        const float lo = lut[byte & 15u] * scale;
-        v[2 * b] = f32_to_f16(hi);
-        v[2 * b + 1] = f32_to_f16(lo);
+        const float2 pr = pair[(word >> (8 * b)) & 0xffu];
+        v[2 * b] = f32_to_f16(pr.x * scale);
+        v[2 * b + 1] = f32_to_f16(pr.y * scale);
       }
       const int chunk = bpart * (L::DPT / 4) + h;
       *reinterpret_cast<half8*>(bt + ((chunk ^ swz32(brow)) << 4)) = v;
@@ -203,7 +203,7 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
   // Iteration kt; j = kt % kD is a compile-time constant (the register ring
   // is indexed statically).  The decode of stage kt + 1 (after the last
   // stage: of a repeated stage, into the B tile nobody reads) runs as
-  // kSteps micro-steps -- code2 read, per code byte the two table reads, the
+  // kSteps micro-steps -- code2 read, per code byte its pair-table read, the
   // scale, per byte two products and a packed conversion, the tile writes --
   // spread between the MFMAs of stage kt (sched_barrier keeps the order):
   // the two waves of a SIMD leave the barrier together, so a wave must
@@ -232,9 +232,9 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
         c2 = code2[next.q & 0xffu];
       } else if (st <= kBytes) {
         const int b = st - 1;
-        const uint32_t byte = (next.codes[b >> 2] >> (8 * (b & 3))) & 0xffu;
-        tv[2 * b] = lut[byte >> 4];
-        tv[2 * b + 1] = lut[byte & 15u];
+        const float2 pr = pair[(next.codes[b >> 2] >> (8 * (b & 3))) & 0xffu];
+        tv[2 * b] = pr.x;
+        tv[2 * b + 1] = pr.y;
       } else if (st == kBytes + 1) {
         scale = c2 * __builtin_bit_cast(float, next.a2) + offset;
       } else if (st <= 2 * kBytes + 1) {

@@ -59,14 +59,15 @@ __global__ __launch_bounds__(256, 2) void nf4_skinny_fwd_kernel(
   using SlotT = Slot<MT, XLDS>;
   __shared__ __attribute__((aligned(16))) half_t sx[XLDS ? 2 : 1][XLDS ? MT * 16 * kSkPitch : 8];
   __shared__ float s_code2[256];
-  __shared__ float s_lut[16];
+  // Both NF4 values of a code byte in one LDS read: {NF4[e >> 4], NF4[e & 15]}.
+  __shared__ __attribute__((aligned(8))) float2 s_pair[256];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r16 = lane & 15;
   const int g = lane >> 4;
   s_code2[tid] = w.code2[tid];
-  if (tid < 16) s_lut[tid] = kNF4[tid];
+  s_pair[tid] = float2{kNF4[tid >> 4], kNF4[tid & 15]};
   const float offset = w.offset[0];
 
   const int64_t kbeg = (int64_t)blockIdx.y * k_split;
@@ -155,8 +156,9 @@ __global__ __launch_bounds__(256, 2) void nf4_skinny_fwd_kernel(
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const uint32_t byte = (sl.codes[nb][j] >> (8 * b)) & 0xffu;
-          bfrag[nb][j][2 * b] = f32_to_f16(s_lut[byte >> 4] * scale);
-          bfrag[nb][j][2 * b + 1] = f32_to_f16(s_lut[byte & 15u] * scale);
+          const float2 pr = s_pair[byte];
+          bfrag[nb][j][2 * b] = f32_to_f16(pr.x * scale);
+          bfrag[nb][j][2 * b + 1] = f32_to_f16(pr.y * scale);
         }
       }
     }
