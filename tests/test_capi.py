@@ -45,11 +45,14 @@ def test_abi_version(lib):
 
 
 def test_workspace_policy_is_host_only(lib):
-    # Large T: the decoded fp16 W (plus any split-K partials).  Small T: room for the
-    # backward's decoded W^T as well as the forward's split partials.  Pure host arithmetic.
+    # Large T: the decoded fp16 W (plus any split-K partials).  Small and middle T: room
+    # for the backward's decoded W^T as well as the forward's split partials.  Pure host
+    # arithmetic.
     dense = 8960 * 1536 * 2
     assert lib.ss_nf4_gemm_workspace_size(16384, 8960, 1536) >= dense
     assert lib.ss_nf4_gemm_workspace_size(16, 8960, 1536) >= dense
+    assert lib.ss_nf4_gemm_workspace_size(200, 8960, 1536) >= dense
+    assert lib.ss_nf4_gemm_workspace_size(200, 8960, 1536) % 256 == 0
     assert lib.ss_nf4_gemm_workspace_size(16, 8960, 1536) % 256 == 0
     assert lib.ss_nf4_gemm_workspace_size(0, 8960, 1536) == 0
 

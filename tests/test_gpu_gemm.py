@@ -95,6 +95,27 @@ def test_dx_matches_oracle(device, t, n, k):
     check(dx, ogemm.linear_dx(dy, w), f"dx t={t} n={n} k={k}")
 
 
+# With the workspace ss_nf4_gemm_workspace_size reports, dX decodes W^T first
+# at every T above the streaming range; with none (NULL, 0 bytes) it runs the
+# in-loop column decoder.  Both match the oracle, accumulate included.
+@pytest.mark.parametrize("t,n,k", [(200, 512, 1536), (130, 192, 64), (300, 1536, 256)])
+def test_dx_without_workspace(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    dy = x_of(t, n, seed=t + 17)
+    dyt = torch.from_numpy(dy).to(device)
+    base = x_of(t, k, seed=t + 18, scale=0.1)
+    for accumulate in (0, 1):
+        out = torch.from_numpy(base).to(device)
+        _lib.call("ss_nf4_gemm_dx", dyt.data_ptr(), n, t, packed.data_ptr(), qs.absmax.data_ptr(),
+                  qs.state2.absmax.data_ptr(), qs.state2.code.data_ptr(), qs.offset.data_ptr(),
+                  n, k, out.data_ptr(), k, accumulate, None, 0, _lib.stream(device))
+        expected = ogemm.linear_dx(dy, w) + (base.astype(np.float64) if accumulate else 0.0)
+        check(out, expected, f"in-loop dx t={t} accumulate={accumulate}")
+    check(nf4_matmul(dyt, packed, qs, transpose=True), ogemm.linear_dx(dy, w),
+          f"decode-first dx t={t}")
+
+
 # The streaming T <= 16 backward (transposed LDS reads of the codes, block
 # scales folded into dY): ragged T, rows not a multiple of the 64-row unit,
 # one to many row ranges, one column stage (K = 256) to many, N % 16 != 0
