@@ -568,13 +568,17 @@ extern "C" size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k) {
     size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);
     const size_t dx_stream = ss::stream_dx_partial_bytes(t, n, k);
     if (dx_stream > dx) dx = dx_stream;
+    const size_t dx_fused = ss::nf4_dx_fused_partial_bytes(t, k, n);
+    if (dx_fused > dx) dx = dx_fused;
     return fwd > dx ? fwd : dx;
   }
   // Below the threshold the forward may run the fused kernel (its split-K
   // partials); the backward still decodes W^T first: the in-loop column
   // decoder is the fallback without scratch only (measured on MI355X at
   // T = 200, 18944 x 3584: 316 us in-loop against 89 us decode-first).
-  const size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);  // dX [t, k]
+  size_t dx = decoded_bytes(n, k) + ss::nt_partial_bytes(t, k, n);  // dX [t, k]
+  const size_t dx_fused = ss::nf4_dx_fused_partial_bytes(t, k, n);
+  if (dx_fused > dx) dx = dx_fused;
   if (t < threshold) {
     const size_t fwd_fused = ss::nf4_fused_partial_bytes(t, n, k);
     return fwd_fused > dx ? fwd_fused : dx;
@@ -606,6 +610,7 @@ namespace ss {
 static bool stream_enabled() { return SS_TUNE_NF4_STREAM != 0; }
 static bool nf4_fused_enabled() { return SS_TUNE_NF4_FUSED != 0; }
 static bool nf4_fused_forced() { return SS_TUNE_NF4_FUSED == 2; }
+static bool nf4_dx_fused_enabled() { return SS_TUNE_NF4_DX_FUSED != 0; }
 
 // Decode-first path with the decode fused into the preparation launch of the
 // QLoRA step (rank-16 jobs + decode in one launch): T above the skinny range,
@@ -680,12 +685,18 @@ static int run_fwd(GemmParams& p, void* workspace, size_t workspace_bytes, hipSt
 template <int EPI>
 static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                   hipStream_t s, PrepJobs* prep = nullptr, bool vp = false, bool vg = false) {
-  const bool fused = prep && fuse_decode(p, n, k, workspace, workspace_bytes) &&
+  // Above the streaming range and up to two 128-row tiles, the fused dX
+  // decodes each W^T tile into LDS (no decoded weight in HBM); a preparation
+  // launch then carries the rank-16 jobs only.
+  const bool nf4dx = p.M > kStreamDxMaxT && nf4_dx_fused_enabled() && gemm_nf4_dx_ok(p, EPI) &&
+                     gemm_nf4_dx_preferred(p);
+  const bool fused = !nf4dx && prep && fuse_decode(p, n, k, workspace, workspace_bytes) &&
                      reinterpret_cast<uintptr_t>(p.w.packed) % 8 == 0;
   if (prep && !fused) {
     const int r = launch_prep(*prep, vp, vg, s);
     if (r) return r;
   }
+  if (nf4dx) return gemm_nf4_dx(p, EPI, s, workspace, workspace_bytes);
   if (p.M <= kStreamDxMaxT && workspace && stream_enabled()) {
     const int rc = nf4_stream_dx(p, EPI, workspace, workspace_bytes, s);
     if (rc != SS_ERR_UNSUPPORTED) return rc;

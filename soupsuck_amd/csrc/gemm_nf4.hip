@@ -288,6 +288,295 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Transposed variant (dX = dY . Wdec): the B tile of stage kt is W^T rows
+// (dX columns) n0 .. n0 + BN - 1 over the 32 weight rows kbeg + 32 kt .. + 31
+// (the reduction).  The codes of a stage are 32 weight rows x BN / 2 bytes.
+//
+// Loads.  Thread t fetches one 8-byte piece (row t / 8, piece t % 8: 64-byte
+// row pieces per instruction) and each wave the (row, column block) scale
+// inputs of 16 of the stage's 32 x BN / 64 scales, in registers D stages
+// ahead, with the same per-iteration pattern as the A tile DMAs (three
+// vector-memory ops per stage and wave, as in the forward).
+//
+// Code and scale tables.  Two iterations before a stage is decoded its pieces
+// go into an LDS code table (row-major, 8-byte pieces XOR-swizzled by
+// (row >> 1) & 7) and its scales, computed from code2 / absmax2 / offset as
+// in the decoder, into a [BN / 64][32] table; the iteration's barrier
+// publishes both.
+//
+// Decode.  Thread (16-lane group G, lane l) owns column 16 (G % 8) + (l ^ 1)
+// and weight rows 16 (G / 8) .. + 15: one gfx950 ds_read_b64_tr_b4 of the 16
+// rows' 8-byte pieces of its group (lane l points at row 16 (G / 8) + l) gives
+// eight bytes, byte j holding rows 2j (low nibble) and 2j + 1 (high nibble) of
+// that column (the layout the streaming backward measured).  A 256-entry LDS
+// table maps a byte to {NF4[low], NF4[high]}; each value times its row's
+// scale rounds to fp16 exactly as the stand-alone transposed decoder does, and
+// the 16 values leave as two 16-byte chunks of the column's B tile row.  The
+// B tiles therefore hold the decoder's W^T bits and the MFMA sequence is the
+// dense kernel's: the result equals decode-first with the same tile plan.
+typedef int nf4t_v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) nf4t_v2i nf4t_lds_v2i;
+
+template <class C>
+struct Nf4tLayout {
+  static_assert(C::BK == 32, "fused NF4 stages are 32 k deep");
+  static constexpr int kCodeRow = C::BN / 2;  // code bytes per weight row and stage
+  static_assert(C::kThreads == 2 * C::BN && 32 * (kCodeRow / 8) == C::kThreads,
+                "one (column, 16-row) unit and one 8-byte code piece per thread and stage");
+  static_assert(C::kThreads / kWave * 16 == 32 * (C::BN / 64), "16 scales per wave and stage");
+  static constexpr int kTileA = C::BM * 64;
+  static constexpr int kTileB = C::BN * 64;
+  static constexpr int kCodeBytes = 32 * kCodeRow;
+  static constexpr int kScaleBytes = C::BN / 64 * 32 * 4;
+  static constexpr int kOffB = C::STAGES * kTileA;
+  static constexpr int kOffCodes = kOffB + 2 * kTileB;
+  static constexpr int kOffScale = kOffCodes + 2 * kCodeBytes;
+  static constexpr int kOffLut = kOffScale + 2 * kScaleBytes;
+  static constexpr int kOffCode2 = kOffLut + kPairBytes;
+  static constexpr int kSmem = kOffCode2 + 1024;
+  static constexpr int kOps = C::kDmaA + 3;  // vector-memory ops per stage and wave
+  static_assert(kSmem <= 160 * 1024, "LDS");
+};
+
+template <class C, int CD>
+__device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
+                                              int64_t kbeg, int64_t klen, unsigned char* smem,
+                                              NtAcc<C>& acc) {
+  using L = Nf4tLayout<C>;
+  constexpr int kS = C::STAGES;
+  constexpr int kD = CD;  // load ring depth (stages in flight)
+  static_assert(kD >= kS + 2 && kD % kS == 0, "ring depth");
+  constexpr int kGroupBytes = 32 * 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm = wave / C::kWavesN;
+  const int wn = wave % C::kWavesN;
+  const Nf4View& w = p.w;
+  const int64_t kb = p.N >> 1;  // code bytes per weight row
+  const int64_t kq = p.N >> 6;  // scale blocks per weight row
+  float2* const pair = reinterpret_cast<float2*>(smem + L::kOffLut);
+  float* const code2 = reinterpret_cast<float*>(smem + L::kOffCode2);
+
+  // Tables first, with tracked loads, before any untracked load is issued:
+  // pair[e] = {NF4[e & 15], NF4[e >> 4]} (low nibble = the lower row).
+  for (int i = tid; i < 256; i += C::kThreads) pair[i] = float2{kNF4[i & 15], kNF4[i >> 4]};
+  for (int i = tid; i < 256; i += C::kThreads) code2[i] = w.code2[i];
+  float offset = w.offset[0];
+  tie(offset);
+  __syncthreads();
+
+  // A tile DMA sources (rows past M clamped; never stored).
+  const uint32_t lds0 = lds_address(smem);
+  const half_t* a_base = p.A + kbeg;
+  uint32_t a_off[C::kDmaA];
+#pragma unroll
+  for (int j = 0; j < C::kDmaA; ++j) {
+    int row, chunk;
+    dma_source<32>(wave * C::kDmaA + j, lane, row, chunk);
+    const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
+    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
+  }
+  const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
+
+  // This thread's code piece and scale input (offsets from the stage-0 base;
+  // each stage adds 32 weight rows).
+  const int crow = tid >> 3, cpiece = tid & 7;
+  const uint32_t code_off = (uint32_t)((kbeg + crow) * kb + (n0 >> 1) + 8 * cpiece);
+  const int sidx = 16 * wave + (lane & 15);
+  const int srow = sidx & 31, sblk = sidx >> 5;
+  const int64_t sblock0 = (kbeg + srow) * kq + (n0 >> 6) + sblk;
+  const int64_t stage_rows = 32;
+
+  auto issue_a = [&](int64_t kt, int slot_a) {
+#pragma unroll
+    for (int j = 0; j < C::kDmaA; ++j)
+      dma16(a_off[j], a_base + kt * 32, lds_a + slot_a * L::kTileA + j * 1024);
+  };
+  auto issue_c = [&](int64_t kt, Nf4Slot& sl) {
+    sl.codes = vload8_off(code_off, w.packed + kt * stage_rows * kb);
+    sl.q = vload1_off((uint32_t)sblock0, w.qabs + kt * stage_rows * kq);
+    sl.a2 = vload4_off((uint32_t)(((sblock0 + kt * stage_rows * kq) >> 8) * 4), w.absmax2);
+  };
+  // Stage data of `sl` into code / scale table `buf`.
+  auto publish = [&](Nf4Slot& sl, int buf) {
+    tie(sl.codes);
+    tie(sl.q);
+    tie(sl.a2);
+    unsigned char* const ct = smem + L::kOffCodes + buf * L::kCodeBytes;
+    *reinterpret_cast<u32x2*>(ct + crow * L::kCodeRow + 8 * (cpiece ^ ((crow >> 1) & 7))) =
+        sl.codes;
+    if (lane < 16) {
+      float* const st = reinterpret_cast<float*>(smem + L::kOffScale + buf * L::kScaleBytes);
+      st[sblk * 32 + srow] = code2[sl.q & 0xffu] * __builtin_bit_cast(float, sl.a2) + offset;
+    }
+  };
+
+  // Decode unit of this thread: column dcol of the tile, rows 16 drh .. + 15.
+  const int dgroup = tid >> 4, dl = tid & 15;
+  const int drh = dgroup >> 3, dcb = dgroup & 7;
+  const int dcol = 16 * dcb + (dl ^ 1);
+  const int drow = 16 * drh + dl;  // the row this lane points the transposed read at
+  const int dpiece_off = drow * L::kCodeRow + 8 * (dcb ^ ((drow >> 1) & 7));
+  const int dscale_off = ((dcol >> 6) * 32 + 16 * drh) * 4;
+  const int dtile_off = dcol * 64;
+
+  int frag_off[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) frag_off[kk] = frag_offset<32>(lane, kk);
+  auto read_frags = [&](int slot_a, int buf, int kk, half8 (&af)[C::FM], half8 (&bf)[C::FN]) {
+    const unsigned char* sa =
+        smem + slot_a * L::kTileA + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
+    const unsigned char* sb =
+        smem + L::kOffB + buf * L::kTileB + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+  };
+
+  // Decode of one stage (code / scale table `buf`) into B tile `bbuf`, as
+  // kSteps micro-steps: the transposed read, the 16 scales, per code byte its
+  // pair lookup, per byte the two products and a packed conversion, the two
+  // chunk writes.
+  constexpr int kSteps = 2 + 8 + 8 + 2;
+  nf4t_v2i cw;
+  float sc[16];
+  float tv[16];
+  half8 outv[2];
+  auto micro = [&](int st, int buf, int bbuf) {
+    if (st == 0) {
+      cw = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+          (nf4t_lds_v2i*)(smem + L::kOffCodes + buf * L::kCodeBytes + dpiece_off));
+    } else if (st == 1) {
+      const float4v* sp = reinterpret_cast<const float4v*>(smem + L::kOffScale +
+                                                           buf * L::kScaleBytes + dscale_off);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4v v = sp[q];
+        sc[4 * q] = v[0];
+        sc[4 * q + 1] = v[1];
+        sc[4 * q + 2] = v[2];
+        sc[4 * q + 3] = v[3];
+      }
+    } else if (st < 10) {
+      const int j = st - 2;
+      const float2 pr = pair[((uint32_t)cw[j >> 2] >> (8 * (j & 3))) & 0xffu];
+      tv[2 * j] = pr.x;
+      tv[2 * j + 1] = pr.y;
+    } else if (st < 18) {
+      const int j = st - 10;
+      outv[j >> 2][2 * (j & 3)] = f32_to_f16(tv[2 * j] * sc[2 * j]);
+      outv[j >> 2][2 * (j & 3) + 1] = f32_to_f16(tv[2 * j + 1] * sc[2 * j + 1]);
+    } else {
+      const int h = st - 18;
+      unsigned char* const bt = smem + L::kOffB + bbuf * L::kTileB + dtile_off;
+      *reinterpret_cast<half8*>(bt + (((2 * drh + h) ^ swz32(dcol)) << 4)) = outv[h];
+    }
+  };
+
+  // Every iteration issues the A tile of stage kt + kS and the loads of stage
+  // kt + kD (past the end: the last stage again, into slots nobody reads), as
+  // in the forward; the prologue is kD virtual iterations -kD .. -1.
+  const int64_t ktiles = klen / 32;
+  auto clampk = [&](int64_t kt) { return kt < ktiles ? kt : ktiles - 1; };
+  Nf4Slot ring[kD];
+#pragma unroll
+  for (int v = -kD; v < 0; ++v) {
+    if (v + kS >= 0) issue_a(clampk(v + kS), v + kS);
+    issue_c(clampk(v + kD), ring[v + kD]);
+  }
+  // A tile 0 was followed by the loads of one virtual iteration and kS - 1
+  // whole virtual iterations; the loads of stages 0 and 1 came before it.
+  wait_vm<3 + (kS - 1) * L::kOps>();
+  publish(ring[0], 0);
+  publish(ring[1], 1);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) micro(st, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+
+  // Iteration kt (j = kt % kD, a compile-time constant): stage kt + 2's loads
+  // into table kt % 2, the decode of stage kt + 1 (table (kt + 1) % 2) into B
+  // tile (kt + 1) % 2 between the MFMAs of stage kt, one barrier, then the
+  // next loads.
+  constexpr int kMfma = 2 * C::FM * C::FN;
+  auto iteration = [&](int64_t kt, int j) {
+    const int sa = j % kS;
+    half8 fa[2][C::FM], fb[2][C::FN];
+    read_frags(sa, (int)(kt & 1), 0, fa[0], fb[0]);
+    read_frags(sa, (int)(kt & 1), 1, fa[1], fb[1]);
+    // Stage kt + 1's A tile was followed by one iteration's loads and kS - 2
+    // whole iterations; stage kt + 2's loads were issued before it.
+    wait_vm<3 + (kS - 2) * L::kOps>();
+    publish(ring[(j + 2) % kD], (int)(kt & 1));
+    const int buf = (int)((kt + 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < kMfma; ++m) {
+      const int kk = m / (C::FM * C::FN);
+      const int i = (m / C::FN) % C::FM;
+      const int jj = m % C::FN;
+      acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk][i], fb[kk][jj], acc[i][jj], 0,
+                                                          0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int st = m * kSteps / kMfma; st < (m + 1) * kSteps / kMfma; ++st) micro(st, buf, buf);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    issue_a(clampk(kt + kS), sa);
+    issue_c(clampk(kt + kD), ring[j]);
+  };
+
+  for (int64_t kt0 = 0; kt0 < ktiles; kt0 += kD) {
+#pragma unroll
+    for (int j = 0; j < kD; ++j) {
+      if (kt0 + j >= ktiles) break;
+      iteration(kt0 + j, j);
+    }
+  }
+  // As in the forward: the ring registers stay allocated until every load
+  // issued into them has retired.
+  wait_vm<0>();
+#pragma unroll
+  for (int s2 = 0; s2 < kD; ++s2) {
+    tie(ring[s2].codes);
+    tie(ring[s2].q);
+    tie(ring[s2].a2);
+  }
+}
+
+template <class C, int CD, int CT, int EPI>
+__global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4t_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4tLayout<C>::kSmem];
+  const int64_t tiles = gridDim.x;
+  int64_t tile, split = 0;
+  if constexpr (EPI == EPI_PARTIAL)
+    split_tile(p.remap, tiles, tile, split);
+  else
+    tile = p.remap ? xcd_remap(blockIdx.x, tiles) : (int64_t)blockIdx.x;
+  int64_t m0, n0;
+  tile_origin<C>(p, tile, m0, n0);
+  int64_t kbeg = 0, klen = p.K;
+  if constexpr (EPI == EPI_PARTIAL) {
+    kbeg = split * p.k_split;
+    klen = p.K - kbeg < p.k_split ? p.K - kbeg : p.k_split;
+  }
+  NtAcc<C> acc;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
+  nf4t_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
+  static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= Nf4tLayout<C>::kSmem, "stage");
+  nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem, split);
+}
+
 template <class C, int CD, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4Layout<C>::kSmem];
@@ -335,6 +624,18 @@ int dispatch_nf4(const GemmParams& p, int cfg, int64_t splits, hipStream_t strea
     case 2: return launch_nf4<Nf4Mid, 12, CT, EPI>(p, splits, stream);
     default: return launch_nf4<Nf4Small, 12, CT, EPI>(p, splits, stream);
   }
+}
+
+using Nf4tMid = Nf4Mid;  // 128x128, 4 waves: one decode unit per thread
+constexpr int kNf4tRing = 8;
+
+template <int CT, int EPI>
+int dispatch_nf4t(const GemmParams& p, int64_t splits, hipStream_t stream) {
+  const dim3 grid((unsigned)(cdiv(p.M, Nf4tMid::BM) * cdiv(p.N, Nf4tMid::BN)), (unsigned)splits);
+  hipLaunchKernelGGL((gemm_nf4t_kernel<Nf4tMid, kNf4tRing, CT, EPI>), grid,
+                     dim3(Nf4tMid::kThreads), 0, stream, p);
+  SS_CHECK_LAUNCH("gemm_nf4t_kernel");
+  return SS_OK;
 }
 
 }  // namespace
@@ -423,6 +724,89 @@ int gemm_nf4_fwd(const GemmParams& p0, int epi, hipStream_t stream, void* partia
     return rc;
   }
   return dispatch_nf4<SS_F16, EPI_PLAIN>(p, plan.cfg, 1, stream);
+}
+
+// Fused dX (dY . Wdec, the weight decoded into the B tiles): 128x128 tiles,
+// split over the weight rows until about 512 workgroups run, each split at
+// least 512 rows deep.  For T up to two 128-row tiles, where each W^T tile is
+// decoded once or twice instead of being written to HBM and read back.
+static NtPlan nf4t_plan(int64_t m, int64_t n, int64_t k) {
+  NtPlan plan{2, 1, k};
+  const int64_t tiles = cdiv(m, 128) * cdiv(n, 128);
+  int64_t s = 512 / tiles;
+  if (s > k / 512) s = k / 512;
+  if (s < 1) s = 1;
+  plan.k_split = cdiv(cdiv(k, s), 64) * 64;
+  plan.splits = cdiv(k, plan.k_split);
+  return plan;
+}
+
+bool gemm_nf4_dx_ok(const GemmParams& p, int epi) {
+  // p.M = T, p.N = weight columns (dX columns), p.K = weight rows.
+  if (p.M <= 0 || p.M > 256 || p.N <= 0 || p.N % 128 != 0 || p.K <= 0 || p.K % 64 != 0)
+    return false;
+  if (reinterpret_cast<uintptr_t>(p.A) % 16 != 0 || p.lda % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(p.w.packed) % 8 != 0)
+    return false;
+  // 32-bit offsets: A rows (DMA), code bytes and qabs from their bases.
+  const int64_t kMaxOff = (int64_t)1 << 32;
+  if (((p.M - 1) * p.lda + p.K) * 2 >= kMaxOff || p.K * (p.N / 2) >= kMaxOff) return false;
+  if (epi != EPI_PLAIN && epi != EPI_RANK) return false;
+  if (epi == EPI_RANK && reinterpret_cast<uintptr_t>(p.lz) % 16 != 0) return false;
+  return true;
+}
+
+// Measured on MI355X (HIP graph, weights rotated through HBM): with 128 or
+// more workgroups in its plan the fused dX is 1.2-2x ahead of decode-first
+// (7B gate 18944 x 3584 at T = 128: 45.7 vs 75.6 us; q/o 3584 x 3584 at
+// T = 32: 18.3 vs 36.3 us); with fewer (7B k/v 512 x 3584: 28 tiles and no
+// split) it is behind (12.9 vs 11.6 us).
+bool gemm_nf4_dx_preferred(const GemmParams& p) {
+  const NtPlan plan = nf4t_plan(p.M, p.N, p.K);
+  return cdiv(p.M, 128) * cdiv(p.N, 128) * plan.splits >= 128;
+}
+
+size_t nf4_dx_fused_partial_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || m > 256 || n <= 0 || k <= 0 || k % 64 != 0) return 0;
+  const NtPlan plan = nf4t_plan(m, n, k);
+  return plan.splits > 1 ? (size_t)(plan.splits * m * n) * sizeof(float) : 0;
+}
+
+int gemm_nf4_dx(const GemmParams& p0, int epi, hipStream_t stream, void* partials,
+                size_t partial_bytes) {
+  if (!gemm_nf4_dx_ok(p0, epi)) return SS_ERR_UNSUPPORTED;
+  // Only the plain and rank-16 epilogues: a caller's SwiGLU epilogue and
+  // rank-16 grad tails stay unrun (glu_done / tail_ran untouched), so the
+  // caller runs them after the product, as after any path without them.
+  GemmParams p = p0;
+  p.glu = 0;
+  p.tail_blocks = p.tail2_blocks = 0;
+  p.c_vec = staged_epilogue_enabled() && !p.beta && p.N % 8 == 0 && p.ldc % 8 == 0 &&
+            reinterpret_cast<uintptr_t>(p.C) % 16 == 0;
+  NtPlan plan = nf4t_plan(p.M, p.N, p.K);
+  const size_t need = (size_t)(plan.splits * p.M * p.N) * sizeof(float);
+  if (plan.splits > 1 && (!partials || partial_bytes < need ||
+                          reinterpret_cast<uintptr_t>(partials) % 16 != 0)) {
+    plan.splits = 1;
+    plan.k_split = p.K;
+  }
+  if (plan.splits > 1) {
+    p.part = reinterpret_cast<float*>(partials);
+    p.k_split = plan.k_split;
+    // As the dense dX: split 0 adds the rank-16 update to its partial and the
+    // reduce only sums.
+    p.fold_rank = epi == EPI_RANK;
+    p.lora_plane = nullptr;
+    const int rc = dispatch_nf4t<SS_F32, EPI_PARTIAL>(p, plan.splits, stream);
+    if (rc) return rc;
+    if (epi == EPI_RANK) {
+      p.alpha = 1.0f;
+      p.bias = nullptr;
+    }
+    return splitk_reduce(p, (int)plan.splits, SS_F16, EPI_PLAIN, stream);
+  }
+  if (epi == EPI_RANK) return dispatch_nf4t<SS_F16, EPI_RANK>(p, 1, stream);
+  return dispatch_nf4t<SS_F16, EPI_PLAIN>(p, 1, stream);
 }
 
 }  // namespace ss

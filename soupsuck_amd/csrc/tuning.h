@@ -32,6 +32,10 @@
 #ifndef SS_TUNE_NF4_FUSED
 #define SS_TUNE_NF4_FUSED 1
 #endif
+// Fused NF4 dX for 16 < T <= 256 (1 on, 0 off: decode-first there).
+#ifndef SS_TUNE_NF4_DX_FUSED
+#define SS_TUNE_NF4_DX_FUSED 1
+#endif
 // NT kernel configuration (0 automatic, 1..10) and split count (0 automatic).
 #ifndef SS_TUNE_NT_TILE
 #define SS_TUNE_NT_TILE 0

@@ -95,10 +95,12 @@ def test_dx_matches_oracle(device, t, n, k):
     check(dx, ogemm.linear_dx(dy, w), f"dx t={t} n={n} k={k}")
 
 
-# With the workspace ss_nf4_gemm_workspace_size reports, dX decodes W^T first
-# at every T above the streaming range; with none (NULL, 0 bytes) it runs the
-# in-loop column decoder.  Both match the oracle, accumulate included.
-@pytest.mark.parametrize("t,n,k", [(200, 512, 1536), (130, 192, 64), (300, 1536, 256)])
+# Without scratch (NULL, 0 bytes) dX runs the fused kernel unsplit where it is
+# taken (T = 200, 8960 dX columns) and the in-loop column decoder elsewhere;
+# with the reported workspace it splits or decodes W^T first.  All match the
+# oracle, accumulate included.
+@pytest.mark.parametrize("t,n,k", [(200, 512, 1536), (200, 512, 8960), (130, 192, 64),
+                                   (300, 1536, 256)])
 def test_dx_without_workspace(device, t, n, k):
     state, w = weight(n, k)
     packed, qs = device_state(state, device)
@@ -114,6 +116,28 @@ def test_dx_without_workspace(device, t, n, k):
         check(out, expected, f"in-loop dx t={t} accumulate={accumulate}")
     check(nf4_matmul(dyt, packed, qs, transpose=True), ogemm.linear_dx(dy, w),
           f"decode-first dx t={t}")
+
+
+# Fused dX for 16 < T <= 256 with dX columns % 128 == 0 and 128 or more
+# workgroups: W^T tiles decoded into LDS inside the GEMM (transposed 4-bit LDS
+# reads, one scale per weight row and block), one or two 128-row tiles, ragged
+# T, unsplit (a 512-row reduction) and split over the weight rows,
+# accumulation.  Its rank-16 epilogue runs in the QLoRA projection tests.
+@pytest.mark.parametrize("t,n,k", [(17, 8960, 1536), (64, 1536, 8960), (128, 8960, 1536),
+                                   (130, 1536, 8960), (200, 512, 8960), (200, 3584, 3584),
+                                   (256, 18944, 512)])
+def test_fused_dx(device, t, n, k):
+    state, w = weight(n, k)
+    packed, qs = device_state(state, device)
+    dy = x_of(t, n, seed=11 * t + n)
+    dyt = torch.from_numpy(dy).to(device)
+    dx = nf4_matmul(dyt, packed, qs, transpose=True)
+    check(dx, ogemm.linear_dx(dy, w), f"fused dx t={t} n={n} k={k}")
+    assert torch.equal(dx, nf4_matmul(dyt, packed, qs, transpose=True)), "fused dx not deterministic"
+    base = x_of(t, k, seed=t + 5, scale=0.1)
+    out = torch.from_numpy(base).to(device)
+    nf4_dx_2d(dyt, packed, qs, n, k, out=out, accumulate=True)
+    check(out, ogemm.linear_dx(dy, w) + base.astype(np.float64), f"fused dx accumulate t={t}")
 
 
 # The streaming T <= 16 backward (transposed LDS reads of the codes, block

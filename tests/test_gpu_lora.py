@@ -49,6 +49,7 @@ def test_epilogue_rounded_product_cancels(device):
 
 
 @pytest.mark.parametrize("t,n,k,bias", [(96, 256, 1536, True), (200, 1536, 1536, False),
+                                        (200, 512, 8960, False),
                                         (37, 8960, 1536, False), (64, 1536, 8960, False),
                                         (300, 256, 1536, True), (990, 8960, 1536, False),
                                         (990, 1536, 8960, False), (2048, 8960, 256, True),
