@@ -1,6 +1,6 @@
 """Compiled-code check (CPU): no register of an in-flight inline-asm load is reused.
 
-The fused NF4 GEMM and the streaming kernels issue vector loads from inline
+The fused NF4 GEMMs (forward and dX) and the streaming kernels issue vector loads from inline
 asm, which the compiler does not track: it takes their destination registers
 as written at the asm statement.  A load whose result is never consumed is
 then dead to the compiler, which may hand its registers to other values while
@@ -79,6 +79,7 @@ def inflight_hazards(asm, name):
 
 
 @pytest.mark.parametrize("source,kernel", [("gemm_nf4.hip", "gemm_nf4_kernel"),
+                                           ("gemm_nf4.hip", "gemm_nf4t_kernel"),
                                            ("nf4_stream.hip", "nf4_stream_fwd_kernel"),
                                            ("nf4_stream_dx.hip", "nf4_stream_dx_kernel")])
 def test_no_register_reuse_under_inflight_asm_loads(tmp_path, source, kernel):
