@@ -23,9 +23,17 @@ Numerics follow the reference's node (bnb fp16 projections, the fp32 SwiGLU
 tile engine of solution/kernels/swiglu_fused.py): every projection output is
 rounded to fp16 before the activation reads it.  One difference: the two
 input-gradient products are summed as fp16(fp16(dgate Wg) + fp32(dup Wu))
-instead of two fp16 results added in fp16 (one rounding fewer).  The
-reference's pinned-host offload pools (solution/mlp.py:105-359) are a memory
-policy outside this path; ``offload`` is accepted and ignored.
+instead of two fp16 results added in fp16 (one rounding fewer).
+
+``offload=True`` keeps the saved gate and up in pinned host memory instead of
+HBM (the reference's pinned-host offload, solution/mlp.py:105-359): the
+device-to-host copies run on a copy stream of default priority after the
+producing stream, the backward copies them back on its own stream after that
+copy has finished, and the pinned buffers return to a per-shape free list once
+the copy back has completed.  The default is off (``SOUP_MLP_OFFLOAD=1`` turns it
+on; the reference defaults to on): with 288 GB of HBM per MI355X the activations
+fit, and the round trip costs PCIe time.  Recomputation excludes offload, as in
+the reference.  Offload is refused under HIP graph capture.
 """
 
 import os
@@ -156,16 +164,82 @@ def mlp_backward_2d(grad2d, parts, gate, up, fuse=None):
     return dx
 
 
+_COPY_STREAMS = {}  # device index -> copy stream (default priority)
+_HOST_FREE = {}     # (device index, rows, width) -> free pinned (gate, up) pairs
+_HOST_PENDING = []  # (event, key, pair): pairs whose copy back may still run
+
+
+def _copy_stream(device):
+    stream = _COPY_STREAMS.get(device.index)
+    if stream is None:
+        stream = _COPY_STREAMS[device.index] = torch.cuda.Stream(device=device)
+    return stream
+
+
+def _host_pair(key):
+    still = []
+    for event, k, pair in _HOST_PENDING:
+        if event.query():
+            _HOST_FREE.setdefault(k, []).append(pair)
+        else:
+            still.append((event, k, pair))
+    _HOST_PENDING[:] = still
+    free = _HOST_FREE.setdefault(key, [])
+    if free:
+        return free.pop()
+    shape = key[1:]
+    return (torch.empty(shape, dtype=torch.float16, pin_memory=True),
+            torch.empty(shape, dtype=torch.float16, pin_memory=True))
+
+
+class HostOffload:
+    """gate and up of one MLP node held in pinned host memory until its backward."""
+
+    def __init__(self, gate, up):
+        device = gate.device
+        self.device = device
+        self.key = (device.index, gate.shape[0], gate.shape[1])
+        self.pair = _host_pair(self.key)
+        producer = torch.cuda.current_stream(device)
+        copy = _copy_stream(device)
+        copy.wait_stream(producer)
+        with torch.cuda.stream(copy):
+            self.pair[0].copy_(gate, non_blocking=True)
+            self.pair[1].copy_(up, non_blocking=True)
+            self.stored = torch.cuda.Event()
+            self.stored.record(copy)
+        # The device tensors may be freed by the caller now: keep their memory
+        # from being reused before the copy stream has read them.
+        gate.record_stream(copy)
+        up.record_stream(copy)
+
+    def restore(self):
+        """(gate, up) back on the device, ordered on the current stream."""
+        stream = torch.cuda.current_stream(self.device)
+        stream.wait_event(self.stored)
+        gate = self.pair[0].to(self.device, non_blocking=True)
+        up = self.pair[1].to(self.device, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(stream)
+        _HOST_PENDING.append((done, self.key, self.pair))
+        self.pair = None
+        return gate, up
+
+
 class _FrozenMLP(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, mlp, recompute):
+    def forward(ctx, x, mlp, recompute, offload=False):
         parts = _projections(mlp)
         shape = x.shape
         x2d = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
         out, gate, up = mlp_forward_2d(x2d, parts, keep=not recompute)
         ctx.mlp, ctx.recompute, ctx.input_dtype, ctx.shape = mlp, recompute, x.dtype, shape
+        ctx.offloaded = None
         if recompute:
             ctx.save_for_backward(x2d)
+        elif offload:
+            ctx.offloaded = HostOffload(gate, up)
+            ctx.save_for_backward()
         else:
             ctx.save_for_backward(gate, up)
         return out.reshape(*shape[:-1], out.shape[-1]).to(x.dtype)
@@ -181,26 +255,34 @@ class _FrozenMLP(torch.autograd.Function):
             (x2d,) = ctx.saved_tensors
             gate = nf4_forward_2d(x2d, *parts[0])
             up = nf4_forward_2d(x2d, *parts[1])
+        elif ctx.offloaded is not None:
+            gate, up = ctx.offloaded.restore()
+            ctx.offloaded = None
         else:
             gate, up = ctx.saved_tensors
         dx = mlp_backward_2d(grad2d, parts, gate, up)
-        return dx.reshape(ctx.shape).to(ctx.input_dtype), None, None
+        return dx.reshape(ctx.shape).to(ctx.input_dtype), None, None, None
 
 
 def fused_qwen2_mlp(mlp, x, recompute=None, offload=None):
-    """Run an eligible frozen NF4 MLP; raise ValueError otherwise (solution/mlp.py:579-594)."""
-    del offload  # pinned-host offload is a memory policy outside this path
+    """Run an eligible frozen NF4 MLP; raise ValueError otherwise (solution/mlp.py:579-612)."""
     if not eligible_mlp(mlp, x):
         raise ValueError("Expected frozen bias-free fp16 NF4 Linear4bit projections on CUDA")
     if recompute is None:
         recompute = os.environ.get("SOUP_MLP_RECOMPUTE") == "1"
+    if offload is None:
+        offload = os.environ.get("SOUP_MLP_OFFLOAD") == "1"
+    offload = bool(offload) and not recompute
+    if offload and torch.cuda.is_current_stream_capturing():
+        raise ValueError("MLP activation offload cannot be captured in a HIP graph; "
+                         "pass offload=False (or unset SOUP_MLP_OFFLOAD) for graph capture")
     with torch.cuda.device(x.device):
         if not torch.is_grad_enabled() or not x.requires_grad:
             shape = x.shape
             x2d = x.reshape(-1, shape[-1]).to(torch.float16).contiguous()
             out, _, _ = mlp_forward_2d(x2d, _projections(mlp), keep=False)
             return out.reshape(*shape[:-1], out.shape[-1]).to(x.dtype)
-        return _FrozenMLP.apply(x, mlp, bool(recompute))
+        return _FrozenMLP.apply(x, mlp, bool(recompute), offload)
 
 
 def patch_qwen2_mlp_fused(module=None):
@@ -216,4 +298,4 @@ def mlp_flops(t, hidden, inter):
 
 
 __all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "eligible_mlp", "gate_up_swiglu", "down_dx_swiglu",
-           "mlp_forward_2d", "mlp_backward_2d", "mlp_flops"]
+           "mlp_forward_2d", "mlp_backward_2d", "mlp_flops", "HostOffload"]

@@ -115,6 +115,41 @@ def test_fused_mlp_matches_fp32_module(device, monkeypatch, epilogue, recompute,
     assert rel.item() <= 1e-2
 
 
+def test_offload_keeps_gate_up_on_host_and_matches_bitwise(device):
+    """offload=True: the saved gate / up live in pinned host memory between
+    forward and backward (no device tensors saved), the gradient equals the
+    on-device node's bit for bit, and a second step reuses the pinned pair."""
+    from soupsuck_amd import mlp as fmlp
+
+    torch.manual_seed(778)
+    mlp = _MLP(128, 320).to(device)
+    x = torch.randn((3, 77, 128), device=device, dtype=torch.float16)
+    upstream = torch.randn((3, 77, 128), device=device, dtype=torch.float16)
+    grads = []
+    for offload in (False, True, True):
+        xi = x.clone().requires_grad_()
+        out = fused_qwen2_mlp(mlp, xi, recompute=False, offload=offload)
+        node = out.grad_fn
+        if offload:
+            assert len(node.saved_tensors) == 0
+            pair = node.offloaded.pair if hasattr(node, "offloaded") else None
+            assert pair is None or all(t.is_pinned() and not t.is_cuda for t in pair)
+        out.backward(upstream)
+        grads.append((out.detach().clone(), xi.grad.clone()))
+        torch.cuda.synchronize()  # the copy back has finished: its pair is free again
+    for out, grad in grads[1:]:
+        assert torch.equal(_bits(out), _bits(grads[0][0]))
+        assert torch.equal(_bits(grad), _bits(grads[0][1]))
+    # The second offloaded step took the pair the first one returned.
+    key = (device.index if device.index is not None else torch.cuda.current_device(), 231, 320)
+    pooled = len(fmlp._HOST_FREE.get(key, [])) + sum(1 for _, k, _ in fmlp._HOST_PENDING
+                                                     if k == key)
+    assert pooled == 1
+    # Recomputation excludes offload.
+    out = fused_qwen2_mlp(mlp, x.clone().requires_grad_(), recompute=True, offload=True)
+    assert out.grad_fn.offloaded is None
+
+
 def test_rejects_ineligible_modules(device):
     mlp = _MLP(128, 320).to(device)
     mlp.down_proj = torch.nn.Linear(320, 128, bias=False).to(device).half()
