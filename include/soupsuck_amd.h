@@ -122,8 +122,11 @@ int ss_nf4_quantize(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint
                     float* absmax2, const float* code2, float* offset, float* absmax_workspace,
                     void* stream);
 
-/* Workspace bytes the NF4 GEMM entry points (plain and LoRA-fused) need for
- * this shape (0 when the fused decode-in-GEMM path is used). */
+/* Workspace bytes the NF4 GEMM entry points (forward, dX, LoRA-fused) use
+ * for this shape: split-K partial planes of the small-T and fused
+ * decode-in-GEMM kernels, or the decoded weight (W, or W^T for dX) plus the
+ * dense GEMM's partials.  A smaller workspace (or NULL) selects a path that
+ * fits. */
 size_t ss_nf4_gemm_workspace_size(int64_t t, int64_t n, int64_t k);
 
 /* A7+A10+A11 fused: the QLoRA projection forward of one Linear4bit with its
