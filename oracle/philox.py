@@ -43,8 +43,9 @@ def philox4x32_10(ctr, key):
 
 
 def threshold(p):
-    """floor((1 - p) * 2^32) for p in (0, 1), as the host computes it (double)."""
-    return int(np.floor((1.0 - float(np.float32(p))) * 4294967296.0))
+    """floor((1 - p) * 2^32) for p in (0, 1), as the host computes it (double), saturated at
+    2^32 - 1 (a p below 2^-32 rounds 1 - p to 1)."""
+    return min(int(np.floor((1.0 - float(np.float32(p))) * 4294967296.0)), 0xFFFFFFFF)
 
 
 def inverse_keep(p):

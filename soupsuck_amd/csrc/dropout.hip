@@ -85,7 +85,10 @@ __global__ __launch_bounds__(256) void qlora_dropout_tail_kernel(RankGradArgs da
 DropoutArgs dropout_args(uint64_t seed, float p) {
   DropoutArgs d;
   d.seed = seed;
-  d.thr = (uint32_t)floor((1.0 - (double)p) * 4294967296.0);
+  // keep(e) = word < thr.  For p below 2^-32, (1 - p) * 2^32 rounds to 2^32, which a
+  // uint32 cannot hold: the threshold saturates, so such a p drops with probability 2^-32.
+  const double thr = floor((1.0 - (double)p) * 4294967296.0);
+  d.thr = thr >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)thr;
   d.inv = (float)(1.0 / (1.0 - (double)p));
   d.on = 1;
   return d;

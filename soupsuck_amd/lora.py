@@ -25,7 +25,9 @@ those PEFT's own Dropout would draw from torch's CUDA RNG (same keep
 probability and scaling, fp32(x) * fp32(1 / (1 - p)), as the reference's fp32
 dropout; solution/lora.py:1-40).
 Otherwise each GEMM and the epilogue run as separate kernels (torch's native
-dropout on an fp32 copy of X for p > 0).
+dropout on an fp32 copy of X for p > 0).  That is also the path of an active
+dropout under HIP graph capture, where a seed fixed at capture would give
+every replay the same mask, while torch's generator advances per replay.
 """
 
 import contextlib
@@ -253,8 +255,9 @@ class _QLoRAProjection(torch.autograd.Function):
         result = nf4_forward_2d(x2d, packed, state, n, k, bias=bias)
         mask = None
         if dropout_p > 0.0 and training:
-            dropped = torch.nn.functional.dropout(x2d.float(), dropout_p, True)
-            mask = dropped != 0
+            # torch's own dropout (graph-safe RNG); its mask, not dropped != 0, so a kept
+            # zero of X still passes its gradient
+            dropped, mask = torch.native_dropout(x2d.float(), dropout_p, True)
             x_in = dropped.to(torch.float16)
         else:
             x_in = x2d
@@ -321,7 +324,9 @@ def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, d
     with _on_device(x.device):
         if fused and not active:
             return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling))
-        if fused and x.data_ptr() % 16 == 0:
+        # The fused dropout's seed is a kernel argument: a HIP graph would replay one mask
+        # forever, so under capture the mask comes from torch's graph-safe generator.
+        if fused and x.data_ptr() % 16 == 0 and not torch.cuda.is_current_stream_capturing():
             return _QLoRAFusedDropout.apply(x, lora_a, lora_b, packed, state, bias,
                                             float(scaling), float(dropout_p), dropout_seed())
         return _QLoRAProjection.apply(x, lora_a, lora_b, packed, state, bias, float(scaling),

@@ -25,7 +25,7 @@ from contextvars import ContextVar
 
 import torch
 
-from .utils import enabled
+from .utils import enabled, hookless
 
 QWEN = "transformers.models.qwen2.modeling_qwen2"
 _OWNER = ContextVar("soupsuck_half_norm_owner", default=None)
@@ -42,8 +42,7 @@ def half_norm_scope(norm):
 
 
 def _hookless(m):
-    return not (m._forward_hooks or m._forward_pre_hooks or m._backward_hooks
-                or getattr(m, "_backward_pre_hooks", None) or "forward" in m.__dict__)
+    return hookless(m)
 
 
 def half_norm_enabled(norm):

@@ -32,16 +32,9 @@ import numbers
 import torch
 
 from .utils import enabled
+from .utils import hookless as _hookless
 
 _ALLOWED_KWARGS = ("adapter_names", "alora_offsets")
-
-
-def _hookless(*modules):
-    for m in modules:
-        if (m._forward_hooks or m._forward_pre_hooks or m._backward_hooks
-                or getattr(m, "_backward_pre_hooks", None) or "forward" in m.__dict__):
-            return False
-    return True
 
 
 def _plain_linear(m, device):

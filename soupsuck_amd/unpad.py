@@ -56,6 +56,11 @@ class PackedBatch:
     lengths: tuple
     indices: torch.Tensor
     _inverse: torch.Tensor = field(default=None, repr=False)
+    # set by the Qwen2Model route: int32 row offsets for the attention kernels, the
+    # attention modules that run packed, and the LoRA dropouts bound to this batch
+    cu_seqlens: torch.Tensor = field(default=None, repr=False)
+    attention_ids: frozenset = frozenset()
+    dropout_ids: frozenset = frozenset()
 
     @property
     def tokens(self):

@@ -34,7 +34,7 @@ def _mask(seed, p, rows, cols, device):
 
 
 @pytest.mark.parametrize("rows, cols, p", [(1, 13, 0.05), (37, 100, 0.1), (990, 1536, 0.5),
-                                           (3, 8960, 0.05)])
+                                           (3, 8960, 0.05), (4, 256, 1e-20)])
 def test_mask_matches_oracle(device, rows, cols, p):
     seed = 0x9E3779B97F4A7C15 ^ (rows * 1000003 + cols)
     got = _mask(seed, p, rows, cols, device).cpu().numpy().astype(bool)
@@ -113,3 +113,52 @@ def test_seeds_and_inactive_dropout(device):
     plain = lora.qlora_projection(x, a, b, packed, state, bias, 2.0)
     assert torch.equal(plain, lora.qlora_projection(x, a, b, packed, state, bias, 2.0,
                                                     dropout_p=0.1, training=False))
+
+
+def test_graph_capture_draws_a_fresh_mask_per_replay(device):
+    """An active dropout captured in a HIP graph takes torch's graph-safe generator (a seed
+    fixed at capture would repeat one mask).  A and B select the first 16 columns, so
+    y[:, :16] - base reveals each replay's mask; every replay is checked bit for bit
+    against fp16(base + fp16(fp16(fp32(x) / (1 - p)) * s)) where kept and base elsewhere."""
+    from soupsuck_amd.kernels.nf4_gemm import nf4_forward_2d
+
+    n, k, t, p, s = 256, 512, 96, 0.5, 2.0
+    packed, state, bias, _, _, x, _ = _case(device, n, k, t, seed=7)
+    a = torch.zeros((16, k), device=device, dtype=torch.float16)
+    b = torch.zeros((n, 16), device=device, dtype=torch.float16)
+    a[torch.arange(16), torch.arange(16)] = 1.0
+    b[torch.arange(16), torch.arange(16)] = 1.0
+    base = nf4_forward_2d(x, packed, state, n, k, bias=bias)
+    kept = (x[:, :16].float() * (1.0 / (1.0 - p))).half()
+    on = (base[:, :16].float() + (kept.float() * s).half().float()).half()
+
+    def run():
+        return lora.qlora_projection(x, a, b, packed, state, bias, s, dropout_p=p, training=True)
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.no_grad(), torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    calls = []
+    _lib.hooks["ss_qlora_forward_dropout"] = (lambda name, args: calls.append(name),
+                                              lambda name, args: None)
+    try:
+        with torch.no_grad(), torch.cuda.graph(graph):
+            y = run()
+    finally:
+        _lib.hooks.pop("ss_qlora_forward_dropout", None)
+    assert calls == []                       # the seeded fused kernel stays out of the graph
+    masks = []
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize(device)
+        assert torch.equal(y[:, 16:], base[:, 16:])
+        mask = y[:, :16] != base[:, :16]
+        assert torch.equal(y[:, :16], torch.where(mask, on, base[:, :16]))
+        masks.append(mask.clone())
+        torch.randn(1000, device=device).sum().item()   # eager work between replays
+    assert not torch.equal(masks[0], masks[1]) and not torch.equal(masks[1], masks[2])
+    rate = torch.stack(masks).float().mean().item()
+    assert 0.35 < rate < 0.65

@@ -230,3 +230,131 @@ def test_unpadded_model_matches_padded_eager(device, monkeypatch):
     assert abs(loss.item() - ref_loss.item()) <= 5e-3 * abs(ref_loss.item())
     for got, ref in zip(grads, ref_grads):
         assert _rel(got, ref) < 5e-2
+
+
+class _FixedMask(torch.nn.Module):
+    """A LoRA dropout replaced by a given keep mask: fp(fp32(x) / (1 - p)) where kept."""
+
+    def __init__(self, keep, p):
+        super().__init__()
+        self.keep, self.inv = keep, 1.0 / (1.0 - p)
+
+    def forward(self, x):
+        return torch.where(self.keep, (x.float() * self.inv).to(x.dtype), torch.zeros_like(x))
+
+
+def test_unpadded_model_packs_under_lora_dropout(device, monkeypatch):
+    """The task's LoRA dropout (p = 0.05 on q / v, fp32 adapters, fp16 autocast, training) keeps
+    the packed path on (reference solution/unpad.py:207-273): the right-padded batch is
+    gathered, attention runs on the packed rows and the q / v projections take the fused
+    Philox dropout.  Against the original padded forward with the same keep masks
+    (ss_dropout_mask of each call's seed, scattered to the padded layout): loss within
+    5e-3 relative, gradients within relative L2 5e-2 (the bars of the dropout-free test)."""
+    from transformers import Qwen2Config
+    from transformers.models.qwen2 import modeling_qwen2 as qwen
+
+    from soupsuck_amd import unpad_route
+
+    peft = _fake_peft_module()
+    for route in (patch.MODEL_ROUTE, patch.ATTENTION_ROUTE, patch.HEAD_ROUTE):
+        assert patch.install_route(route, qwen)
+    assert patch.install_route(patch.PEFT_ROUTE, peft)
+    cfg = Qwen2Config(hidden_size=256, intermediate_size=512, num_attention_heads=2,
+                      num_key_value_heads=1, num_hidden_layers=2, vocab_size=1000,
+                      use_cache=False, attn_implementation="sdpa")
+    torch.manual_seed(6)
+    model = qwen.Qwen2ForCausalLM(cfg).to(device=device, dtype=torch.float16)
+    p = 0.05
+    adapters = []
+    for layer in model.model.layers:
+        for name in ("q_proj", "v_proj"):
+            old = getattr(layer.self_attn, name)
+            base = Linear4bit(old.in_features, old.out_features, bias=True,
+                              compute_dtype=torch.float16)
+            with torch.no_grad():
+                base.weight.data.normal_(0, 0.02)
+                base.bias.normal_(0, 0.02)
+            wrapped = peft.Linear4bit(base.to(device), 16, 32).to(device)
+            with torch.no_grad():
+                wrapped.lora_B["default"].weight.normal_(0, 0.01)
+            wrapped.lora_dropout["default"] = torch.nn.Dropout(p)
+            setattr(layer.self_attn, name, wrapped)
+            adapters.append(wrapped)
+    model.train()
+    lengths = [37, 12, 50]
+    b, s = len(lengths), max(lengths)
+    ids = torch.randint(0, 1000, (b, s), device=device)
+    mask = torch.zeros((b, s), device=device, dtype=torch.long)
+    for r, n in enumerate(lengths):
+        mask[r, :n] = 1
+    labels = ids.masked_fill(mask == 0, -100)
+
+    def run():
+        model.zero_grad()
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = model(input_ids=ids, attention_mask=mask, labels=labels)
+        out.loss.backward()
+        grads = [t.grad.detach().float().clone() for t in (
+            adapters[0].lora_A["default"].weight, adapters[0].lora_B["default"].weight,
+            adapters[3].lora_A["default"].weight, adapters[3].lora_B["default"].weight,
+            model.model.layers[1].mlp.down_proj.weight,
+            model.model.layers[0].input_layernorm.weight)]
+        return out.loss.detach().float(), grads
+
+    seeds = []
+    _lib.hooks["ss_qlora_forward_dropout"] = (
+        lambda name, args: seeds.append((args[14], args[2], args[9])), lambda name, args: None)
+    try:
+        with _Recorder(["ss_unpad_gather", "ss_attn_varlen_fwd", "ss_attn_varlen_bwd",
+                        "ss_qlora_backward_dropout", "ss_ce_stats"]) as rec:
+            torch.manual_seed(11)
+            loss, grads = run()
+    finally:
+        _lib.hooks.pop("ss_qlora_forward_dropout", None)
+    assert unpad_route.last_refusal() is None
+    assert "ss_unpad_gather" in rec.calls and rec.calls.count("ss_attn_varlen_fwd") == 2
+    assert "ss_attn_varlen_bwd" in rec.calls and "ss_ce_stats" in rec.calls
+    assert rec.calls.count("ss_qlora_backward_dropout") == 4
+    tokens = sum(lengths)
+    assert len(seeds) == 4 and all(t == tokens for _, t, _ in seeds)
+    # the same masks on the padded layout, in call order (layer 0 q, v; layer 1 q, v)
+    batch_index = torch.cat([torch.arange(r * s, r * s + n, device=device)
+                             for r, n in enumerate(lengths)])
+    for layer_drop, (seed, t, k) in zip(adapters, seeds):
+        keep = torch.empty(t * k, dtype=torch.uint8, device=device)
+        _lib.call("ss_dropout_mask", seed, p, t, k, keep.data_ptr(), _lib.stream(device))
+        padded = torch.zeros((b * s, k), dtype=torch.bool, device=device)
+        padded.index_copy_(0, batch_index, keep.reshape(t, k).bool())
+        layer_drop.lora_dropout["default"] = _FixedMask(padded.reshape(b, s, k), p)
+    monkeypatch.setenv("SOUP_FUSED_DISABLE", "1")
+    ref_loss, ref_grads = run()
+    assert abs(loss.item() - ref_loss.item()) <= 5e-3 * abs(ref_loss.item())
+    for i, (got, ref) in enumerate(zip(grads, ref_grads)):
+        assert _rel(got, ref) < 5e-2, i
+
+
+def test_packed_lora_dropout_fallback_keeps_the_padded_masks(device):
+    """A LoRA dropout packing accepted, reached through PEFT's own forward (its routed call
+    declined), draws torch's masks on the padded layout: the same generator state gives
+    the padded run's mask at every real token, and zeros nowhere else are produced."""
+    from soupsuck_amd import unpad
+    from soupsuck_amd.unpad_route import _PACKED, _bind_dropout
+
+    lengths, s, k = (5, 9, 3), 9, 64
+    batch = unpad.make_batch(lengths, s, device)
+    drop = torch.nn.Dropout(0.3).train()
+    x_padded = torch.randn((len(lengths), s, k), device=device)
+    torch.manual_seed(21)
+    want = drop(x_padded)
+    _bind_dropout(drop)
+    batch.dropout_ids = frozenset({id(drop)})
+    packed = unpad.pack(x_padded, batch)
+    token = _PACKED.set(batch)
+    try:
+        torch.manual_seed(21)
+        got = drop(packed)
+    finally:
+        _PACKED.reset(token)
+    assert torch.equal(got, unpad.pack(want, batch))
+    torch.manual_seed(21)
+    assert torch.equal(drop(x_padded), want)        # outside a packed batch: the module itself

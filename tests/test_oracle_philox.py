@@ -66,3 +66,12 @@ def test_dropped_values():
     assert out.dtype == np.float32
     assert np.array_equal(out, np.array([[1.5 * inv, 0.0, 3.0 * inv, 0.25 * inv]], np.float32))
     assert philox.threshold(0.5) == 2 ** 31
+
+
+def test_tiny_p_threshold_saturates():
+    """(1 - p) * 2^32 rounds to 2^32 for p below about 1.1e-16; the threshold then saturates
+    at 2^32 - 1 instead of wrapping to 0 (which would drop every element)."""
+    assert philox.threshold(1e-20) == 0xFFFFFFFF
+    assert philox.threshold(float(np.float32(2.0 ** -40))) == 0xFFFFFFFF
+    assert philox.threshold(2.0 ** -31) == 2 ** 32 - 2
+    assert philox.keep_mask(42, 1e-20, 4, 256).all()
