@@ -832,7 +832,14 @@ extern "C" int ss_nf4_gemm_fwd_noalloc(const uint16_t* x, int64_t ldx, int64_t t
   if (t == 0) return SS_OK;
   SS_CHECK_ARG(x && y, "%s: null activation/output pointer", fn);
   SS_CHECK_ARG(ldx >= k && ldy >= n, "%s: leading dimensions too small", fn);
-  const size_t need = fwd_workspace_bytes(t, n, k);
+  // The streaming, skinny and fused kernels read X with 16-byte loads.  An X they cannot
+  // take sends run_fwd to the decode-first path, as ss_nf4_gemm_fwd with its full
+  // workspace does, so the scratch must then hold the decoded weight and the dense
+  // product's partials; sizing it for the fast paths alone would fall through to the
+  // in-loop decoder, a different kernel.
+  const bool x_vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 8 == 0;
+  const size_t need = x_vec ? fwd_workspace_bytes(t, n, k)
+                            : decoded_bytes(n, k) + ss::nt_partial_bytes(t, n, k);
   SS_CHECK_ARG(need <= kNoAllocScratchBytes,
                "%s: T=%lld N=%lld K=%lld needs %zu bytes of scratch, more than the fixed "
                "%zu-byte device scratch of this entry point; use ss_nf4_gemm_fwd with a "

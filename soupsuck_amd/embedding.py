@@ -14,14 +14,13 @@ fp32, write the fp16 candidate, raise a flag on any inexact element) and one
 flag read, instead of the reference's 32 MiB chunks compared by torch; the
 candidate is the eventual storage, so nothing fp32-sized is allocated.
 
-Acceptance (anything else declines, reporting the reason once per process):
-routing enabled; an exact Qwen2ForCausalLM under any PEFT / DDP wrapping; a
-plain ``Embedding`` and a plain bias-free ``Linear`` head sharing one
-Parameter, frozen, fp32, CUDA, contiguous and 2-D, no max_norm and no
-per-instance forward; a PEFT LoRA configuration targeting only q_proj /
-v_proj, with no modules_to_save, trainable tokens or bias; PEFT's own
-``save_embedding_layers="auto"`` policy saving LoRA tensors only (a resized
-vocabulary would make PEFT save the table); and an exact round trip.
+Acceptance is data: routing enabled and an exact Qwen2ForCausalLM under any
+PEFT / DDP wrapping, then the ordered TABLE_RULES on its embedding and head,
+then _LORA_CONFIG on every adapter configuration (LoRA on q_proj / v_proj
+only, nothing else saved or trained), then PEFT's own
+``save_embedding_layers="auto"`` policy storing LoRA tensors only (a resized
+vocabulary would make PEFT save the table), then an exact round trip.  The
+first rule that fails is the decline reason, reported once per process.
 
 ``route_soup_setup`` installs the call after Soup's
 ``SFTTrainerWrapper._setup_transformers`` (solution/embedding.py:146-169).
@@ -29,11 +28,12 @@ vocabulary would make PEFT save the table); and an exact round trip.
 
 import importlib
 import sys
-from types import MethodType
+from types import MethodType, SimpleNamespace
 
 import torch
 
 from . import _lib
+from .contract import Rule
 from .utils import enabled
 
 ACTIVE = "_soupsuck_lossless_embedding"
@@ -74,29 +74,87 @@ def exact_half(weight):
     return None if int(flag.item()) else out
 
 
+_QV = frozenset({"q_proj", "v_proj"})
+
+# What every PEFT adapter configuration must hold: (attribute, value when absent, test).
+_LORA_CONFIG = (
+    ("peft_type", None, lambda v: getattr(v, "value", v) == "LORA"),
+    ("target_modules", None,
+     lambda v: isinstance(v, (tuple, list, set)) and len(v) > 0 and set(v) <= _QV),
+    ("modules_to_save", None, lambda v: not v),
+    ("trainable_token_indices", None, lambda v: not v),
+    ("bias", "none", lambda v: v == "none"),
+)
+
+
+def _saves_only_lora(model, names):
+    """True when PEFT's save_embedding_layers="auto" policy stores LoRA tensors only for
+    every adapter (it adds the table when the vocabulary was resized)."""
+    from peft import get_peft_model_state_dict
+
+    for name in names:
+        state = get_peft_model_state_dict(model, adapter_name=name, save_embedding_layers="auto")
+        if not state or not all("lora_" in key for key in state):
+            return False
+    return True
+
+
 def _adapter_reason(model):
+    """Why the adapter setup rules the fp16 table out, or None when it allows it."""
     configs = getattr(model, "peft_config", None)
     if not isinstance(configs, dict) or not configs:
         return "no PEFT adapter configuration on the model"
-    for config in configs.values():
-        targets = getattr(config, "target_modules", None)
-        kind = getattr(config, "peft_type", None)
-        if (getattr(kind, "value", kind) != "LORA"
-                or not isinstance(targets, (tuple, list, set)) or not targets
-                or not set(targets) <= {"q_proj", "v_proj"}
-                or getattr(config, "modules_to_save", None)
-                or getattr(config, "trainable_token_indices", None)
-                or getattr(config, "bias", "none") != "none"):
-            return "needs q_proj / v_proj-only LoRA without saved modules, tokens or bias"
+    if not all(test(getattr(config, attr, absent)) for config in configs.values()
+               for attr, absent, test in _LORA_CONFIG):
+        return ("the LoRA adapters must be q_proj / v_proj-only, with no saved modules, "
+                "trainable tokens or bias")
     try:
-        from peft import get_peft_model_state_dict
+        lora_only = _saves_only_lora(model, list(configs))
     except ImportError:
         return "peft is not importable, so its embedding save policy cannot be checked"
-    for name in configs:
-        saved = get_peft_model_state_dict(model, adapter_name=name, save_embedding_layers="auto")
-        if not saved or any("lora_" not in key for key in saved):
-            return "PEFT's auto save policy would store non-LoRA tensors (e.g. a resized vocabulary)"
+    if not lora_only:
+        return "PEFT's auto save policy would store non-LoRA tensors (e.g. a resized vocabulary)"
     return None
+
+
+def _plain_pair(c):
+    return type(c.embedding) is torch.nn.Embedding and type(c.head) is torch.nn.Linear
+
+
+def _storable(c):
+    w = c.embedding.weight
+    return (not w.requires_grad and w.dtype == torch.float32 and w.is_cuda
+            and w.is_contiguous() and w.ndim == 2)
+
+
+def _default_forwards(c):
+    return (c.embedding.max_norm is None and c.head.bias is None
+            and "forward" not in c.embedding.__dict__ and "forward" not in c.head.__dict__)
+
+
+# Checked in order on the unwrapped model; the first failure is the decline reason.
+TABLE_RULES = (
+    Rule("the input / output embeddings are not a plain Embedding and a plain Linear",
+         _plain_pair),
+    Rule("the input embedding and the output head are not tied to one shared Parameter",
+         lambda c: c.head.weight is c.embedding.weight),
+    Rule("the tied table must be a frozen, contiguous 2-D fp32 tensor on CUDA", _storable),
+    Rule("the embedding has max_norm, the head has a bias, or either has its own forward",
+         _default_forwards),
+)
+
+
+def _fp32_lookup(self, ids):
+    """Embedding forward over the fp16 table: the rows come back in fp32, as before."""
+    return torch.nn.Embedding.forward(self, ids).to(torch.float32)
+
+
+def _head_product(self, hidden):
+    """Head forward over the fp16 table: autocast multiplies in fp16 exactly as it did
+    with the fp32 table; without autocast the product runs on an fp32 copy."""
+    if torch.is_autocast_enabled("cuda"):
+        return torch.nn.Linear.forward(self, hidden)
+    return torch.nn.functional.linear(hidden, self.weight.to(torch.float32))
 
 
 def compress_tied_embedding(model):
@@ -112,41 +170,26 @@ def compress_tied_embedding(model):
         return False
     raw = unwrap(model, cls)
     if raw is None:
-        return _decline("not an exact Qwen2ForCausalLM")
-    embedding, head = raw.get_input_embeddings(), raw.get_output_embeddings()
-    if type(embedding) is not torch.nn.Embedding or type(head) is not torch.nn.Linear:
-        return _decline("the input / output embeddings are wrapped or not plain modules")
-    weight = embedding.weight
-    if head.weight is not weight:
-        return _decline("lm_head and embed_tokens do not share one Parameter")
+        return _decline("not an exact Qwen2ForCausalLM under the PEFT / DDP wrappers")
+    pair = SimpleNamespace(embedding=raw.get_input_embeddings(),
+                           head=raw.get_output_embeddings())
     if getattr(raw, ACTIVE, False):
-        return weight.dtype == torch.float16 and not weight.requires_grad
-    if (weight.requires_grad or weight.dtype != torch.float32 or not weight.is_cuda
-            or not weight.is_contiguous() or weight.ndim != 2):
-        return _decline("the tied table must be frozen, fp32, CUDA, contiguous and 2-D")
-    if (embedding.max_norm is not None or head.bias is not None
-            or "forward" in embedding.__dict__ or "forward" in head.__dict__):
-        return _decline("max_norm embedding, biased head or per-instance forward")
+        table = pair.embedding.weight
+        return table.dtype == torch.float16 and not table.requires_grad
+    for rule in TABLE_RULES:
+        if not rule.holds(pair):
+            return _decline(rule.text)
     reason = _adapter_reason(model)
     if reason is not None:
         return _decline(reason)
-    candidate = exact_half(weight.detach())
-    if candidate is None:
+    table = pair.embedding.weight
+    storage = exact_half(table.detach())
+    if storage is None:
         return _decline("an element of the table has no exact fp16 representation")
-    embed_forward, head_forward = type(embedding).forward, type(head).forward
-
-    def embedding_forward(self, ids):
-        return embed_forward(self, ids).to(torch.float32)
-
-    def linear_forward(self, x):
-        if torch.is_autocast_enabled("cuda"):
-            return head_forward(self, x)
-        return torch.nn.functional.linear(x, self.weight.float(), self.bias)
-
     with torch.no_grad():
-        weight.data = candidate
-    embedding.forward = MethodType(embedding_forward, embedding)
-    head.forward = MethodType(linear_forward, head)
+        table.data = storage          # same Parameter: ties, names and references survive
+    pair.embedding.forward = MethodType(_fp32_lookup, pair.embedding)
+    pair.head.forward = MethodType(_head_product, pair.head)
     setattr(raw, ACTIVE, True)
     return True
 

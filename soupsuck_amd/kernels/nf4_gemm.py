@@ -20,6 +20,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
+from ..contract import Rule, enforce
 from .nf4 import _validate_state
 
 
@@ -134,23 +135,39 @@ def nf4_dx_2d(dy2d, packed, state, n, k, out=None, accumulate=False):
     return out
 
 
-def _check_x(x, packed, width_in, name="X"):
-    if (not isinstance(x, torch.Tensor) or x.device != packed.device
-            or x.dtype != torch.float16 or not x.is_contiguous() or x.ndim < 2
-            or x.shape[-1] != width_in):
-        raise ValueError(f"Expected contiguous CUDA fp16 {name} matching canonical nested NF4 weight")
+def _activation_ok(a):
+    x = a.x
+    return (isinstance(x, torch.Tensor) and x.device == a.packed.device and x.ndim >= 2
+            and x.shape[-1] == a.width_in)
+
+
+def _bias_ok(a):
+    b = a.bias
+    if b is None:
+        return True
+    return (not a.transpose and isinstance(b, torch.Tensor) and b.device == a.x.device
+            and b.dtype == torch.float16 and tuple(b.shape) == (a.width_out,)
+            and b.is_contiguous() and not b.requires_grad)
+
+
+# nf4_matmul's operands once the NF4 state itself is accepted (NESTED_STATE_RULES).
+MATMUL_RULES = (
+    Rule("nf4_matmul: the activation must be a tensor of two or more dimensions on the "
+         "weight's CUDA device whose last extent is the product's reduction length",
+         _activation_ok),
+    Rule("nf4_matmul: the activation must be fp16 and contiguous",
+         lambda a: a.x.dtype == torch.float16 and a.x.is_contiguous()),
+    Rule("nf4_matmul: a bias belongs to the forward product only, as a frozen contiguous "
+         "fp16 vector of the output width", _bias_ok),
+)
 
 
 def nf4_matmul(x, packed, state, *, transpose=False, bias=None):
     """X[..., K] . W^T (+bias) or, with transpose, dY[..., N] . W (reference nf4_gemm.py:74-96)."""
     n, k = _validate_state(packed, state, torch.float16)
-    _check_x(x, packed, n if transpose else k)
     width = k if transpose else n
-    if bias is not None and (transpose or not isinstance(bias, torch.Tensor)
-                             or bias.device != x.device or bias.dtype != torch.float16
-                             or bias.shape != (width,) or not bias.is_contiguous()
-                             or bias.requires_grad):
-        raise ValueError("Only frozen contiguous fp16 forward bias is supported")
+    enforce(MATMUL_RULES, x=x, packed=packed, bias=bias, transpose=transpose,
+            width_in=n if transpose else k, width_out=width)
     m = x.numel() // x.shape[-1]
     x2d = x.reshape(m, x.shape[-1])
     with torch.cuda.device(x.device):

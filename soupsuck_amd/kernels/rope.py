@@ -1,95 +1,140 @@
 """Joint q/k rotary position embedding (Qwen2 ``apply_rotary_pos_emb``).
 
-Mirrors the reference's solution/kernels/rope.py:101-152 (``_RoPE`` and
-``fused_rope``) and solution/rope.py:55-80 (``patch_qwen2_rope``): q [B, Hq,
-S, D] and k [B, Hk, S, D] with any batch / head / token strides (e.g. the
-transposed projection views), cos / sin [1|B, S, D] detached; outputs are
-contiguous in promote(x, cos); every product is rounded to the output dtype
-before the add (eager PyTorch's order), the backward rounds products to the
-input dtype.  Kernels: ss_rope_fwd / ss_rope_bwd.  Saves only cos and sin.
+Interface of the reference's ``fused_rope`` (solution/kernels/rope.py:146-152)
+and its route (solution/rope.py:55-80): q [B, Hq, S, D] and k [B, Hk, S, D]
+with any batch / head / token strides (the transposed projection views), and
+detached cos / sin [1|B, S, D].  Results are contiguous in promote(x, cos);
+every product is rounded to that dtype before the add (eager PyTorch's order),
+and the backward -- the inverse rotation -- rounds its products to the input
+dtype.  Kernels: ss_rope_fwd / ss_rope_bwd; only cos and sin are saved.
+
+Accepted inputs are the rule table ROPE_RULES; ``fused_rope`` raises
+ValueError with the first broken rule, ``rope_supported`` answers without
+raising (the route's eligibility test).
 """
+
+from typing import NamedTuple
 
 import torch
 from torch.autograd.function import once_differentiable
 
 from .. import _lib
+from ..contract import Rule, enforce, is_tensor
 
 _DTYPES = (torch.float16, torch.float32)
 
 
+def _same_cuda_device(a):
+    return a.q.is_cuda and all(t.device == a.q.device for t in (a.k, a.cos, a.sin))
+
+
+def _pair_shapes(a):
+    q, k = a.q, a.k
+    return (q.ndim == 4 and k.ndim == 4 and q.shape[-1] % 2 == 0
+            and k.shape[0] == q.shape[0] and tuple(k.shape[2:]) == tuple(q.shape[2:]))
+
+
+def _table_shape(a):
+    b, _, s, d = a.q.shape
+    return (a.cos.ndim == 3 and a.sin.shape == a.cos.shape and a.cos.shape[0] in (1, b)
+            and tuple(a.cos.shape[1:]) == (s, d))
+
+
+ROPE_RULES = (
+    Rule("fused_rope: q, k, cos and sin must be tensors", lambda a: is_tensor(a.q, a.k, a.cos,
+                                                                             a.sin)),
+    Rule("fused_rope: heads must be dimension 1 (unsqueeze_dim=1)", lambda a: a.unsqueeze == 1),
+    Rule("fused_rope: all four tensors must live on one CUDA device", _same_cuda_device),
+    Rule("fused_rope: q and k must be [B, H, S, D] sharing B, S and an even D", _pair_shapes),
+    Rule("fused_rope: cos and sin must both be [1 or B, S, D]", _table_shape),
+    Rule("fused_rope: cos and sin must not require grad",
+         lambda a: not (a.cos.requires_grad or a.sin.requires_grad)),
+    Rule("fused_rope: dtypes must be fp16 or fp32, with cos and sin alike",
+         lambda a: all(t.dtype in _DTYPES for t in (a.q, a.k, a.cos, a.sin))
+         and a.cos.dtype == a.sin.dtype),
+    Rule("fused_rope: the last dimension of every tensor must be dense (stride 1)",
+         lambda a: all(t.stride(-1) == 1 for t in (a.q, a.k, a.cos, a.sin))),
+)
+
+
 def rope_supported(q, k, cos, sin, unsqueeze_dim=1):
-    tensors = (q, k, cos, sin)
-    if not all(isinstance(t, torch.Tensor) for t in tensors) or unsqueeze_dim != 1:
+    try:
+        enforce(ROPE_RULES, q=q, k=k, cos=cos, sin=sin, unsqueeze=unsqueeze_dim)
+    except ValueError:
         return False
-    if not q.is_cuda or any(t.device != q.device for t in tensors):
-        return False
-    if q.ndim != 4 or k.ndim != 4 or cos.ndim != 3 or sin.shape != cos.shape:
-        return False
-    b, _, s, d = q.shape
-    if d % 2 or k.shape[0] != b or k.shape[2:] != (s, d) or cos.shape[1:] != (s, d):
-        return False
-    if cos.shape[0] not in (1, b) or cos.requires_grad or sin.requires_grad:
-        return False
-    if any(t.dtype not in _DTYPES for t in tensors) or cos.dtype != sin.dtype:
-        return False
-    return all(t.stride(-1) == 1 for t in tensors)
+    return True
 
 
-def _cs_args(cos, sin):
+class _Geometry(NamedTuple):
+    batches: int
+    qheads: int
+    kheads: int
+    tokens: int
+    half: int
+
+    @property
+    def empty(self):
+        return not (self.batches and self.tokens and self.qheads + self.kheads)
+
+
+def _operand(t, strides):
+    """(pointer, dtype code, strides...) of one [B, H, S, D] operand; zeros when absent."""
+    if t is None:
+        return (None, 0) + (0,) * strides
+    return (t.data_ptr(), _lib.dtype_code(t.dtype)) + tuple(t.stride()[:strides])
+
+
+def _table(cos, sin):
     return (cos.data_ptr(), sin.data_ptr(), _lib.dtype_code(cos.dtype), cos.stride(0),
             cos.stride(1), sin.stride(0), sin.stride(1), cos.shape[0])
 
 
-class _RoPE(torch.autograd.Function):
+def _target(t):
+    return (_lib.ptr(t), _lib.dtype_code(t.dtype) if t is not None else 0)
+
+
+class _RotaryPair(torch.autograd.Function):
+    """Both rotations in one launch each way; the backward rotates by -theta."""
+
     @staticmethod
     def forward(ctx, q, k, cos, sin):
-        b, hq, s, d = q.shape
-        hk = k.shape[1]
-        yq = torch.empty(q.shape, device=q.device, dtype=torch.promote_types(q.dtype, cos.dtype))
-        yk = torch.empty(k.shape, device=k.device, dtype=torch.promote_types(k.dtype, cos.dtype))
-        if b and s and hq + hk:
-            _lib.call("ss_rope_fwd", q.data_ptr(), _lib.dtype_code(q.dtype), *q.stride()[:3],
-                      k.data_ptr(), _lib.dtype_code(k.dtype), *k.stride()[:3],
-                      *_cs_args(cos, sin), yq.data_ptr(), _lib.dtype_code(yq.dtype),
-                      yk.data_ptr(), _lib.dtype_code(yk.dtype), b, hq, hk, s, d // 2,
-                      _lib.stream(q.device))
+        geo = _Geometry(q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3] // 2)
+        outs = tuple(torch.empty(x.shape, device=x.device,
+                                 dtype=torch.promote_types(x.dtype, cos.dtype)) for x in (q, k))
+        if not geo.empty:
+            _lib.call("ss_rope_fwd", *_operand(q, 3), *_operand(k, 3), *_table(cos, sin),
+                      *_target(outs[0]), *_target(outs[1]), *geo, _lib.stream(q.device))
         ctx.save_for_backward(cos, sin)
-        ctx.qshape, ctx.kshape, ctx.qdtype, ctx.kdtype = q.shape, k.shape, q.dtype, k.dtype
+        ctx.geo = geo
+        ctx.inputs = ((q.shape, q.dtype), (k.shape, k.dtype))
         ctx.set_materialize_grads(False)
-        frozen = tuple(o for o, req in zip((yq, yk), ctx.needs_input_grad[:2]) if not req)
+        # an output whose input takes no gradient carries none, as in eager PyTorch
+        frozen = [y for y, wanted in zip(outs, ctx.needs_input_grad) if not wanted]
         if frozen:
             ctx.mark_non_differentiable(*frozen)
-        return yq, yk
+        return outs
 
     @staticmethod
     @once_differentiable
     def backward(ctx, gq, gk):
         cos, sin = ctx.saved_tensors
-        b, hq, s, d = ctx.qshape
-        hk = ctx.kshape[1]
-        need_q = gq is not None and ctx.needs_input_grad[0]
-        need_k = gk is not None and ctx.needs_input_grad[1]
-        dq = torch.empty(ctx.qshape, device=cos.device, dtype=ctx.qdtype) if need_q else None
-        dk = torch.empty(ctx.kshape, device=cos.device, dtype=ctx.kdtype) if need_k else None
-        if (need_q or need_k) and b and s and hq + hk:
-            qs = gq.stride() if need_q else (0, 0, 0, 0)
-            ks = gk.stride() if need_k else (0, 0, 0, 0)
-            _lib.call("ss_rope_bwd", gq.data_ptr() if need_q else None,
-                      _lib.dtype_code(gq.dtype) if need_q else 0, *qs,
-                      gk.data_ptr() if need_k else None,
-                      _lib.dtype_code(gk.dtype) if need_k else 0, *ks, *_cs_args(cos, sin),
-                      _lib.ptr(dq), _lib.dtype_code(ctx.qdtype), _lib.ptr(dk),
-                      _lib.dtype_code(ctx.kdtype), b, hq, hk, s, d // 2, _lib.stream(cos.device))
-        return dq, dk, None, None
+        grads, results = [], []
+        for g, wanted, (shape, dtype) in zip((gq, gk), ctx.needs_input_grad, ctx.inputs):
+            live = g is not None and wanted
+            grads.append(g if live else None)
+            results.append(torch.empty(shape, device=cos.device, dtype=dtype) if live else None)
+        if any(r is not None for r in results) and not ctx.geo.empty:
+            _lib.call("ss_rope_bwd", *_operand(grads[0], 4), *_operand(grads[1], 4),
+                      *_table(cos, sin), *_target(results[0]), *_target(results[1]), *ctx.geo,
+                      _lib.stream(cos.device))
+        return results[0], results[1], None, None
 
 
 def fused_rope(q, k, cos, sin):
-    """Rotate q / k on the GPU; cos / sin are detached [1|B, S, D] (rope.py:146-152)."""
-    if not rope_supported(q, k, cos, sin):
-        raise ValueError("Expected CUDA q/k[B,H,S,even D] and detached cos/sin[1|B,S,D], "
-                         "last stride 1")
+    """(q', k') rotated on the GPU; cos / sin detached [1|B, S, D] (rope.py:146-152)."""
+    enforce(ROPE_RULES, q=q, k=k, cos=cos, sin=sin, unsqueeze=1)
     with torch.cuda.device(q.device):
-        return _RoPE.apply(q, k, cos, sin)
+        return _RotaryPair.apply(q, k, cos, sin)
 
 
 def patch_qwen2_rope(module=None):

@@ -87,7 +87,7 @@ def test_cpu_and_untied_tables_are_declined(monkeypatch):
     assert embedding.compress_tied_embedding(_tiny_lm()) is False
     assert "CUDA" in messages[-1]
     assert embedding.compress_tied_embedding(_tiny_lm(tie=False)) is False
-    assert "share one Parameter" in messages[-1]
+    assert "tied to one shared Parameter" in messages[-1]
     assert embedding.compress_tied_embedding(torch.nn.Linear(2, 2)) is False
     assert "exact Qwen2ForCausalLM" in messages[-1]
     monkeypatch.setenv("SOUP_FUSED_DISABLE", "1")

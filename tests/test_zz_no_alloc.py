@@ -90,3 +90,25 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(device):
         _noalloc(x, packed, st, n, k, None, y)
     torch.cuda.synchronize()
     assert not bool(y.any()), "rejected call must not launch"
+
+
+def test_noalloc_unvectorisable_x_takes_the_workspace_path(device):
+    """X rows 1540 halves apart (ldx % 8 != 0) rule out the 16-byte-load kernels; at T = 200
+    both entry points then decode W first, so the scratch holds the decoded weight and the
+    outputs stay bit-identical.  The second call (T = 100, dense X) is the skinny kernel."""
+    n, k = 8960, 1536
+    print(f"case noalloc unvectorisable X N={n} K={k} T=200 then T=100", flush=True)
+    packed, st = _weight(n, k, device, seed=11)
+    gen = torch.Generator(device=device).manual_seed(3)
+    x1 = torch.randn((200, k + 4), device=device, generator=gen).half()[:, :k]
+    x2 = torch.randn((100, k), device=device, generator=gen).half()
+    assert x1.stride(0) % 8 != 0
+    ref1 = _with_workspace(x1, packed, st, n, k, None)
+    ref2 = _with_workspace(x2, packed, st, n, k, None)
+    torch.cuda.synchronize()
+    y1 = torch.full((200, n), float("nan"), device=device, dtype=torch.float16)
+    y2 = torch.full((100, n), float("nan"), device=device, dtype=torch.float16)
+    _noalloc(x1, packed, st, n, k, None, y1)
+    _noalloc(x2, packed, st, n, k, None, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, ref1) and torch.equal(y2, ref2)
