@@ -6,8 +6,10 @@
  *     default stream), enqueues work on that stream and returns immediately.
  *   - Return value: 0 on success, a negative SS_ERR_* code otherwise.  Invalid
  *     arguments are rejected BEFORE any launch; ss_last_error() then returns a
- *     thread-local message.  No entry point throws, allocates device memory,
- *     synchronizes the stream or keeps mutable global state.
+ *     thread-local message.  No entry point throws, allocates device memory or
+ *     synchronizes the stream, and none keeps mutable global state except
+ *     ss_nf4_gemm_fwd_noalloc, whose fixed device scratch and per-device
+ *     pointer cache are described at its declaration.
  *   - fp16 tensors are passed as uint16_t* (IEEE binary16 bits); "dtype" codes
  *     are SS_F16 / SS_F32.
  *   - Reference citations are file:line in the reference tree (Khasuetolog/
