@@ -191,10 +191,17 @@ def ptr(t):
 
 
 def stream(device=None):
-    """Raw hipStream_t of torch's current stream on ``device``."""
+    """Raw hipStream_t of torch's current stream on ``device`` (a torch.device, an index,
+    or None for the current device), read without building a Stream object."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, torch.device):
+        index = device.index
+    else:
+        index = device
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def dtype_code(dtype):

@@ -41,10 +41,6 @@ from .kernels.nf4 import _validate_state
 from .kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d
 
 
-def _workspace(nbytes, device):
-    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
-
-
 def _nf4_args(packed, state):
     return (packed.data_ptr(), state.absmax.data_ptr(), state.state2.absmax.data_ptr(),
             state.state2.code.data_ptr(), state.offset.data_ptr())
@@ -70,9 +66,48 @@ def _size_of(query, t, n, k, device):
     return size
 
 
-def _gemm_ws(t, n, k, device):
+_GEMM_WORKSPACE = {}
+
+
+def _gemm_ws(t, n, k, device, stream):
+    """(workspace, bytes) of the NF4 GEMM for this shape: one buffer per (device, stream),
+    grown on demand and reused by every call issued on that stream (calls on one stream
+    run in order, and the workspace holds nothing between calls).  A buffer replaced by
+    a larger one is kept alive, as the rank workspace's are, for HIP graphs captured
+    with it."""
     size = _size_of("ss_nf4_gemm_workspace_size", t, n, k, device)
-    return (_workspace(size, device), size) if size else (None, 0)
+    if not size:
+        return None, 0
+    key = (device.index, stream)
+    ws = _GEMM_WORKSPACE.get(key)
+    if ws is None or ws.numel() < size:
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
+        grown = 2 * ws.numel() if ws is not None else 0
+        ws = torch.empty(max(size, grown), dtype=torch.uint8, device=device)
+        _GEMM_WORKSPACE[key] = ws
+    return ws, ws.numel()
+
+
+_CHECKED = {}
+
+
+def _checked_state(packed, state):
+    """(n, k, NF4 pointer arguments) of an accepted nested-NF4 state.  The full rule table
+    runs once per (state, storage); later calls with the same objects and buffers (the
+    frozen weight of a projection) reuse its verdict."""
+    key = (id(state), id(packed), packed.data_ptr(), state.absmax.data_ptr(),
+           state.state2.absmax.data_ptr(), state.state2.code.data_ptr(),
+           state.offset.data_ptr())
+    hit = _CHECKED.get(key)
+    if hit is not None and hit[0] is state and hit[1] is packed:
+        return hit[2]
+    n, k = _validate_state(packed, state, torch.float16)
+    verdict = (n, k, _nf4_args(packed, state))
+    if len(_CHECKED) > 4096:
+        _CHECKED.clear()
+    _CHECKED[key] = (state, packed, verdict)
+    return verdict
 
 
 _RANK_WORKSPACE = {}
@@ -132,117 +167,89 @@ def _qlora_rank_ws(t, n, k, device, stream):
                            stream)
 
 
+def _half(w):
+    """fp16 contiguous copy of a LoRA weight (itself when it already is one)."""
+    if w.dtype == torch.float16 and w.is_contiguous():
+        return w
+    return w.to(torch.float16).contiguous()
+
+
+def _grads(ctx, dx, da, db):
+    x_dtype, a_dtype, b_dtype = ctx.dtypes
+    dx = dx.view(ctx.shape)
+    return (dx if x_dtype == torch.float16 else dx.to(x_dtype),
+            da if a_dtype == torch.float16 else da.to(a_dtype),
+            db if b_dtype == torch.float16 else db.to(b_dtype))
+
+
 class _QLoRAFused(torch.autograd.Function):
-    """Rank-16, dropout-free projection on the fused entry points: forward
-    ss_qlora_forward (Z and the NF4 GEMM with the LoRA epilogue), backward
-    ss_qlora_backward (dZ, dB, dX with the rank-16 update, dA)."""
+    """Rank-16 projection on the fused entry points: forward ss_qlora_forward (Z and the
+    NF4 GEMM with the LoRA epilogue), backward ss_qlora_backward (dZ, dB, dX with the
+    rank-16 update, dA); with a seed, the dropout variants of both (the keep mask is a
+    Philox function of (seed, element of X), recomputed wherever X is used, so only the
+    8-byte seed is saved for the backward).  ``nf4``: (n, k, NF4 pointer arguments) from
+    _checked_state."""
 
     @staticmethod
-    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling):
-        n, k = state.shape
+    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling, nf4, dropout):
+        n, k, w_args = nf4
         t = x.numel() // k
-        x2d = x.reshape(t, k)
-        a16 = lora_a.to(torch.float16).contiguous()
-        b16 = lora_b.to(torch.float16).contiguous()
-        z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
-        y = torch.empty((t, n), device=x.device, dtype=torch.float16)
-        stream = _lib.stream(x.device)
-        ws, size = _gemm_ws(t, n, k, x.device)
-        rws = _qlora_rank_ws(t, n, k, x.device, stream)
-        _lib.call("ss_qlora_forward", x2d.data_ptr(), x2d.stride(0), t, *_nf4_args(packed, state),
-                  n, k, _lib.ptr(bias), a16.data_ptr(), b16.data_ptr(), float(scaling),
-                  z.data_ptr(), y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(),
-                  rws.numel(), stream)
-        ctx.save_for_backward(x2d, z, a16, b16, packed)
-        ctx.state, ctx.scaling = state, float(scaling)
+        x2d = x.view(t, k)
+        a16, b16 = _half(lora_a), _half(lora_b)
+        dev = x.device
+        z = torch.empty((t, 16), device=dev, dtype=torch.float16)
+        y = torch.empty((t, n), device=dev, dtype=torch.float16)
+        stream = _lib.stream(dev)
+        ws, size = _gemm_ws(t, n, k, dev, stream)
+        rws = _qlora_rank_ws(t, n, k, dev, stream)
+        head = (x2d.data_ptr(), k, t, *w_args, n, k, _lib.ptr(bias), a16.data_ptr(),
+                b16.data_ptr(), scaling)
+        tail = (z.data_ptr(), y.data_ptr(), n, _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
+                stream)
+        if dropout is None:
+            _lib.call("ss_qlora_forward", *head, *tail)
+        else:
+            _lib.call("ss_qlora_forward_dropout", *head, dropout[0], dropout[1], *tail)
+        ctx.save_for_backward(x2d, z, a16, b16)
+        # the NF4 arguments are raw pointers: the reference keeps the weight alive
+        ctx.packed, ctx.nf4, ctx.scaling, ctx.dropout = packed, nf4, scaling, dropout
         ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
-        return y.reshape(*x.shape[:-1], n)
+        return y.view(*x.shape[:-1], n)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad):
-        x2d, z, a16, b16, packed = ctx.saved_tensors
-        state = ctx.state
-        n, k = state.shape
+        x2d, z, a16, b16 = ctx.saved_tensors
+        n, k, w_args = ctx.nf4
         t = x2d.shape[0]
-        g = grad.reshape(t, n).to(torch.float16).contiguous()
+        g = grad.reshape(t, n)
+        if g.dtype != torch.float16 or not g.is_contiguous():
+            g = g.to(torch.float16).contiguous()
         dev = g.device
-        dz = torch.empty((t, 16), device=dev, dtype=torch.float16)   # fp16(fp16(g*s) . B)
-        db = torch.empty((n, 16), device=dev, dtype=torch.float16)   # fp16(fp16(g*s)^T . Z)
-        da = torch.empty((16, k), device=dev, dtype=torch.float16)   # fp16(dZ^T . X)
+        # dZ (used inside the call), dB and dA in one allocation; dX apart
+        rank = torch.empty(t * 16 + n * 16 + 16 * k, device=dev, dtype=torch.float16)
+        dz = rank[:t * 16]
+        db = rank[t * 16:t * 16 + n * 16].view(n, 16)   # fp16(fp16(g*s)^T . Z)
+        da = rank[t * 16 + n * 16:].view(16, k)          # fp16(dZ^T . X)
         dx = torch.empty((t, k), device=dev, dtype=torch.float16)
         stream = _lib.stream(dev)
-        ws, size = _gemm_ws(t, n, k, dev)
+        ws, size = _gemm_ws(t, n, k, dev, stream)
         rws = _qlora_rank_ws(t, n, k, dev, stream)
-        _lib.call("ss_qlora_backward", g.data_ptr(), g.stride(0), t, *_nf4_args(packed, state), n,
-                  k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(), a16.data_ptr(), b16.data_ptr(),
-                  ctx.scaling, dx.data_ptr(), dx.stride(0), dz.data_ptr(), da.data_ptr(),
-                  db.data_ptr(), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
-                  stream)
-        x_dtype, a_dtype, b_dtype = ctx.dtypes
-        return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
-                None, None, None, None)
+        head = (g.data_ptr(), n, t, *w_args, n, k, x2d.data_ptr(), k, z.data_ptr(),
+                a16.data_ptr(), b16.data_ptr(), ctx.scaling)
+        tail = (dx.data_ptr(), k, dz.data_ptr(), da.data_ptr(), db.data_ptr(), _lib.ptr(ws),
+                size, rws.data_ptr(), rws.numel(), stream)
+        if ctx.dropout is None:
+            _lib.call("ss_qlora_backward", *head, *tail)
+        else:
+            _lib.call("ss_qlora_backward_dropout", *head, *ctx.dropout, *tail)
+        return (*_grads(ctx, dx, da, db), None, None, None, None, None, None)
 
 
 def dropout_seed():
     """A 64-bit seed for one dropout call, drawn from torch's default CPU generator (so
     torch.manual_seed makes the masks reproducible)."""
     return int(torch.empty((), dtype=torch.int64).random_().item())
-
-
-class _QLoRAFusedDropout(torch.autograd.Function):
-    """Rank-16 projection with LoRA dropout p > 0 on the fused entry points
-    (ss_qlora_forward_dropout / ss_qlora_backward_dropout): the keep mask is a
-    Philox function of (seed, element of X), drawn again wherever it is used,
-    so only the 8-byte seed is saved for the backward."""
-
-    @staticmethod
-    def forward(ctx, x, lora_a, lora_b, packed, state, bias, scaling, dropout_p, seed):
-        n, k = state.shape
-        t = x.numel() // k
-        x2d = x.reshape(t, k)
-        a16 = lora_a.to(torch.float16).contiguous()
-        b16 = lora_b.to(torch.float16).contiguous()
-        z = torch.empty((t, 16), device=x.device, dtype=torch.float16)
-        y = torch.empty((t, n), device=x.device, dtype=torch.float16)
-        stream = _lib.stream(x.device)
-        ws, size = _gemm_ws(t, n, k, x.device)
-        rws = _qlora_rank_ws(t, n, k, x.device, stream)
-        _lib.call("ss_qlora_forward_dropout", x2d.data_ptr(), x2d.stride(0), t,
-                  *_nf4_args(packed, state), n, k, _lib.ptr(bias), a16.data_ptr(),
-                  b16.data_ptr(), float(scaling), seed, float(dropout_p), z.data_ptr(),
-                  y.data_ptr(), y.stride(0), _lib.ptr(ws), size, rws.data_ptr(), rws.numel(),
-                  stream)
-        ctx.save_for_backward(x2d, z, a16, b16, packed)
-        ctx.state, ctx.scaling, ctx.dropout = state, float(scaling), (seed, float(dropout_p))
-        ctx.shape, ctx.dtypes = x.shape, (x.dtype, lora_a.dtype, lora_b.dtype)
-        return y.reshape(*x.shape[:-1], n)
-
-    @staticmethod
-    @once_differentiable
-    def backward(ctx, grad):
-        x2d, z, a16, b16, packed = ctx.saved_tensors
-        state = ctx.state
-        n, k = state.shape
-        t = x2d.shape[0]
-        seed, p = ctx.dropout
-        g = grad.reshape(t, n).to(torch.float16).contiguous()
-        dev = g.device
-        dz = torch.empty((t, 16), device=dev, dtype=torch.float16)
-        db = torch.empty((n, 16), device=dev, dtype=torch.float16)
-        da = torch.empty((16, k), device=dev, dtype=torch.float16)
-        dx = torch.empty((t, k), device=dev, dtype=torch.float16)
-        stream = _lib.stream(dev)
-        ws, size = _gemm_ws(t, n, k, dev)
-        rws = _qlora_rank_ws(t, n, k, dev, stream)
-        _lib.call("ss_qlora_backward_dropout", g.data_ptr(), g.stride(0), t,
-                  *_nf4_args(packed, state), n, k, x2d.data_ptr(), x2d.stride(0), z.data_ptr(),
-                  a16.data_ptr(), b16.data_ptr(), ctx.scaling, seed, p, dx.data_ptr(),
-                  dx.stride(0), dz.data_ptr(), da.data_ptr(), db.data_ptr(), _lib.ptr(ws), size,
-                  rws.data_ptr(), rws.numel(), stream)
-        x_dtype, a_dtype, b_dtype = ctx.dtypes
-        return (dx.reshape(ctx.shape).to(x_dtype), da.to(a_dtype), db.to(b_dtype),
-                None, None, None, None, None, None)
 
 
 class _QLoRAProjection(torch.autograd.Function):
@@ -306,7 +313,8 @@ class _QLoRAProjection(torch.autograd.Function):
 def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, dropout_p=0.0,
                      training=True):
     """out = X . Wdec^T + bias + scaling * (drop(X) . A^T) . B^T with NF4 W (fp16 compute)."""
-    n, k = _validate_state(packed, state, torch.float16)
+    nf4 = _checked_state(packed, state)
+    n, k = nf4[0], nf4[1]
     if x.dtype != torch.float16 or not x.is_cuda or x.shape[-1] != k or not x.is_contiguous():
         raise ValueError("Expected contiguous CUDA fp16 X[..., K]")
     if lora_a.ndim != 2 or lora_b.ndim != 2 or lora_a.shape[1] != k or lora_b.shape[0] != n \
@@ -323,11 +331,12 @@ def qlora_projection(x, lora_a, lora_b, packed, state, bias=None, scaling=2.0, d
     active = dropout_p > 0.0 and training
     with _on_device(x.device):
         if fused and not active:
-            return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling))
+            return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling), nf4,
+                                     None)
         # The fused dropout's seed is a kernel argument: a HIP graph would replay one mask
         # forever, so under capture the mask comes from torch's graph-safe generator.
         if fused and x.data_ptr() % 16 == 0 and not torch.cuda.is_current_stream_capturing():
-            return _QLoRAFusedDropout.apply(x, lora_a, lora_b, packed, state, bias,
-                                            float(scaling), float(dropout_p), dropout_seed())
+            return _QLoRAFused.apply(x, lora_a, lora_b, packed, state, bias, float(scaling), nf4,
+                                     (dropout_seed(), float(dropout_p)))
         return _QLoRAProjection.apply(x, lora_a, lora_b, packed, state, bias, float(scaling),
                                       float(dropout_p), bool(training))
