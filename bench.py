@@ -89,6 +89,11 @@ def parse():
     p.add_argument("--profile-ce", action="store_true",
                    help="only run the configs[3] fused CE forward + backward --reps times and "
                         "exit (for a rocprofv3 kernel trace)")
+    p.add_argument("--profile-read", default="", metavar="NAME",
+                   help="only run the HBM read probe over the codes of one configs[4] weight "
+                        "(NAME as in --profile-sweep) --reps times with --read-blocks "
+                        "workgroups, rotating copies, and exit (for a rocprofv3 kernel trace)")
+    p.add_argument("--read-blocks", type=int, default=1024)
     p.add_argument("--reps", type=int, default=20)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run 10 device-to-device copies of MIB MiB (scales rocprofv3 "
@@ -333,31 +338,53 @@ def sweep(torch, _lib):
                 del call
         del weight
         torch.cuda.empty_cache()
-    out["vendor_ceiling"] = vendor_ceiling(torch)
+    ceiling = vendor_ceiling(torch)
+    out["vendor_ceiling"] = ceiling
+    reads = read_ceiling(torch, _lib)
+    out["hbm_read_ceiling"] = reads
+    # T = 1 forward against a plain read of the same codes: how far the NF4 stream is
+    # from the board's read floor (the roofline fraction is against 8 TB/s)
+    for name, _, _ in SWEEP_SHAPES:
+        point, floor = out.get(f"{name} T=1 fwd"), reads.get(f"{name} codes")
+        if point and floor:
+            point["vs_read_ceiling_time"] = round(point["us"] / floor["us"], 3)
+    # T = 2048: this build's call time over hipBLASLt's time for the same product (the
+    # call includes the NF4 decode; the vendor product reads fp16 weights)
+    for name, _, _ in SWEEP_SHAPES:
+        for mode in ("fwd", "dx"):
+            ours, vendor = out.get(f"{name} T=2048 {mode}"), ceiling.get(f"{name} T=2048 {mode}")
+            if ours and vendor:
+                ours["vs_vendor_time"] = round(ours["us"] / vendor["us"], 3)
     return out
 
 
 def vendor_ceiling(torch):
     """Same-box reference point: torch.matmul (hipBLASLt) on fp16 operands already
-    in HBM, at 8192^3 and at the configs[4] T=16384 gate/up and down products
-    (X [T, K] . W^T with W [N, K] row-major).  Average of 10 calls between HIP
-    events after 3 warm-ups; a probe of what the vendor GEMM reaches on this
-    board, not a target."""
+    in HBM, at 8192^3, at the configs[4] T=16384 gate/up and down products and at
+    every configs[4] product at T=2048, forward X [T, K] . W^T and dX dY [T, N] . W
+    with W [N, K] row-major.  Average of 10 calls between HIP events after 3
+    warm-ups; a probe of what the vendor GEMM reaches on this board, not a
+    target."""
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(3)
     res = {}
-    for label, m, n, k in (("8192^3", 8192, 8192, 8192),
-                           ("gate_up T=16384 (16384x18944x3584)", 16384, 18944, 3584),
-                           ("down T=16384 (16384x3584x18944)", 16384, 3584, 18944)):
-        a = torch.randn((m, k), device=dev, generator=gen).half()
+    products = [("8192^3", 8192, 8192, 8192, "fwd"),
+                ("gate_up T=16384 (16384x18944x3584)", 16384, 18944, 3584, "fwd"),
+                ("down T=16384 (16384x3584x18944)", 16384, 3584, 18944, "fwd")]
+    for name, n, k in SWEEP_SHAPES:
+        for mode in ("fwd", "dx"):
+            products.append((f"{name} T=2048 {mode}", 2048, n, k, mode))
+    for label, m, n, k, mode in products:
+        a = torch.randn((m, n if mode == "dx" else k), device=dev, generator=gen).half()
         w = torch.randn((n, k), device=dev, generator=gen).half()
-        c = torch.empty((m, n), device=dev, dtype=torch.float16)
+        c = torch.empty((m, k if mode == "dx" else n), device=dev, dtype=torch.float16)
+        b = w if mode == "dx" else w.t()
         for _ in range(3):
-            torch.matmul(a, w.t(), out=c)
+            torch.matmul(a, b, out=c)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(10):
-            torch.matmul(a, w.t(), out=c)
+            torch.matmul(a, b, out=c)
         e1.record()
         e1.synchronize()
         us = e0.elapsed_time(e1) / 10 * 1e3
@@ -391,6 +418,29 @@ def profile_sweep(spec, reps):
                       "weight_copies": weight["copies"]}), flush=True)
 
 
+def profile_read(name, blocks, reps):
+    """Repeat the HBM read probe over one configs[4] weight's code bytes, rotating copies."""
+    import torch
+
+    from soupsuck_amd import _lib
+
+    n, k = next((n, k) for nm, n, k in SWEEP_SHAPES if nm == name)
+    dev = torch.device("cuda:0")
+    nbytes = n * k // 2
+    copies = max(2, -(-300_000_000 // nbytes))
+    bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8).fill_(i & 0xFF)
+            for i in range(copies)]
+    sink = torch.empty(blocks, device=dev, dtype=torch.int32)
+    stream = _lib.stream(dev)
+    torch.cuda.synchronize()
+    for i in range(reps):
+        _lib.call("ss_hbm_read_probe", bufs[i % copies].data_ptr(), nbytes, blocks,
+                  sink.data_ptr(), stream)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_read": name, "bytes": nbytes, "blocks": blocks, "reps": reps,
+                      "copies": copies}), flush=True)
+
+
 def graph_us(torch, _lib, call, reps):
     """Average µs of one call(i, stream) over reps calls captured in one HIP graph."""
     dev = torch.device("cuda:0")
@@ -412,6 +462,38 @@ def graph_us(torch, _lib, call, reps):
     e1.synchronize()
     del graph
     return e0.elapsed_time(e1) / reps * 1e3
+
+
+def read_ceiling(torch, _lib):
+    """What a plain cold read costs on this board (ss_hbm_read_probe), at the code sizes of
+    the configs[4] weights: the yardstick for the small-T NF4 kernels, which read their
+    codes once.  Buffers are rotated over > 300 MB (reads come from HBM, not the 256 MB
+    last-level cache); each size is timed at several grid sizes in HIP graphs and the
+    fastest is reported, with the matching T = 1 forward of the sweep for comparison."""
+    dev = torch.device("cuda:0")
+    res = {}
+    for name, n, k in SWEEP_SHAPES:
+        nbytes = n * k // 2
+        copies = max(2, -(-300_000_000 // nbytes))
+        bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8).fill_(i & 0xFF)
+                for i in range(copies)]
+        best = None
+        for blocks in (256, 512, 1024, 2048, 4096):
+            sink = torch.empty(blocks, device=dev, dtype=torch.int32)
+
+            def call(i, stream, blocks=blocks, sink=sink):
+                _lib.call("ss_hbm_read_probe", bufs[i % copies].data_ptr(), nbytes, blocks,
+                          sink.data_ptr(), stream)
+
+            us = graph_us(torch, _lib, call, 32)
+            if best is None or us < best[0]:
+                best = (us, blocks)
+        res[f"{name} codes"] = {"bytes": nbytes, "us": round(best[0], 2), "blocks": best[1],
+                                "GB/s": round(nbytes / best[0] / 1e3, 1),
+                                "frac_of_8TBs": round(nbytes / PEAK_HBM_GBS / 1e3 / best[0], 4)}
+        del bufs
+        torch.cuda.empty_cache()
+    return res
 
 
 def hbm_point(us, moved, copies):
@@ -876,6 +958,9 @@ def main():
         return
     if args.profile_sweep:
         profile_sweep(args.profile_sweep, args.reps)
+        return
+    if args.profile_read:
+        profile_read(args.profile_read, args.read_blocks, args.reps)
         return
     if args.profile_ce:
         profile_ce(args.reps)

@@ -513,6 +513,15 @@ int ss_attn_varlen_bwd(const void* q, int64_t q_tok, int64_t q_head, const void*
  * Any alignment (16-byte aligned src / dst take the vector path). */
 int ss_f32_to_f16_exact(const float* src, uint16_t* dst, int64_t n, int* flag, void* stream);
 
+/* ------------------------------------------- HBM read ceiling (measurement) ---
+ * No counterpart in the reference: a plain streaming read of `bytes` (a
+ * multiple of 16, 16-byte aligned src) by `blocks` workgroups of 256 threads,
+ * folded to one word per workgroup in sink[blocks].  bench.py times it on
+ * weight-sized buffers to measure what a cold read costs on the board, the
+ * yardstick for the weight-streaming NF4 kernels at small T. */
+int ss_hbm_read_probe(const void* src, int64_t bytes, int64_t blocks, uint32_t* sink,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

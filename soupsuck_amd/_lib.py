@@ -126,6 +126,7 @@ SIGNATURES = {
                           + [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _size, _c_void_p],
     "ss_attn_varlen_bwd_workspace_size": [_int, _int, _i64],
     "ss_f32_to_f16_exact": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p],
+    "ss_hbm_read_probe": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "ss_ce_finalize_dx": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
                           _c_void_p],
 }
