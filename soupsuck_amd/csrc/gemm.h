@@ -89,6 +89,10 @@ struct GemmParams {
   // instead of recomputing it from lora_B rows.
   half_t* lora_plane;
   int pingpong;     // 8-wave NT configurations: ping-pong main loop (set by gemm_nt)
+  // Dense NT kernels: A (B) stored K-major, element (m, k) at A[k * lda + m]
+  // ((n, k) at B[k * ldb + n]), as a transposed view stores it; plain and
+  // split-K epilogues only.
+  int a_t, b_t;
   // Optional rank-16 grads riding on the dense NT launch (unsplit) or on its
   // split-K reduce: tail_blocks + tail2_blocks extra workgroups each run one
   // block of `tail`, then of `tail2` (rank_grad_block, vector loads).  The

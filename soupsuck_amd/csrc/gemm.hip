@@ -497,15 +497,16 @@ static int dispatch(const GemmParams& p, hipStream_t stream, const char* name,
       return launch<TileBig, OPA, OPB, CT, EPI>(p, stream, name);
     return launch<TileSmall, OPA, OPB, CT, EPI>(p, stream, name);
   } else {
-    if constexpr (OPA == OP_ROW && OPB == OP_ROW) {
-      // Both operands K-contiguous: the pipelined direct-to-LDS kernel when its
-      // alignment / K % 32 requirements hold.
-      if (nt_enabled()) {
-        GemmParams q = p;
-        q.remap = remap_setting();
-        const int rc = gemm_nt(q, CT, EPI, stream, partials, partial_bytes);
-        if (rc != SS_ERR_UNSUPPORTED) return rc;
-      }
+    // The pipelined direct-to-LDS kernel when its alignment / K % 64
+    // requirements hold: K-contiguous operands as they are, K-major (OP_COL)
+    // ones read through transposed LDS reads (plain epilogues).
+    if (nt_enabled()) {
+      GemmParams q = p;
+      q.remap = remap_setting();
+      q.a_t = OPA == OP_COL;
+      q.b_t = OPB == OP_COL;
+      const int rc = gemm_nt(q, CT, EPI, stream, partials, partial_bytes);
+      if (rc != SS_ERR_UNSUPPORTED) return rc;
     }
     switch (pick_tile(p.M, p.N)) {
       case TILE_WIDE: return launch<TileWide, OPA, OPB, CT, EPI>(p, stream, name);
@@ -1229,17 +1230,17 @@ static int gemm_f16_impl(const char* fn, int a_trans, int b_trans, int64_t m, in
   hipStream_t s = (hipStream_t)stream;
   // b_trans = 1: B stored [N,K] -> OP_ROW; b_trans = 0: B stored [K,N] -> OP_COL.
   const int code = (a_trans ? 2 : 0) + (b_trans ? 0 : 1) + (c_dtype == SS_F32 ? 4 : 0);
+  void* const w = workspace;
+  const size_t wb = workspace_bytes;
   switch (code) {
-    case 0: return dispatch<OP_ROW, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 nt>", workspace,
-                                                    workspace_bytes);
-    case 1: return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>");
-    case 2: return dispatch<OP_COL, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 tt>");
-    case 3: return dispatch<OP_COL, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 tn>");
-    case 4: return dispatch<OP_ROW, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 nt>", workspace,
-                                                    workspace_bytes);
-    case 5: return dispatch<OP_ROW, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 nn>");
-    case 6: return dispatch<OP_COL, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 tt>");
-    default: return dispatch<OP_COL, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 tn>");
+    case 0: return dispatch<OP_ROW, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 nt>", w, wb);
+    case 1: return dispatch<OP_ROW, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 nn>", w, wb);
+    case 2: return dispatch<OP_COL, OP_ROW, SS_F16>(p, s, "gemm_kernel<f16 tt>", w, wb);
+    case 3: return dispatch<OP_COL, OP_COL, SS_F16>(p, s, "gemm_kernel<f16 tn>", w, wb);
+    case 4: return dispatch<OP_ROW, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 nt>", w, wb);
+    case 5: return dispatch<OP_ROW, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 nn>", w, wb);
+    case 6: return dispatch<OP_COL, OP_ROW, SS_F32>(p, s, "gemm_kernel<f32 tt>", w, wb);
+    default: return dispatch<OP_COL, OP_COL, SS_F32>(p, s, "gemm_kernel<f32 tn>", w, wb);
   }
 }
 
@@ -1253,8 +1254,10 @@ extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64
 
 extern "C" size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m, int64_t n,
                                              int64_t k) {
-  // Split-K partials of the dense NT kernel (both operands K-contiguous).
-  return !a_trans && b_trans ? ss::nt_partial_bytes(m, n, k) : 0;
+  // Split-K partials of the dense NT kernel (every operand layout).
+  (void)a_trans;
+  (void)b_trans;
+  return ss::nt_partial_bytes(m, n, k);
 }
 
 extern "C" int ss_gemm_f16_split(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,

@@ -32,62 +32,131 @@ namespace {
 // the pipelined direct-to-LDS main loop.  All of the workgroup's LDS DMAs
 // have completed when it returns; the caller puts a barrier between two calls
 // (the last k-step's LDS reads of one call and the first DMAs of the next).
-template <class C>
+// Operand sources of one workgroup's tile (both main loops): per-lane DMA
+// sources as 32-bit byte offsets from the per-stage operand base, and the
+// per-stage advance of that base.  Rows past M / N (row-major operands) or
+// chunks past M / N (K-major operands, L bits 0 / 1) are clamped to the last
+// valid ones: they only feed accumulator rows / columns that are never stored.
+template <class C, int L>
+struct NtSources {
+  static constexpr bool AT = (L & 1) != 0, BT = (L & 2) != 0;
+  uint32_t a_off[C::kDmaA];
+  uint32_t b_off[C::kDmaB];
+  const half_t* a_base;
+  const half_t* b_base;
+  int64_t a_step, b_step;  // elements per stage
+
+  __device__ __forceinline__ NtSources(const GemmParams& p, int64_t m0, int64_t n0, int64_t kbeg,
+                                       int wave, int lane) {
+    a_base = AT ? p.A + kbeg * p.lda : p.A + kbeg;
+    b_base = BT ? p.B + kbeg * p.ldb : p.B + kbeg;
+    a_step = AT ? (int64_t)C::BK * p.lda : C::BK;
+    b_step = BT ? (int64_t)C::BK * p.ldb : C::BK;
+#pragma unroll
+    for (int j = 0; j < C::kDmaA; ++j) {
+      int row, chunk;
+      if constexpr (AT) {
+        dma_source_t<C::BM>(wave * C::kDmaA + j, lane, row, chunk);
+        const int64_t col = m0 + 8 * chunk <= p.M - 8 ? m0 + 8 * chunk : p.M - 8;
+        a_off[j] = (uint32_t)((row * p.lda + col) * 2);
+      } else {
+        dma_source<C::BK>(wave * C::kDmaA + j, lane, row, chunk);
+        const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
+        a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::kDmaB; ++j) {
+      int row, chunk;
+      if constexpr (BT) {
+        dma_source_t<C::BN>(wave * C::kDmaB + j, lane, row, chunk);
+        const int64_t col = n0 + 8 * chunk <= p.N - 8 ? n0 + 8 * chunk : p.N - 8;
+        b_off[j] = (uint32_t)((row * p.ldb + col) * 2);
+      } else {
+        dma_source<C::BK>(wave * C::kDmaB + j, lane, row, chunk);
+        const int64_t gr = n0 + row < p.N ? n0 + row : p.N - 1;
+        b_off[j] = (uint32_t)((gr * p.ldb + chunk * 8) * 2);
+      }
+    }
+  }
+};
+
+// Fragment offsets of one wave (both main loops): for a row-major operand the
+// lane's offset per k-step plus the 32-row group stride; for a K-major one the
+// offset of every (k-step, block) pair, read with read_frag_t.
+template <class C, int L>
+struct NtFrags {
+  static constexpr bool AT = (L & 1) != 0, BT = (L & 2) != 0;
+  static constexpr int kGroupBytes = 32 * C::BK * 2;
+  int row_off[C::KK];
+  int a_off[AT ? C::KK : 1][AT ? C::FM : 1];
+  int b_off[BT ? C::KK : 1][BT ? C::FN : 1];
+  int a_base, b_base;
+
+  __device__ __forceinline__ NtFrags(int lane, int wm, int wn) {
+#pragma unroll
+    for (int kk = 0; kk < C::KK; ++kk) row_off[kk] = frag_offset<C::BK>(lane, kk);
+    a_base = (wm * C::WM / 32) * kGroupBytes;
+    b_base = C::kTileA + (wn * C::WN / 32) * kGroupBytes;
+    if constexpr (AT) {
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+          a_off[kk][i] = frag_offset_t<C::BM>(lane, kk, wm * C::WM + 32 * i);
+    }
+    if constexpr (BT) {
+#pragma unroll
+      for (int kk = 0; kk < C::KK; ++kk)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+          b_off[kk][j] = C::kTileA + frag_offset_t<C::BN>(lane, kk, wn * C::WN + 32 * j);
+    }
+  }
+  __device__ __forceinline__ half8 a(const unsigned char* stage, int kk, int i) const {
+    if constexpr (AT)
+      return read_frag_t(stage + a_off[kk][i], C::BM * 2);
+    else
+      return *reinterpret_cast<const half8*>(stage + a_base + row_off[kk] + i * kGroupBytes);
+  }
+  __device__ __forceinline__ half8 b(const unsigned char* stage, int kk, int j) const {
+    if constexpr (BT)
+      return read_frag_t(stage + b_off[kk][j], C::BN * 2);
+    else
+      return *reinterpret_cast<const half8*>(stage + b_base + row_off[kk] + j * kGroupBytes);
+  }
+};
+
+template <class C, int L = 0>
 __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
                                             int64_t kbeg, int64_t klen, unsigned char* smem,
                                             NtAcc<C>& acc) {
-  constexpr int kGroupBytes = 32 * C::BK * 2;  // one 32-row group of a stage tile
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / C::kWavesN;
   const int wn = wave % C::kWavesN;
   const uint32_t lds0 = lds_address(smem);
-  const half_t* a_base = p.A + kbeg;
-  const half_t* b_base = p.B + kbeg;
-
-  // Per-lane DMA sources as 32-bit byte offsets from the operand base (the
-  // host checks that they fit).  Rows past M / N are clamped to the last
-  // row: they only feed accumulator rows that are never stored.
-  uint32_t a_off[C::kDmaA];
-  uint32_t b_off[C::kDmaB];
-#pragma unroll
-  for (int j = 0; j < C::kDmaA; ++j) {
-    int row, chunk;
-    dma_source<C::BK>(wave * C::kDmaA + j, lane, row, chunk);
-    const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
-    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
-  }
-#pragma unroll
-  for (int j = 0; j < C::kDmaB; ++j) {
-    int row, chunk;
-    dma_source<C::BK>(wave * C::kDmaB + j, lane, row, chunk);
-    const int64_t gr = n0 + row < p.N ? n0 + row : p.N - 1;
-    b_off[j] = (uint32_t)((gr * p.ldb + chunk * 8) * 2);
-  }
+  const NtSources<C, L> src(p, m0, n0, kbeg, wave, lane);
   const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
   const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds0 + C::kTileA + wave * C::kDmaB * 1024);
-
-  int frag_off[C::KK];
-#pragma unroll
-  for (int kk = 0; kk < C::KK; ++kk) frag_off[kk] = frag_offset<C::BK>(lane, kk);
+  const NtFrags<C, L> frags(lane, wm, wn);
 
   auto dma_one = [&](int64_t kt, int stage, int idx) {
     if (idx < C::kDmaA) {
-      dma16(a_off[idx], a_base + kt * C::BK, lds_a + stage * C::kStageBytes + idx * 1024);
+      dma16(src.a_off[idx], src.a_base + kt * src.a_step,
+            lds_a + stage * C::kStageBytes + idx * 1024);
     } else {
       const int j = idx - C::kDmaA;
-      dma16(b_off[j], b_base + kt * C::BK, lds_b + stage * C::kStageBytes + j * 1024);
+      dma16(src.b_off[j], src.b_base + kt * src.b_step, lds_b + stage * C::kStageBytes + j * 1024);
     }
   };
   auto read_frags = [&](int64_t kt, int kk, half8 (&af)[C::FM], half8 (&bf)[C::FN]) {
     const unsigned char* base = smem + (kt % C::STAGES) * C::kStageBytes;
-    const unsigned char* sa = base + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
-    const unsigned char* sb = base + C::kTileA + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
+    for (int i = 0; i < C::FM; ++i) af[i] = frags.a(base, kk, i);
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+    for (int j = 0; j < C::FN; ++j) bf[j] = frags.b(base, kk, j);
   };
   // MFMA phases raise the wave's issue priority (s_setprio 1), so a SIMD's
   // other wave, in its load / LDS phase, does not delay them (measured +7 % at
@@ -172,12 +241,11 @@ __device__ __forceinline__ void nt_mainloop(const GemmParams& p, int64_t m0, int
 // precedes a barrier that ends before either group reads that stage.  The
 // MFMAs of every accumulator run in the order of nt_mainloop, so the results
 // are the same bit for bit.
-template <class C>
+template <class C, int L = 0>
 __device__ __forceinline__ void nt_mainloop_pp(const GemmParams& p, int64_t m0, int64_t n0,
                                                int64_t kbeg, int64_t klen, unsigned char* smem,
                                                NtAcc<C>& acc) {
   static_assert(C::kWaves == 8 && C::KK == 2, "ping-pong: 8 waves, two k-steps per stage");
-  constexpr int kGroupBytes = 32 * C::BK * 2;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: scalar branches
@@ -185,29 +253,10 @@ __device__ __forceinline__ void nt_mainloop_pp(const GemmParams& p, int64_t m0, 
   const int wn = wave % C::kWavesN;
   const bool late = wave >= 4;  // SIMD partner of wave - 4
   const uint32_t lds0 = lds_address(smem);
-  const half_t* a_base = p.A + kbeg;
-  const half_t* b_base = p.B + kbeg;
-  uint32_t a_off[C::kDmaA];
-  uint32_t b_off[C::kDmaB];
-#pragma unroll
-  for (int j = 0; j < C::kDmaA; ++j) {
-    int row, chunk;
-    dma_source<C::BK>(wave * C::kDmaA + j, lane, row, chunk);
-    const int64_t gr = m0 + row < p.M ? m0 + row : p.M - 1;
-    a_off[j] = (uint32_t)((gr * p.lda + chunk * 8) * 2);
-  }
-#pragma unroll
-  for (int j = 0; j < C::kDmaB; ++j) {
-    int row, chunk;
-    dma_source<C::BK>(wave * C::kDmaB + j, lane, row, chunk);
-    const int64_t gr = n0 + row < p.N ? n0 + row : p.N - 1;
-    b_off[j] = (uint32_t)((gr * p.ldb + chunk * 8) * 2);
-  }
+  const NtSources<C, L> src(p, m0, n0, kbeg, wave, lane);
   const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
   const uint32_t lds_b = __builtin_amdgcn_readfirstlane(lds0 + C::kTileA + wave * C::kDmaB * 1024);
-  int frag_off[2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) frag_off[kk] = frag_offset<C::BK>(lane, kk);
+  const NtFrags<C, L> frags(lane, wm, wn);
 
   constexpr int kS = C::STAGES;
   const int64_t ktiles = klen / C::BK;
@@ -216,10 +265,10 @@ __device__ __forceinline__ void nt_mainloop_pp(const GemmParams& p, int64_t m0, 
     const int stage = (int)(kt % kS);
 #pragma unroll
     for (int j = 0; j < C::kDmaA; ++j)
-      dma16(a_off[j], a_base + kt * C::BK, lds_a + stage * C::kStageBytes + j * 1024);
+      dma16(src.a_off[j], src.a_base + kt * src.a_step, lds_a + stage * C::kStageBytes + j * 1024);
 #pragma unroll
     for (int j = 0; j < C::kDmaB; ++j)
-      dma16(b_off[j], b_base + kt * C::BK, lds_b + stage * C::kStageBytes + j * 1024);
+      dma16(src.b_off[j], src.b_base + kt * src.b_step, lds_b + stage * C::kStageBytes + j * 1024);
   };
   auto barrier = [&]() {
     __builtin_amdgcn_sched_barrier(0);
@@ -238,14 +287,10 @@ __device__ __forceinline__ void nt_mainloop_pp(const GemmParams& p, int64_t m0, 
     const unsigned char* base = smem + (kt % kS) * C::kStageBytes;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const unsigned char* sa = base + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
-      const unsigned char* sb = base + C::kTileA + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
 #pragma unroll
-      for (int i = 0; i < C::FM; ++i)
-        fa[kk][i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
+      for (int i = 0; i < C::FM; ++i) fa[kk][i] = frags.a(base, kk, i);
 #pragma unroll
-      for (int j = 0; j < C::FN; ++j)
-        fb[kk][j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+      for (int j = 0; j < C::FN; ++j) fb[kk][j] = frags.b(base, kk, j);
     }
     if (kt >= 1) issue_stage(kt - 1 + kS);
     {
@@ -284,7 +329,7 @@ constexpr int nt_smem_bytes() {
 // EPI_PARTIAL stores its fp32 accumulator to split plane `split`).  Workgroups past the tiles run the
 // optional rank-16 grad tail (p.tail; rank-16 epilogue, unsplit launches)
 // after the GEMM tiles, filling CUs the GEMM leaves idle.
-template <class C, int CT, int EPI>
+template <class C, int CT, int EPI, int L = 0>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[nt_smem_bytes<C, EPI>()];
   const int64_t tiles = gridDim.x - p.tail_blocks - p.tail2_blocks;
@@ -313,11 +358,11 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
   if constexpr (C::kWaves == 8 && C::KK == 2) {
     if (p.pingpong)
-      nt_mainloop_pp<C>(p, m0, n0, kbeg, klen, smem, acc);
+      nt_mainloop_pp<C, L>(p, m0, n0, kbeg, klen, smem, acc);
     else
-      nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+      nt_mainloop<C, L>(p, m0, n0, kbeg, klen, smem, acc);
   } else {
-    nt_mainloop<C>(p, m0, n0, kbeg, klen, smem, acc);
+    nt_mainloop<C, L>(p, m0, n0, kbeg, klen, smem, acc);
   }
   static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= nt_smem_bytes<C, EPI>(), "stage");
   nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem, split);
@@ -487,19 +532,42 @@ using NtBig8s4 = NtCfg<256, 256, 2, 4, 32, 4, 2>;   // 8 waves of 128x64, 128 Ki
 using NtWide8s4 = NtCfg<256, 128, 4, 2, 32, 4, 1>;  // 8 waves of 64x64, 96 KiB LDS
 using NtTall8s4 = NtCfg<128, 256, 2, 4, 32, 4, 1>;  // 8 waves of 64x64, 96 KiB LDS
 
-template <class C, int CT, int EPI>
+template <class C, int CT, int EPI, int L = 0>
 int launch_nt(const GemmParams& p, int64_t splits, hipStream_t stream) {
   const dim3 grid((unsigned)(cdiv(p.M, C::BM) * cdiv(p.N, C::BN) + p.tail_blocks +
                              p.tail2_blocks),
                   (unsigned)splits);
-  hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI>), grid, dim3(C::kThreads), 0, stream, p);
+  hipLaunchKernelGGL((gemm_nt_kernel<C, CT, EPI, L>), grid, dim3(C::kThreads), 0, stream, p);
   SS_CHECK_LAUNCH("gemm_nt_kernel");
   if (EPI == EPI_GLU && p.glu_done) *p.glu_done = 1;
   return SS_OK;
 }
 
+// K-major operands (L != 0) take the configurations nt_plan picks (1, 2, 8, 9,
+// 10); the others are reached only through a build-time override and keep
+// row-major operands.
+template <int CT, int EPI, int L>
+int dispatch_nt_t(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
+  switch (cfg) {
+    case 10: return launch_nt<NtTall8s4, CT, EPI, L>(p, splits, stream);
+    case 9: return launch_nt<NtWide8s4, CT, EPI, L>(p, splits, stream);
+    case 8: return launch_nt<NtBig8s4, CT, EPI, L>(p, splits, stream);
+    case 2: return launch_nt<NtMid, CT, EPI, L>(p, splits, stream);
+    case 1: return launch_nt<NtSmall, CT, EPI, L>(p, splits, stream);
+    default: return SS_ERR_UNSUPPORTED;
+  }
+}
+
 template <int CT, int EPI>
 int dispatch_nt(const GemmParams& p, int cfg, int64_t splits, hipStream_t stream) {
+  const int layout = (p.a_t ? 1 : 0) | (p.b_t ? 2 : 0);
+  if constexpr (EPI == EPI_PLAIN || EPI == EPI_PARTIAL) {
+    if (layout == 1) return dispatch_nt_t<CT, EPI, 1>(p, cfg, splits, stream);
+    if (layout == 2) return dispatch_nt_t<CT, EPI, 2>(p, cfg, splits, stream);
+    if (layout == 3) return dispatch_nt_t<CT, EPI, 3>(p, cfg, splits, stream);
+  } else {
+    if (layout) return SS_ERR_UNSUPPORTED;
+  }
   switch (cfg) {
     case 10: return launch_nt<NtTall8s4, CT, EPI>(p, splits, stream);
     case 9: return launch_nt<NtWide8s4, CT, EPI>(p, splits, stream);
@@ -637,10 +705,16 @@ int gemm_nt(const GemmParams& p0, int ct, int epi, hipStream_t stream, void* par
   if (p.M <= 0 || p.N <= 0 || p.K <= 0 || p.K % 64 != 0) return SS_ERR_UNSUPPORTED;  // K % 64
   if (!aligned16(p.A) || !aligned16(p.B) || p.lda % 8 != 0 || p.ldb % 8 != 0)
     return SS_ERR_UNSUPPORTED;
-  // The DMA addresses operands with 32-bit byte offsets from their base.
+  // K-major operands: whole 16-byte chunks along M / N, plain or split-K
+  // epilogues only.
+  if ((p.a_t && p.M % 8 != 0) || (p.b_t && p.N % 8 != 0)) return SS_ERR_UNSUPPORTED;
+  if ((p.a_t || p.b_t) && (epi != EPI_PLAIN || p.glu)) return SS_ERR_UNSUPPORTED;
+  // The DMA addresses operands with 32-bit byte offsets from their base (per
+  // stage for K-major operands, whose base moves BK rows a stage).
   const int64_t kMaxOff = (int64_t)1 << 32;
-  if (((p.M - 1) * p.lda + p.K) * 2 >= kMaxOff || ((p.N - 1) * p.ldb + p.K) * 2 >= kMaxOff)
-    return SS_ERR_UNSUPPORTED;
+  const int64_t a_span = p.a_t ? 64 * p.lda + p.M : (p.M - 1) * p.lda + p.K;
+  const int64_t b_span = p.b_t ? 64 * p.ldb + p.N : (p.N - 1) * p.ldb + p.K;
+  if (a_span * 2 >= kMaxOff || b_span * 2 >= kMaxOff) return SS_ERR_UNSUPPORTED;
   if (epi != EPI_PLAIN && (!aligned16(p.lz) || (epi == EPI_LORA && !aligned16(p.lb))))
     return SS_ERR_UNSUPPORTED;
   if (ct != SS_F16 && epi != EPI_PLAIN) return SS_ERR_UNSUPPORTED;

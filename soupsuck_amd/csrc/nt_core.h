@@ -114,6 +114,53 @@ __device__ __forceinline__ int frag_offset(int lane, int kk) {
   }
 }
 
+// K-major operands (GemmParams::a_t / b_t: element (r, k) of the M x K or
+// N x K operand at X[k * ld + r], as a transposed view stores it).  Their stage
+// tile sits in LDS as BK rows (k) of W halves (W = BM or BN), row-major, with
+// 16-byte chunk L of row k at chunk L ^ tsw(k).  A DMA moves 64 / (W / 8) whole
+// rows; each lane fetches the global chunk that belongs at its LDS slot.
+//
+// Fragments come from two gfx950 ds_read_b64_tr_b16.  Measured lane layout: in
+// every 16-lane group, the 16 lanes' 8-byte reads form a 16 x 4 matrix M (row =
+// reading lane); lane i of the group receives M[4 j + i / 4][i % 4] for j = 0..3.
+// With lane l of group g = l / 16 pointing at row 16 kk + 8 (l / 32) + 4 h +
+// (l % 16) / 4 and column c + 16 (g % 2) + 4 (l % 4), read h = 0, 1 delivers k =
+// 16 kk + 8 (l / 32) + 4 h + 0..3 of column c + l % 32: the MFMA 32x32x16 operand
+// layout (8 consecutive k of one row / column per lane).  A group reads 4 rows x
+// 32 B; tsw spreads the 4 rows over 4 distinct 32-byte bank groups (W = 64, 128,
+// 256), so the reads are conflict-free.
+__device__ __forceinline__ int tsw(int k) { return (k & 3) << 1; }
+
+template <int W>
+__device__ __forceinline__ void dma_source_t(int g, int lane, int& row, int& chunk) {
+  constexpr int kChunks = W / 8;       // 16-byte chunks per row (>= 8)
+  constexpr int kRows = 64 / kChunks;  // rows per 1 KiB DMA
+  static_assert(kChunks >= 8 && 64 % kChunks == 0, "K-major tile width");
+  row = g * kRows + lane / kChunks;
+  chunk = (lane % kChunks) ^ tsw(row);
+}
+
+// Byte offset, in a K-major tile of width W, of the lane's first transposed read
+// for k-step kk and the 32-wide block at column cb; the second read is 4 rows
+// (4 W * 2 bytes) further.
+template <int W>
+__device__ __forceinline__ int frag_offset_t(int lane, int kk, int cb) {
+  const int k = 16 * kk + 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int col = cb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return k * (W * 2) + (((col >> 3) ^ tsw(k)) << 4) + ((col & 7) << 1);
+}
+
+typedef short nt_short4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) nt_short4 nt_lds_short4;
+
+__device__ __forceinline__ half8 read_frag_t(const unsigned char* p, int w_bytes) {
+  const nt_short4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((nt_lds_short4*)p);
+  const nt_short4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((nt_lds_short4*)(p + 4 * w_bytes));
+  typedef short short8 __attribute__((ext_vector_type(8)));
+  const short8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(half8, v);
+}
+
 template <class C>
 using NtAcc = float16v[C::FM][C::FN];
 

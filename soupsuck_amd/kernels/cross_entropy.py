@@ -23,10 +23,12 @@ gradient dW_c = dz'^T . h is also produced, from a second fp16 copy dz' of the
 derivative scaled by one global gain max_r |g_r| / 1024 (a per-row gain cannot
 be factored out of a sum over rows).
 
-Layout for the MFMA engine: the dense NT kernel wants both operands contiguous
-along the reduced dimension, so dX = dz . W_c uses W_c^T [H, width] per chunk
-(ss_transpose_f16) and dW_c = dz'^T . h uses h^T [H, T'] (built once, T' =
-rows with a target padded to 64 with zero columns) and dz'^T per chunk.
+Layout for the MFMA engine: the dense direct-to-LDS kernel reads operands stored
+along the reduced dimension (K-major) through transposed LDS reads, so dX = dz .
+W_c takes the head rows W_c [width, H] as they are, and dW_c = dz'^T . h takes
+dz' [T', width] and h [T', H] as they are, T' = rows with a target padded to a
+multiple of 64 with zero rows (the kernel reduces whole 64-deep steps).  No
+operand is transposed in memory.
 """
 
 import torch
@@ -34,7 +36,7 @@ from torch.autograd.function import once_differentiable
 
 from .. import _lib
 from ..contract import FLOAT_DTYPES, Rule, enforce, on_one_cuda_device
-from .nf4_gemm import gemm_f16, transpose_f16
+from .nf4_gemm import gemm_f16
 
 MAX_CHUNK = 8192            # BASELINE configs[3]'s vocabulary chunk
 TILE_BUDGET = 64 << 20      # bytes of one fp16 [rows, chunk] logits tile
@@ -58,9 +60,11 @@ def _head_rows(weight, start, width):
         w.to(torch.float16).contiguous()
 
 
-def _gather_rows(src, index):
-    """src[index] for a contiguous tensor and a device int64 index (ss_unpad_gather)."""
-    out = torch.empty((index.numel(), *src.shape[1:]), device=src.device, dtype=src.dtype)
+def _gather_rows(src, index, out=None):
+    """src[index] for a contiguous tensor and a device int64 index (ss_unpad_gather),
+    into ``out`` (contiguous, index.numel() rows) when given."""
+    if out is None:
+        out = torch.empty((index.numel(), *src.shape[1:]), device=src.device, dtype=src.dtype)
     row_bytes = (src[0].numel() if src.ndim > 1 else 1) * src.element_size()
     _lib.call("ss_unpad_gather", src.data_ptr(), src.shape[0], out.data_ptr(), index.data_ptr(),
               index.numel(), row_bytes, _lib.stream(src.device))
@@ -122,50 +126,55 @@ class _Backward:
         self.kept = kept.indices()
         self.count = self.kept.numel()
         if self.count:
-            self.h = _gather_rows(hidden16, self.kept)
+            # Rows with a target, then zero rows up to a multiple of 64: the K of the
+            # head-gradient product.
+            self.padded = -(-self.count // 64) * 64
+            self.h_pad = torch.empty((self.padded, hidden16.shape[1]), device=self.dev,
+                                     dtype=hidden16.dtype)
+            if self.padded > self.count:
+                self.h_pad[self.count:].zero_()
+            self.h = _gather_rows(hidden16, self.kept, out=self.h_pad[:self.count])
             self.targets = _gather_rows(targets, self.kept)
             self.lse = _gather_rows(lse, self.kept)
             self.grad = _gather_rows(grad, self.kept)
 
     def run(self, dx, dw):
         width_max = min(self.chunk, self.weight.shape[0])
+        count, padded = self.count, self.padded
         hdim = self.h.shape[1]
-        logits = torch.empty((self.count, width_max), device=self.dev, dtype=torch.float16)
+        logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
         dz = torch.empty_like(logits)
-        acc = torch.zeros((self.count, hdim), device=self.dev, dtype=torch.float32) \
-            if dx is not None else None
-        wt = torch.empty((hdim, width_max), device=self.dev, dtype=torch.float16) \
+        acc = torch.zeros((count, hdim), device=self.dev, dtype=torch.float32) \
             if dx is not None else None
         head_gain = 1.0
         if dw is not None:
             head_gain = max(self.grad.abs().max().item(), 1e-30) / 1024.0
-            padded = -(-self.count // 64) * 64
-            ht = torch.zeros((hdim, padded), device=self.dev, dtype=torch.float16)
-            transpose_f16(self.h, out=ht[:, :self.count])
-            dz_head = torch.empty_like(logits)
-            dz_head_t = torch.zeros((width_max, padded), device=self.dev, dtype=torch.float16)
+            # dz' per chunk as [padded, width] (dense rows): the rows past `count`
+            # stay zero; they are written only by a wider chunk's rows, so only a
+            # narrower chunk clears them.
+            dz_head = torch.zeros(padded * width_max, device=self.dev, dtype=torch.float16)
         for start, width in _vocab_chunks(self.weight.shape[0], self.chunk):
             w = _head_rows(self.weight, start, width)
             z = logits[:, :width]
             gemm_f16(self.h, w, b_trans=True, out=z)
-            d = dz.view(-1)[:self.count * width].view(self.count, width)
-            dh = dz_head.view(-1)[:self.count * width].view(self.count, width) \
-                if dw is not None else None
+            d = dz.view(-1)[:count * width].view(count, width)
+            dh = None
+            if dw is not None:
+                dh = dz_head[:padded * width].view(padded, width)
+                if width < width_max and padded > count:
+                    dz_head[count * width:padded * width].zero_()
             _lib.call("ss_ce_derivative", z.data_ptr(), logits.stride(0),
                       self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
-                      d.data_ptr(), _lib.ptr(dh), float(head_gain), self.count, width, start,
+                      d.data_ptr(), _lib.ptr(dh), float(head_gain), count, width, start,
                       self.ignore, self.stream)
             if acc is not None:
-                gemm_f16(d, transpose_f16(w, out=wt[:, :width]), b_trans=True, out=acc,
-                         accumulate=True, split_k=True)
+                gemm_f16(d, w, out=acc, accumulate=True, split_k=True)
             if dw is not None:
-                transpose_f16(dh, out=dz_head_t[:width, :self.count])
                 rows_w = dw.narrow(0, start, width)
                 if rows_w.dtype in FLOAT_DTYPES:
-                    gemm_f16(dz_head_t[:width], ht, b_trans=True, out=rows_w,
-                             alpha=float(head_gain))
+                    gemm_f16(dh, self.h_pad, a_trans=True, out=rows_w, alpha=float(head_gain))
                 else:
-                    rows_w.copy_(gemm_f16(dz_head_t[:width], ht, b_trans=True,
+                    rows_w.copy_(gemm_f16(dh, self.h_pad, a_trans=True,
                                           out_dtype=torch.float32, alpha=float(head_gain)))
         if acc is not None:
             rows, hd = dx.shape
@@ -201,15 +210,23 @@ class LinearCrossEntropy(torch.autograd.Function):
         if grad_loss is None or not (want_x or want_w):
             return nothing
         hidden16, weight, targets, lse = ctx.saved_tensors
-        dx = torch.zeros(hidden16.shape, device=hidden16.device, dtype=hidden_dtype) \
+        # Uninitialised: with a labelled row, ss_ce_finalize_dx writes every row of dX and
+        # the chunk GEMMs every row of dW (a 467 MB fill at V = 151936 saved); without
+        # one both gradients are zero.
+        dx = torch.empty(hidden16.shape, device=hidden16.device, dtype=hidden_dtype) \
             if want_x else None
-        dw = torch.zeros(weight.shape, device=weight.device, dtype=weight.dtype) \
+        dw = torch.empty(weight.shape, device=weight.device, dtype=weight.dtype) \
             if want_w else None
+        back = None
         if hidden16.shape[0]:
             grad = grad_loss.float().contiguous()
             back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk, ctx.kept)
-            if back.count:
-                back.run(dx, dw)
+        if back is not None and back.count:
+            back.run(dx, dw)
+        else:
+            for g in (dx, dw):
+                if g is not None:
+                    g.zero_()
         return dx, dw, None, None, None, None
 
 

@@ -343,3 +343,47 @@ def test_forward_bitwise_equals_decode_then_dense(device, t, n, k):
               wd.data_ptr(), n * k, _lib.stream(device))
     ref = gemm_f16(x, wd, b_trans=True, split_k=True)
     assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("m,n,k,split", [
+    (2048, 3584, 512, False),   # 128x256 tiles (8 waves)
+    (4096, 4096, 128, False),   # 256x256 tiles, ping-pong main loop
+    (1024, 2048, 256, False),   # 128x128 tiles
+    (1000, 2008, 320, False),   # 128x128 tiles, ragged M and N
+    (200, 136, 1024, False),    # 64x64 tiles
+    (200, 136, 1024, True),     # 64x64 tiles split over K
+    (990, 1536, 8960, True),    # 256x128 tiles split over K
+    (1536, 1024, 4096, True),   # 128x128 tiles split over K
+    (8, 16, 64, False),         # one 64x64 tile, 8-wide chunks clamped at M / N
+])
+@pytest.mark.parametrize("a_trans,b_trans", [(False, False), (True, False), (True, True)])
+def test_dense_nt_k_major_operands(device, m, n, k, split, a_trans, b_trans):
+    """K-major operands (a_trans: A stored [K,M]; b_trans False: B stored [K,N]) on the
+    direct-to-LDS kernel, read with transposed LDS reads: the same tiles, splits and MFMA
+    order as the K-contiguous layout, so the output equals that layout's bit for bit, and
+    matches the float64 product (fp16 gate; fp32 out within 1e-5 relative).  A K-major
+    operand whose M / N is not a multiple of 8 takes the general kernel (no bitwise
+    comparison there)."""
+    rng = np.random.default_rng(m * 3 + n * 5 + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+    ad = torch.from_numpy(np.ascontiguousarray(a.T if a_trans else a)).to(device)
+    bd = torch.from_numpy(np.ascontiguousarray(b.T if b_trans else b)).to(device)
+    a_row = torch.from_numpy(a).to(device)
+    b_row = torch.from_numpy(np.ascontiguousarray(b.T)).to(device)
+    prod = a.astype(np.float64) @ b.astype(np.float64)
+    for out_dtype in (torch.float16, torch.float32):
+        c = gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out_dtype=out_dtype,
+                     split_k=split)
+        ref = gemm_f16(a_row, b_row, b_trans=True, out_dtype=out_dtype, split_k=split)
+        torch.cuda.synchronize()
+        if (not a_trans or m % 8 == 0) and (b_trans or n % 8 == 0):
+            assert torch.equal(c, ref), f"layout {a_trans},{b_trans} differs from K-contiguous"
+        if out_dtype == torch.float16:
+            check(c, prod, f"k-major {m}x{n}x{k}")
+        else:
+            np.testing.assert_allclose(np16(c), prod, rtol=1e-5, atol=5e-4)
+    base = rng.standard_normal((m, n)).astype(np.float32)
+    acc = torch.from_numpy(base).to(device)
+    gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out=acc, accumulate=True, split_k=split)
+    np.testing.assert_allclose(np16(acc), base + prod, rtol=1e-5, atol=5e-4)
