@@ -453,12 +453,14 @@ int ss_ce_outputs(const float* state, const int64_t* targets, float* loss, float
 /* dz[r, c] = fp16((exp(z - lse[r]) - [start + c == target[r]]) * grad[r] / gain[r]),
  * gain[r] = max(|grad[r]|, 1e-30) / 1024 (zero on ignored rows); when dz_global
  * is not NULL it also receives the same derivative scaled by 1/global_gain
- * instead of 1/gain[r] (for the lm_head gradient).  Replaces
- * vocabulary_derivative_kernel (solution/kernels/cross_entropy.py:108-122). */
-int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* targets, const float* lse,
-                     const float* grad, uint16_t* dz, uint16_t* dz_global, float global_gain,
-                     int64_t n, int64_t width, int64_t start, int64_t ignore_index,
-                     void* stream);
+ * instead of 1/gain[r] (for the lm_head gradient).  dz and dz_global are dense
+ * [n, width].  Row r of the logits is z[z_rows[r]] when z_rows (int64 [n]) is
+ * not NULL, else z[r] (row stride ldz).  Replaces vocabulary_derivative_kernel
+ * (solution/kernels/cross_entropy.py:108-122). */
+int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
+                     const int64_t* targets, const float* lse, const float* grad, uint16_t* dz,
+                     uint16_t* dz_global, float global_gain, int64_t n, int64_t width,
+                     int64_t start, int64_t ignore_index, void* stream);
 
 /* out[r, :] = cast(acc[inverse[r], :] * max(|grad[r]|, 1e-30) / 1024) when
  * inverse[r] >= 0 (a valid row, compacted to position inverse[r]), else 0:

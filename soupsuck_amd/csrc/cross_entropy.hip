@@ -8,7 +8,11 @@
 // ce_stats: one 256-thread workgroup per row; pass 1 finds the chunk max and
 // its first index, pass 2 accumulates sum exp(z - m) and sum exp(z - m) * z
 // against the merged running max.  Lanes read 8 consecutive fp16 logits
-// (16 B), so a wave reads 1 KiB contiguous per access.
+// (16 B), so a wave reads 1 KiB contiguous per access.  Chunks up to 8192 wide
+// are read once, all of a lane's loads issued together into registers, and both
+// passes run from there (one memory round trip per row instead of one per
+// 2048 logits and pass); wider chunks re-read the row in pass 2.  Both forms
+// add in the same order, so they give the same bits.
 
 #include "elementwise.h"
 
@@ -54,6 +58,9 @@ __device__ __forceinline__ void load_logits8(const half_t* __restrict__ row, int
   }
 }
 
+constexpr int kStatsHeld = 4;  // 2048-logit steps a lane holds in registers (width <= 8192)
+
+template <bool HELD>
 __global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict__ z, int64_t ldz,
                                                        const int64_t* __restrict__ targets,
                                                        float* __restrict__ state,
@@ -67,26 +74,16 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict_
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const half_t* zr = z + row * ldz;
-
-  MaxArg ma{-INFINITY, kNoIndex};
-  for (int64_t c = (int64_t)tid * 8; c < width; c += 256 * 8) {
-    float v[8];
-    load_logits8(zr, c, width, vec, v);
+  // The lane's steps, logits c = 8 tid + 2048 i .. + 7 for c < width, in order.
+  // HELD: all of them loaded up front (load_logits8 touches no memory at or
+  // past `width`, so the loads of absent steps read nothing).
+  float held[HELD ? kStatsHeld : 1][8];
+  if constexpr (HELD) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (c + j < width && v[j] > ma.m) {
-        ma.m = v[j];
-        ma.a = start + c + j;
-      }
-    }
+    for (int i = 0; i < kStatsHeld; ++i)
+      load_logits8(zr, (int64_t)tid * 8 + 2048 * i, width, vec, held[i]);
   }
-  ma = wave_maxarg(ma);
-  if (lane == 0) s_ma[wave] = ma;
-  __syncthreads();
-  MaxArg tile = s_ma[0];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) tile = better(tile, s_ma[w]);
-
+  // The row's running state, read before the passes so its latency overlaps them.
   float old_m = -INFINITY, old_s = 0.0f, old_t = 0.0f, tz = 0.0f;
   int64_t old_arg = kNoIndex;
   if (!first) {
@@ -96,13 +93,43 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict_
     tz = state[row * 4 + 3];
     old_arg = best[row];
   }
-  const float new_m = fmaxf(old_m, tile.m);
   const int64_t tgt = targets[row];
+  auto each_step = [&](auto&& f) {
+    if constexpr (HELD) {
+#pragma unroll
+      for (int i = 0; i < kStatsHeld; ++i) {
+        const int64_t c = (int64_t)tid * 8 + 2048 * i;
+        if (c < width) f(c, held[i]);
+      }
+    } else {
+      for (int64_t c = (int64_t)tid * 8; c < width; c += 2048) {
+        float v[8];
+        load_logits8(zr, c, width, vec, v);
+        f(c, v);
+      }
+    }
+  };
+
+  MaxArg ma{-INFINITY, kNoIndex};
+  each_step([&](int64_t c, const float* v) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (c + j < width && v[j] > ma.m) {
+        ma.m = v[j];
+        ma.a = start + c + j;
+      }
+    }
+  });
+  ma = wave_maxarg(ma);
+  if (lane == 0) s_ma[wave] = ma;
+  __syncthreads();
+  MaxArg tile = s_ma[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) tile = better(tile, s_ma[w]);
+  const float new_m = fmaxf(old_m, tile.m);
 
   float sp = 0.0f, spz = 0.0f, found = 0.0f;
-  for (int64_t c = (int64_t)tid * 8; c < width; c += 256 * 8) {
-    float v[8];
-    load_logits8(zr, c, width, vec, v);
+  each_step([&](int64_t c, const float* v) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (c + j < width) {
@@ -113,7 +140,7 @@ __global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict_
         if (tgt != ignore && tgt == start + c + j) found += v[j];
       }
     }
-  }
+  });
   sp = wave_sum(sp);
   spz = wave_sum(spz);
   found = wave_sum(found);
@@ -168,7 +195,8 @@ __global__ __launch_bounds__(256) void ce_outputs_kernel(const float* __restrict
 }
 
 __global__ __launch_bounds__(256) void ce_derivative_kernel(
-    const half_t* __restrict__ z, int64_t ldz, const int64_t* __restrict__ targets,
+    const half_t* __restrict__ z, int64_t ldz, const int64_t* __restrict__ z_rows,
+    const int64_t* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ grad, half_t* __restrict__ dz,
     half_t* __restrict__ dzg, float global_gain, int64_t width, int64_t start, int64_t ignore,
     int vec) {
@@ -181,7 +209,7 @@ __global__ __launch_bounds__(256) void ce_derivative_kernel(
   const float gain = fmaxf(fabsf(g), 1e-30f) / 1024.0f;
   const float l = lse[row];
   float v[8];
-  load_logits8(z + row * ldz, c, width, vec, v);
+  load_logits8(z + (z_rows ? z_rows[row] : row) * ldz, c, width, vec, v);
   union {
     uint4 u;
     half8 h;
@@ -242,9 +270,14 @@ extern "C" int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* target
   if (n == 0) return SS_OK;
   SS_CHECK_ARG(z && targets && state && best, "ss_ce_stats: null pointer");
   const int vec = al16(z) && ldz % 8 == 0;
-  hipLaunchKernelGGL(ce_stats_kernel, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream,
-                     reinterpret_cast<const half_t*>(z), ldz, targets, state, best, width, start,
-                     ignore_index, first ? 1 : 0, vec);
+  if (width <= 2048 * kStatsHeld)
+    hipLaunchKernelGGL(ce_stats_kernel<true>, dim3((unsigned)n), dim3(256), 0,
+                       (hipStream_t)stream, reinterpret_cast<const half_t*>(z), ldz, targets,
+                       state, best, width, start, ignore_index, first ? 1 : 0, vec);
+  else
+    hipLaunchKernelGGL(ce_stats_kernel<false>, dim3((unsigned)n), dim3(256), 0,
+                       (hipStream_t)stream, reinterpret_cast<const half_t*>(z), ldz, targets,
+                       state, best, width, start, ignore_index, first ? 1 : 0, vec);
   SS_CHECK_LAUNCH("ce_stats_kernel");
   return SS_OK;
 }
@@ -261,10 +294,11 @@ extern "C" int ss_ce_outputs(const float* state, const int64_t* targets, float* 
   return SS_OK;
 }
 
-extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* targets,
-                                const float* lse, const float* grad, uint16_t* dz,
-                                uint16_t* dz_global, float global_gain, int64_t n, int64_t width,
-                                int64_t start, int64_t ignore_index, void* stream) {
+extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
+                                const int64_t* targets, const float* lse, const float* grad,
+                                uint16_t* dz, uint16_t* dz_global, float global_gain, int64_t n,
+                                int64_t width, int64_t start, int64_t ignore_index,
+                                void* stream) {
   SS_CHECK_ARG(n >= 0 && width > 0 && ldz >= width, "ss_ce_derivative: bad sizes");
   SS_CHECK_ARG(!dz_global || global_gain > 0.0f, "ss_ce_derivative: global_gain must be > 0");
   if (n == 0) return SS_OK;
@@ -274,7 +308,7 @@ extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* t
   SS_CHECK_ARG(cdiv(width, 256 * 8) < 65536, "ss_ce_derivative: width too large");
   const dim3 grid((unsigned)n, (unsigned)cdiv(width, 256 * 8));
   hipLaunchKernelGGL(ce_derivative_kernel, grid, dim3(256), 0, (hipStream_t)stream,
-                     reinterpret_cast<const half_t*>(z), ldz, targets, lse, grad,
+                     reinterpret_cast<const half_t*>(z), ldz, z_rows, targets, lse, grad,
                      reinterpret_cast<half_t*>(dz), reinterpret_cast<half_t*>(dz_global),
                      dz_global ? global_gain : 1.0f, width, start, ignore_index, vec);
   SS_CHECK_LAUNCH("ce_derivative_kernel");

@@ -23,6 +23,13 @@ gradient dW_c = dz'^T . h is also produced, from a second fp16 copy dz' of the
 derivative scaled by one global gain max_r |g_r| / 1024 (a per-row gain cannot
 be factored out of a sum over rows).
 
+Kept logits: when the fp16 logits [N, V] fit KEEP_LOGITS_BUDGET (1 GiB; 251 MB
+at configs[3]) and a backward may run, the forward's chunk products write into
+one [N, V] buffer and the backward reads each chunk from there (rows picked
+through the labelled-row indices) instead of recomputing h . W_c^T: the same
+bits, one product per chunk fewer.  Above the budget the backward recomputes,
+as the reference does, holding one [rows, chunk] tile at a time.
+
 Layout for the MFMA engine: the dense direct-to-LDS kernel reads operands stored
 along the reduced dimension (K-major) through transposed LDS reads, so dX = dz .
 W_c takes the head rows W_c [width, H] as they are, and dW_c = dz'^T . h takes
@@ -40,6 +47,11 @@ from .nf4_gemm import gemm_f16
 
 MAX_CHUNK = 8192            # BASELINE configs[3]'s vocabulary chunk
 TILE_BUDGET = 64 << 20      # bytes of one fp16 [rows, chunk] logits tile
+# Bytes of fp16 logits [rows, V] the forward may keep for the backward, which
+# then reads them instead of recomputing each chunk's product (the same bits:
+# the backward's recomputed chunk equals the forward's).  Larger outputs are
+# recomputed chunk by chunk, holding one [rows, chunk] tile at a time.
+KEEP_LOGITS_BUDGET = 1 << 30
 
 
 def default_chunk(rows):
@@ -71,7 +83,9 @@ def _gather_rows(src, index, out=None):
     return out
 
 
-def _forward(hidden16, weight, targets, ignore_index, chunk):
+def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
+    """Loss, entropy, first argmax and lse; with ``keep`` also the fp16 logits [rows, V]
+    (the chunk products write straight into their columns), else None."""
     rows = hidden16.shape[0]
     dev = hidden16.device
     loss = torch.empty(rows, device=dev, dtype=torch.float32)
@@ -79,19 +93,21 @@ def _forward(hidden16, weight, targets, ignore_index, chunk):
     lse = torch.empty(rows, device=dev, dtype=torch.float32)
     best = torch.empty(rows, device=dev, dtype=torch.int64)
     if rows == 0:
-        return loss, entropy, best, lse
+        return loss, entropy, best, lse, None
     stream = _lib.stream(dev)
     online = torch.empty((rows, 4), device=dev, dtype=torch.float32)
-    tile = torch.empty((rows, min(chunk, weight.shape[0])), device=dev, dtype=torch.float16)
-    for start, width in _vocab_chunks(weight.shape[0], chunk):
-        logits = tile[:, :width]
+    vocab = weight.shape[0]
+    tile = torch.empty((rows, vocab if keep else min(chunk, vocab)), device=dev,
+                       dtype=torch.float16)
+    for start, width in _vocab_chunks(vocab, chunk):
+        logits = tile[:, start:start + width] if keep else tile[:, :width]
         gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True, out=logits)
         _lib.call("ss_ce_stats", logits.data_ptr(), tile.stride(0), targets.data_ptr(),
                   online.data_ptr(), best.data_ptr(), rows, width, start, ignore_index,
                   int(start == 0), stream)
     _lib.call("ss_ce_outputs", online.data_ptr(), targets.data_ptr(), loss.data_ptr(),
               entropy.data_ptr(), lse.data_ptr(), rows, ignore_index, stream)
-    return loss, entropy, best, lse
+    return loss, entropy, best, lse, tile if keep else None
 
 
 class _KeptRows:
@@ -118,8 +134,10 @@ class _KeptRows:
 class _Backward:
     """Gradients of the summed loss w.r.t. hidden and (optionally) the head."""
 
-    def __init__(self, hidden16, weight, targets, lse, grad, ignore_index, chunk, kept):
+    def __init__(self, hidden16, weight, targets, lse, grad, ignore_index, chunk, kept,
+                 logits=None):
         self.weight, self.ignore, self.chunk = weight, ignore_index, chunk
+        self.logits = logits  # the forward's fp16 [rows, V] logits, or None: recompute
         self.dev = hidden16.device
         self.stream = _lib.stream(self.dev)
         self.full_grad = grad
@@ -142,8 +160,10 @@ class _Backward:
         width_max = min(self.chunk, self.weight.shape[0])
         count, padded = self.count, self.padded
         hdim = self.h.shape[1]
-        logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
-        dz = torch.empty_like(logits)
+        kept_z = self.logits
+        if kept_z is None:
+            logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
+        dz = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
         acc = torch.zeros((count, hdim), device=self.dev, dtype=torch.float32) \
             if dx is not None else None
         head_gain = 1.0
@@ -155,15 +175,19 @@ class _Backward:
             dz_head = torch.zeros(padded * width_max, device=self.dev, dtype=torch.float16)
         for start, width in _vocab_chunks(self.weight.shape[0], self.chunk):
             w = _head_rows(self.weight, start, width)
-            z = logits[:, :width]
-            gemm_f16(self.h, w, b_trans=True, out=z)
+            if kept_z is None:
+                z, ldz, z_rows = logits[:, :width], logits.stride(0), None
+                gemm_f16(self.h, w, b_trans=True, out=z)
+            else:
+                # The forward's chunk, its rows picked through the kept-row indices.
+                z, ldz, z_rows = kept_z[:, start:start + width], kept_z.stride(0), self.kept
             d = dz.view(-1)[:count * width].view(count, width)
             dh = None
             if dw is not None:
                 dh = dz_head[:padded * width].view(padded, width)
                 if width < width_max and padded > count:
                     dz_head[count * width:padded * width].zero_()
-            _lib.call("ss_ce_derivative", z.data_ptr(), logits.stride(0),
+            _lib.call("ss_ce_derivative", z.data_ptr(), ldz, _lib.ptr(z_rows),
                       self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
                       d.data_ptr(), _lib.ptr(dh), float(head_gain), count, width, start,
                       self.ignore, self.stream)
@@ -193,7 +217,11 @@ class LinearCrossEntropy(torch.autograd.Function):
         targets = targets.contiguous()
         chunk = chunk or default_chunk(hidden16.shape[0])
         ctx.kept = _KeptRows(targets, ignore_index) if hidden16.shape[0] else None
-        loss, entropy, best, lse = _forward(hidden16, weight, targets, ignore_index, chunk)
+        backward_may_run = ctx.needs_input_grad[0] or (weight_grad and ctx.needs_input_grad[1])
+        keep = backward_may_run and \
+            hidden16.shape[0] * weight.shape[0] * 2 <= KEEP_LOGITS_BUDGET
+        loss, entropy, best, lse, ctx.logits = _forward(hidden16, weight, targets, ignore_index,
+                                                        chunk, keep)
         ctx.save_for_backward(hidden16, weight, targets, lse)
         ctx.setup = (hidden.dtype, ignore_index, chunk, weight_grad)
         ctx.mark_non_differentiable(entropy, best, lse)
@@ -204,6 +232,7 @@ class LinearCrossEntropy(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_loss, *_unused):
         hidden_dtype, ignore_index, chunk, weight_grad = ctx.setup
+        logits, ctx.logits = ctx.logits, None  # kept logits serve one backward
         want_x = ctx.needs_input_grad[0]
         want_w = weight_grad and ctx.needs_input_grad[1]
         nothing = (None,) * 6
@@ -220,7 +249,8 @@ class LinearCrossEntropy(torch.autograd.Function):
         back = None
         if hidden16.shape[0]:
             grad = grad_loss.float().contiguous()
-            back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk, ctx.kept)
+            back = _Backward(hidden16, weight, targets, lse, grad, ignore_index, chunk, ctx.kept,
+                             logits)
         if back is not None and back.count:
             back.run(dx, dw)
         else:

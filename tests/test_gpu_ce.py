@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import cross_entropy as oce
+from soupsuck_amd.kernels import cross_entropy as ce_mod
 from soupsuck_amd.kernels.cross_entropy import default_chunk, fused_linear_cross_entropy
 from tests.gpu_util import np16, rel_norm
 
@@ -39,6 +40,7 @@ def inputs(n, h, v, ignored="some", scale=1.0, seed=123):
     (77, 64, 1000, "all", 1.0, None), (77, 64, 1000, "none", 20.0, None),
     (77, 80, 4103, "some", 1.0, 4096), (1, 33, 7, "none", 1.0, None),
     (300, 128, 9000, "some", 1.0, 8192),
+    (200, 64, 20000, "some", 1.0, 16384),   # a chunk wider than the stats kernel holds
 ])
 @pytest.mark.parametrize("weight_grad", [False, True])
 def test_matches_oracle(device, n, h, v, ignored, scale, chunk, weight_grad):
@@ -154,3 +156,27 @@ def test_config4_full_shape_against_fp32_torch(device):
     rdx = torch.cat(ref_dx)
     assert ((x.grad.float() - rdx).norm() / rdx.norm()).item() <= 1e-2
     assert ((w.grad.float() - ref_dw).norm() / ref_dw.norm()).item() <= 1e-2
+
+
+@pytest.mark.parametrize("n,h,v", [(600, 256, 20000), (826, 1536, 151936)])
+def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v):
+    """The backward reading the forward's kept logits gives the same bits as the
+    backward that recomputes each chunk (budget 0), outputs and both gradients."""
+    gen = torch.Generator(device="cpu").manual_seed(n)
+    x0 = torch.randn((n, h), generator=gen).to(torch.float16).to(device)
+    w0 = (torch.randn((v, h), generator=gen) * 0.02).to(torch.float16).to(device)
+    y = torch.randint(0, v, (n,), generator=gen)
+    y[torch.rand(n, generator=gen) < 0.365] = -100
+    y = y.to(device)
+    g = torch.randn(n, generator=gen).to(device)
+    runs = []
+    for budget in (ce_mod.KEEP_LOGITS_BUDGET, 0):
+        monkeypatch.setattr(ce_mod, "KEEP_LOGITS_BUDGET", budget)
+        x = x0.clone().requires_grad_()
+        w = w0.clone().requires_grad_()
+        outs = fused_linear_cross_entropy(x, w, y, chunk=8192, weight_grad=True)
+        outs[0].backward(g)
+        torch.cuda.synchronize()
+        runs.append((*outs, x.grad, w.grad))
+    for kept, recomputed in zip(*runs):
+        assert torch.equal(kept, recomputed)
