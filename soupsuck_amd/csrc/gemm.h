@@ -296,8 +296,8 @@ bool gemm_nf4_fwd_preferred(const GemmParams& p);
 // The fused kernel's tile / split plan and its split-K scratch (0: no split).
 NtPlan nf4_plan(int64_t m, int64_t n, int64_t k);
 size_t nf4_fused_partial_bytes(int64_t m, int64_t n, int64_t k);
-// Fused NF4 dX for T <= 256 (gemm_nf4.hip): the W^T tiles decoded into LDS
-// inside the GEMM; plain (beta) and rank-16 epilogues.  Split-K partials in
+// Fused NF4 dX for T <= 256 (gemm_nf4.hip): the weight tiles decoded into LDS
+// (K-major B tiles) inside the GEMM; plain (beta) and rank-16 epilogues.  Split-K partials in
 // `partials` (nf4_dx_fused_partial_bytes); SS_ERR_UNSUPPORTED when
 // gemm_nf4_dx_ok fails.
 bool gemm_nf4_dx_ok(const GemmParams& p, int epi);

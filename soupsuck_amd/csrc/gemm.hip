@@ -687,7 +687,7 @@ template <int EPI>
 static int run_dx(GemmParams& p, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                   hipStream_t s, PrepJobs* prep = nullptr, bool vp = false, bool vg = false) {
   // Above the streaming range and up to two 128-row tiles, the fused dX
-  // decodes each W^T tile into LDS (no decoded weight in HBM); a preparation
+  // decodes each weight tile into LDS (no decoded weight in HBM); a preparation
   // launch then carries the rank-16 jobs only.
   const bool nf4dx = p.M > kStreamDxMaxT && nf4_dx_fused_enabled() && gemm_nf4_dx_ok(p, EPI) &&
                      gemm_nf4_dx_preferred(p);

@@ -289,79 +289,41 @@ __device__ __forceinline__ void nf4_mainloop(const GemmParams& p, int64_t m0, in
 }
 
 // ---------------------------------------------------------------------------
-// Transposed variant (dX = dY . Wdec): the B tile of stage kt is W^T rows
-// (dX columns) n0 .. n0 + BN - 1 over the 32 weight rows kbeg + 32 kt .. + 31
-// (the reduction).  The codes of a stage are 32 weight rows x BN / 2 bytes.
-//
-// Loads.  Thread t fetches one 8-byte piece (row t / 8, piece t % 8: 64-byte
-// row pieces per instruction) and each wave the (row, column block) scale
-// inputs of 16 of the stage's 32 x BN / 64 scales, in registers D stages
-// ahead, with the same per-iteration pattern as the A tile DMAs (three
-// vector-memory ops per stage and wave, as in the forward).
-//
-// Code and scale tables.  Two iterations before a stage is decoded its pieces
-// go into an LDS code table (row-major, 8-byte pieces XOR-swizzled by
-// (row >> 1) & 7) and its scales, computed from code2 / absmax2 / offset as
-// in the decoder, into a [BN / 64][32] table; the iteration's barrier
-// publishes both.
-//
-// Decode.  Thread (16-lane group G, lane l) owns column 16 (G % 8) + (l ^ 1)
-// and weight rows 16 (G / 8) .. + 15: one gfx950 ds_read_b64_tr_b4 of the 16
-// rows' 8-byte pieces of its group (lane l points at row 16 (G / 8) + l) gives
-// eight bytes, byte j holding rows 2j (low nibble) and 2j + 1 (high nibble) of
-// that column (the layout the streaming backward measured).  A 256-entry LDS
-// table maps a byte to {NF4[low], NF4[high]}; each value times its row's
-// scale rounds to fp16 exactly as the stand-alone transposed decoder does, and
-// the 16 values leave as two 16-byte chunks of the column's B tile row.  The
-// B tiles therefore hold the decoder's W^T bits and the MFMA sequence is the
-// dense kernel's: the result equals decode-first with the same tile plan.
-typedef int nf4t_v2i __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) nf4t_v2i nf4t_lds_v2i;
-
-template <class C>
-struct Nf4tLayout {
-  static_assert(C::BK == 32, "fused NF4 stages are 32 k deep");
-  static constexpr int kCodeRow = C::BN / 2;  // code bytes per weight row and stage
-  static_assert(C::kThreads == 2 * C::BN && 32 * (kCodeRow / 8) == C::kThreads,
-                "one (column, 16-row) unit and one 8-byte code piece per thread and stage");
-  static_assert(C::kThreads / kWave * 16 == 32 * (C::BN / 64), "16 scales per wave and stage");
-  static constexpr int kTileA = C::BM * 64;
-  static constexpr int kTileB = C::BN * 64;
-  static constexpr int kCodeBytes = 32 * kCodeRow;
-  static constexpr int kScaleBytes = C::BN / 64 * 32 * 4;
-  static constexpr int kOffB = C::STAGES * kTileA;
-  static constexpr int kOffCodes = kOffB + 2 * kTileB;
-  static constexpr int kOffScale = kOffCodes + 2 * kCodeBytes;
-  static constexpr int kOffLut = kOffScale + 2 * kScaleBytes;
-  static constexpr int kOffCode2 = kOffLut + kPairBytes;
-  static constexpr int kSmem = kOffCode2 + 1024;
-  static constexpr int kOps = C::kDmaA + 3;  // vector-memory ops per stage and wave
-  static_assert(kSmem <= 160 * 1024, "LDS");
-};
-
+// Fused dX (dX = dY . Wdec).  The weight's rows are the reduction of
+// dX = dY . Wdec, so a stage's 32 weight rows, each contiguous over the dX
+// columns, are the B operand stored K-major: they are decoded as they lie,
+// row pieces as in the forward kernel, into a K-major B tile (32 rows of BN
+// halves, 16-byte chunk L of row r at L ^ tsw(r)), and the MFMA fragments
+// come out of it through transposed LDS reads (read_frag_t), as in the dense
+// kernel's K-major operands.  Thread t owns weight row t / (BN / 16) of the
+// stage and its 16 columns 16 (t % (BN / 16)) .. + 15: one 8-byte code piece,
+// one block scale (the 16 columns lie in one 64-wide block), eight pair
+// lookups and two contiguous 16-byte chunk writes; no code or scale table,
+// no transposed code read.  Same fp16 B values (fp16_rne(NF4[c] * scale),
+// scale = code2[q] * absmax2 + offset), same MFMA order: the result equals
+// the decode-first path's with the same tile plan.
 template <class C, int CD>
-__device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
+__device__ __forceinline__ void nf4k_mainloop(const GemmParams& p, int64_t m0, int64_t n0,
                                               int64_t kbeg, int64_t klen, unsigned char* smem,
                                               NtAcc<C>& acc) {
-  using L = Nf4tLayout<C>;
+  using L = Nf4Layout<C>;  // A ring, two B tiles of BN x 64 bytes, pair and code2 tables
   constexpr int kS = C::STAGES;
-  constexpr int kD = CD;  // load ring depth (stages in flight)
-  static_assert(kD >= kS + 2 && kD % kS == 0, "ring depth");
-  constexpr int kGroupBytes = 32 * 64;
+  constexpr int kD = CD;  // code ring depth (stages of codes in flight)
+  static_assert(kD >= kS && kD % kS == 0, "code ring depth");
+  constexpr int kTpr = C::BN / 16;  // threads per weight row and stage, 8 code bytes each
+  static_assert(C::kThreads == 32 * kTpr, "one 8-byte code piece per thread and stage");
+  constexpr int kGroupBytes = 32 * 64;  // one 32-row group of the A tile
+  constexpr int kRowBytes = C::BN * 2;  // one K-major B tile row
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / C::kWavesN;
   const int wn = wave % C::kWavesN;
   const Nf4View& w = p.w;
-  const int64_t kb = p.N >> 1;  // code bytes per weight row
-  const int64_t kq = p.N >> 6;  // scale blocks per weight row
-  float2* const pair = reinterpret_cast<float2*>(smem + L::kOffLut);
   float* const code2 = reinterpret_cast<float*>(smem + L::kOffCode2);
 
-  // Tables first, with tracked loads, before any untracked load is issued:
-  // pair[e] = {NF4[e & 15], NF4[e >> 4]} (low nibble = the lower row).
-  for (int i = tid; i < 256; i += C::kThreads) pair[i] = float2{kNF4[i & 15], kNF4[i >> 4]};
+  // Tables first, with tracked loads, before any untracked load is issued.
+  const float2* const pair = load_pairs(smem + L::kOffLut);
   for (int i = tid; i < 256; i += C::kThreads) code2[i] = w.code2[i];
   float offset = w.offset[0];
   tie(offset);
@@ -380,14 +342,16 @@ __device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, i
   }
   const uint32_t lds_a = __builtin_amdgcn_readfirstlane(lds0 + wave * C::kDmaA * 1024);
 
-  // This thread's code piece and scale input (offsets from the stage-0 base;
-  // each stage adds 32 weight rows).
-  const int crow = tid >> 3, cpiece = tid & 7;
-  const uint32_t code_off = (uint32_t)((kbeg + crow) * kb + (n0 >> 1) + 8 * cpiece);
-  const int sidx = 16 * wave + (lane & 15);
-  const int srow = sidx & 31, sblk = sidx >> 5;
-  const int64_t sblock0 = (kbeg + srow) * kq + (n0 >> 6) + sblk;
-  const int64_t stage_rows = 32;
+  // This thread's weight row of a stage and its first column (columns past N
+  // clamped to the last 16; never stored).  Each stage adds 32 weight rows.
+  const int brow = tid / kTpr;
+  const int bpart = tid % kTpr;
+  const int64_t col = n0 + 16 * bpart <= p.N - 16 ? n0 + 16 * bpart : p.N - 16;
+  const int64_t kb = p.N >> 1;  // code bytes per weight row
+  const int64_t kq = p.N >> 6;  // scale blocks per weight row
+  const uint32_t code_off = (uint32_t)((kbeg + brow) * kb + (col >> 1));
+  const int64_t block0 = (kbeg + brow) * kq + (col >> 6);
+  const uint32_t q_off = (uint32_t)block0;
 
   auto issue_a = [&](int64_t kt, int slot_a) {
 #pragma unroll
@@ -395,90 +359,60 @@ __device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, i
       dma16(a_off[j], a_base + kt * 32, lds_a + slot_a * L::kTileA + j * 1024);
   };
   auto issue_c = [&](int64_t kt, Nf4Slot& sl) {
-    sl.codes = vload8_off(code_off, w.packed + kt * stage_rows * kb);
-    sl.q = vload1_off((uint32_t)sblock0, w.qabs + kt * stage_rows * kq);
-    sl.a2 = vload4_off((uint32_t)(((sblock0 + kt * stage_rows * kq) >> 8) * 4), w.absmax2);
+    sl.codes = vload8_off(code_off, w.packed + kt * 32 * kb);
+    sl.q = vload1_off(q_off, w.qabs + kt * 32 * kq);
+    sl.a2 = vload4_off((uint32_t)(((block0 + kt * 32 * kq) >> 8) * 4), w.absmax2);
   };
-  // Stage data of `sl` into code / scale table `buf`.
-  auto publish = [&](Nf4Slot& sl, int buf) {
-    tie(sl.codes);
-    tie(sl.q);
-    tie(sl.a2);
-    unsigned char* const ct = smem + L::kOffCodes + buf * L::kCodeBytes;
-    *reinterpret_cast<u32x2*>(ct + crow * L::kCodeRow + 8 * (cpiece ^ ((crow >> 1) & 7))) =
-        sl.codes;
-    if (lane < 16) {
-      float* const st = reinterpret_cast<float*>(smem + L::kOffScale + buf * L::kScaleBytes);
-      st[sblk * 32 + srow] = code2[sl.q & 0xffu] * __builtin_bit_cast(float, sl.a2) + offset;
+
+  // Micro-steps of one stage's decode into B tile `buf`: the code2 read, per
+  // code byte its pair-table read, the scale, per byte two products and a
+  // packed conversion, the two chunk writes.
+  constexpr int kSteps = 2 * 8 + 2 + 2;
+  float c2 = 0.0f, scale = 0.0f;
+  float tv[16];
+  half8 outv[2];
+  auto micro = [&](int st, const Nf4Slot& sl, int buf) {
+    if (st == 0) {
+      c2 = code2[sl.q & 0xffu];
+    } else if (st <= 8) {
+      const int b = st - 1;
+      const float2 pr = pair[(sl.codes[b >> 2] >> (8 * (b & 3))) & 0xffu];
+      tv[2 * b] = pr.x;
+      tv[2 * b + 1] = pr.y;
+    } else if (st == 9) {
+      scale = c2 * __builtin_bit_cast(float, sl.a2) + offset;
+    } else if (st <= 17) {
+      const int b = st - 10;
+      outv[b >> 2][2 * (b & 3)] = f32_to_f16(tv[2 * b] * scale);
+      outv[b >> 2][2 * (b & 3) + 1] = f32_to_f16(tv[2 * b + 1] * scale);
+    } else {
+      const int h = st - 18;
+      unsigned char* const bt = smem + L::kOffB + buf * L::kTileB + brow * kRowBytes;
+      *reinterpret_cast<half8*>(bt + (((2 * bpart + h) ^ tsw(brow)) << 4)) = outv[h];
     }
   };
 
-  // Decode unit of this thread: column dcol of the tile, rows 16 drh .. + 15.
-  const int dgroup = tid >> 4, dl = tid & 15;
-  const int drh = dgroup >> 3, dcb = dgroup & 7;
-  const int dcol = 16 * dcb + (dl ^ 1);
-  const int drow = 16 * drh + dl;  // the row this lane points the transposed read at
-  const int dpiece_off = drow * L::kCodeRow + 8 * (dcb ^ ((drow >> 1) & 7));
-  const int dscale_off = ((dcol >> 6) * 32 + 16 * drh) * 4;
-  const int dtile_off = dcol * 64;
-
-  int frag_off[2];
+  int a_frag[2];
+  int b_frag[2][C::FN];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) frag_off[kk] = frag_offset<32>(lane, kk);
+  for (int kk = 0; kk < 2; ++kk) {
+    a_frag[kk] = (wm * C::WM / 32) * kGroupBytes + frag_offset<32>(lane, kk);
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+      b_frag[kk][j] = L::kOffB + frag_offset_t<C::BN>(lane, kk, wn * C::WN + 32 * j);
+  }
   auto read_frags = [&](int slot_a, int buf, int kk, half8 (&af)[C::FM], half8 (&bf)[C::FN]) {
-    const unsigned char* sa =
-        smem + slot_a * L::kTileA + (wm * C::WM / 32) * kGroupBytes + frag_off[kk];
-    const unsigned char* sb =
-        smem + L::kOffB + buf * L::kTileB + (wn * C::WN / 32) * kGroupBytes + frag_off[kk];
+    const unsigned char* sa = smem + slot_a * L::kTileA + a_frag[kk];
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) af[i] = *reinterpret_cast<const half8*>(sa + i * kGroupBytes);
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) bf[j] = *reinterpret_cast<const half8*>(sb + j * kGroupBytes);
+    for (int j = 0; j < C::FN; ++j)
+      bf[j] = read_frag_t(smem + buf * L::kTileB + b_frag[kk][j], kRowBytes);
   };
 
-  // Decode of one stage (code / scale table `buf`) into B tile `bbuf`, as
-  // kSteps micro-steps: the transposed read, the 16 scales, per code byte its
-  // pair lookup, per byte the two products and a packed conversion, the two
-  // chunk writes.
-  constexpr int kSteps = 2 + 8 + 8 + 2;
-  nf4t_v2i cw;
-  float sc[16];
-  float tv[16];
-  half8 outv[2];
-  auto micro = [&](int st, int buf, int bbuf) {
-    if (st == 0) {
-      cw = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
-          (nf4t_lds_v2i*)(smem + L::kOffCodes + buf * L::kCodeBytes + dpiece_off));
-    } else if (st == 1) {
-      const float4v* sp = reinterpret_cast<const float4v*>(smem + L::kOffScale +
-                                                           buf * L::kScaleBytes + dscale_off);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4v v = sp[q];
-        sc[4 * q] = v[0];
-        sc[4 * q + 1] = v[1];
-        sc[4 * q + 2] = v[2];
-        sc[4 * q + 3] = v[3];
-      }
-    } else if (st < 10) {
-      const int j = st - 2;
-      const float2 pr = pair[((uint32_t)cw[j >> 2] >> (8 * (j & 3))) & 0xffu];
-      tv[2 * j] = pr.x;
-      tv[2 * j + 1] = pr.y;
-    } else if (st < 18) {
-      const int j = st - 10;
-      outv[j >> 2][2 * (j & 3)] = f32_to_f16(tv[2 * j] * sc[2 * j]);
-      outv[j >> 2][2 * (j & 3) + 1] = f32_to_f16(tv[2 * j + 1] * sc[2 * j + 1]);
-    } else {
-      const int h = st - 18;
-      unsigned char* const bt = smem + L::kOffB + bbuf * L::kTileB + dtile_off;
-      *reinterpret_cast<half8*>(bt + (((2 * drh + h) ^ swz32(dcol)) << 4)) = outv[h];
-    }
-  };
-
-  // Every iteration issues the A tile of stage kt + kS and the loads of stage
-  // kt + kD (past the end: the last stage again, into slots nobody reads), as
-  // in the forward; the prologue is kD virtual iterations -kD .. -1.
+  // The forward kernel's pipeline: every iteration issues the A tile of stage
+  // kt + kS and the codes of stage kt + kD (past the end: the last stage
+  // again, into slots nobody reads); the prologue is kD virtual iterations.
   const int64_t ktiles = klen / 32;
   auto clampk = [&](int64_t kt) { return kt < ktiles ? kt : ktiles - 1; };
   Nf4Slot ring[kD];
@@ -487,32 +421,27 @@ __device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, i
     if (v + kS >= 0) issue_a(clampk(v + kS), v + kS);
     issue_c(clampk(v + kD), ring[v + kD]);
   }
-  // A tile 0 was followed by the loads of one virtual iteration and kS - 1
-  // whole virtual iterations; the loads of stages 0 and 1 came before it.
   wait_vm<3 + (kS - 1) * L::kOps>();
-  publish(ring[0], 0);
-  publish(ring[1], 1);
+  tie(ring[0].codes);
+  tie(ring[0].q);
+  tie(ring[0].a2);
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) micro(st, ring[0], 0);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   asm volatile("s_barrier" ::: "memory");
-#pragma unroll
-  for (int st = 0; st < kSteps; ++st) micro(st, 0, 0);
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("s_barrier" ::: "memory");
 
-  // Iteration kt (j = kt % kD, a compile-time constant): stage kt + 2's loads
-  // into table kt % 2, the decode of stage kt + 1 (table (kt + 1) % 2) into B
-  // tile (kt + 1) % 2 between the MFMAs of stage kt, one barrier, then the
-  // next loads.
+  // Iteration kt: the decode of stage kt + 1 into B tile (kt + 1) % 2 runs as
+  // micro-steps between the MFMAs of stage kt; one barrier; the next loads.
   constexpr int kMfma = 2 * C::FM * C::FN;
-  auto iteration = [&](int64_t kt, int j) {
+  auto iteration = [&](int64_t kt, int j, Nf4Slot& next, Nf4Slot& own) {
     const int sa = j % kS;
     half8 fa[2][C::FM], fb[2][C::FN];
     read_frags(sa, (int)(kt & 1), 0, fa[0], fb[0]);
     read_frags(sa, (int)(kt & 1), 1, fa[1], fb[1]);
-    // Stage kt + 1's A tile was followed by one iteration's loads and kS - 2
-    // whole iterations; stage kt + 2's loads were issued before it.
     wait_vm<3 + (kS - 2) * L::kOps>();
-    publish(ring[(j + 2) % kD], (int)(kt & 1));
+    tie(next.codes);
+    tie(next.q);
+    tie(next.a2);
     const int buf = (int)((kt + 1) & 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -524,20 +453,20 @@ __device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, i
                                                           0, 0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int st = m * kSteps / kMfma; st < (m + 1) * kSteps / kMfma; ++st) micro(st, buf, buf);
+      for (int st = m * kSteps / kMfma; st < (m + 1) * kSteps / kMfma; ++st) micro(st, next, buf);
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("s_barrier" ::: "memory");
     issue_a(clampk(kt + kS), sa);
-    issue_c(clampk(kt + kD), ring[j]);
+    issue_c(clampk(kt + kD), own);
   };
 
   for (int64_t kt0 = 0; kt0 < ktiles; kt0 += kD) {
 #pragma unroll
     for (int j = 0; j < kD; ++j) {
       if (kt0 + j >= ktiles) break;
-      iteration(kt0 + j, j);
+      iteration(kt0 + j, j, ring[(j + 1) % kD], ring[j]);
     }
   }
   // As in the forward: the ring registers stay allocated until every load
@@ -553,7 +482,7 @@ __device__ __forceinline__ void nf4t_mainloop(const GemmParams& p, int64_t m0, i
 
 template <class C, int CD, int CT, int EPI>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4t_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4tLayout<C>::kSmem];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[Nf4Layout<C>::kSmem];
   const int64_t tiles = gridDim.x;
   int64_t tile, split = 0;
   if constexpr (EPI == EPI_PARTIAL)
@@ -572,8 +501,8 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nf4t_kernel(GemmPar
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) acc[i][j] = float16v{};
-  nf4t_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
-  static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= Nf4tLayout<C>::kSmem, "stage");
+  nf4k_mainloop<C, CD>(p, m0, n0, kbeg, klen, smem, acc);
+  static_assert(!GluStage<C>::kOk || GluStage<C>::kBytes <= Nf4Layout<C>::kSmem, "stage");
   nt_epilogue<C, CT, EPI>(p, m0, n0, acc, smem, split);
 }
 
@@ -626,8 +555,8 @@ int dispatch_nf4(const GemmParams& p, int cfg, int64_t splits, hipStream_t strea
   }
 }
 
-using Nf4tMid = Nf4Mid;  // 128x128, 4 waves: one decode unit per thread
-constexpr int kNf4tRing = 8;
+using Nf4tMid = Nf4Mid;  // 128x128, 4 waves: one 8-byte code piece per thread and stage
+constexpr int kNf4tRing = 12;
 
 template <int CT, int EPI>
 int dispatch_nf4t(const GemmParams& p, int64_t splits, hipStream_t stream) {
@@ -728,7 +657,7 @@ int gemm_nf4_fwd(const GemmParams& p0, int epi, hipStream_t stream, void* partia
 
 // Fused dX (dY . Wdec, the weight decoded into the B tiles): 128x128 tiles,
 // split over the weight rows until about 512 workgroups run, each split at
-// least 512 rows deep.  For T up to two 128-row tiles, where each W^T tile is
+// least 512 rows deep.  For T up to two 128-row tiles, where each weight tile is
 // decoded once or twice instead of being written to HBM and read back.
 static NtPlan nf4t_plan(int64_t m, int64_t n, int64_t k) {
   NtPlan plan{2, 1, k};

@@ -119,8 +119,8 @@ def test_dx_without_workspace(device, t, n, k):
 
 
 # Fused dX for 16 < T <= 256 with dX columns % 128 == 0 and 128 or more
-# workgroups: W^T tiles decoded into LDS inside the GEMM (transposed 4-bit LDS
-# reads, one scale per weight row and block), one or two 128-row tiles, ragged
+# workgroups: weight tiles decoded into LDS inside the GEMM (K-major B tiles,
+# one scale per code piece), one or two 128-row tiles, ragged
 # T, unsplit (a 512-row reduction) and split over the weight rows,
 # accumulation.  Its rank-16 epilogue runs in the QLoRA projection tests.
 @pytest.mark.parametrize("t,n,k", [(17, 8960, 1536), (64, 1536, 8960), (128, 8960, 1536),
