@@ -421,7 +421,11 @@ StreamPlan stream_plan(int64_t t, int64_t n, int64_t k) {
   const int64_t s = k / kStK;
   const int mt = t <= 16 ? 1 : 2;
   const int64_t max_waves = mt == 1 ? kStMaxWaves : kStMaxWaves / 2;
-  const int64_t n_ranges = cdiv(n, 32);
+  // Row ranges of at least 32 rows; 16 for a small weight (below), whose
+  // latency-bound stream gains from spreading over twice the CUs (7B k/v at
+  // T = 1: 7.1 -> 6.1 us, q/o 7.6 -> 6.6 us).
+  const bool small_w = n * (k / 2) <= kStSmallBytes && s <= max_waves;
+  const int64_t n_ranges = cdiv(n, small_w ? 16 : 32);
   int64_t g = cdiv(s, max_waves);
   int64_t g_fill = cdiv(cus, n_ranges);
   if (g_fill > s) g_fill = s;
@@ -430,7 +434,7 @@ StreamPlan stream_plan(int64_t t, int64_t n, int64_t k) {
   // bandwidth-bound: every stage in one workgroup, so the epilogue runs in
   // the kernel and no partial planes or reduce launch follow (7B k/v at T =
   // 1: 10.8 -> 7.0 us, q/o: 9.8 -> 7.6 us, although fewer CUs stream it).
-  if (n * (k / 2) <= kStSmallBytes && s <= max_waves) g = 1;
+  if (small_w) g = 1;
   plan.sg = cdiv(s, g);
   plan.groups = cdiv(s, plan.sg);
   plan.waves = (int)plan.sg;
