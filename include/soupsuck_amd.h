@@ -266,24 +266,18 @@ int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float
                 const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
                 void* stream);
 
-/* Same product with scratch for splitting the reduction over workgroups
- * (dense NT case: a_trans = 0, b_trans = 1, both operands K-contiguous, K %
- * 64 == 0): ss_gemm_f16_workspace_size(a_trans, b_trans, m, n, k) bytes; a
- * smaller workspace means no split.  Serves the vocabulary-chunk dX product
- * of the fused cross-entropy backward (solution/kernels/cross_entropy.py:202),
- * whose output tile count is small. */
+/* Same product with scratch for splitting the reduction over workgroups (the
+ * direct-to-LDS kernel: K % 64 == 0, 16-byte aligned operands, M % 8 == 0
+ * for a_trans = 1 and N % 8 == 0 for b_trans = 0):
+ * ss_gemm_f16_workspace_size(a_trans, b_trans, m, n, k) bytes; a smaller
+ * workspace means no split.  Serves the vocabulary-chunk dX product of the
+ * fused cross-entropy backward (solution/kernels/cross_entropy.py:202), whose
+ * output tile count is small. */
 size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k);
 int ss_gemm_f16_split(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
                       const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                       const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
                       void* workspace, size_t workspace_bytes, void* stream);
-
-/* dst[c][r] = src[r][c] for a rows x cols fp16 matrix (row strides lds,
- * ldd in elements).  No counterpart in the reference (its cuBLAS calls take
- * transposed operands directly): it lays out the fused cross-entropy
- * backward's operands for the dense NT kernel. */
-int ss_transpose_f16(const uint16_t* src, int64_t lds, int64_t rows, int64_t cols, uint16_t* dst,
-                     int64_t ldd, void* stream);
 
 /* ---------------------------------------------------------- LoRA (A11) ---
  * out = round_out(fp32(base) + fp32(scaled)), scaled = round_adapter(adapter*s),

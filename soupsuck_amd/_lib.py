@@ -79,7 +79,6 @@ SIGNATURES = {
     "ss_gemm_f16_workspace_size": [_int, _int, _i64, _i64, _i64],
     "ss_gemm_f16_split": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
                           _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p, _size, _c_void_p],
-    "ss_transpose_f16": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "ss_lora_epilogue_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _f32, _int,
                              _c_void_p],
     "ss_lora_epilogue_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _f32, _c_void_p],

@@ -81,22 +81,6 @@ def gemm_f16(a, b, *, a_trans=False, b_trans=False, out=None, out_dtype=torch.fl
     return out
 
 
-def transpose_f16(src, out=None):
-    """out[c, r] = src[r, c] for a 2-D fp16 tensor with unit column stride (ss_transpose_f16);
-    ``out`` may be a strided view (unit column stride), e.g. the leading block of a
-    wider zero-padded buffer."""
-    if src.dtype != torch.float16 or src.ndim != 2 or src.stride(-1) != 1:
-        raise ValueError("transpose_f16 expects a 2-D fp16 tensor with unit column stride")
-    rows, cols = src.shape
-    if out is None:
-        out = torch.empty((cols, rows), device=src.device, dtype=torch.float16)
-    if out.shape != (cols, rows) or out.stride(-1) != 1 or out.dtype != torch.float16:
-        raise ValueError("transpose_f16: bad output buffer")
-    _lib.call("ss_transpose_f16", src.data_ptr(), src.stride(0), rows, cols, out.data_ptr(),
-              out.stride(0), _lib.stream(src.device))
-    return out
-
-
 def nf4_forward_2d(x2d, packed, state, n, k, bias=None, out=None):
     """y[T,N] = x2d[T,K] . Wdec^T (+bias) into ``out`` (allocated if None)."""
     t = x2d.shape[0]

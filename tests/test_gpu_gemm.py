@@ -16,8 +16,7 @@ import torch
 from oracle import gemm as ogemm
 from oracle import nf4 as onf4
 from soupsuck_amd import _lib
-from soupsuck_amd.kernels.nf4_gemm import (gemm_f16, nf4_dx_2d, nf4_forward_2d, nf4_matmul,
-                                           transpose_f16)
+from soupsuck_amd.kernels.nf4_gemm import gemm_f16, nf4_dx_2d, nf4_forward_2d, nf4_matmul
 from tests.gpu_util import device_state, np16, random_weight
 
 pytestmark = pytest.mark.gpu
@@ -301,26 +300,6 @@ def test_dense_split_k(device, m, n, k):
     np.testing.assert_allclose(np16(c), base + prod, rtol=1e-5, atol=5e-4)
     h = gemm_f16(ad, bd, b_trans=True, alpha=0.25, split_k=True)
     check(h, 0.25 * prod, f"split fp16 {m}x{n}x{k}")
-
-
-@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 130), (64, 64), (518, 1536), (1536, 518),
-                                       (100, 8192), (65, 63)])
-def test_transpose_f16(device, rows, cols):
-    """ss_transpose_f16 is a bit-exact permutation, also into a strided view of a
-    wider buffer whose padding it must leave untouched."""
-    rng = np.random.default_rng(rows * 131 + cols)
-    a = rng.standard_normal((rows, cols)).astype(np.float16)
-    src = torch.from_numpy(a).to(device)
-    out = transpose_f16(src)
-    assert np.array_equal(np16(out), a.T)
-    pad = torch.full((cols, rows + 70), 7.0, device=device, dtype=torch.float16)
-    transpose_f16(src, out=pad[:, :rows])
-    got = np16(pad)
-    assert np.array_equal(got[:, :rows], a.T)
-    assert np.all(got[:, rows:] == 7.0)
-    # a strided source (a column window of a wider matrix)
-    wide = torch.from_numpy(rng.standard_normal((rows, cols + 9)).astype(np.float16)).to(device)
-    assert np.array_equal(np16(transpose_f16(wide[:, 3:3 + cols])), np16(wide)[:, 3:3 + cols].T)
 
 
 @pytest.mark.parametrize("t,n,k", [(990, 8960, 1536),   # 256x256 tiles, 4 M tiles
