@@ -52,7 +52,10 @@ def test_epilogue_rounded_product_cancels(device):
                                         (200, 512, 8960, False),
                                         (37, 8960, 1536, False), (64, 1536, 8960, False),
                                         (300, 256, 1536, True), (990, 8960, 1536, False),
-                                        (990, 1536, 8960, False), (2048, 8960, 256, True),
+                                        (990, 1536, 8960, False),
+                                        # configs[1] q (bias), k / v (bias) and o at T = 990
+                                        (990, 1536, 1536, True), (990, 256, 1536, True),
+                                        (990, 1536, 1536, False), (2048, 8960, 256, True),
                                         (16, 8960, 1536, True), (29, 1000, 3584, False),
                                         # 592 tiles of 256x256 in the forward (LoRA
                                         # epilogue) and in the dX product (rank-16)
