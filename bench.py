@@ -360,9 +360,10 @@ def sweep(torch, _lib):
 
 def vendor_ceiling(torch):
     """Same-box reference point: torch.matmul (hipBLASLt) on fp16 operands already
-    in HBM, at 8192^3, at the configs[4] T=16384 gate/up and down products and at
-    every configs[4] product at T=2048, forward X [T, K] . W^T and dX dY [T, N] . W
-    with W [N, K] row-major.  Average of 10 calls between HIP events after 3
+    in HBM, at 8192^3, at the configs[4] T=16384 gate/up and down products, at
+    every configs[4] product at T=2048 and at every configs[1] projection's product
+    at T=990 (the dense part of the headline step), forward X [T, K] . W^T and dX
+    dY [T, N] . W with W [N, K] row-major.  Average of 10 calls between HIP events after 3
     warm-ups; a probe of what the vendor GEMM reaches on this board, not a
     target."""
     dev = torch.device("cuda:0")
@@ -374,6 +375,10 @@ def vendor_ceiling(torch):
     for name, n, k in SWEEP_SHAPES:
         for mode in ("fwd", "dx"):
             products.append((f"{name} T=2048 {mode}", 2048, n, k, mode))
+    for name, n, k in (("gate/up", 8960, 1536), ("down", 1536, 8960), ("q/o", 1536, 1536),
+                       ("k/v", 256, 1536)):
+        for mode in ("fwd", "dx"):
+            products.append((f"configs[1] {name} T=990 {mode}", 990, n, k, mode))
     for label, m, n, k, mode in products:
         a = torch.randn((m, n if mode == "dx" else k), device=dev, generator=gen).half()
         w = torch.randn((n, k), device=dev, generator=gen).half()
