@@ -20,6 +20,11 @@
 // wave owns 16 queries (forward, dQ) or 16 keys (dK / dV); 4 waves per
 // workgroup share the LDS tiles of the other operand.
 //
+// Operands whose MFMA layout runs along the token axis of a row-major LDS tile
+// (V in O^T += V^T . P^T, K in dQ += dS . K, Q and dO in dK / dV) are read
+// straight from that tile with gfx950's ds_read_b64_tr_b16 (ld4_tr): no
+// transposed copy of any tile is built.
+//
 // Backward: a dQ kernel per (row, 64 queries, q head), which also writes
 // delta = rowsum(dO . O); then a dK / dV kernel per (row, 64 keys, q head)
 // over the causal query tiles; with GQA each q head writes fp32 partials that
@@ -32,7 +37,6 @@ namespace {
 constexpr int kD = 128;        // head dimension
 constexpr int kBlk = 64;       // queries / keys per workgroup (4 waves x 16)
 constexpr int kLdRow = kD + 8; // padded LDS row of a [token][d] tile (halfs, 16-byte rows)
-constexpr int kLdT = 64 + 4;   // padded LDS row of a [d][token] tile (halfs)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -57,6 +61,22 @@ __device__ __forceinline__ float4v mfma16(half4 a, half4 b, float4v c) {
 }
 
 __device__ __forceinline__ half4 ld4(const half_t* p) { return *reinterpret_cast<const half4*>(p); }
+
+typedef short attn_short4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) attn_short4 attn_lds_short4;
+
+// MFMA 16x16x16 operand of a row-major LDS tile T[token][d] along its token
+// axis: lane l (column c = l % 16, group g = l / 16) receives T[t0 + 4 g + j][d0 +
+// c] for j = 0..3.  One ds_read_b64_tr_b16: in each 16-lane group the lanes'
+// 8-byte reads form a 16 x 4 matrix M (row = reading lane) and lane i receives
+// M[4 j + i / 4][i % 4] (measured on gfx950), so lane r of the group points at
+// T[t0 + 4 g + r / 4][d0 + 4 (r % 4)].
+__device__ __forceinline__ half4 ld4_tr(const half_t (*tile)[kLdRow], int t0, int d0, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  const half_t* p = &tile[t0 + 4 * g + (r >> 2)][d0 + 4 * (r & 3)];
+  const attn_short4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((attn_lds_short4*)p);
+  return __builtin_bit_cast(half4, v);
+}
 __device__ __forceinline__ half8 ld8(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
 
 __device__ __forceinline__ float xor_max(float v) {
@@ -69,20 +89,14 @@ __device__ __forceinline__ float xor_sum(float v) {
 }
 
 // Cooperative load of 64 token rows [t0, t0 + 64) of one head into LDS as a
-// row-major tile (and, when `tr` is given, its transpose [d][token]); rows
-// past the row end re-read the last row (their results are masked).
+// row-major tile; rows past the row end re-read the last row (their results
+// are masked).
 __device__ __forceinline__ void load_rows64(const half_t* base, int64_t tok, int start, int len,
-                                            int t0, half_t (*rows)[kLdRow],
-                                            half_t (*tr)[kLdT]) {
+                                            int t0, half_t (*rows)[kLdRow]) {
   for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
     const int r = c >> 4, ch = c & 15;
     const int t = min(t0 + r, len - 1);
-    const half8 v = ld8(base + (int64_t)(start + t) * tok + ch * 8);
-    *reinterpret_cast<half8*>(&rows[r][ch * 8]) = v;
-    if (tr) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) tr[ch * 8 + j][r] = v[j];
-    }
+    *reinterpret_cast<half8*>(&rows[r][ch * 8]) = ld8(base + (int64_t)(start + t) * tok + ch * 8);
   }
 }
 
@@ -100,7 +114,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const float sl2 = a.scale * kLog2e;
 
   __shared__ __align__(16) half_t sK[kBlk][kLdRow];
-  __shared__ __align__(16) half_t sVt[kD][kLdT];
+  __shared__ __align__(16) half_t sV[kBlk][kLdRow];
 
   half4 qf[8];  // B operand of S^T = K . Q^T: Q[myq][16 ks + 4 grp + j]
   {
@@ -118,14 +132,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
   for (int kb = 0; kb < kend; kb += kBlk) {
     __syncthreads();
-    load_rows64(kbase, a.k_tok, start, len, kb, sK, nullptr);
-    // V block transposed into LDS: sVt[d][key].
-    for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
-      const int r = c >> 4, ch = c & 15;
-      const half8 v = ld8(vbase + (int64_t)(start + min(kb + r, len - 1)) * a.v_tok + ch * 8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sVt[ch * 8 + j][r] = v[j];
-    }
+    load_rows64(kbase, a.k_tok, start, len, kb, sK);
+    load_rows64(vbase, a.v_tok, start, len, kb, sV);
     __syncthreads();
     float4v s[4];
 #pragma unroll
@@ -166,7 +174,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       acc[dt] *= alpha;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        acc[dt] = mfma16(ld4(&sVt[dt * 16 + col][kt * 16 + grp * 4]), p[kt], acc[dt]);
+        acc[dt] = mfma16(ld4_tr(sV, kt * 16, dt * 16, lane), p[kt], acc[dt]);
     }
   }
   if (myq < len) {
@@ -199,7 +207,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const float sl2 = a.scale * kLog2e;
 
   __shared__ __align__(16) half_t sK[kBlk][kLdRow];
-  __shared__ __align__(16) half_t sKt[kD][kLdT];
   __shared__ __align__(16) half_t sV[kBlk][kLdRow];
 
   half4 qf[8], df[8];  // Q[myq][16 ks + 4 grp + j], dO[myq][...]
@@ -230,8 +237,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
   for (int kb = 0; kb < kend; kb += kBlk) {
     __syncthreads();
-    load_rows64(kbase, a.k_tok, start, len, kb, sK, sKt);
-    load_rows64(vbase, a.v_tok, start, len, kb, sV, nullptr);
+    load_rows64(kbase, a.k_tok, start, len, kb, sK);
+    load_rows64(vbase, a.v_tok, start, len, kb, sV);
     __syncthreads();
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
-        dq[dt] = mfma16(ds, ld4(&sKt[dt * 16 + col][kt * 16 + grp * 4]), dq[dt]);
+        dq[dt] = mfma16(ds, ld4_tr(sK, kt * 16, dt * 16, lane), dq[dt]);
     }
   }
   half_t* base = a.out + (int64_t)h * a.out_head;
@@ -268,7 +275,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 // ------------------------------------------------------------ backward dK/dV
 
 constexpr int kQt = 32;           // queries per LDS tile of the dK / dV kernel
-constexpr int kLdTq = kQt + 4;    // padded LDS row of a [d][query] tile (halfs)
 
 // One workgroup per (row, 64 keys, q head): 4 waves of 16 keys walk the row's
 // causal query tiles.  With GQA (hq > hk) the q heads of a group write fp32
@@ -289,9 +295,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
   const float sl2 = a.scale * kLog2e;
 
   __shared__ __align__(16) half_t sQ[kQt][kLdRow];
-  __shared__ __align__(16) half_t sQt[kD][kLdTq];
   __shared__ __align__(16) half_t sO[kQt][kLdRow];    // dO rows
-  __shared__ __align__(16) half_t sOt[kD][kLdTq];     // dO transposed
   __shared__ float sL[kQt], sDl[kQt];                 // lse2 and delta of the tile's queries
 
   half4 kf[8], vf[8];  // K[mykey][16 ks + 4 grp + j], V[mykey][...]
@@ -315,19 +319,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
   const half_t* dbase = a.dout + (int64_t)h * a.do_head;
   for (int qt = k0; qt < len; qt += kQt) {
     __syncthreads();
-    // Query tile [qt, qt + 32): Q and dO rows and transposes, lse2, delta.
+    // Query tile [qt, qt + 32): Q and dO rows, lse2, delta.
     for (int c = threadIdx.x; c < kQt * (kD / 8); c += 256) {
       const int r = c >> 4, ch = c & 15;
       const int t = min(qt + r, len - 1);
-      const half8 qv = ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
-      const half8 dvv = ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
-      *reinterpret_cast<half8*>(&sQ[r][ch * 8]) = qv;
-      *reinterpret_cast<half8*>(&sO[r][ch * 8]) = dvv;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        sQt[ch * 8 + j][r] = qv[j];
-        sOt[ch * 8 + j][r] = dvv[j];
-      }
+      *reinterpret_cast<half8*>(&sQ[r][ch * 8]) =
+          ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
+      *reinterpret_cast<half8*>(&sO[r][ch * 8]) =
+          ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
     }
     if (threadIdx.x < kQt) {
       const int64_t idx = (int64_t)h * a.total + start + min(qt + (int)threadIdx.x, len - 1);
@@ -355,8 +354,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
       }
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
-        dv[dt] = mfma16(p16, ld4(&sOt[dt * 16 + col][sub * 16 + grp * 4]), dv[dt]);
-        dk[dt] = mfma16(ds16, ld4(&sQt[dt * 16 + col][sub * 16 + grp * 4]), dk[dt]);
+        dv[dt] = mfma16(p16, ld4_tr(sO, sub * 16, dt * 16, lane), dv[dt]);
+        dk[dt] = mfma16(ds16, ld4_tr(sQ, sub * 16, dt * 16, lane), dk[dt]);
       }
     }
   }
