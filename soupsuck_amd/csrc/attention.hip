@@ -88,17 +88,36 @@ __device__ __forceinline__ float xor_sum(float v) {
   return v + __shfl_xor(v, 32, kWave);
 }
 
-// Cooperative load of 64 token rows [t0, t0 + 64) of one head into LDS as a
-// row-major tile; rows past the row end re-read the last row (their results
-// are masked).
-__device__ __forceinline__ void load_rows64(const half_t* base, int64_t tok, int start, int len,
-                                            int t0, half_t (*rows)[kLdRow]) {
-  for (int c = threadIdx.x; c < kBlk * (kD / 8); c += 256) {
-    const int r = c >> 4, ch = c & 15;
-    const int t = min(t0 + r, len - 1);
-    *reinterpret_cast<half8*>(&rows[r][ch * 8]) = ld8(base + (int64_t)(start + t) * tok + ch * 8);
+// Register staging of ROWS token rows [t0, t0 + ROWS) of two operands of one
+// head (K and V, or Q and dO): fetch() issues the global loads (rows past the
+// row end re-read the last row; their results are masked), stage() writes
+// them into row-major LDS tiles.  The loops fetch the next tile before
+// computing on the current one, so its loads are in flight meanwhile.
+template <int ROWS>
+struct TilePair {
+  static constexpr int kPer = ROWS * (kD / 8) / 256;  // 16-byte chunks per thread and operand
+  half8 a[kPer], b[kPer];
+  __device__ __forceinline__ void fetch(const half_t* base_a, int64_t tok_a, const half_t* base_b,
+                                        int64_t tok_b, int start, int len, int t0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c >> 4, ch = c & 15;
+      const int64_t t = start + min(t0 + r, len - 1);
+      a[i] = ld8(base_a + t * tok_a + ch * 8);
+      b[i] = ld8(base_b + t * tok_b + ch * 8);
+    }
   }
-}
+  __device__ __forceinline__ void stage(half_t (*ta)[kLdRow], half_t (*tb)[kLdRow]) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int r = c >> 4, ch = c & 15;
+      *reinterpret_cast<half8*>(&ta[r][ch * 8]) = a[i];
+      *reinterpret_cast<half8*>(&tb[r][ch * 8]) = b[i];
+    }
+  }
+};
 
 // ------------------------------------------------------------------ forward
 
@@ -130,11 +149,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int kend = min(len, q0 + kBlk);  // causal: keys beyond the block's last query unused
   const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
+  TilePair<kBlk> kv;
+  kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, 0);
   for (int kb = 0; kb < kend; kb += kBlk) {
     __syncthreads();
-    load_rows64(kbase, a.k_tok, start, len, kb, sK);
-    load_rows64(vbase, a.v_tok, start, len, kb, sV);
+    kv.stage(sK, sV);
     __syncthreads();
+    if (kb + kBlk < kend) kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kb + kBlk);
     float4v s[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -235,11 +256,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int kend = min(len, q0 + kBlk);
   const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
+  TilePair<kBlk> kv;
+  kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, 0);
   for (int kb = 0; kb < kend; kb += kBlk) {
     __syncthreads();
-    load_rows64(kbase, a.k_tok, start, len, kb, sK);
-    load_rows64(vbase, a.v_tok, start, len, kb, sV);
+    kv.stage(sK, sV);
     __syncthreads();
+    if (kb + kBlk < kend) kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kb + kBlk);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
@@ -317,23 +340,27 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
 
   const half_t* qbase = a.q + (int64_t)h * a.q_head;
   const half_t* dbase = a.dout + (int64_t)h * a.do_head;
-  for (int qt = k0; qt < len; qt += kQt) {
-    __syncthreads();
-    // Query tile [qt, qt + 32): Q and dO rows, lse2, delta.
-    for (int c = threadIdx.x; c < kQt * (kD / 8); c += 256) {
-      const int r = c >> 4, ch = c & 15;
-      const int t = min(qt + r, len - 1);
-      *reinterpret_cast<half8*>(&sQ[r][ch * 8]) =
-          ld8(qbase + (int64_t)(start + t) * a.q_tok + ch * 8);
-      *reinterpret_cast<half8*>(&sO[r][ch * 8]) =
-          ld8(dbase + (int64_t)(start + t) * a.do_tok + ch * 8);
-    }
+  // Query tile [qt, qt + 32): Q and dO rows, lse2, delta (fetched one tile ahead).
+  TilePair<kQt> qo;
+  float nl = 0.f, nd = 0.f;
+  auto fetch = [&](int qt) {
+    qo.fetch(qbase, a.q_tok, dbase, a.do_tok, start, len, qt);
     if (threadIdx.x < kQt) {
       const int64_t idx = (int64_t)h * a.total + start + min(qt + (int)threadIdx.x, len - 1);
-      sL[threadIdx.x] = a.lse2[idx];
-      sDl[threadIdx.x] = a.delta[idx];
+      nl = a.lse2[idx];
+      nd = a.delta[idx];
+    }
+  };
+  fetch(k0);
+  for (int qt = k0; qt < len; qt += kQt) {
+    __syncthreads();
+    qo.stage(sQ, sO);
+    if (threadIdx.x < kQt) {
+      sL[threadIdx.x] = nl;
+      sDl[threadIdx.x] = nd;
     }
     __syncthreads();
+    if (qt + kQt < len) fetch(qt + kQt);
 #pragma unroll
     for (int sub = 0; sub < kQt / 16; ++sub) {
       float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
