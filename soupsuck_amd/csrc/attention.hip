@@ -149,13 +149,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int kend = min(len, q0 + kBlk);  // causal: keys beyond the block's last query unused
   const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
-  TilePair<kBlk> kv;
-  kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, 0);
-  for (int kb = 0; kb < kend; kb += kBlk) {
+  // Two tiles in flight: block kb computes while blocks kb + 64 and kb + 128 load.
+  TilePair<kBlk> kv0, kv1;
+  kv0.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, 0);
+  if (kBlk < kend) kv1.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kBlk);
+  auto block = [&](int kb, TilePair<kBlk>& kv) {
     __syncthreads();
     kv.stage(sK, sV);
     __syncthreads();
-    if (kb + kBlk < kend) kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kb + kBlk);
+    if (kb + 2 * kBlk < kend)
+      kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kb + 2 * kBlk);
     float4v s[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
@@ -197,6 +200,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       for (int kt = 0; kt < 4; ++kt)
         acc[dt] = mfma16(ld4_tr(sV, kt * 16, dt * 16, lane), p[kt], acc[dt]);
     }
+  };
+  for (int kb = 0; kb < kend; kb += 2 * kBlk) {
+    block(kb, kv0);
+    if (kb + kBlk < kend) block(kb + kBlk, kv1);
   }
   if (myq < len) {
     const float inv = 1.0f / l;
@@ -256,6 +263,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int kend = min(len, q0 + kBlk);
   const half_t* kbase = a.k + (int64_t)kvh * a.k_head;
   const half_t* vbase = a.v + (int64_t)kvh * a.v_head;
+  // One tile ahead (a second one in flight measured slower here: more registers).
   TilePair<kBlk> kv;
   kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, 0);
   for (int kb = 0; kb < kend; kb += kBlk) {
@@ -297,7 +305,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------ backward dK/dV
 
-constexpr int kQt = 32;           // queries per LDS tile of the dK / dV kernel
+constexpr int kQt = 64;           // queries per LDS tile of the dK / dV kernel
 
 // One workgroup per (row, 64 keys, q head): 4 waves of 16 keys walk the row's
 // causal query tiles.  With GQA (hq > hk) the q heads of a group write fp32
@@ -340,7 +348,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
 
   const half_t* qbase = a.q + (int64_t)h * a.q_head;
   const half_t* dbase = a.dout + (int64_t)h * a.do_head;
-  // Query tile [qt, qt + 32): Q and dO rows, lse2, delta (fetched one tile ahead).
+  // Query tile [qt, qt + kQt): Q and dO rows, lse2, delta (fetched one tile ahead).
   TilePair<kQt> qo;
   float nl = 0.f, nd = 0.f;
   auto fetch = [&](int qt) {
