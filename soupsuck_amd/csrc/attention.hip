@@ -13,12 +13,14 @@
 // softmax in fp32 with an online maximum, P rounded to fp16 for the P.V MFMA,
 // O accumulated in fp32 and rounded once.
 //
-// MFMA: v_mfma_f32_16x16x16_f16.  Its accumulator layout (lane l holds rows
-// 4 (l / 16) + i of column l % 16) is the B-operand layout of the next product
-// (k = 4 (l / 16) + i, column l % 16), so the score tile S^T = K . Q^T becomes
-// the B operand P^T of O^T += V^T . P^T in registers, with no shuffle.  Each
-// wave owns 16 queries (forward, dQ) or 16 keys (dK / dV); 4 waves per
-// workgroup share the LDS tiles of the other operand.
+// MFMA: gfx950's v_mfma_f32_16x16x32_f16 (lane l supplies k 8 (l / 16) .. + 7
+// of row / column l % 16; the accumulator gives lane l rows 4 (l / 16) + i of
+// column l % 16).  The k order inside one MFMA is free as long as both operands
+// use it, so two 16-key score tiles' accumulators (keys 4 (l / 16) + i and
+// 16 + 4 (l / 16) + i of one column) form the 8-slot B operand P^T of O^T +=
+// V^T . P^T in registers, with no shuffle, and V^T supplies the same keys in the
+// same slots.  Each wave owns 16 queries (forward, dQ) or 16 keys (dK / dV); 4
+// waves per workgroup share the LDS tiles of the other operand.
 //
 // Operands whose MFMA layout runs along the token axis of a row-major LDS tile
 // (V in O^T += V^T . P^T, K in dQ += dS . K, Q and dO in dK / dV) are read
@@ -56,11 +58,13 @@ struct AttnArgs {
   float scale;      // softmax scale (1/sqrt(128) for Qwen2)
 };
 
-__device__ __forceinline__ float4v mfma16(half4 a, half4 b, float4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ float4v mfma32(half8 a, half8 b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ half8 cat8(half4 lo, half4 hi) {
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-__device__ __forceinline__ half4 ld4(const half_t* p) { return *reinterpret_cast<const half4*>(p); }
 
 typedef short attn_short4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) attn_short4 attn_lds_short4;
@@ -135,11 +139,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __align__(16) half_t sK[kBlk][kLdRow];
   __shared__ __align__(16) half_t sV[kBlk][kLdRow];
 
-  half4 qf[8];  // B operand of S^T = K . Q^T: Q[myq][16 ks + 4 grp + j]
+  half8 qf[4];  // B operand of S^T = K . Q^T: Q[myq][32 ks + 8 grp + j]
   {
     const half_t* qp = a.q + (int64_t)(start + min(myq, len - 1)) * a.q_tok + (int64_t)h * a.q_head;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = ld4(qp + ks * 16 + grp * 4);
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = ld8(qp + ks * 32 + grp * 8);
   }
   float4v acc[8];  // O^T tiles: [d = 16 dt + 4 grp + i][q = myq]
 #pragma unroll
@@ -164,8 +168,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     for (int kt = 0; kt < 4; ++kt) {
       s[kt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        s[kt] = mfma16(ld4(&sK[kt * 16 + col][ks * 16 + grp * 4]), qf[ks], s[kt]);
+      for (int ks = 0; ks < 4; ++ks)
+        s[kt] = mfma32(ld8(&sK[kt * 16 + col][ks * 32 + grp * 8]), qf[ks], s[kt]);
     }
     // s[kt][i] = S^T[key = kb + 16 kt + 4 grp + i][q = myq]; base-2 scaled, masked.
     float mx = m;
@@ -193,12 +197,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     rs = xor_sum(rs);
     l = l * alpha + rs;
     m = mx;
+    // O^T += V^T . P^T over the block's 64 keys in two 32-deep steps: step u pairs
+    // key tiles 2u and 2u + 1 (k slots 8 grp + i <-> key 32 u + 4 grp + i, 8 grp + 4 + i
+    // <-> key 32 u + 16 + 4 grp + i), the same slot order for V^T (two transposed
+    // reads) and P^T (the two score tiles' registers).
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       acc[dt] *= alpha;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        acc[dt] = mfma16(ld4_tr(sV, kt * 16, dt * 16, lane), p[kt], acc[dt]);
+      for (int u = 0; u < 2; ++u)
+        acc[dt] = mfma32(cat8(ld4_tr(sV, 32 * u, dt * 16, lane),
+                              ld4_tr(sV, 32 * u + 16, dt * 16, lane)),
+                         cat8(p[2 * u], p[2 * u + 1]), acc[dt]);
     }
   };
   for (int kb = 0; kb < kend; kb += 2 * kBlk) {
@@ -237,19 +247,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   __shared__ __align__(16) half_t sK[kBlk][kLdRow];
   __shared__ __align__(16) half_t sV[kBlk][kLdRow];
 
-  half4 qf[8], df[8];  // Q[myq][16 ks + 4 grp + j], dO[myq][...]
+  half8 qf[4], df[4];  // Q[myq][32 ks + 8 grp + j], dO[myq][...]
   float dsum = 0.f;    // this lane's part of rowsum(dO . O)
   {
     const half_t* qp = a.q + (int64_t)(start + qc) * a.q_tok + (int64_t)h * a.q_head;
     const half_t* dp = a.dout + (int64_t)(start + qc) * a.do_tok + (int64_t)h * a.do_head;
     const half_t* op = a.o + (int64_t)(start + qc) * a.o_tok + (int64_t)h * a.o_head;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      qf[ks] = ld4(qp + ks * 16 + grp * 4);
-      df[ks] = ld4(dp + ks * 16 + grp * 4);
-      const half4 ov = ld4(op + ks * 16 + grp * 4);
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[ks] = ld8(qp + ks * 32 + grp * 8);
+      df[ks] = ld8(dp + ks * 32 + grp * 8);
+      const half8 ov = ld8(op + ks * 32 + grp * 8);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dsum += (float)df[ks][j] * (float)ov[j];
+      for (int j = 0; j < 8; ++j) dsum += (float)df[ks][j] * (float)ov[j];
     }
   }
   const float delta = xor_sum(dsum);
@@ -271,25 +281,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     kv.stage(sK, sV);
     __syncthreads();
     if (kb + kBlk < kend) kv.fetch(kbase, a.k_tok, vbase, a.v_tok, start, len, kb + kBlk);
+    half4 ds[4];  // dS^T[key = kb + 16 kt + 4 grp + i][q = myq] = A of dS (rows q)
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        s = mfma16(ld4(&sK[kt * 16 + col][ks * 16 + grp * 4]), qf[ks], s);   // S^T
-        dp = mfma16(ld4(&sV[kt * 16 + col][ks * 16 + grp * 4]), df[ks], dp); // dP^T
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32(ld8(&sK[kt * 16 + col][ks * 32 + grp * 8]), qf[ks], s);   // S^T
+        dp = mfma32(ld8(&sV[kt * 16 + col][ks * 32 + grp * 8]), df[ks], dp); // dP^T
       }
-      half4 ds;  // dS^T[key = kb + 16 kt + 4 grp + i][q = myq] = A of dS (rows q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kb + kt * 16 + grp * 4 + i;
         const float p = (key <= myq && key < len) ? exp2f(s[i] * sl2 - lse) : 0.f;
-        ds[i] = f32_to_f16(p * (dp[i] - delta));
+        ds[kt][i] = f32_to_f16(p * (dp[i] - delta));
       }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        dq[dt] = mfma16(ds, ld4_tr(sK, kt * 16, dt * 16, lane), dq[dt]);
     }
+    // dQ += dS . K over the block's keys in two 32-deep steps (the forward's P.V slot order).
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        dq[dt] = mfma32(cat8(ds[2 * u], ds[2 * u + 1]),
+                        cat8(ld4_tr(sK, 32 * u, dt * 16, lane),
+                             ld4_tr(sK, 32 * u + 16, dt * 16, lane)), dq[dt]);
   }
   half_t* base = a.out + (int64_t)h * a.out_head;
 #pragma unroll
@@ -329,14 +344,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
   __shared__ __align__(16) half_t sO[kQt][kLdRow];    // dO rows
   __shared__ float sL[kQt], sDl[kQt];                 // lse2 and delta of the tile's queries
 
-  half4 kf[8], vf[8];  // K[mykey][16 ks + 4 grp + j], V[mykey][...]
+  half8 kf[4], vf[4];  // K[mykey][32 ks + 8 grp + j], V[mykey][...]
   {
     const half_t* kp = a.k + (int64_t)(start + kc) * a.k_tok + (int64_t)kvh * a.k_head;
     const half_t* vp = a.v + (int64_t)(start + kc) * a.v_tok + (int64_t)kvh * a.v_head;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      kf[ks] = ld4(kp + ks * 16 + grp * 4);
-      vf[ks] = ld4(vp + ks * 16 + grp * 4);
+    for (int ks = 0; ks < 4; ++ks) {
+      kf[ks] = ld8(kp + ks * 32 + grp * 8);
+      vf[ks] = ld8(vp + ks * 32 + grp * 8);
     }
   }
   float4v dk[8], dv[8];  // [key = k0w + 4 grp + i][d = 16 dt + col]
@@ -369,30 +384,39 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, float* p
     }
     __syncthreads();
     if (qt + kQt < len) fetch(qt + kQt);
+    // P^T / dS^T as A operands: [key = mykey][q = qt + 16 sub + 4 grp + i]
+    half4 p16[kQt / 16], ds16[kQt / 16];
 #pragma unroll
     for (int sub = 0; sub < kQt / 16; ++sub) {
       float4v s = float4v{0.f, 0.f, 0.f, 0.f}, dp = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        s = mfma16(ld4(&sQ[sub * 16 + col][ks * 16 + grp * 4]), kf[ks], s);   // S[q][key]
-        dp = mfma16(ld4(&sO[sub * 16 + col][ks * 16 + grp * 4]), vf[ks], dp); // dP[q][key]
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32(ld8(&sQ[sub * 16 + col][ks * 32 + grp * 8]), kf[ks], s);   // S[q][key]
+        dp = mfma32(ld8(&sO[sub * 16 + col][ks * 32 + grp * 8]), vf[ks], dp); // dP[q][key]
       }
-      half4 p16, ds16;  // P^T / dS^T as A operands: [key = mykey][q = qt + 16 sub + 4 grp + i]
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ql = sub * 16 + grp * 4 + i;
         const int q = qt + ql;
         const float p = (mykey <= q && q < len && mykey < len)
                             ? exp2f(s[i] * sl2 - sL[ql]) : 0.f;
-        p16[i] = f32_to_f16(p);
-        ds16[i] = f32_to_f16(p * (dp[i] - sDl[ql]));
-      }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        dv[dt] = mfma16(p16, ld4_tr(sO, sub * 16, dt * 16, lane), dv[dt]);
-        dk[dt] = mfma16(ds16, ld4_tr(sQ, sub * 16, dt * 16, lane), dk[dt]);
+        p16[sub][i] = f32_to_f16(p);
+        ds16[sub][i] = f32_to_f16(p * (dp[i] - sDl[ql]));
       }
     }
+    // dV += P^T . dO and dK += dS^T . Q over the tile's queries, 32 per step (the
+    // forward's P.V slot order).
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int u = 0; u < kQt / 32; ++u) {
+        dv[dt] = mfma32(cat8(p16[2 * u], p16[2 * u + 1]),
+                        cat8(ld4_tr(sO, 32 * u, dt * 16, lane),
+                             ld4_tr(sO, 32 * u + 16, dt * 16, lane)), dv[dt]);
+        dk[dt] = mfma32(cat8(ds16[2 * u], ds16[2 * u + 1]),
+                        cat8(ld4_tr(sQ, 32 * u, dt * 16, lane),
+                             ld4_tr(sQ, 32 * u + 16, dt * 16, lane)), dk[dt]);
+      }
   }
   const bool direct = a.hq == a.hk;
 #pragma unroll
