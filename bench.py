@@ -708,9 +708,10 @@ def other_configs(torch, _lib):
                   yk.data_ptr(), f16, 1, hq, hk, t, hd // 2, stream)
 
     def rope_bwd(i, stream):
+        # gradients written back in the projection views' layout (as the autograd node does)
         _lib.call("ss_rope_bwd", qv.data_ptr(), f16, *qst, 1, kv.data_ptr(), f16, *kst, 1,
-                  cs[0].data_ptr(), cs[1].data_ptr(), f16, *cst, yq.data_ptr(), f16,
-                  yk.data_ptr(), f16, 1, hq, hk, t, hd // 2, stream)
+                  cs[0].data_ptr(), cs[1].data_ptr(), f16, *cst, yq.data_ptr(), f16, *qst,
+                  yk.data_ptr(), f16, *kst, 1, hq, hk, t, hd // 2, stream)
 
     moved = (hq + hk) * t * hd * 4 + 2 * t * hd * 2
     out[f"rope_fwd_T{t}"] = hbm_point(graph_us(torch, _lib, rope_fwd, 64), moved, 1)

@@ -324,8 +324,10 @@ int ss_nf4_gemm_dx_swiglu(const uint16_t* dy, int64_t lddy, int64_t t, const uin
  * with strides (batch, token) and last stride 1, half = D / 2.  Forward
  * y1 = R(x1 c1) + R(-x2 s1), y2 = R(x2 c2) + R(x1 s2), R = rounding to the
  * output dtype promote(x, cos); backward d1 = R'(g1 c1) + R'(g2 s2),
- * d2 = R'(g2 c2) - R'(g1 s1), R' = rounding to the input dtype.  Outputs are
- * contiguous [B, H, S, D]; a NULL q (or k) operand is skipped.  Replace
+ * d2 = R'(g2 c2) - R'(g1 s1), R' = rounding to the input dtype.  Forward
+ * outputs are contiguous [B, H, S, D]; the backward writes dq / dk with the
+ * given element strides (batch, head, token; last dimension 1), e.g. the
+ * layout of the forward's input views.  A NULL q (or k) operand is skipped.  Replace
  * rope_pair_forward_kernel / rope_pair_backward_kernel
  * (solution/kernels/rope.py:24-98) as launched by _RoPE (:101-144). */
 int ss_rope_fwd(const void* q, int q_dtype, int64_t qb, int64_t qh, int64_t qt, const void* k,
@@ -338,8 +340,9 @@ int ss_rope_fwd(const void* q, int q_dtype, int64_t qb, int64_t qh, int64_t qt, 
 int ss_rope_bwd(const void* gq, int gq_dtype, int64_t qb, int64_t qh, int64_t qt, int64_t qd,
                 const void* gk, int gk_dtype, int64_t kb, int64_t kh, int64_t kt, int64_t kd,
                 const void* cos, const void* sin, int cs_dtype, int64_t cb, int64_t ct,
-                int64_t sb, int64_t st, int64_t c_batches, void* dq, int dq_dtype, void* dk,
-                int dk_dtype, int64_t batches, int64_t qheads, int64_t kheads, int64_t tokens,
+                int64_t sb, int64_t st, int64_t c_batches, void* dq, int dq_dtype, int64_t dqb,
+                int64_t dqh, int64_t dqt, void* dk, int dk_dtype, int64_t dkb, int64_t dkh,
+                int64_t dkt, int64_t batches, int64_t qheads, int64_t kheads, int64_t tokens,
                 int64_t half, void* stream);
 
 /* ------------------------------------------------------------ SwiGLU ---

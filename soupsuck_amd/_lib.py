@@ -92,7 +92,8 @@ SIGNATURES = {
     "ss_rope_fwd": [_c_void_p, _int, _i64, _i64, _i64] * 2 + [_c_void_p, _c_void_p, _int]
                    + [_i64] * 5 + [_c_void_p, _int] * 2 + [_i64] * 5 + [_c_void_p],
     "ss_rope_bwd": [_c_void_p, _int, _i64, _i64, _i64, _i64] * 2 + [_c_void_p, _c_void_p, _int]
-                   + [_i64] * 5 + [_c_void_p, _int] * 2 + [_i64] * 5 + [_c_void_p],
+                   + [_i64] * 5 + [_c_void_p, _int, _i64, _i64, _i64] * 2 + [_i64] * 5
+                   + [_c_void_p],
     "ss_swiglu_fwd": ([_c_void_p, _int, _i64, _i64] * 3) + [_i64, _i64, _c_void_p],
     "ss_swiglu_bwd": ([_c_void_p, _int, _i64, _i64] * 5) + [_i64, _i64, _c_void_p],
     "ss_add_rmsnorm_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _c_void_p,

@@ -11,8 +11,10 @@
 // fp32 arithmetic, no contraction (-ffp-contract=off), so the results equal
 // the numpy restatement bit for bit.  Inputs take runtime strides (batch,
 // head, token; the last dimension stride is given for gradients and must be
-// 1 for q / k / cos / sin); cos / sin have 1 or B batches; outputs are
-// contiguous [B, H, S, D].  HBM-bound: 2 x 2 B per fp16 element of q / k
+// 1 for q / k / cos / sin); cos / sin have 1 or B batches; forward outputs
+// are contiguous [B, H, S, D], the backward's gradients take the caller's
+// (batch, head, token) strides, so they can share the memory layout of the
+// forward's inputs (the transposed projection views).  HBM-bound: 2 x 2 B per fp16 element of q / k
 // plus cos / sin (shared by all heads of a token, mostly cache hits).
 // Aligned layouts take the vector kernel (4 columns per thread).
 
@@ -29,6 +31,7 @@ struct RopeOperand {
   void* y;
   int yd;
   int64_t heads;
+  int64_t yb, yh, yt;  // output element strides: batch, head, token (last dim 1)
 };
 
 struct RopeArgs {
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int64_t coff = cbatch * a.cb + token * a.ct;
   const int64_t soff = cbatch * a.sb + token * a.st;
   const int64_t xoff = batch * o.sb + h * o.sh + token * o.st;
-  const int64_t yoff = ((batch * o.heads + h) * a.tokens + token) * (2 * a.half);
+  const int64_t yoff = batch * o.yb + h * o.yh + token * o.yt;
   for (int64_t c = lane; c < a.half; c += 64) {
     const float c1 = ld_elem(a.c, a.cd, coff + c), c2 = ld_elem(a.c, a.cd, coff + c + a.half);
     const float s1 = ld_elem(a.s, a.cd, soff + c), s2 = ld_elem(a.s, a.cd, soff + c + a.half);
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
   const int64_t coff = cbatch * a.cb + token * a.ct + c;
   const int64_t soff = cbatch * a.sb + token * a.st + c;
   const int64_t xoff = batch * o.sb + h * o.sh + token * o.st + c;
-  const int64_t yoff = ((batch * o.heads + h) * a.tokens + token) * (2 * a.half) + c;
+  const int64_t yoff = batch * o.yb + h * o.yh + token * o.yt + c;
   float c1[4], c2[4], s1[4], s2[4], x1[4], x2[4], lo[4], hi[4];
   load4(o.x, o.xd, xoff, x1);
   load4(o.x, o.xd, xoff + a.half, x2);
@@ -155,7 +158,8 @@ bool vec_ok(const RopeArgs& a) {
     return false;
   for (const RopeOperand* o : {&a.q, &a.k}) {
     if (!o->x) continue;
-    if (o->sd != 1 || !al16(o->x) || !al16(o->y) || o->sb % 4 || o->sh % 4 || o->st % 4)
+    if (o->sd != 1 || !al16(o->x) || !al16(o->y) || o->sb % 4 || o->sh % 4 || o->st % 4 ||
+        o->yb % 4 || o->yh % 4 || o->yt % 4)
       return false;
   }
   return true;
@@ -199,8 +203,10 @@ extern "C" int ss_rope_fwd(const void* q, int q_dtype, int64_t qb, int64_t qh, i
   const char* fn = "ss_rope_fwd";
   SS_CHECK_ARG(yq_dtype == promote(q_dtype, cs_dtype) && yk_dtype == promote(k_dtype, cs_dtype),
                "%s: outputs must be promote(x, cos)", fn);
-  RopeArgs a{{q, q_dtype, qb, qh, qt, 1, yq, yq_dtype, qheads},
-             {k, k_dtype, kb, kh, kt, 1, yk, yk_dtype, kheads},
+  // Contiguous [B, H, S, D] outputs.
+  const int64_t d = 2 * half;
+  RopeArgs a{{q, q_dtype, qb, qh, qt, 1, yq, yq_dtype, qheads, qheads * tokens * d, tokens * d, d},
+             {k, k_dtype, kb, kh, kt, 1, yk, yk_dtype, kheads, kheads * tokens * d, tokens * d, d},
              cos, sin, cs_dtype, cb, ct, sb, st, c_batches, batches, tokens, half};
   return launch_rope(false, a, stream, fn);
 }
@@ -209,12 +215,13 @@ extern "C" int ss_rope_bwd(const void* gq, int gq_dtype, int64_t qb, int64_t qh,
                            int64_t qd, const void* gk, int gk_dtype, int64_t kb, int64_t kh,
                            int64_t kt, int64_t kd, const void* cos, const void* sin,
                            int cs_dtype, int64_t cb, int64_t ct, int64_t sb, int64_t st,
-                           int64_t c_batches, void* dq, int dq_dtype, void* dk, int dk_dtype,
-                           int64_t batches, int64_t qheads, int64_t kheads, int64_t tokens,
-                           int64_t half, void* stream) {
+                           int64_t c_batches, void* dq, int dq_dtype, int64_t dqb, int64_t dqh,
+                           int64_t dqt, void* dk, int dk_dtype, int64_t dkb, int64_t dkh,
+                           int64_t dkt, int64_t batches, int64_t qheads, int64_t kheads,
+                           int64_t tokens, int64_t half, void* stream) {
   const char* fn = "ss_rope_bwd";
-  RopeArgs a{{gq, gq_dtype, qb, qh, qt, qd, dq, dq_dtype, qheads},
-             {gk, gk_dtype, kb, kh, kt, kd, dk, dk_dtype, kheads},
+  RopeArgs a{{gq, gq_dtype, qb, qh, qt, qd, dq, dq_dtype, qheads, dqb, dqh, dqt},
+             {gk, gk_dtype, kb, kh, kt, kd, dk, dk_dtype, kheads, dkb, dkh, dkt},
              cos, sin, cs_dtype, cb, ct, sb, st, c_batches, batches, tokens, half};
   return launch_rope(true, a, stream, fn);
 }

@@ -93,6 +93,28 @@ def _target(t):
     return (_lib.ptr(t), _lib.dtype_code(t.dtype) if t is not None else 0)
 
 
+def _strided_target(t):
+    """(pointer, dtype code, batch / head / token strides) of a gradient output."""
+    if t is None:
+        return (None, 0, 0, 0, 0)
+    return (t.data_ptr(), _lib.dtype_code(t.dtype)) + tuple(t.stride()[:3])
+
+
+def _layout_of(shape, stride, dtype, device):
+    """An uninitialised [B, H, S, D] tensor in the memory order of `stride` when that is
+    a dense permutation with a unit last stride (a head-split view of a projection's
+    [B, S, H * D] output), else contiguous: a gradient written that way reaches the
+    projection's backward without a copy."""
+    expect, dense = 1, stride[-1] == 1 or shape[-1] == 1
+    for i in sorted(range(len(shape)), key=lambda i: stride[i]):
+        if shape[i] != 1:
+            dense = dense and stride[i] == expect
+            expect *= shape[i]
+    if dense:
+        return torch.empty_strided(shape, stride, device=device, dtype=dtype)
+    return torch.empty(shape, device=device, dtype=dtype)
+
+
 class _RotaryPair(torch.autograd.Function):
     """Both rotations in one launch each way; the backward rotates by -theta."""
 
@@ -106,7 +128,7 @@ class _RotaryPair(torch.autograd.Function):
                       *_target(outs[0]), *_target(outs[1]), *geo, _lib.stream(q.device))
         ctx.save_for_backward(cos, sin)
         ctx.geo = geo
-        ctx.inputs = ((q.shape, q.dtype), (k.shape, k.dtype))
+        ctx.inputs = ((q.shape, q.stride(), q.dtype), (k.shape, k.stride(), k.dtype))
         ctx.set_materialize_grads(False)
         # an output whose input takes no gradient carries none, as in eager PyTorch
         frozen = [y for y, wanted in zip(outs, ctx.needs_input_grad) if not wanted]
@@ -119,14 +141,15 @@ class _RotaryPair(torch.autograd.Function):
     def backward(ctx, gq, gk):
         cos, sin = ctx.saved_tensors
         grads, results = [], []
-        for g, wanted, (shape, dtype) in zip((gq, gk), ctx.needs_input_grad, ctx.inputs):
+        for g, wanted, (shape, stride, dtype) in zip((gq, gk), ctx.needs_input_grad,
+                                                     ctx.inputs):
             live = g is not None and wanted
             grads.append(g if live else None)
-            results.append(torch.empty(shape, device=cos.device, dtype=dtype) if live else None)
+            results.append(_layout_of(shape, stride, dtype, cos.device) if live else None)
         if any(r is not None for r in results) and not ctx.geo.empty:
             _lib.call("ss_rope_bwd", *_operand(grads[0], 4), *_operand(grads[1], 4),
-                      *_table(cos, sin), *_target(results[0]), *_target(results[1]), *ctx.geo,
-                      _lib.stream(cos.device))
+                      *_table(cos, sin), *_strided_target(results[0]),
+                      *_strided_target(results[1]), *ctx.geo, _lib.stream(cos.device))
         return results[0], results[1], None, None
 
 
