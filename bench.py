@@ -780,8 +780,8 @@ def other_configs(torch, _lib):
         "bound": "mfma",
         "roofline_frac": round((f_fwd + f_bwd) / PEAK_FP16_TFLOPS / 1e9 / tot, 4),
         "timing": "HIP events on the stream (GPU clock) around the forward and the backward, "
-                  "median of 5 after 1 warm-up; the backward reads the head-gradient gain "
-                  "max|g|/1024 on the host once (its idle gap is inside the time)"}
+                  "median of 5 after 1 warm-up; the backward's head-gradient gain max|g|/1024 "
+                  "stays on the device (no host round trip between forward and backward)"}
     del hd, hw
     torch.cuda.empty_cache()
     return out

@@ -270,14 +270,16 @@ int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float
  * direct-to-LDS kernel: K % 64 == 0, 16-byte aligned operands, M % 8 == 0
  * for a_trans = 1 and N % 8 == 0 for b_trans = 0):
  * ss_gemm_f16_workspace_size(a_trans, b_trans, m, n, k) bytes; a smaller
- * workspace means no split.  Serves the vocabulary-chunk dX product of the
- * fused cross-entropy backward (solution/kernels/cross_entropy.py:202), whose
+ * workspace (or none) means no split.  alpha_dev, when not NULL, is a device
+ * fp32 scalar that multiplies alpha (a scale computed on the device needs no
+ * host round trip).  Serves the vocabulary-chunk products of the fused
+ * cross-entropy backward (solution/kernels/cross_entropy.py:195,202), whose
  * output tile count is small. */
 size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k);
 int ss_gemm_f16_split(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k, float alpha,
-                      const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                      const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      const float* alpha_dev, const uint16_t* a, int64_t lda, const uint16_t* b,
+                      int64_t ldb, const uint16_t* bias, float beta, void* c, int c_dtype,
+                      int64_t ldc, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------- LoRA (A11) ---
  * out = round_out(fp32(base) + fp32(scaled)), scaled = round_adapter(adapter*s),
@@ -450,13 +452,14 @@ int ss_ce_outputs(const float* state, const int64_t* targets, float* loss, float
 /* dz[r, c] = fp16((exp(z - lse[r]) - [start + c == target[r]]) * grad[r] / gain[r]),
  * gain[r] = max(|grad[r]|, 1e-30) / 1024 (zero on ignored rows); when dz_global
  * is not NULL it also receives the same derivative scaled by 1/global_gain
- * instead of 1/gain[r] (for the lm_head gradient).  dz and dz_global are dense
+ * instead of 1/gain[r] (for the lm_head gradient; global_gain points at one
+ * fp32 value > 0 in device memory).  dz and dz_global are dense
  * [n, width].  Row r of the logits is z[z_rows[r]] when z_rows (int64 [n]) is
  * not NULL, else z[r] (row stride ldz).  Replaces vocabulary_derivative_kernel
  * (solution/kernels/cross_entropy.py:108-122). */
 int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
                      const int64_t* targets, const float* lse, const float* grad, uint16_t* dz,
-                     uint16_t* dz_global, float global_gain, int64_t n, int64_t width,
+                     uint16_t* dz_global, const float* global_gain, int64_t n, int64_t width,
                      int64_t start, int64_t ignore_index, void* stream);
 
 /* out[r, :] = cast(acc[inverse[r], :] * max(|grad[r]|, 1e-30) / 1024) when

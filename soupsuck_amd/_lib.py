@@ -77,8 +77,9 @@ SIGNATURES = {
     "ss_gemm_f16": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
                     _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p],
     "ss_gemm_f16_workspace_size": [_int, _int, _i64, _i64, _i64],
-    "ss_gemm_f16_split": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _i64, _c_void_p, _i64,
-                          _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p, _size, _c_void_p],
+    "ss_gemm_f16_split": [_int, _int, _i64, _i64, _i64, _f32, _c_void_p, _c_void_p, _i64,
+                          _c_void_p, _i64, _c_void_p, _f32, _c_void_p, _int, _i64, _c_void_p,
+                          _size, _c_void_p],
     "ss_lora_epilogue_fwd": [_c_void_p, _int, _c_void_p, _int, _c_void_p, _int, _i64, _f32, _int,
                              _c_void_p],
     "ss_lora_epilogue_bwd": [_c_void_p, _int, _c_void_p, _int, _i64, _f32, _c_void_p],
@@ -117,7 +118,7 @@ SIGNATURES = {
                     _int, _c_void_p],
     "ss_ce_outputs": [_c_void_p] * 5 + [_i64, _i64, _c_void_p],
     "ss_ce_derivative": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                         _c_void_p, _f32, _i64, _i64, _i64, _i64, _c_void_p],
+                         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
     "ss_attn_varlen_fwd": [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _int, _int, _i64, _int,
                                                            _int, _int, _f32, _c_void_p, _i64,
                                                            _i64, _c_void_p, _c_void_p],

@@ -198,8 +198,8 @@ __global__ __launch_bounds__(256) void ce_derivative_kernel(
     const half_t* __restrict__ z, int64_t ldz, const int64_t* __restrict__ z_rows,
     const int64_t* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ grad, half_t* __restrict__ dz,
-    half_t* __restrict__ dzg, float global_gain, int64_t width, int64_t start, int64_t ignore,
-    int vec) {
+    half_t* __restrict__ dzg, const float* __restrict__ global_gain_p, int64_t width,
+    int64_t start, int64_t ignore, int vec) {
   const int64_t row = blockIdx.x;
   const int64_t c = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 8;
   if (c >= width) return;
@@ -207,6 +207,7 @@ __global__ __launch_bounds__(256) void ce_derivative_kernel(
   const bool valid = tgt != ignore;
   const float g = valid ? grad[row] : 0.0f;
   const float gain = fmaxf(fabsf(g), 1e-30f) / 1024.0f;
+  const float global_gain = dzg ? *global_gain_p : 1.0f;
   const float l = lse[row];
   float v[8];
   load_logits8(z + (z_rows ? z_rows[row] : row) * ldz, c, width, vec, v);
@@ -296,11 +297,11 @@ extern "C" int ss_ce_outputs(const float* state, const int64_t* targets, float* 
 
 extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
                                 const int64_t* targets, const float* lse, const float* grad,
-                                uint16_t* dz, uint16_t* dz_global, float global_gain, int64_t n,
-                                int64_t width, int64_t start, int64_t ignore_index,
+                                uint16_t* dz, uint16_t* dz_global, const float* global_gain,
+                                int64_t n, int64_t width, int64_t start, int64_t ignore_index,
                                 void* stream) {
   SS_CHECK_ARG(n >= 0 && width > 0 && ldz >= width, "ss_ce_derivative: bad sizes");
-  SS_CHECK_ARG(!dz_global || global_gain > 0.0f, "ss_ce_derivative: global_gain must be > 0");
+  SS_CHECK_ARG(!dz_global || global_gain, "ss_ce_derivative: dz_global needs global_gain");
   if (n == 0) return SS_OK;
   SS_CHECK_ARG(z && targets && lse && grad && dz, "ss_ce_derivative: null pointer");
   const int vec = al16(z) && ldz % 8 == 0 && al16(dz) && width % 8 == 0 &&
@@ -310,7 +311,7 @@ extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z
   hipLaunchKernelGGL(ce_derivative_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      reinterpret_cast<const half_t*>(z), ldz, z_rows, targets, lse, grad,
                      reinterpret_cast<half_t*>(dz), reinterpret_cast<half_t*>(dz_global),
-                     dz_global ? global_gain : 1.0f, width, start, ignore_index, vec);
+                     global_gain, width, start, ignore_index, vec);
   SS_CHECK_LAUNCH("ce_derivative_kernel");
   return SS_OK;
 }

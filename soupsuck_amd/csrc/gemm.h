@@ -75,6 +75,10 @@ struct GemmParams {
   void* C;
   int64_t ldc;
   float alpha;
+  // Device fp32 scalar multiplying alpha when not null (read once per
+  // workgroup; the plain dense GEMMs and their split-K reduce), so a caller
+  // whose scale is computed on the device needs no host round trip.
+  const float* alpha_dev;
   int beta;
   const half_t* lz;   // Z or dZ, [M, 16] contiguous
   const half_t* lb;   // lora_B [N, 16] (EPI_LORA) or lora_A [16, ldlb] (EPI_RANK)

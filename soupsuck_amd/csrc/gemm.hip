@@ -296,6 +296,7 @@ struct Tile {
 
 template <class T, int OPA, int OPB, int CT, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams p) {
+  if (p.alpha_dev) p.alpha *= *p.alpha_dev;
   constexpr int BM = T::kBM, BN = T::kBN, BK = T::kBK, WM = T::kWM, WN = T::kWN;
   constexpr int LDK = T::kLdk;
   constexpr bool kNf4 = OPA >= OP_NF4_ROW || OPB >= OP_NF4_ROW;
@@ -1207,7 +1208,8 @@ extern "C" int ss_qlora_backward_dropout(const uint16_t* dy, int64_t lddy, int64
 }
 
 static int gemm_f16_impl(const char* fn, int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,
-                         float alpha, const uint16_t* a, int64_t lda, const uint16_t* b,
+                         float alpha, const float* alpha_dev, const uint16_t* a, int64_t lda,
+                         const uint16_t* b,
                          int64_t ldb, const uint16_t* bias, float beta, void* c, int c_dtype,
                          int64_t ldc, void* workspace, size_t workspace_bytes, void* stream) {
   SS_CHECK_ARG(m >= 0 && n >= 0 && k >= 0, "%s: negative size", fn);
@@ -1226,7 +1228,7 @@ static int gemm_f16_impl(const char* fn, int a_trans, int b_trans, int64_t m, in
   p.B = reinterpret_cast<const half_t*>(b); p.ldb = ldb;
   p.b_vec = aligned16(b, ldb) && (b_trans ? k % 8 == 0 : n % 8 == 0);
   p.bias = reinterpret_cast<const half_t*>(bias);
-  p.C = c; p.ldc = ldc; p.alpha = alpha; p.beta = beta != 0.0f;
+  p.C = c; p.ldc = ldc; p.alpha = alpha; p.alpha_dev = alpha_dev; p.beta = beta != 0.0f;
   hipStream_t s = (hipStream_t)stream;
   // b_trans = 1: B stored [N,K] -> OP_ROW; b_trans = 0: B stored [K,N] -> OP_COL.
   const int code = (a_trans ? 2 : 0) + (b_trans ? 0 : 1) + (c_dtype == SS_F32 ? 4 : 0);
@@ -1248,8 +1250,8 @@ extern "C" int ss_gemm_f16(int a_trans, int b_trans, int64_t m, int64_t n, int64
                            const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                            const uint16_t* bias, float beta, void* c, int c_dtype, int64_t ldc,
                            void* stream) {
-  return gemm_f16_impl("ss_gemm_f16", a_trans, b_trans, m, n, k, alpha, a, lda, b, ldb, bias,
-                       beta, c, c_dtype, ldc, nullptr, 0, stream);
+  return gemm_f16_impl("ss_gemm_f16", a_trans, b_trans, m, n, k, alpha, nullptr, a, lda, b, ldb,
+                       bias, beta, c, c_dtype, ldc, nullptr, 0, stream);
 }
 
 extern "C" size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m, int64_t n,
@@ -1261,10 +1263,11 @@ extern "C" size_t ss_gemm_f16_workspace_size(int a_trans, int b_trans, int64_t m
 }
 
 extern "C" int ss_gemm_f16_split(int a_trans, int b_trans, int64_t m, int64_t n, int64_t k,
-                                 float alpha, const uint16_t* a, int64_t lda, const uint16_t* b,
-                                 int64_t ldb, const uint16_t* bias, float beta, void* c,
-                                 int c_dtype, int64_t ldc, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
-  return gemm_f16_impl("ss_gemm_f16_split", a_trans, b_trans, m, n, k, alpha, a, lda, b, ldb,
-                       bias, beta, c, c_dtype, ldc, workspace, workspace_bytes, stream);
+                                 float alpha, const float* alpha_dev, const uint16_t* a,
+                                 int64_t lda, const uint16_t* b, int64_t ldb,
+                                 const uint16_t* bias, float beta, void* c, int c_dtype,
+                                 int64_t ldc, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return gemm_f16_impl("ss_gemm_f16_split", a_trans, b_trans, m, n, k, alpha, alpha_dev, a, lda,
+                       b, ldb, bias, beta, c, c_dtype, ldc, workspace, workspace_bytes, stream);
 }

@@ -332,6 +332,7 @@ constexpr int nt_smem_bytes() {
 template <class C, int CT, int EPI, int L = 0>
 __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[nt_smem_bytes<C, EPI>()];
+  if (EPI == EPI_PLAIN && p.alpha_dev) p.alpha *= *p.alpha_dev;
   const int64_t tiles = gridDim.x - p.tail_blocks - p.tail2_blocks;
   if constexpr (EPI == EPI_RANK) {
     if ((int64_t)blockIdx.x >= tiles) {
@@ -378,6 +379,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINW) void gemm_nt_kernel(GemmParam
 // need launches of their own.
 template <int CT, int EPI, bool TAIL = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits) {
+  if (EPI == EPI_PLAIN && p.alpha_dev) p.alpha *= *p.alpha_dev;
   int64_t block = blockIdx.x;
   if constexpr (TAIL) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[kRankGradSmem];

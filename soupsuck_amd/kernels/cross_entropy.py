@@ -166,9 +166,11 @@ class _Backward:
         dz = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
         acc = torch.zeros((count, hdim), device=self.dev, dtype=torch.float32) \
             if dx is not None else None
-        head_gain = 1.0
+        head_gain = None
         if dw is not None:
-            head_gain = max(self.grad.abs().max().item(), 1e-30) / 1024.0
+            # max_r |g_r| / 1024 as a device scalar: no host round trip between the
+            # forward and the backward's launches
+            head_gain = (self.grad.abs().amax().clamp_min(1e-30) / 1024.0).reshape(1)
             # dz' per chunk as [padded, width] (dense rows): the rows past `count`
             # stay zero; they are written only by a wider chunk's rows, so only a
             # narrower chunk clears them.
@@ -189,17 +191,17 @@ class _Backward:
                     dz_head[count * width:padded * width].zero_()
             _lib.call("ss_ce_derivative", z.data_ptr(), ldz, _lib.ptr(z_rows),
                       self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
-                      d.data_ptr(), _lib.ptr(dh), float(head_gain), count, width, start,
+                      d.data_ptr(), _lib.ptr(dh), _lib.ptr(head_gain), count, width, start,
                       self.ignore, self.stream)
             if acc is not None:
                 gemm_f16(d, w, out=acc, accumulate=True, split_k=True)
             if dw is not None:
                 rows_w = dw.narrow(0, start, width)
                 if rows_w.dtype in FLOAT_DTYPES:
-                    gemm_f16(dh, self.h_pad, a_trans=True, out=rows_w, alpha=float(head_gain))
+                    gemm_f16(dh, self.h_pad, a_trans=True, out=rows_w, alpha_dev=head_gain)
                 else:
                     rows_w.copy_(gemm_f16(dh, self.h_pad, a_trans=True,
-                                          out_dtype=torch.float32, alpha=float(head_gain)))
+                                          out_dtype=torch.float32, alpha_dev=head_gain))
         if acc is not None:
             rows, hd = dx.shape
             inverse = torch.empty(rows, device=self.dev, dtype=torch.int32)

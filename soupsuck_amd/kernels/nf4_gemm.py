@@ -44,13 +44,14 @@ def _dense_weight(packed, state, n, k):
 
 
 def gemm_f16(a, b, *, a_trans=False, b_trans=False, out=None, out_dtype=torch.float16,
-             alpha=1.0, accumulate=False, bias=None, split_k=False):
+             alpha=1.0, accumulate=False, bias=None, split_k=False, alpha_dev=None):
     """C = alpha * op(A) . op(B) (+bias) (+C) on the MFMA engine (ss_gemm_f16).
 
     a: [M,K] (or [K,M] when a_trans), b: [K,N] (or [N,K] when b_trans); fp16,
     row-major with unit column stride.  Returns C [M,N] of out_dtype.
     split_k: give the dense NT kernel scratch to split a long reduction over
-    workgroups when the output has few tiles (ss_gemm_f16_split).
+    workgroups when the output has few tiles (ss_gemm_f16_split).  alpha_dev: a
+    one-element fp32 device tensor multiplying alpha (no host synchronisation).
     """
     if a.dtype != torch.float16 or b.dtype != torch.float16:
         raise ValueError("gemm_f16 expects fp16 operands")
@@ -66,14 +67,18 @@ def gemm_f16(a, b, *, a_trans=False, b_trans=False, out=None, out_dtype=torch.fl
         out = torch.empty((m, n), device=a.device, dtype=out_dtype)
     if out.shape != (m, n) or out.stride(-1) != 1:
         raise ValueError("gemm_f16: bad output buffer")
+    if alpha_dev is not None and (alpha_dev.dtype != torch.float32 or alpha_dev.numel() != 1
+                                  or alpha_dev.device != a.device):
+        raise ValueError("gemm_f16: alpha_dev must be one fp32 element on the operands' device")
     size = _lib.load().ss_gemm_f16_workspace_size(int(a_trans), int(b_trans), m, n, k) \
         if split_k else 0
-    if size:
-        ws = torch.empty(size, dtype=torch.uint8, device=a.device)
+    if size or alpha_dev is not None:
+        ws = torch.empty(size, dtype=torch.uint8, device=a.device) if size else None
         _lib.call("ss_gemm_f16_split", int(a_trans), int(b_trans), m, n, k, float(alpha),
-                  a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), _lib.ptr(bias),
-                  1.0 if accumulate else 0.0, out.data_ptr(), _lib.dtype_code(out.dtype),
-                  out.stride(0), ws.data_ptr(), size, _lib.stream(a.device))
+                  _lib.ptr(alpha_dev), a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+                  _lib.ptr(bias), 1.0 if accumulate else 0.0, out.data_ptr(),
+                  _lib.dtype_code(out.dtype), out.stride(0), _lib.ptr(ws), size,
+                  _lib.stream(a.device))
         return out
     _lib.call("ss_gemm_f16", int(a_trans), int(b_trans), m, n, k, float(alpha), a.data_ptr(),
               a.stride(0), b.data_ptr(), b.stride(0), _lib.ptr(bias), 1.0 if accumulate else 0.0,

@@ -366,3 +366,25 @@ def test_dense_nt_k_major_operands(device, m, n, k, split, a_trans, b_trans):
     acc = torch.from_numpy(base).to(device)
     gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out=acc, accumulate=True, split_k=split)
     np.testing.assert_allclose(np16(acc), base + prod, rtol=1e-5, atol=5e-4)
+
+
+@pytest.mark.parametrize("m,n,k,a_trans,b_trans,split", [
+    (990, 1536, 8960, False, True, True),    # split-K: the reduce applies the scale
+    (8192, 1536, 576, True, False, False),   # the CE head-gradient product (K-major operands)
+    (300, 200, 100, False, False, False),    # K % 64 != 0: the general kernel
+])
+def test_dense_gemm_device_alpha(device, m, n, k, a_trans, b_trans, split):
+    """alpha_dev (a device fp32 scalar) multiplies alpha in every dense path: the same bits
+    as the host alpha of the product (0.5 x 3.0 = 1.5 exactly)."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((k, m) if a_trans else (m, k)).astype(np.float16)
+    b = (rng.standard_normal((n, k) if b_trans else (k, n)) * 0.05).astype(np.float16)
+    ad, bd = torch.from_numpy(a).to(device), torch.from_numpy(b).to(device)
+    scale = torch.tensor([3.0], device=device, dtype=torch.float32)
+    for out_dtype in (torch.float16, torch.float32):
+        got = gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out_dtype=out_dtype,
+                       alpha=0.5, alpha_dev=scale, split_k=split)
+        ref = gemm_f16(ad, bd, a_trans=a_trans, b_trans=b_trans, out_dtype=out_dtype,
+                       alpha=1.5, split_k=split)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
