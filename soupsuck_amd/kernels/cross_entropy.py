@@ -24,11 +24,13 @@ derivative scaled by one global gain max_r |g_r| / 1024 (a per-row gain cannot
 be factored out of a sum over rows).
 
 Kept logits: when the fp16 logits [N, V] fit KEEP_LOGITS_BUDGET (1 GiB; 251 MB
-at configs[3]) and a backward may run, the forward's chunk products write into
-one [N, V] buffer and the backward reads each chunk from there (rows picked
-through the labelled-row indices) instead of recomputing h . W_c^T: the same
-bits, one product per chunk fewer.  Above the budget the backward recomputes,
-as the reference does, holding one [rows, chunk] tile at a time.
+at configs[3]) and a backward may run, the forward's products write into one
+[N, V] buffer and the backward reads the logits from there (rows picked through
+the labelled-row indices) instead of recomputing h . W_c^T: one product per
+chunk fewer.  The products then span several chunks (as many as fill one wave
+of 256 x 256 output tiles: two at configs[3]); the statistics still merge chunk
+by chunk, so the forward's outputs are the same bits.  Above the budget the
+backward recomputes, as the reference does, one [rows, chunk] tile at a time.
 
 Layout for the MFMA engine: the dense direct-to-LDS kernel reads operands stored
 along the reduced dimension (K-major) through transposed LDS reads, so dX = dz .
@@ -83,9 +85,25 @@ def _gather_rows(src, index, out=None):
     return out
 
 
+_CUS = {}
+
+
+def _product_span(rows, chunk, dev):
+    """Vocabulary columns per logits product when the forward keeps its logits: whole
+    chunks, as many as fit one wave of 256 x 256 output tiles on the device's CUs (T =
+    826: two chunks of 8192, 256 tiles, against 224 tiles of 128 x 256 for one chunk).
+    The statistics still merge chunk by chunk, and an output element does not depend on
+    the product's width, so the results are the same bits."""
+    if dev not in _CUS:
+        _CUS[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    tiles = -(-rows // 256) * -(-chunk // 256)
+    return max(1, _CUS[dev] // tiles) * chunk
+
+
 def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
     """Loss, entropy, first argmax and lse; with ``keep`` also the fp16 logits [rows, V]
-    (the chunk products write straight into their columns), else None."""
+    (the products write straight into their columns, several chunks at a time), else
+    None."""
     rows = hidden16.shape[0]
     dev = hidden16.device
     loss = torch.empty(rows, device=dev, dtype=torch.float32)
@@ -99,12 +117,19 @@ def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
     vocab = weight.shape[0]
     tile = torch.empty((rows, vocab if keep else min(chunk, vocab)), device=dev,
                        dtype=torch.float16)
-    for start, width in _vocab_chunks(vocab, chunk):
-        logits = tile[:, start:start + width] if keep else tile[:, :width]
-        gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True, out=logits)
-        _lib.call("ss_ce_stats", logits.data_ptr(), tile.stride(0), targets.data_ptr(),
-                  online.data_ptr(), best.data_ptr(), rows, width, start, ignore_index,
-                  int(start == 0), stream)
+    span = _product_span(rows, chunk, dev) if keep else chunk
+    for pstart, pwidth in _vocab_chunks(vocab, span):
+        if keep:
+            gemm_f16(hidden16, _head_rows(weight, pstart, pwidth), b_trans=True,
+                     out=tile[:, pstart:pstart + pwidth])
+        for start, width in _vocab_chunks(pwidth, chunk):
+            start += pstart
+            logits = tile[:, start:start + width] if keep else tile[:, :width]
+            if not keep:
+                gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True, out=logits)
+            _lib.call("ss_ce_stats", logits.data_ptr(), tile.stride(0), targets.data_ptr(),
+                      online.data_ptr(), best.data_ptr(), rows, width, start, ignore_index,
+                      int(start == 0), stream)
     _lib.call("ss_ce_outputs", online.data_ptr(), targets.data_ptr(), loss.data_ptr(),
               entropy.data_ptr(), lse.data_ptr(), rows, ignore_index, stream)
     return loss, entropy, best, lse, tile if keep else None
@@ -157,10 +182,13 @@ class _Backward:
             self.grad = _gather_rows(grad, self.kept)
 
     def run(self, dx, dw):
-        width_max = min(self.chunk, self.weight.shape[0])
         count, padded = self.count, self.padded
         hdim = self.h.shape[1]
         kept_z = self.logits
+        # With the kept logits every step spans several chunks (the derivative is
+        # elementwise and the products take any width); recomputing, one chunk at a time.
+        span = self.chunk if kept_z is None else _product_span(count, self.chunk, self.dev)
+        width_max = min(span, self.weight.shape[0])
         if kept_z is None:
             logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
         dz = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
@@ -171,17 +199,17 @@ class _Backward:
             # max_r |g_r| / 1024 as a device scalar: no host round trip between the
             # forward and the backward's launches
             head_gain = (self.grad.abs().amax().clamp_min(1e-30) / 1024.0).reshape(1)
-            # dz' per chunk as [padded, width] (dense rows): the rows past `count`
-            # stay zero; they are written only by a wider chunk's rows, so only a
-            # narrower chunk clears them.
+            # dz' per step as [padded, width] (dense rows): the rows past `count`
+            # stay zero; they are written only by a wider step's rows, so only a
+            # narrower step clears them.
             dz_head = torch.zeros(padded * width_max, device=self.dev, dtype=torch.float16)
-        for start, width in _vocab_chunks(self.weight.shape[0], self.chunk):
+        for start, width in _vocab_chunks(self.weight.shape[0], span):
             w = _head_rows(self.weight, start, width)
             if kept_z is None:
                 z, ldz, z_rows = logits[:, :width], logits.stride(0), None
                 gemm_f16(self.h, w, b_trans=True, out=z)
             else:
-                # The forward's chunk, its rows picked through the kept-row indices.
+                # The forward's logits of the step, rows picked through the kept-row indices.
                 z, ldz, z_rows = kept_z[:, start:start + width], kept_z.stride(0), self.kept
             d = dz.view(-1)[:count * width].view(count, width)
             dh = None

@@ -160,8 +160,10 @@ def test_config4_full_shape_against_fp32_torch(device):
 
 @pytest.mark.parametrize("n,h,v", [(600, 256, 20000), (826, 1536, 151936)])
 def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v):
-    """The backward reading the forward's kept logits gives the same bits as the
-    backward that recomputes each chunk (budget 0), outputs and both gradients."""
+    """The path that keeps the forward's logits (its products spanning several chunks)
+    against the one that recomputes chunk by chunk (budget 0): loss, entropy, argmax,
+    lse and the head gradient are the same bits; dX, whose split-K reductions then run
+    over different depths, agrees to fp32 summation order (relative L2 1e-4)."""
     gen = torch.Generator(device="cpu").manual_seed(n)
     x0 = torch.randn((n, h), generator=gen).to(torch.float16).to(device)
     w0 = (torch.randn((v, h), generator=gen) * 0.02).to(torch.float16).to(device)
@@ -178,5 +180,7 @@ def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v):
         outs[0].backward(g)
         torch.cuda.synchronize()
         runs.append((*outs, x.grad, w.grad))
-    for kept, recomputed in zip(*runs):
+    for kept, recomputed in zip(runs[0][:4] + runs[0][5:], runs[1][:4] + runs[1][5:]):
         assert torch.equal(kept, recomputed)
+    dx_k, dx_r = runs[0][4].float(), runs[1][4].float()
+    assert ((dx_k - dx_r).norm() / dx_r.norm()).item() <= 1e-4
