@@ -435,19 +435,28 @@ int ss_unpad_scatter(const void* packed, int64_t tokens, void* padded, const int
                      int64_t rows, int64_t row_bytes, void* stream);
 
 /* ----------------------------------------------- fused linear CE (A17-19) ---
- * Online vocabulary statistics over one chunk of fp16 logits z[n, width]
- * (row stride ldz) whose first column is vocabulary index `start`; state is
- * fp32[n,4] = (max, sum exp(z-max), sum exp(z-max)*z, target logit), best
- * int64[n] is the first argmax.  first != 0 initialises the state.
- * Replaces vocabulary_statistics_kernel (solution/kernels/cross_entropy.py:51-89). */
-int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* targets, float* state,
-                int64_t* best, int64_t n, int64_t width, int64_t start, int64_t ignore_index,
-                int first, void* stream);
+ * Vocabulary statistics of fp16 logits z[n, width] (row stride ldz) whose first
+ * column is vocabulary index `start`, in pieces of `piece` columns (1..8192;
+ * the last may be narrower): piece p of row r writes its partial state to slot
+ * slot0 + p of row r of partial fp32[n, slots, 4] = (max m, sum exp(z - m),
+ * sum exp(z - m) * z, target logit) and of partial_arg int64[n, slots] (first
+ * argmax).  One call may cover any number of vocabulary chunks; the partial
+ * row holds every piece of the vocabulary.  partial must be 16-byte aligned.
+ * Replaces vocabulary_statistics_kernel (solution/kernels/cross_entropy.py:51-89),
+ * whose per-chunk running state becomes one slot per piece, folded by
+ * ss_ce_outputs. */
+int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* targets, float* partial,
+                int64_t* partial_arg, int64_t n, int64_t width, int64_t piece, int64_t start,
+                int64_t slot0, int64_t slots, int64_t ignore_index, void* stream);
 
-/* lse = max + log(sum), entropy = lse - t/sum, loss = lse - z_target (0 when
- * ignored).  Replaces vocabulary_outputs_kernel (cross_entropy.py:92-105). */
-int ss_ce_outputs(const float* state, const int64_t* targets, float* loss, float* entropy,
-                  float* lse, int64_t n, int64_t ignore_index, void* stream);
+/* Folds each row's `slots` partial states in slot order (both sums rescaled to
+ * the larger max; ties of the max keep the lower index) into max M, sum S, sum
+ * T, target logit Z and argmax; then lse = M + log S, entropy = lse - T/S,
+ * loss = lse - Z (0 when ignored), best = the first argmax (int64[n]).
+ * Replaces vocabulary_outputs_kernel (cross_entropy.py:92-105). */
+int ss_ce_outputs(const float* partial, const int64_t* partial_arg, int64_t slots,
+                  const int64_t* targets, float* loss, float* entropy, float* lse,
+                  int64_t* best, int64_t n, int64_t ignore_index, void* stream);
 
 /* dz[r, c] = fp16((exp(z - lse[r]) - [start + c == target[r]]) * grad[r] / gain[r]),
  * gain[r] = max(|grad[r]|, 1e-30) / 1024 (zero on ignored rows); when dz_global

@@ -114,9 +114,9 @@ SIGNATURES = {
     "ss_unpad_gather": [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "ss_unpad_inverse": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p],
     "ss_unpad_scatter": [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
-    "ss_ce_stats": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
-                    _int, _c_void_p],
-    "ss_ce_outputs": [_c_void_p] * 5 + [_i64, _i64, _c_void_p],
+    "ss_ce_stats": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 7 +
+                   [_c_void_p],
+    "ss_ce_outputs": [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p],
     "ss_ce_derivative": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                          _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
     "ss_attn_varlen_fwd": [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _int, _int, _i64, _int,

@@ -79,6 +79,21 @@ __device__ __forceinline__ float nested_scale(const uint8_t* __restrict__ qabs,
 
 __host__ __device__ constexpr int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Compute units of the current device, queried once per device (256 when the
+// query fails).  Concurrent first calls store the same value.
+inline int device_cu_count() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int v = 0;
+    const bool ok =
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+    cus[dev] = ok && v > 0 ? v : 256;
+  }
+  return cus[dev];
+}
+
 // Thread-local last-error text for the C ABI.
 void set_error(const char* fmt, ...);
 

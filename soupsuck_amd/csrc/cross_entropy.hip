@@ -5,40 +5,20 @@
 // rescale and scatter).  The logits of a chunk are fp16 (the reference
 // rounds logits before any statistic); all statistics are fp32.
 //
-// ce_stats: one 256-thread workgroup per row; pass 1 finds the chunk max and
-// its first index, pass 2 accumulates sum exp(z - m) and sum exp(z - m) * z
-// against the merged running max.  Lanes read 8 consecutive fp16 logits
-// (16 B), so a wave reads 1 KiB contiguous per access.  Chunks up to 8192 wide
-// are read once, all of a lane's loads issued together into registers, and both
-// passes run from there (one memory round trip per row instead of one per
-// 2048 logits and pass); wider chunks re-read the row in pass 2.  Both forms
-// add in the same order, so they give the same bits.
+// ce_stats: one 256-thread workgroup per (row, piece), a piece being up to
+// kStatsPiece consecutive logits of the row; one launch covers any number of
+// pieces (a whole product of several vocabulary chunks).  All of a lane's loads
+// (8 consecutive fp16 logits, 16 B, per 2048-logit step) are issued together
+// into registers; pass 1 finds the piece max m_p and its first index, pass 2
+// sums exp(z - m_p) and exp(z - m_p) * z.  The piece's partial state goes to
+// its slot of partial[row, pieces]; ce_outputs folds the slots of a row in
+// vocabulary order (online-softmax merge: rescale both sides to the larger
+// max), so the results depend only on where the pieces start, not on how many
+// a launch covered.
 
 #include "elementwise.h"
 
 namespace ss {
-
-struct MaxArg {
-  float m;
-  int64_t a;
-};
-
-__device__ __forceinline__ MaxArg better(MaxArg x, MaxArg y) {
-  // Larger value wins; equal values keep the lower vocabulary index.
-  if (y.m > x.m || (y.m == x.m && y.a < x.a)) return y;
-  return x;
-}
-
-__device__ __forceinline__ MaxArg wave_maxarg(MaxArg v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    MaxArg o;
-    o.m = __shfl_xor(v.m, s, kWave);
-    o.a = __shfl_xor(v.a, s, kWave);
-    v = better(v, o);
-  }
-  return v;
-}
 
 constexpr int64_t kNoIndex = 0x7fffffffffffffffLL;
 
@@ -58,140 +38,220 @@ __device__ __forceinline__ void load_logits8(const half_t* __restrict__ row, int
   }
 }
 
-constexpr int kStatsHeld = 4;  // 2048-logit steps a lane holds in registers (width <= 8192)
+constexpr int kStatsHeld = 4;                  // 2048-logit steps a lane holds in registers
+constexpr int64_t kStatsPiece = 2048 * kStatsHeld;  // widest piece one workgroup reduces
 
-template <bool HELD>
-__global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict__ z, int64_t ldz,
-                                                       const int64_t* __restrict__ targets,
-                                                       float* __restrict__ state,
-                                                       int64_t* __restrict__ best, int64_t width,
-                                                       int64_t start, int64_t ignore, int first,
-                                                       int vec) {
-  __shared__ MaxArg s_ma[4];
-  __shared__ float s_sum[4][3];
-  const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const half_t* zr = z + row * ldz;
-  // The lane's steps, logits c = 8 tid + 2048 i .. + 7 for c < width, in order.
-  // HELD: all of them loaded up front (load_logits8 touches no memory at or
-  // past `width`, so the loads of absent steps read nothing).
-  float held[HELD ? kStatsHeld : 1][8];
-  if constexpr (HELD) {
+struct Partial {
+  float m, s, t, f;  // max, sum exp(z - m), sum exp(z - m) * z, target logit
+  int64_t a;         // first index of the max
+};
+
+// State a folded with the next piece b: both sums rescaled to the larger max (a
+// side whose max is -inf holds no finite logit and contributes nothing); the
+// argmax keeps the lower index on ties.
+__device__ __forceinline__ Partial fold(Partial a, const Partial& b) {
+  const float m = fmaxf(a.m, b.m);
+  const float ra = a.m == -INFINITY ? 0.0f : __expf(a.m - m);
+  const float rb = b.m == -INFINITY ? 0.0f : __expf(b.m - m);
+  int64_t arg = a.a;
+  if (b.m > a.m)
+    arg = b.a;
+  else if (b.m == a.m && b.a < a.a)
+    arg = b.a;
+  return Partial{m, a.s * ra + b.s * rb, a.t * ra + b.t * rb, a.f + b.f, arg};
+}
+
+// Max and first index within one piece (index local to the piece, < 8192); the
+// larger value wins, equal values keep the lower index.
+struct LocalMax {
+  float m;
+  int a;
+};
+
+__device__ __forceinline__ LocalMax better(LocalMax x, LocalMax y) {
+  if (y.m > x.m || (y.m == x.m && y.a < x.a)) return y;
+  return x;
+}
+
+__device__ __forceinline__ LocalMax wave_maxarg(LocalMax v) {
 #pragma unroll
-    for (int i = 0; i < kStatsHeld; ++i)
-      load_logits8(zr, (int64_t)tid * 8 + 2048 * i, width, vec, held[i]);
+  for (int s = 32; s >= 1; s >>= 1) {
+    LocalMax o;
+    o.m = __shfl_xor(v.m, s, kWave);
+    o.a = __shfl_xor(v.a, s, kWave);
+    v = better(v, o);
   }
-  // The row's running state, read before the passes so its latency overlaps them.
-  float old_m = -INFINITY, old_s = 0.0f, old_t = 0.0f, tz = 0.0f;
-  int64_t old_arg = kNoIndex;
-  if (!first) {
-    old_m = state[row * 4 + 0];
-    old_s = state[row * 4 + 1];
-    old_t = state[row * 4 + 2];
-    tz = state[row * 4 + 3];
-    old_arg = best[row];
-  }
-  const int64_t tgt = targets[row];
-  auto each_step = [&](auto&& f) {
-    if constexpr (HELD) {
+  return v;
+}
+
+constexpr int kNoLocal = 0x7fffffff;
+
+// The lane's logits c = 8 tid + 2048 i .. + 7 of one piece (c < w), as fp16.
+// No branch around a load (a lane past w reads column 0 again), so a wave's
+// loads are all in flight together.  VEC: rows and pieces 16-byte aligned and
+// w % 8 == 0, so a lane's 8 logits are all present or all absent (a step with
+// c >= w is skipped whole) and columns 0 .. 7 exist; otherwise absent logits
+// read as -inf.
+template <bool VEC>
+__device__ __forceinline__ void stats_load(const half_t* __restrict__ zr, int w, int tid,
+                                           half8 (&held)[kStatsHeld]) {
+  const half_t ninf = (half_t)-INFINITY;
 #pragma unroll
-      for (int i = 0; i < kStatsHeld; ++i) {
-        const int64_t c = (int64_t)tid * 8 + 2048 * i;
-        if (c < width) f(c, held[i]);
-      }
+  for (int i = 0; i < kStatsHeld; ++i) {
+    const int c = tid * 8 + 2048 * i;
+    if constexpr (VEC) {
+      held[i] = *reinterpret_cast<const half8*>(zr + (c < w ? c : 0));
     } else {
-      for (int64_t c = (int64_t)tid * 8; c < width; c += 2048) {
-        float v[8];
-        load_logits8(zr, c, width, vec, v);
-        f(c, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const half_t v = zr[c + j < w ? c + j : 0];
+        held[i][j] = c + j < w ? v : ninf;
       }
     }
-  };
-
-  MaxArg ma{-INFINITY, kNoIndex};
-  each_step([&](int64_t c, const float* v) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (c + j < width && v[j] > ma.m) {
-        ma.m = v[j];
-        ma.a = start + c + j;
-      }
-    }
-  });
-  ma = wave_maxarg(ma);
-  if (lane == 0) s_ma[wave] = ma;
-  __syncthreads();
-  MaxArg tile = s_ma[0];
-#pragma unroll
-  for (int w = 1; w < 4; ++w) tile = better(tile, s_ma[w]);
-  const float new_m = fmaxf(old_m, tile.m);
-
-  float sp = 0.0f, spz = 0.0f, found = 0.0f;
-  each_step([&](int64_t c, const float* v) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (c + j < width) {
-        const float p = __expf(v[j] - new_m);
-        sp += p;
-        const float pz = p * v[j];
-        spz += pz;
-        if (tgt != ignore && tgt == start + c + j) found += v[j];
-      }
-    }
-  });
-  sp = wave_sum(sp);
-  spz = wave_sum(spz);
-  found = wave_sum(found);
-  if (lane == 0) {
-    s_sum[wave][0] = sp;
-    s_sum[wave][1] = spz;
-    s_sum[wave][2] = found;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float a = 0.f, b = 0.f, f = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      a += s_sum[w][0];
-      b += s_sum[w][1];
-      f += s_sum[w][2];
-    }
-    const float rescale = __expf(old_m - new_m);
-    const float total_s = old_s * rescale + a;
-    const float total_t = old_t * rescale + b;
-    int64_t arg;
-    if (tile.m > old_m)
-      arg = tile.a;
-    else if (tile.m == old_m)
-      arg = old_arg < tile.a ? old_arg : tile.a;
-    else
-      arg = old_arg;
-    state[row * 4 + 0] = new_m;
-    state[row * 4 + 1] = total_s;
-    state[row * 4 + 2] = total_t;
-    state[row * 4 + 3] = tz + f;
-    best[row] = arg;
   }
 }
 
-__global__ __launch_bounds__(256) void ce_outputs_kernel(const float* __restrict__ state,
+constexpr float kLog2e = 1.4426950408889634f;
+
+// One workgroup per (row, piece).  The lane's logits, 4 steps of 8, are loaded
+// together; each step takes its max with packed fp16 max (NaN loses, as in an
+// ordered compare; fp16 order is the fp32 order), and its terms as
+// p = 2^(z log2e - m log2e) with z read from fp16 by the fused multiply-add.
+// The running state (max m, sums against m) rescales when a step raises m.
+// The first index of the max and the target logit are picked once per piece.
+template <bool VEC>
+__global__ __launch_bounds__(256) void ce_stats_kernel(const half_t* __restrict__ z, int64_t ldz,
+                                                       const int64_t* __restrict__ targets,
+                                                       float4* __restrict__ partial,
+                                                       int64_t* __restrict__ partial_arg,
+                                                       int64_t width, int64_t piece,
+                                                       int64_t start, int64_t slot0,
+                                                       int64_t slots, int64_t ignore) {
+  __shared__ Partial s_state[4];
+  __shared__ float s_found;
+  const int64_t row = blockIdx.x;
+  const int64_t c0 = (int64_t)blockIdx.y * piece;  // the piece's first column in z
+  const int w = (int)(width - c0 < piece ? width - c0 : piece);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t first_index = start + c0;  // vocabulary index of the piece's column 0
+  half8 held[kStatsHeld];
+  stats_load<VEC>(z + row * ldz + c0, w, tid, held);
+  const int64_t tgt = targets[row];
+  const int local_t = tgt != ignore && tgt >= first_index && tgt < first_index + w
+                          ? (int)(tgt - first_index) : -1;
+
+  float m = -INFINITY, sum = 0.0f, wsum = 0.0f;
+  int best_step = -1;
+#pragma unroll
+  for (int i = 0; i < kStatsHeld; ++i) {
+    const int c = tid * 8 + 2048 * i;
+    if (c < w) {
+      const half8 h = held[i];
+      half2_t q = __builtin_elementwise_max(__builtin_elementwise_max(h.s01, h.s23),
+                                            __builtin_elementwise_max(h.s45, h.s67));
+      const float gm = (float)__builtin_elementwise_max(q.x, q.y);
+      if (gm > m) {
+        const float r = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - gm) * kLog2e);
+        sum *= r;
+        wsum *= r;
+        m = gm;
+        best_step = i;
+      }
+      // 2^(z log2e - sh); sh = 0 while no finite logit was seen (its -inf terms add 0)
+      const float sh = m == -INFINITY ? 0.0f : m * kLog2e;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (!VEC && c + j >= w) continue;
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)h[j], kLog2e, -sh));
+        sum += p;
+        wsum = __builtin_fmaf(p, (float)h[j], wsum);
+      }
+    }
+  }
+  // The lane's first index of m (only its best step can hold it).
+  int arg = kNoLocal;
+  if (best_step >= 0) {
+    half8 h = held[0];
+#pragma unroll
+    for (int i = 1; i < kStatsHeld; ++i)
+      if (best_step == i) h = held[i];
+    const half_t hm = (half_t)m;
+#pragma unroll
+    for (int j = 7; j >= 0; --j)
+      if (h[j] == hm) arg = tid * 8 + 2048 * best_step + j;
+  }
+  // The target's logit, from the lane that holds it.
+  if (local_t >= 0 && tid == (local_t & 2047) >> 3) {
+    const int ti = local_t >> 11, tj = local_t & 7;
+    half8 h = held[0];
+#pragma unroll
+    for (int i = 1; i < kStatsHeld; ++i)
+      if (ti == i) h = held[i];
+    float v = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (tj == j) v = (float)h[j];
+    s_found = v;
+  }
+  Partial st{m, sum, wsum, 0.0f, arg};
+  // Lanes, then waves, merged as the pieces are folded.
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    Partial other{__shfl_xor(st.m, o, kWave), __shfl_xor(st.s, o, kWave),
+                  __shfl_xor(st.t, o, kWave), 0.0f, (int64_t)__shfl_xor((int)st.a, o, kWave)};
+    st = fold(st, other);
+  }
+  if (lane == 0) s_state[wave] = st;
+  __syncthreads();
+  if (tid == 0) {
+    Partial b = s_state[0];
+#pragma unroll
+    for (int v = 1; v < 4; ++v) b = fold(b, s_state[v]);
+    const int64_t slot = row * slots + slot0 + blockIdx.y;
+    // s_found was written before the barrier by the one lane holding the target.
+    partial[slot] = make_float4(b.m, b.s, b.t, local_t >= 0 ? s_found : 0.0f);
+    partial_arg[slot] = b.a == kNoLocal ? kNoIndex : first_index + b.a;
+  }
+}
+
+// One wave per row: lane l folds slots l, l + 64, ... in order, then the lanes
+// fold pairwise (xor butterfly; fold is commutative, so every lane ends with the
+// same state).  The fold order is fixed by the slot count alone.
+__global__ __launch_bounds__(256) void ce_outputs_kernel(const float4* __restrict__ partial,
+                                                         const int64_t* __restrict__ partial_arg,
+                                                         int64_t slots,
                                                          const int64_t* __restrict__ targets,
                                                          float* __restrict__ loss,
                                                          float* __restrict__ entropy,
-                                                         float* __restrict__ lse, int64_t n,
+                                                         float* __restrict__ lse,
+                                                         int64_t* __restrict__ best, int64_t n,
                                                          int64_t ignore) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= n) return;
-  const float m = state[r * 4 + 0];
-  const float s = state[r * 4 + 1];
-  const float t = state[r * 4 + 2];
-  const float zt = state[r * 4 + 3];
-  const float l = m + __logf(s);
-  lse[r] = l;
-  entropy[r] = l - t / s;
-  loss[r] = targets[r] != ignore ? l - zt : 0.0f;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const float4* pr = partial + r * slots;
+  const int64_t* ar = partial_arg + r * slots;
+  Partial st{-INFINITY, 0.0f, 0.0f, 0.0f, kNoIndex};
+  for (int64_t k = lane; k < slots; k += kWave) {
+    const float4 q = pr[k];
+    st = fold(st, Partial{q.x, q.y, q.z, q.w, ar[k]});
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const int64_t oa = __shfl_xor(st.a, o, kWave);
+    Partial other{__shfl_xor(st.m, o, kWave), __shfl_xor(st.s, o, kWave),
+                  __shfl_xor(st.t, o, kWave), __shfl_xor(st.f, o, kWave), oa};
+    st = fold(st, other);
+  }
+  if (lane == 0) {
+    const float l = st.m + __logf(st.s);
+    lse[r] = l;
+    entropy[r] = l - st.t / st.s;
+    loss[r] = targets[r] != ignore ? l - st.f : 0.0f;
+    best[r] = st.a;
+  }
 }
 
 __global__ __launch_bounds__(256) void ce_derivative_kernel(
@@ -264,33 +324,47 @@ static bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 
 
 using namespace ss;
 
-extern "C" int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* targets, float* state,
-                           int64_t* best, int64_t n, int64_t width, int64_t start,
-                           int64_t ignore_index, int first, void* stream) {
+extern "C" int ss_ce_stats(const uint16_t* z, int64_t ldz, const int64_t* targets,
+                           float* partial, int64_t* partial_arg, int64_t n, int64_t width,
+                           int64_t piece, int64_t start, int64_t slot0, int64_t slots,
+                           int64_t ignore_index, void* stream) {
   SS_CHECK_ARG(n >= 0 && width > 0 && start >= 0 && ldz >= width, "ss_ce_stats: bad sizes");
+  SS_CHECK_ARG(piece > 0 && piece <= kStatsPiece, "ss_ce_stats: piece outside [1, 8192]");
+  const int64_t pieces = cdiv(width, piece);
+  SS_CHECK_ARG(pieces < 65536 && slot0 >= 0 && slot0 + pieces <= slots,
+               "ss_ce_stats: pieces outside the partial row");
+  SS_CHECK_ARG(n < (int64_t)1 << 31, "ss_ce_stats: too many rows");
   if (n == 0) return SS_OK;
-  SS_CHECK_ARG(z && targets && state && best, "ss_ce_stats: null pointer");
-  const int vec = al16(z) && ldz % 8 == 0;
-  if (width <= 2048 * kStatsHeld)
-    hipLaunchKernelGGL(ce_stats_kernel<true>, dim3((unsigned)n), dim3(256), 0,
-                       (hipStream_t)stream, reinterpret_cast<const half_t*>(z), ldz, targets,
-                       state, best, width, start, ignore_index, first ? 1 : 0, vec);
+  SS_CHECK_ARG(z && targets && partial && partial_arg, "ss_ce_stats: null pointer");
+  SS_CHECK_ARG(al16(partial), "ss_ce_stats: partial not 16-byte aligned");
+  const bool vec = al16(z) && ldz % 8 == 0 && piece % 8 == 0 && width % 8 == 0;
+  const dim3 grid((unsigned)n, (unsigned)pieces);
+  if (vec)
+    hipLaunchKernelGGL(ce_stats_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<const half_t*>(z), ldz, targets,
+                       reinterpret_cast<float4*>(partial), partial_arg, width, piece, start,
+                       slot0, slots, ignore_index);
   else
-    hipLaunchKernelGGL(ce_stats_kernel<false>, dim3((unsigned)n), dim3(256), 0,
-                       (hipStream_t)stream, reinterpret_cast<const half_t*>(z), ldz, targets,
-                       state, best, width, start, ignore_index, first ? 1 : 0, vec);
+    hipLaunchKernelGGL(ce_stats_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<const half_t*>(z), ldz, targets,
+                       reinterpret_cast<float4*>(partial), partial_arg, width, piece, start,
+                       slot0, slots, ignore_index);
   SS_CHECK_LAUNCH("ce_stats_kernel");
   return SS_OK;
 }
 
-extern "C" int ss_ce_outputs(const float* state, const int64_t* targets, float* loss,
-                             float* entropy, float* lse, int64_t n, int64_t ignore_index,
-                             void* stream) {
-  SS_CHECK_ARG(n >= 0, "ss_ce_outputs: negative n");
+extern "C" int ss_ce_outputs(const float* partial, const int64_t* partial_arg, int64_t slots,
+                             const int64_t* targets, float* loss, float* entropy, float* lse,
+                             int64_t* best, int64_t n, int64_t ignore_index, void* stream) {
+  SS_CHECK_ARG(n >= 0 && slots > 0, "ss_ce_outputs: bad sizes");
   if (n == 0) return SS_OK;
-  SS_CHECK_ARG(state && targets && loss && entropy && lse, "ss_ce_outputs: null pointer");
-  hipLaunchKernelGGL(ce_outputs_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
-                     (hipStream_t)stream, state, targets, loss, entropy, lse, n, ignore_index);
+  SS_CHECK_ARG(partial && partial_arg && targets && loss && entropy && lse && best,
+               "ss_ce_outputs: null pointer");
+  SS_CHECK_ARG(al16(partial), "ss_ce_outputs: partial not 16-byte aligned");
+  SS_CHECK_ARG(cdiv(n, 4) < (int64_t)1 << 31, "ss_ce_outputs: too many rows");
+  hipLaunchKernelGGL(ce_outputs_kernel, dim3((unsigned)cdiv(n, 4)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const float4*>(partial), partial_arg,
+                     slots, targets, loss, entropy, lse, best, n, ignore_index);
   SS_CHECK_LAUNCH("ce_outputs_kernel");
   return SS_OK;
 }

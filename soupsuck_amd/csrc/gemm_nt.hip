@@ -604,6 +604,8 @@ bool aligned16(const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 =
 //   128x256 tiles still fit one wave on the CUs (K < 8192);
 //   256x256 (8 waves, 4-stage ring) once it gives at least half the CUs a
 //   tile;
+//   a very long K (32768 or more) over at most 128 tiles of 256x256: those
+//   tiles split over k into one wave of workgroups;
 //   long K with few 128x128 tiles: split over k (each split at least 1024
 //   k), 256x128 tiles with about one workgroup per CU where M fills 256-row
 //   tiles, else 128x128 with about 512 workgroups;
@@ -626,6 +628,15 @@ NtPlan nt_plan(int64_t m, int64_t n, int64_t k) {
     plan.cfg = 10;
   } else if (t256 >= 128) {
     plan.cfg = 8;
+  } else if (k >= 32768 && t256 <= 128) {
+    // A very long K over few output tiles (the cross-entropy dX over the whole
+    // vocabulary, 523 x 1536 x 151936): 256x256 tiles split over K into one wave
+    // of workgroups, one 8-wave workgroup per CU (14 splits: 403 us against 485
+    // us for 128x128 split 8; 16 or 18 splits, a second partial wave: 490 us).
+    plan.cfg = 8;
+    int64_t s = 256 / t256;
+    if (s > k / 2048) s = k / 2048;
+    plan.splits = s < 1 ? 1 : s;
   } else if (k >= 2048 && t128 < 256) {
     plan.cfg = 2;
     int64_t s = 512 / t128;

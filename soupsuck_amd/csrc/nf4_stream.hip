@@ -397,18 +397,6 @@ __global__ __launch_bounds__(kStMaxWaves / MT * kWave) void nf4_stream_fwd_kerne
   }
 }
 
-int cu_count() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
-      cus = 256;
-    else
-      cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-  }
-  return cus;
-}
 
 // Stage groups: one stage per wave, at most 16 waves (T <= 16) or 8 (T <= 32:
 // twice the X fragments and accumulators); more groups while there are too
@@ -417,7 +405,7 @@ int cu_count() {
 StreamPlan stream_plan(int64_t t, int64_t n, int64_t k) {
   StreamPlan plan{};
   if (t < 1 || t > kStreamMaxT || n < 1 || k < kStK || k % kStK != 0) return plan;
-  const int64_t cus = cu_count();
+  const int64_t cus = device_cu_count();
   const int64_t s = k / kStK;
   const int mt = t <= 16 ? 1 : 2;
   const int64_t max_waves = mt == 1 ? kStMaxWaves : kStMaxWaves / 2;

@@ -295,18 +295,6 @@ __global__ __launch_bounds__(kDxWaves * kWave) void nf4_stream_dx_kernel(GemmPar
   }
 }
 
-int dx_cu_count() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    hipDeviceProp_t prop;
-    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
-      cus = 256;
-    else
-      cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-  }
-  return cus;
-}
 
 // Column stages of 256; row ranges so that at most one workgroup per CU runs
 // (the LDS holds one), each range at least 8 units (one per wave) when the
@@ -315,7 +303,7 @@ StreamDxPlan stream_dx_plan(int64_t t, int64_t nr, int64_t nc) {
   StreamDxPlan plan{};
   if (t < 1 || t > kStreamDxMaxT || nr < 16 || nr % 16 != 0 || nc < kDxCols || nc % kDxCols != 0)
     return plan;
-  const int64_t cus = dx_cu_count();
+  const int64_t cus = device_cu_count();
   plan.col_stages = nc / kDxCols;
   int64_t g = cus / plan.col_stages;  // at most one workgroup per CU
   const int64_t g_max = cdiv(nr, kDxRows * kDxWaves);

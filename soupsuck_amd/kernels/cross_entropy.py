@@ -5,9 +5,11 @@ returned tensors loss / entropy / first argmax / lse with only ``loss``
 differentiable, ValueError before launch) and its numerics (:1-43):
 
   forward   per vocabulary chunk c: z = fp16(h16 . W_c16^T) on the MFMA GEMM
-            (ss_gemm_f16); the per-row online state (max m, sum e^(z-m), sum
-            e^(z-m) z, target logit) and the first argmax are merged chunk by
-            chunk (ss_ce_stats); lse = m + log s, loss = lse - z_target (0 for
+            (ss_gemm_f16); per row and piece of at most 8192 columns of a chunk,
+            the partial state (max m_p, sum e^(z-m_p), sum e^(z-m_p) z, target
+            logit, first argmax; ss_ce_stats); the pieces folded in vocabulary
+            order as the online softmax merges (m = max, s = sum s_p
+            e^(m_p-m), ...), lse = m + log s, loss = lse - z_target (0 for
             ignored rows), entropy = lse - t/s (ss_ce_outputs);
   backward  rows with a target only (found in the forward: a stable sort and a
             count copied to pinned memory early, so no stall); each chunk
@@ -27,10 +29,14 @@ Kept logits: when the fp16 logits [N, V] fit KEEP_LOGITS_BUDGET (1 GiB; 251 MB
 at configs[3]) and a backward may run, the forward's products write into one
 [N, V] buffer and the backward reads the logits from there (rows picked through
 the labelled-row indices) instead of recomputing h . W_c^T: one product per
-chunk fewer.  The products then span several chunks (as many as fill one wave
-of 256 x 256 output tiles: two at configs[3]); the statistics still merge chunk
-by chunk, so the forward's outputs are the same bits.  Above the budget the
-backward recomputes, as the reference does, one [rows, chunk] tile at a time.
+chunk fewer.  The forward's products then span several chunks (as many as fill
+one wave of 256 x 256 output tiles: two at configs[3]) and one statistics launch
+follows them all; its pieces are those of a chunk-by-chunk forward, so the
+outputs are the same bits.  The backward's
+steps span as many chunks as DERIVATIVE_BUDGET holds of dz and dz' (the whole
+vocabulary at configs[3]): one derivative launch and two long products.  Above
+KEEP_LOGITS_BUDGET the backward recomputes, as the reference does, one [rows,
+chunk] tile at a time.
 
 Layout for the MFMA engine: the dense direct-to-LDS kernel reads operands stored
 along the reduced dimension (K-major) through transposed LDS reads, so dX = dz .
@@ -54,6 +60,9 @@ TILE_BUDGET = 64 << 20      # bytes of one fp16 [rows, chunk] logits tile
 # the backward's recomputed chunk equals the forward's).  Larger outputs are
 # recomputed chunk by chunk, holding one [rows, chunk] tile at a time.
 KEEP_LOGITS_BUDGET = 1 << 30
+STATS_PIECE = 8192          # widest vocabulary piece one ss_ce_stats workgroup reduces
+# Bytes of the backward's two fp16 derivative buffers when it reads kept logits.
+DERIVATIVE_BUDGET = 1 << 30
 
 
 def default_chunk(rows):
@@ -92,12 +101,21 @@ def _product_span(rows, chunk, dev):
     """Vocabulary columns per logits product when the forward keeps its logits: whole
     chunks, as many as fit one wave of 256 x 256 output tiles on the device's CUs (T =
     826: two chunks of 8192, 256 tiles, against 224 tiles of 128 x 256 for one chunk).
-    The statistics still merge chunk by chunk, and an output element does not depend on
-    the product's width, so the results are the same bits."""
+    The statistics pieces do not change, and an output element does not depend on the
+    product's width, so the results are the same bits."""
     if dev not in _CUS:
         _CUS[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
     tiles = -(-rows // 256) * -(-chunk // 256)
     return max(1, _CUS[dev] // tiles) * chunk
+
+
+def _backward_span(count, padded, chunk):
+    """Vocabulary columns per backward step over kept logits: whole chunks whose fp16
+    derivatives dz [count, span] and dz' [padded, span] fit DERIVATIVE_BUDGET together
+    (T = 826 with 523 labelled rows: the whole vocabulary in one step).  dW's rows do
+    not depend on the step's width; dX's fp32 sum over the vocabulary is split
+    differently, so it matches a chunked backward to rounding."""
+    return max(1, DERIVATIVE_BUDGET // (2 * (count + padded) * chunk)) * chunk
 
 
 def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
@@ -113,25 +131,43 @@ def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
     if rows == 0:
         return loss, entropy, best, lse, None
     stream = _lib.stream(dev)
-    online = torch.empty((rows, 4), device=dev, dtype=torch.float32)
     vocab = weight.shape[0]
+    # Statistics pieces: each chunk splits into per_chunk pieces of `piece` columns
+    # (the last narrower), each with a slot of partial state, folded in vocabulary
+    # order by ss_ce_outputs.  The pieces depend only on the chunk, so a call over a
+    # product of several chunks gives the bits of one call per chunk.
+    piece = min(chunk, STATS_PIECE)
+    per_chunk = -(-chunk // piece)
+    last = vocab - (vocab - 1) // chunk * chunk
+    slots = (vocab - 1) // chunk * per_chunk + -(-last // piece)
+    partial = torch.empty((rows, slots, 4), device=dev, dtype=torch.float32)
+    partial_arg = torch.empty((rows, slots), device=dev, dtype=torch.int64)
     tile = torch.empty((rows, vocab if keep else min(chunk, vocab)), device=dev,
                        dtype=torch.float16)
-    span = _product_span(rows, chunk, dev) if keep else chunk
-    for pstart, pwidth in _vocab_chunks(vocab, span):
-        if keep:
-            gemm_f16(hidden16, _head_rows(weight, pstart, pwidth), b_trans=True,
-                     out=tile[:, pstart:pstart + pwidth])
-        for start, width in _vocab_chunks(pwidth, chunk):
-            start += pstart
-            logits = tile[:, start:start + width] if keep else tile[:, :width]
-            if not keep:
-                gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True, out=logits)
-            _lib.call("ss_ce_stats", logits.data_ptr(), tile.stride(0), targets.data_ptr(),
-                      online.data_ptr(), best.data_ptr(), rows, width, start, ignore_index,
-                      int(start == 0), stream)
-    _lib.call("ss_ce_outputs", online.data_ptr(), targets.data_ptr(), loss.data_ptr(),
-              entropy.data_ptr(), lse.data_ptr(), rows, ignore_index, stream)
+
+    def stats(z, start):
+        _lib.call("ss_ce_stats", z.data_ptr(), tile.stride(0), targets.data_ptr(),
+                  partial.data_ptr(), partial_arg.data_ptr(), rows, z.shape[1], piece, start,
+                  start // chunk * per_chunk, slots, ignore_index, stream)
+
+    if keep:
+        for start, width in _vocab_chunks(vocab, _product_span(rows, chunk, dev)):
+            gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True,
+                     out=tile[:, start:start + width])
+        # Every logit at hand: one statistics launch when the pieces tile whole chunks
+        # (and fit one launch's grid).
+        whole = chunk % piece == 0 and slots < 65536
+        calls = [(0, vocab)] if whole else _vocab_chunks(vocab, chunk)
+        for start, width in calls:
+            stats(tile[:, start:start + width], start)
+    else:
+        for start, width in _vocab_chunks(vocab, chunk):
+            gemm_f16(hidden16, _head_rows(weight, start, width), b_trans=True,
+                     out=tile[:, :width])
+            stats(tile[:, :width], start)
+    _lib.call("ss_ce_outputs", partial.data_ptr(), partial_arg.data_ptr(), slots,
+              targets.data_ptr(), loss.data_ptr(), entropy.data_ptr(), lse.data_ptr(),
+              best.data_ptr(), rows, ignore_index, stream)
     return loss, entropy, best, lse, tile if keep else None
 
 
@@ -185,9 +221,10 @@ class _Backward:
         count, padded = self.count, self.padded
         hdim = self.h.shape[1]
         kept_z = self.logits
-        # With the kept logits every step spans several chunks (the derivative is
-        # elementwise and the products take any width); recomputing, one chunk at a time.
-        span = self.chunk if kept_z is None else _product_span(count, self.chunk, self.dev)
+        # With the kept logits a step spans as many chunks as the derivative buffers'
+        # budget holds (the derivative is elementwise and the products take any width:
+        # fewer, longer products); recomputing, one chunk at a time.
+        span = self.chunk if kept_z is None else _backward_span(count, padded, self.chunk)
         width_max = min(span, self.weight.shape[0])
         if kept_z is None:
             logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
@@ -199,10 +236,11 @@ class _Backward:
             # max_r |g_r| / 1024 as a device scalar: no host round trip between the
             # forward and the backward's launches
             head_gain = (self.grad.abs().amax().clamp_min(1e-30) / 1024.0).reshape(1)
-            # dz' per step as [padded, width] (dense rows): the rows past `count`
-            # stay zero; they are written only by a wider step's rows, so only a
-            # narrower step clears them.
-            dz_head = torch.zeros(padded * width_max, device=self.dev, dtype=torch.float16)
+            # dz' per step as [padded, width] (dense rows): the rows past `count` must
+            # read zero.  They are cleared for the first step's width and again when the
+            # width changes (a narrower step's tail rows hold a wider step's rows).
+            dz_head = torch.empty(padded * width_max, device=self.dev, dtype=torch.float16)
+            cleared = None
         for start, width in _vocab_chunks(self.weight.shape[0], span):
             w = _head_rows(self.weight, start, width)
             if kept_z is None:
@@ -215,8 +253,9 @@ class _Backward:
             dh = None
             if dw is not None:
                 dh = dz_head[:padded * width].view(padded, width)
-                if width < width_max and padded > count:
+                if padded > count and width != cleared:
                     dz_head[count * width:padded * width].zero_()
+                    cleared = width
             _lib.call("ss_ce_derivative", z.data_ptr(), ldz, _lib.ptr(z_rows),
                       self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
                       d.data_ptr(), _lib.ptr(dh), _lib.ptr(head_gain), count, width, start,

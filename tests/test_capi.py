@@ -68,7 +68,11 @@ def test_workspace_policy_is_host_only(lib):
     ("ss_add_rmsnorm_fwd", (None, 0, None, 0, None, 0, 1, None, 1, None, 0, None, 4, 8, 1e-6,
                             None), "promote"),
     ("ss_unpad_gather", (None, 4, None, None, 2, 3, None), "even"),
-    ("ss_ce_stats", (None, 4, None, None, None, 2, 8, 0, -100, 1, None), "bad sizes"),
+    ("ss_ce_stats", (None, 4, None, None, None, 2, 8, 8192, 0, 0, 1, -100, None), "bad sizes"),
+    ("ss_ce_stats", (None, 8, None, None, None, 2, 8, 8193, 0, 0, 1, -100, None), "piece"),
+    ("ss_ce_stats", (None, 8, None, None, None, 2, 8, 4, 0, 0, 1, -100, None), "partial row"),
+    ("ss_ce_outputs", (None, None, 0, None, None, None, None, None, 2, -100, None),
+     "bad sizes"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(lib, name, args, needle):
     rc = getattr(lib, name)(*args)

@@ -40,7 +40,9 @@ def inputs(n, h, v, ignored="some", scale=1.0, seed=123):
     (77, 64, 1000, "all", 1.0, None), (77, 64, 1000, "none", 20.0, None),
     (77, 80, 4103, "some", 1.0, 4096), (1, 33, 7, "none", 1.0, None),
     (300, 128, 9000, "some", 1.0, 8192),
-    (200, 64, 20000, "some", 1.0, 16384),   # a chunk wider than the stats kernel holds
+    (200, 64, 20000, "some", 1.0, 16384),   # two statistics pieces a chunk
+    (150, 64, 23000, "some", 1.0, 10000),   # pieces 8192 + 1808 a chunk, one call each
+    (90, 64, 5000, "some", 1.0, 999),       # odd pieces: unaligned scalar loads
 ])
 @pytest.mark.parametrize("weight_grad", [False, True])
 def test_matches_oracle(device, n, h, v, ignored, scale, chunk, weight_grad):
@@ -158,12 +160,15 @@ def test_config4_full_shape_against_fp32_torch(device):
     assert ((w.grad.float() - ref_dw).norm() / ref_dw.norm()).item() <= 1e-2
 
 
-@pytest.mark.parametrize("n,h,v", [(600, 256, 20000), (826, 1536, 151936)])
-def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v):
-    """The path that keeps the forward's logits (its products spanning several chunks)
-    against the one that recomputes chunk by chunk (budget 0): loss, entropy, argmax,
-    lse and the head gradient are the same bits; dX, whose split-K reductions then run
-    over different depths, agrees to fp32 summation order (relative L2 1e-4)."""
+@pytest.mark.parametrize("n,h,v,chunk", [(600, 256, 20000, 8192), (600, 256, 20000, 10000),
+                                         (826, 1536, 151936, 8192)])
+def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v, chunk):
+    """The path that keeps the forward's logits (its products spanning several chunks,
+    the backward's steps the whole vocabulary or, with a derivative budget of one byte,
+    one chunk each and a narrower last step) against the one that recomputes chunk by
+    chunk (budget 0): loss, entropy, argmax, lse and the head gradient are the same
+    bits; dX, whose split-K reductions then run over different depths, agrees to fp32
+    summation order (relative L2 1e-4)."""
     gen = torch.Generator(device="cpu").manual_seed(n)
     x0 = torch.randn((n, h), generator=gen).to(torch.float16).to(device)
     w0 = (torch.randn((v, h), generator=gen) * 0.02).to(torch.float16).to(device)
@@ -172,15 +177,19 @@ def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v):
     y = y.to(device)
     g = torch.randn(n, generator=gen).to(device)
     runs = []
-    for budget in (ce_mod.KEEP_LOGITS_BUDGET, 0):
+    keep, derivative = ce_mod.KEEP_LOGITS_BUDGET, ce_mod.DERIVATIVE_BUDGET
+    for budget, steps in ((keep, derivative), (keep, 1), (0, derivative)):
         monkeypatch.setattr(ce_mod, "KEEP_LOGITS_BUDGET", budget)
+        monkeypatch.setattr(ce_mod, "DERIVATIVE_BUDGET", steps)
         x = x0.clone().requires_grad_()
         w = w0.clone().requires_grad_()
-        outs = fused_linear_cross_entropy(x, w, y, chunk=8192, weight_grad=True)
+        outs = fused_linear_cross_entropy(x, w, y, chunk=chunk, weight_grad=True)
         outs[0].backward(g)
         torch.cuda.synchronize()
         runs.append((*outs, x.grad, w.grad))
-    for kept, recomputed in zip(runs[0][:4] + runs[0][5:], runs[1][:4] + runs[1][5:]):
-        assert torch.equal(kept, recomputed)
-    dx_k, dx_r = runs[0][4].float(), runs[1][4].float()
-    assert ((dx_k - dx_r).norm() / dx_r.norm()).item() <= 1e-4
+    recomputed = runs[-1]
+    dx_r = recomputed[4].float()
+    for kept in runs[:-1]:
+        for a, b in zip(kept[:4] + kept[5:], recomputed[:4] + recomputed[5:]):
+            assert torch.equal(a, b)
+        assert ((kept[4].float() - dx_r).norm() / dx_r.norm()).item() <= 1e-4
