@@ -154,6 +154,77 @@ __global__ __launch_bounds__(256) void add_rmsnorm_fwd_kernel(FwdArgs a) {
   }
 }
 
+// Fast forward: fp16 r (and d), s and y with 16-byte aligned rows, h = 512 NCH
+// (every lane chunk full) and a contiguous gamma (fp16, or fp32 with WF32).  A
+// lane issues all its loads -- its chunks of r and d and of gamma -- before the
+// first use with no branch between them, so a row costs one memory round trip
+// (the generic kernel's per-chunk dtype and length branches made each load wait
+// for the previous one).  The arithmetic is the generic kernel's, in the same
+// order, so the results are the same bits.
+template <int NCH, bool HAS_D, bool WF32>
+__global__ __launch_bounds__(256) void add_rmsnorm_fwd_fast_kernel(FwdArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t base = row * a.h;
+  const half_t* rp = reinterpret_cast<const half_t*>(a.r) + row * a.r_row;
+  half8 rv[NCH], dv[NCH], wh[NCH];
+  float4v wf[WF32 ? NCH : 1][2];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int col0 = (c * 64 + lane) * 8;
+    rv[c] = *reinterpret_cast<const half8*>(rp + col0);
+    if constexpr (HAS_D)
+      dv[c] = *reinterpret_cast<const half8*>(reinterpret_cast<const half_t*>(a.d) + base + col0);
+    if constexpr (WF32) {
+      const float* wp = reinterpret_cast<const float*>(a.w) + col0;
+      wf[c][0] = *reinterpret_cast<const float4v*>(wp);
+      wf[c][1] = *reinterpret_cast<const float4v*>(wp + 4);
+    } else {
+      wh[c] = *reinterpret_cast<const half8*>(reinterpret_cast<const half_t*>(a.w) + col0);
+    }
+  }
+  float sv[NCH][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (HAS_D)
+        sv[c][j] = (float)f32_to_f16((float)rv[c][j] + (float)dv[c][j]);
+      else
+        sv[c][j] = (float)rv[c][j];
+      const float sq = sv[c][j] * sv[c][j];
+      ss += sq;
+    }
+    if (HAS_D && a.s) {
+      half8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f32_to_f16(sv[c][j]);
+      *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.s) + base + (c * 64 + lane) * 8) = o;
+    }
+  }
+  ss = wave_sum(ss);
+  const float mean = ss / (float)a.h;
+  const float rstd = rsqrtf(mean + a.eps);
+  if (lane == 0) a.rstd[row] = rstd;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    half8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float w;
+      if constexpr (WF32)
+        w = j < 4 ? wf[c][0][j] : wf[c][1][j - 4];
+      else
+        w = (float)wh[c][j];
+      const float q = (float)f32_to_f16(sv[c][j] * rstd);
+      o[j] = f32_to_f16(q * w);
+    }
+    *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.y) + base + (c * 64 + lane) * 8) = o;
+  }
+}
+
 struct BwdArgs {
   const void* s; int sd;
   const void* w; int wd; int64_t w_stride;
@@ -245,13 +316,95 @@ __device__ __forceinline__ void bwd_row(const BwdArgs& a, int64_t row, int lane,
   }
 }
 
-template <int NCH>
+// Fast backward row: fp16 s, gy, gs, dr and dd, 16-byte aligned contiguous
+// rows, h = 512 NCH and a contiguous gamma (fp16, or fp32 with WF32).  Every
+// load of the row (s, gy, gamma and gs; without gs the lane re-reads s and
+// ignores it) is issued before the first use with no branch between them.  The
+// arithmetic is bwd_row's, in the same order.
+template <int NCH, bool DG, bool WF32>
+__device__ __forceinline__ void bwd_row_fast(const BwdArgs& a, int64_t row, int lane,
+                                             float (&dg)[NCH][8], int half_products) {
+  const int64_t base = row * a.h;
+  const half_t* sp = reinterpret_cast<const half_t*>(a.s) + base;
+  const half_t* gp = reinterpret_cast<const half_t*>(a.gy) + row * a.gy_row;
+  const half_t* gsp = a.gs ? reinterpret_cast<const half_t*>(a.gs) + row * a.gs_row : sp;
+  half8 sv[NCH], gv[NCH], gsv[NCH], wh[NCH];
+  float4v wf[WF32 ? NCH : 1][2];
+  const float rstd = a.rstd[row];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int col0 = (c * 64 + lane) * 8;
+    sv[c] = *reinterpret_cast<const half8*>(sp + col0);
+    gv[c] = *reinterpret_cast<const half8*>(gp + col0);
+    gsv[c] = *reinterpret_cast<const half8*>(gsp + col0);
+    if constexpr (WF32) {
+      const float* wp = reinterpret_cast<const float*>(a.w) + col0;
+      wf[c][0] = *reinterpret_cast<const float4v*>(wp);
+      wf[c][1] = *reinterpret_cast<const float4v*>(wp + 4);
+    } else {
+      wh[c] = *reinterpret_cast<const half8*>(reinterpret_cast<const half_t*>(a.w) + col0);
+    }
+  }
+  float av[NCH][8], ds[NCH][8];
+  float dot = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float w;
+      if constexpr (WF32)
+        w = j < 4 ? wf[c][0][j] : wf[c][1][j - 4];
+      else
+        w = (float)wh[c][j];
+      const float g = (float)gv[c][j];
+      const float av_ = (float)sv[c][j] * rstd;
+      const float u = (float)f32_to_f16(g * w);
+      av[c][j] = av_;
+      ds[c][j] = u;
+      const float ua = u * av_;
+      dot += ua;
+      if constexpr (DG) {
+        float prod = g * (float)f32_to_f16(av_);
+        if (half_products) prod = (float)f32_to_f16(prod);
+        dg[c][j] += prod;
+      }
+    }
+  dot = wave_sum(dot);
+  const float proj = dot / (float)a.h;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    half8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float t = av[c][j] * proj;
+      const float diff = ds[c][j] - t;
+      float v = (float)f32_to_f16(rstd * diff);
+      if (a.gs) v += (float)gsv[c][j];
+      o[j] = f32_to_f16(v);
+    }
+    const int64_t off = base + (c * 64 + lane) * 8;
+    if (a.dr) *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.dr) + off) = o;
+    if (a.dd) *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(a.dd) + off) = o;
+  }
+}
+
+// MODE: 0 the generic row, 1 the fast row with an fp16 gamma, 2 with an fp32 gamma.
+template <int NCH, bool DG, int MODE>
+__device__ __forceinline__ void bwd_row_any(const BwdArgs& a, int64_t row, int lane,
+                                            float (&dg)[NCH][8], int half_products) {
+  if constexpr (MODE == 0)
+    bwd_row<NCH, DG>(a, row, lane, dg, half_products);
+  else
+    bwd_row_fast<NCH, DG, MODE == 2>(a, row, lane, dg, half_products);
+}
+
+template <int NCH, int MODE>
 __global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   float unused[NCH][8];
-  bwd_row<NCH, false>(a, row, lane, unused, 0);
+  bwd_row_any<NCH, false, MODE>(a, row, lane, unused, 0);
 }
 
 // Backward with the weight gradient in the same pass over s and gy: a
@@ -261,7 +414,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_bwd_kernel(BwdArgs a) {
 // partial[workgroup][h].
 constexpr int kDgWaves = 8;
 
-template <int NCH>
+template <int NCH, int MODE>
 __global__ __launch_bounds__(kDgWaves * 64) void add_rmsnorm_bwd_dg_kernel(
     BwdArgs a, int half_products, float* __restrict__ partial) {
   extern __shared__ float s_dg[];  // [kDgWaves][h]
@@ -273,7 +426,7 @@ __global__ __launch_bounds__(kDgWaves * 64) void add_rmsnorm_bwd_dg_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) dg[c][j] = 0.0f;
   const int64_t row = (int64_t)blockIdx.x * kDgWaves + k;
-  if (row < a.rows) bwd_row<NCH, true>(a, row, lane, dg, half_products);
+  if (row < a.rows) bwd_row_any<NCH, true, MODE>(a, row, lane, dg, half_products);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t col0 = ((int64_t)c * 64 + lane) * 8;
@@ -377,6 +530,91 @@ using namespace ss;
     default: hipLaunchKernelGGL(KERNEL<16>, GRID, dim3(256), 0, STREAM, ARGS); break;           \
   }
 
+// The fast forward applies to fp16 rows (r, d, s, y), 16-byte aligned, with h a
+// multiple of 512 up to 4096 and a contiguous fp16 or fp32 gamma.
+static bool fwd_fast_ok(const FwdArgs& a, bool has_d) {
+  const bool rows16 = a.rd == SS_F16 && a.sd == SS_F16 && a.yd == SS_F16 &&
+                      (!has_d || a.dd == SS_F16);
+  return rows16 && a.vec && a.w_stride == 1 && a.h % 512 == 0 && a.h <= 4096;
+}
+
+template <bool HAS_D, bool WF32>
+static void launch_fwd_fast(const FwdArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.h / 512) {
+#define SS_FAST_CASE(N)                                                                        \
+  case N:                                                                                      \
+    hipLaunchKernelGGL((add_rmsnorm_fwd_fast_kernel<N, HAS_D, WF32>), grid, dim3(256), 0, st,  \
+                       a);                                                                     \
+    break;
+    SS_FAST_CASE(1) SS_FAST_CASE(2) SS_FAST_CASE(3) SS_FAST_CASE(4) SS_FAST_CASE(5)
+    SS_FAST_CASE(6) SS_FAST_CASE(7) SS_FAST_CASE(8)
+#undef SS_FAST_CASE
+  }
+}
+
+static void launch_fwd(const FwdArgs& a, bool has_d, dim3 grid, hipStream_t st) {
+  if (fwd_fast_ok(a, has_d)) {
+    if (has_d)
+      a.wd == SS_F32 ? launch_fwd_fast<true, true>(a, grid, st)
+                     : launch_fwd_fast<true, false>(a, grid, st);
+    else
+      a.wd == SS_F32 ? launch_fwd_fast<false, true>(a, grid, st)
+                     : launch_fwd_fast<false, false>(a, grid, st);
+    return;
+  }
+  const int nch = (int)cdiv(a.h, 512);
+  SS_ROW_KERNEL_SWITCH(add_rmsnorm_fwd_kernel, nch, a, grid, st);
+}
+
+// Backward row mode (bwd_row_any): the fast row for fp16 s, gy, gs, dr and dd in
+// 16-byte aligned contiguous rows, h a multiple of 512 up to 4096 and a
+// contiguous gamma; else the generic row.
+static int bwd_mode(const BwdArgs& a) {
+  const bool f16 = a.sd == SS_F16 && a.gy && a.gyd == SS_F16 && a.vec_gy &&
+                   (!a.gs || (a.gsd == SS_F16 && a.vec_gs)) && (!a.dr || a.drd == SS_F16) &&
+                   (!a.dd || a.ddd == SS_F16);
+  if (!f16 || !a.vec || a.w_stride != 1 || a.h % 512 != 0 || a.h > 4096) return 0;
+  return a.wd == SS_F32 ? 2 : 1;
+}
+
+template <int MODE>
+static void launch_bwd_mode(const BwdArgs& a, dim3 grid, hipStream_t st) {
+  switch (cdiv(a.h, 512)) {
+#define SS_BWD_CASE(N)                                                                         \
+  case N:                                                                                      \
+    hipLaunchKernelGGL((add_rmsnorm_bwd_kernel<N, MODE>), grid, dim3(256), 0, st, a);          \
+    break;
+    SS_BWD_CASE(1) SS_BWD_CASE(2) SS_BWD_CASE(3) SS_BWD_CASE(4) SS_BWD_CASE(5)
+    SS_BWD_CASE(6) SS_BWD_CASE(7) SS_BWD_CASE(8)
+#undef SS_BWD_CASE
+    default:
+      if constexpr (MODE == 0)
+        hipLaunchKernelGGL((add_rmsnorm_bwd_kernel<16, 0>), grid, dim3(256), 0, st, a);
+      break;
+  }
+}
+
+template <int MODE>
+static void launch_dg_mode(const BwdArgs& a, int half_products, float* partial, dim3 grid,
+                           size_t lds, hipStream_t st) {
+  const dim3 block(kDgWaves * 64);
+  switch (cdiv(a.h, 512)) {
+#define SS_DG_CASE(N)                                                                          \
+  case N:                                                                                      \
+    hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<N, MODE>), grid, block, lds, st, a,          \
+                       half_products, partial);                                                \
+    break;
+    SS_DG_CASE(1) SS_DG_CASE(2) SS_DG_CASE(3) SS_DG_CASE(4) SS_DG_CASE(5) SS_DG_CASE(6)
+    SS_DG_CASE(7) SS_DG_CASE(8)
+#undef SS_DG_CASE
+    default:
+      if constexpr (MODE == 0)
+        hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<16, 0>), grid, block, lds, st, a,
+                           half_products, partial);
+      break;
+  }
+}
+
 extern "C" int ss_add_rmsnorm_fwd(const void* r, int r_dtype, const void* d, int d_dtype,
                                   const void* w, int w_dtype, int64_t w_stride, void* s,
                                   int s_dtype, void* y, int y_dtype, float* rstd, int64_t rows,
@@ -400,10 +638,8 @@ extern "C" int ss_add_rmsnorm_fwd(const void* r, int r_dtype, const void* d, int
   FwdArgs a{r, r_dtype, h, d, d_dtype, w, w_dtype, w_stride, s, s_dtype, y, y_dtype, rstd, rows,
             h, eps, 0};
   a.vec = (h % 8 == 0) && al16(r) && al16(d) && al16(s) && al16(y) && (w_stride != 1 || al16(w));
-  const int nch = (int)cdiv(h, 512);
   const dim3 grid((unsigned)cdiv(rows, 4));
-  hipStream_t st = (hipStream_t)stream;
-  SS_ROW_KERNEL_SWITCH(add_rmsnorm_fwd_kernel, nch, a, grid, st);
+  launch_fwd(a, true, grid, (hipStream_t)stream);
   SS_CHECK_LAUNCH("add_rmsnorm_fwd_kernel");
   return SS_OK;
 }
@@ -431,10 +667,8 @@ extern "C" int ss_rmsnorm_fwd(const void* x, int x_dtype, int64_t x_row, const v
   const int64_t xs = x_dtype == SS_F16 ? 2 : 4;
   a.vec = (h % 8 == 0) && al16(x) && (x_row * xs) % 16 == 0 && al16(y) &&
           (w_stride != 1 || al16(w));
-  const int nch = (int)cdiv(h, 512);
   const dim3 grid((unsigned)cdiv(rows, 4));
-  hipStream_t st = (hipStream_t)stream;
-  SS_ROW_KERNEL_SWITCH(add_rmsnorm_fwd_kernel, nch, a, grid, st);
+  launch_fwd(a, false, grid, (hipStream_t)stream);
   SS_CHECK_LAUNCH("add_rmsnorm_fwd_kernel");
   return SS_OK;
 }
@@ -465,10 +699,13 @@ extern "C" int ss_add_rmsnorm_bwd(const void* s, int s_dtype, const void* w, int
           (w_stride != 1 || al16(w));
   a.vec_gs = gs && gs_col == 1 && gs_row % 8 == 0 && al16(gs) && a.vec;
   a.vec_gy = gy && gy_col == 1 && gy_row % 8 == 0 && al16(gy) && a.vec;
-  const int nch = (int)cdiv(h, 512);
   const dim3 grid((unsigned)cdiv(rows, 4));
   hipStream_t st = (hipStream_t)stream;
-  SS_ROW_KERNEL_SWITCH(add_rmsnorm_bwd_kernel, nch, a, grid, st);
+  switch (bwd_mode(a)) {
+    case 1: launch_bwd_mode<1>(a, grid, st); break;
+    case 2: launch_bwd_mode<2>(a, grid, st); break;
+    default: launch_bwd_mode<0>(a, grid, st); break;
+  }
   SS_CHECK_LAUNCH("add_rmsnorm_bwd_kernel");
   return SS_OK;
 }
@@ -523,24 +760,13 @@ extern "C" int ss_add_rmsnorm_bwd_dgamma(const void* s, int s_dtype, const void*
             (w_stride != 1 || al16(w));
     a.vec_gs = gs && gs_col == 1 && gs_row % 8 == 0 && al16(gs) && a.vec;
     a.vec_gy = gy && gy_col == 1 && gy_row % 8 == 0 && al16(gy) && a.vec;
-    const int nch = (int)cdiv(h, 512);
     const size_t lds = (size_t)kDgWaves * h * sizeof(float);
     const dim3 grid((unsigned)groups);
-    const dim3 block(kDgWaves * 64);
-#define SS_DG_CASE(N)                                                                           \
-  case N:                                                                                       \
-    hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<N>), grid, block, lds, st, a, half_products,  \
-                       partial);                                                                \
-    break;
-    switch (nch) {
-      SS_DG_CASE(1) SS_DG_CASE(2) SS_DG_CASE(3) SS_DG_CASE(4) SS_DG_CASE(5) SS_DG_CASE(6)
-      SS_DG_CASE(7) SS_DG_CASE(8)
-      default:
-        hipLaunchKernelGGL((add_rmsnorm_bwd_dg_kernel<16>), grid, block, lds, st, a,
-                           half_products, partial);
-        break;
+    switch (bwd_mode(a)) {
+      case 1: launch_dg_mode<1>(a, half_products, partial, grid, lds, st); break;
+      case 2: launch_dg_mode<2>(a, half_products, partial, grid, lds, st); break;
+      default: launch_dg_mode<0>(a, half_products, partial, grid, lds, st); break;
     }
-#undef SS_DG_CASE
     SS_CHECK_LAUNCH("add_rmsnorm_bwd_dg_kernel");
   }
   hipLaunchKernelGGL(dgamma_groups_final_kernel, dim3((unsigned)cdiv(h, 64)), dim3(1024), 0, st,
