@@ -106,11 +106,28 @@ __device__ __forceinline__ void store4(void* p, int dt, int64_t off, const float
   }
 }
 
+template <int DT>
+__device__ __forceinline__ void load4t(const void* p, int64_t off, float (&v)[4]) {
+  if constexpr (DT == SS_F16) {
+    const half4 h = *reinterpret_cast<const half4*>(static_cast<const half_t*>(p) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (float)h[e];
+  } else {
+    const float4v f = *reinterpret_cast<const float4v*>(static_cast<const float*>(p) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = f[e];
+  }
+}
+
 // Vector form: each thread takes 4 consecutive columns of one row's half
 // width (8- or 16-byte accesses), half / 4 threads per row, rows packed
 // across the workgroup.  Needs half % 4 == 0, unit last-dimension strides,
 // every other stride a multiple of 4 and 16-byte aligned bases (vec_ok).
-template <bool BWD>
+// CD: the cos / sin dtype, or -1 to read it (and every other dtype) at run
+// time; with CD set, q / k and their outputs are fp16, and the six loads of a
+// thread go out together (a run-time dtype branch around each load makes it
+// wait for the previous one).
+template <bool BWD, int CD>
 __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
   const int64_t quads = a.half / 4;
   const int64_t heads = a.q.heads + a.k.heads;
@@ -122,33 +139,51 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
   const int64_t head = (row / a.tokens) % heads;
   const int64_t batch = row / (heads * a.tokens);
   const bool is_q = head < a.q.heads;
-  const RopeOperand& o = is_q ? a.q : a.k;
+  // The operand's fields picked one by one (each a select of two kernel
+  // arguments), not through a reference chosen at run time, which would be
+  // read from the argument segment by a dependent load before the data loads.
+  const void* ox = is_q ? a.q.x : a.k.x;
+  if (!ox) return;
+  void* oy = is_q ? a.q.y : a.k.y;
+  const int xd = is_q ? a.q.xd : a.k.xd;
+  const int yd_rt = is_q ? a.q.yd : a.k.yd;
   const int64_t h = is_q ? head : head - a.q.heads;
-  if (!o.x) return;
   const int64_t cbatch = a.c_batches == 1 ? 0 : batch;
   const int64_t coff = cbatch * a.cb + token * a.ct + c;
   const int64_t soff = cbatch * a.sb + token * a.st + c;
-  const int64_t xoff = batch * o.sb + h * o.sh + token * o.st + c;
-  const int64_t yoff = batch * o.yb + h * o.yh + token * o.yt + c;
+  const int64_t xoff = batch * (is_q ? a.q.sb : a.k.sb) + h * (is_q ? a.q.sh : a.k.sh) +
+                       token * (is_q ? a.q.st : a.k.st) + c;
+  const int64_t yoff = batch * (is_q ? a.q.yb : a.k.yb) + h * (is_q ? a.q.yh : a.k.yh) +
+                       token * (is_q ? a.q.yt : a.k.yt) + c;
   float c1[4], c2[4], s1[4], s2[4], x1[4], x2[4], lo[4], hi[4];
-  load4(o.x, o.xd, xoff, x1);
-  load4(o.x, o.xd, xoff + a.half, x2);
-  load4(a.c, a.cd, coff, c1);
-  load4(a.c, a.cd, coff + a.half, c2);
-  load4(a.s, a.cd, soff, s1);
-  load4(a.s, a.cd, soff + a.half, s2);
+  if constexpr (CD < 0) {
+    load4(ox, xd, xoff, x1);
+    load4(ox, xd, xoff + a.half, x2);
+    load4(a.c, a.cd, coff, c1);
+    load4(a.c, a.cd, coff + a.half, c2);
+    load4(a.s, a.cd, soff, s1);
+    load4(a.s, a.cd, soff + a.half, s2);
+  } else {
+    load4t<SS_F16>(ox, xoff, x1);
+    load4t<SS_F16>(ox, xoff + a.half, x2);
+    load4t<CD>(a.c, coff, c1);
+    load4t<CD>(a.c, coff + a.half, c2);
+    load4t<CD>(a.s, soff, s1);
+    load4t<CD>(a.s, soff + a.half, s2);
+  }
+  const int yd = CD < 0 ? yd_rt : SS_F16;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     if (BWD) {
-      lo[e] = round_to(o.yd, x1[e] * c1[e]) + round_to(o.yd, x2[e] * s2[e]);
-      hi[e] = round_to(o.yd, x2[e] * c2[e]) - round_to(o.yd, x1[e] * s1[e]);
+      lo[e] = round_to(yd, x1[e] * c1[e]) + round_to(yd, x2[e] * s2[e]);
+      hi[e] = round_to(yd, x2[e] * c2[e]) - round_to(yd, x1[e] * s1[e]);
     } else {
-      lo[e] = round_to(o.yd, x1[e] * c1[e]) + round_to(o.yd, -x2[e] * s1[e]);
-      hi[e] = round_to(o.yd, x2[e] * c2[e]) + round_to(o.yd, x1[e] * s2[e]);
+      lo[e] = round_to(yd, x1[e] * c1[e]) + round_to(yd, -x2[e] * s1[e]);
+      hi[e] = round_to(yd, x2[e] * c2[e]) + round_to(yd, x1[e] * s2[e]);
     }
   }
-  store4(o.y, o.yd, yoff, lo);
-  store4(o.y, o.yd, yoff + a.half, hi);
+  store4(oy, yd, yoff, lo);
+  store4(oy, yd, yoff + a.half, hi);
 }
 
 bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -177,7 +212,12 @@ int launch_rope(bool bwd, const RopeArgs& a, void* stream, const char* fn) {
   SS_CHECK_ARG(a.c && a.s && (!a.q.x || a.q.y) && (!a.k.x || a.k.y), "%s: null pointer", fn);
   SS_CHECK_ARG(cdiv(rows, 4) <= 0x7fffffff, "%s: too many rows", fn);
   if (vec_ok(a) && cdiv(rows * (a.half / 4), 256) <= 0x7fffffff) {
-    auto kern = bwd ? rope_vec_kernel<true> : rope_vec_kernel<false>;
+    // fp16 q / k in and out: the dtypes are template arguments.
+    const bool f16 = (!a.q.x || (a.q.xd == SS_F16 && a.q.yd == SS_F16)) &&
+                     (!a.k.x || (a.k.xd == SS_F16 && a.k.yd == SS_F16));
+    auto kern = !f16 ? (bwd ? rope_vec_kernel<true, -1> : rope_vec_kernel<false, -1>)
+                : a.cd == SS_F16 ? (bwd ? rope_vec_kernel<true, SS_F16> : rope_vec_kernel<false, SS_F16>)
+                                 : (bwd ? rope_vec_kernel<true, SS_F32> : rope_vec_kernel<false, SS_F32>);
     hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(rows * (a.half / 4), 256)), dim3(256), 0,
                        (hipStream_t)stream, a);
     SS_CHECK_LAUNCH(fn);
