@@ -17,8 +17,10 @@
 // VALU operations per element.  Contiguous rows take the vector kernel: a
 // workgroup (grid x: row tiles, y: column tiles) covers 8 rows x 256
 // columns, each thread one 8-element chunk (16-byte loads and stores for
-// fp16, two for fp32), all loads issued before the arithmetic.  Measured at
-// [990, 8960] fp16: 8-row tiles 10.2 / 20.4 us (forward / backward), 16-row
+// fp16, two for fp32), all loads issued before the arithmetic (with fp16
+// operands the dtype is a template argument, so no run-time dtype branch
+// separates them).  Measured at [990, 8960] fp16: 8-row tiles 10.2 / 20.4 us
+// (forward / backward) before that change, 16-row
 // tiles (two chunks per thread) 11.4 / 23.2 us, 32-row tiles 11.5 / 26.6 us.  Anything
 // else (column strides, unaligned rows, widths not a multiple of 8) runs the
 // element-wise kernel over the same tiles.
@@ -76,8 +78,34 @@ __device__ __forceinline__ void store8(const Mat& m, int64_t off, const float (&
   }
 }
 
-// Vector kernel: unit column strides, 16-byte aligned rows, cols % 8 == 0.
-template <bool BWD>
+// fp16 operands (F16): plain 16-byte accesses, no run-time dtype branch, so a
+// thread's loads go out together instead of each waiting for the previous one.
+template <bool F16>
+__device__ __forceinline__ void load8t(const Mat& m, int64_t off, float (&v)[kChunk]) {
+  if constexpr (F16) {
+    const half8 h = *reinterpret_cast<const half8*>(static_cast<const half_t*>(m.p) + off);
+#pragma unroll
+    for (int e = 0; e < kChunk; ++e) v[e] = (float)h[e];
+  } else {
+    load8(m, off, v);
+  }
+}
+
+template <bool F16>
+__device__ __forceinline__ void store8t(const Mat& m, int64_t off, const float (&v)[kChunk]) {
+  if constexpr (F16) {
+    half8 h;
+#pragma unroll
+    for (int e = 0; e < kChunk; ++e) h[e] = f32_to_f16(v[e]);
+    *reinterpret_cast<half8*>(static_cast<half_t*>(m.p) + off) = h;
+  } else {
+    store8(m, off, v);
+  }
+}
+
+// Vector kernel: unit column strides, 16-byte aligned rows, cols % 8 == 0;
+// F16: every operand fp16.
+template <bool BWD, bool F16>
 __global__ __launch_bounds__(256) void swiglu_vec_kernel(Mat g, Mat u, Mat da, Mat o0, Mat o1,
                                                          int64_t rows, int64_t cols) {
   const int64_t c = blockIdx.y * (int64_t)kCols + (threadIdx.x & 31) * kChunk;
@@ -89,9 +117,9 @@ __global__ __launch_bounds__(256) void swiglu_vec_kernel(Mat g, Mat u, Mat da, M
   for (int k = 0; k < kU; ++k) {
     const int64_t r = r0 + 8 * k;
     if (r < rows) {
-      load8(g, r * g.rs + c, gv[k]);
-      load8(u, r * u.rs + c, uv[k]);
-      if (BWD) load8(da, r * da.rs + c, dv[k]);
+      load8t<F16>(g, r * g.rs + c, gv[k]);
+      load8t<F16>(u, r * u.rs + c, uv[k]);
+      if (BWD) load8t<F16>(da, r * da.rs + c, dv[k]);
     }
   }
 #pragma unroll
@@ -110,8 +138,8 @@ __global__ __launch_bounds__(256) void swiglu_vec_kernel(Mat g, Mat u, Mat da, M
         a[e] = t.act * uv[k][e];
       }
     }
-    store8(o0, r * o0.rs + c, a);
-    if (BWD) store8(o1, r * o1.rs + c, b);
+    store8t<F16>(o0, r * o0.rs + c, a);
+    if (BWD) store8t<F16>(o1, r * o1.rs + c, b);
   }
 }
 
@@ -153,8 +181,11 @@ int launch(bool bwd, const Mat* mats, int count, int64_t rows, int64_t cols, voi
   const Mat& o0 = bwd ? mats[3] : mats[2];
   const Mat& o1 = bwd ? mats[4] : none;
   const dim3 grid((unsigned)cdiv(rows, kRows), (unsigned)cdiv(cols, kCols));
-  auto kern = vec ? (bwd ? swiglu_vec_kernel<true> : swiglu_vec_kernel<false>)
-                  : (bwd ? swiglu_any_kernel<true> : swiglu_any_kernel<false>);
+  bool f16 = true;
+  for (int i = 0; i < count; ++i) f16 = f16 && mats[i].dt == SS_F16;
+  auto kern = !vec ? (bwd ? swiglu_any_kernel<true> : swiglu_any_kernel<false>)
+              : f16 ? (bwd ? swiglu_vec_kernel<true, true> : swiglu_vec_kernel<false, true>)
+                    : (bwd ? swiglu_vec_kernel<true, false> : swiglu_vec_kernel<false, false>);
   hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, g, u, da, o0, o1, rows, cols);
   SS_CHECK_LAUNCH(fn);
   return SS_OK;
