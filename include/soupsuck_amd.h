@@ -462,14 +462,34 @@ int ss_ce_outputs(const float* partial, const int64_t* partial_arg, int64_t slot
  * gain[r] = max(|grad[r]|, 1e-30) / 1024 (zero on ignored rows); when dz_global
  * is not NULL it also receives the same derivative scaled by 1/global_gain
  * instead of 1/gain[r] (for the lm_head gradient; global_gain points at one
- * fp32 value > 0 in device memory).  dz and dz_global are dense
- * [n, width].  Row r of the logits is z[z_rows[r]] when z_rows (int64 [n]) is
- * not NULL, else z[r] (row stride ldz).  Replaces vocabulary_derivative_kernel
+ * fp32 value > 0 in device memory).  dz is dense [n, width], dz_global dense
+ * [global_rows, width] with rows n .. global_rows - 1 written as zeros
+ * (global_rows = n without dz_global).  Row r of the logits is z[z_rows[r]]
+ * when z_rows (int64 [n]) is not NULL, else z[r] (row stride ldz).  Replaces
+ * vocabulary_derivative_kernel
  * (solution/kernels/cross_entropy.py:108-122). */
 int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
                      const int64_t* targets, const float* lse, const float* grad, uint16_t* dz,
-                     uint16_t* dz_global, const float* global_gain, int64_t n, int64_t width,
-                     int64_t start, int64_t ignore_index, void* stream);
+                     uint16_t* dz_global, const float* global_gain, int64_t n,
+                     int64_t global_rows, int64_t width, int64_t start, int64_t ignore_index,
+                     void* stream);
+
+/* Labelled rows of targets[n] and their validation, in one launch: order[0 ..
+ * count) holds the rows whose target is not ignore_index, ascending (the
+ * reference's row compaction before its backward), order[count .. order_len)
+ * is -1 (order_len >= n: an index vector padded for ss_unpad_gather, which
+ * writes a zero row for -1); count[0] = count (int64, device); ok[0] = 1 when
+ * every target is ignore_index or in [0, vocab), else 0 (the reference's
+ * "Target outside vocabulary" check, solution/kernels/cross_entropy.py:235-238,
+ * read by a device-side assertion). */
+int ss_ce_rows(const int64_t* targets, int64_t n, int64_t vocab, int64_t ignore_index,
+               int64_t* order, int64_t order_len, int64_t* count, uint8_t* ok, void* stream);
+
+/* gain[0] = max(max_r |grad[r]|, 1e-30) / 1024 over grad[n] (NaN if a grad is
+ * NaN): the global gain of the lm_head gradient's derivative copy.  No
+ * counterpart in the reference (its head is frozen); this build's weight_grad
+ * extension. */
+int ss_ce_head_gain(const float* grad, int64_t n, float* gain, void* stream);
 
 /* out[r, :] = cast(acc[inverse[r], :] * max(|grad[r]|, 1e-30) / 1024) when
  * inverse[r] >= 0 (a valid row, compacted to position inverse[r]), else 0:

@@ -118,7 +118,9 @@ SIGNATURES = {
                    [_c_void_p],
     "ss_ce_outputs": [_c_void_p, _c_void_p, _i64] + [_c_void_p] * 5 + [_i64, _i64, _c_void_p],
     "ss_ce_derivative": [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
+                         _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p],
+    "ss_ce_rows": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "ss_ce_head_gain": [_c_void_p, _i64, _c_void_p, _c_void_p],
     "ss_attn_varlen_fwd": [_c_void_p, _i64, _i64] * 3 + [_c_void_p, _int, _int, _i64, _int,
                                                            _int, _int, _f32, _c_void_p, _i64,
                                                            _i64, _c_void_p, _c_void_p],

@@ -259,10 +259,23 @@ __global__ __launch_bounds__(256) void ce_derivative_kernel(
     const int64_t* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ grad, half_t* __restrict__ dz,
     half_t* __restrict__ dzg, const float* __restrict__ global_gain_p, int64_t width,
-    int64_t start, int64_t ignore, int vec) {
+    int64_t start, int64_t ignore, int vec, int64_t n) {
   const int64_t row = blockIdx.x;
   const int64_t c = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 8;
   if (c >= width) return;
+  if (row >= n) {
+    // Rows n .. of dz_global (its padding up to the head-gradient product's depth):
+    // zeros, so the product needs no separate fill.
+    half_t* outg = dzg + row * width + c;
+    if (vec && c + 8 <= width) {
+      *reinterpret_cast<uint4*>(outg) = make_uint4(0, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c + j < width) outg[j] = (half_t)0.0f;
+    }
+    return;
+  }
   const int64_t tgt = targets[row];
   const bool valid = tgt != ignore;
   const float g = valid ? grad[row] : 0.0f;
@@ -316,6 +329,84 @@ __global__ __launch_bounds__(256) void ce_finalize_kernel(const float* __restric
     v = acc[(int64_t)j * h + c] * gain;
   }
   st_elem(out, od, r * h + c, v);
+}
+
+// Labelled rows and target validation in one workgroup: thread t takes rows
+// [t per, (t + 1) per); pass 1 counts its labelled rows and checks its targets,
+// a scan over the threads places them, pass 2 writes the labelled rows' indices
+// in row order; the rest of `order` is filled with -1.
+constexpr int kRowsThreads = 1024;
+
+__global__ __launch_bounds__(kRowsThreads) void ce_rows_kernel(
+    const int64_t* __restrict__ targets, int64_t n, int64_t vocab, int64_t ignore,
+    int64_t* __restrict__ order, int64_t order_len, int64_t* __restrict__ count,
+    uint8_t* __restrict__ ok) {
+  __shared__ int64_t s_scan[kRowsThreads];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_bad = 0;
+  const int64_t per = (n + kRowsThreads - 1) / kRowsThreads;
+  const int64_t r0 = tid * per < n ? tid * per : n;
+  const int64_t r1 = r0 + per < n ? r0 + per : n;
+  int64_t mine = 0;
+  bool bad = false;
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t t = targets[r];
+    if (t != ignore) {
+      ++mine;
+      bad = bad || t < 0 || t >= vocab;
+    }
+  }
+  s_scan[tid] = mine;
+  __syncthreads();
+  if (bad) s_bad = 1;  // benign race: every writer stores 1
+  // Inclusive scan (Hillis-Steele) over the thread counts.
+  for (int off = 1; off < kRowsThreads; off <<= 1) {
+    const int64_t v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  const int64_t total = s_scan[kRowsThreads - 1];
+  int64_t kept_at = s_scan[tid] - mine;   // labelled rows before this thread's
+  for (int64_t r = r0; r < r1; ++r)
+    if (targets[r] != ignore) order[kept_at++] = r;
+  for (int64_t i = total + tid; i < order_len; i += kRowsThreads) order[i] = -1;
+  if (tid == 0) {
+    count[0] = total;
+    ok[0] = s_bad ? 0 : 1;
+  }
+}
+
+// gain[0] = max(max_r |grad[r]|, 1e-30) / 1024, NaN when a grad is NaN.
+__global__ __launch_bounds__(256) void ce_head_gain_kernel(const float* __restrict__ grad,
+                                                           int64_t n, float* __restrict__ gain) {
+  __shared__ float s_max[4];
+  __shared__ int s_nan[4];
+  float m = 0.0f;
+  int nan = 0;
+  for (int64_t r = threadIdx.x; r < n; r += 256) {
+    const float v = fabsf(grad[r]);
+    nan |= v != v;
+    m = fmaxf(m, v);
+  }
+  m = wave_max(m);
+  for (int o = 32; o >= 1; o >>= 1) nan |= __shfl_xor(nan, o, kWave);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    s_max[wave] = m;
+    s_nan[wave] = nan;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v = s_max[0];
+    int any_nan = s_nan[0];
+    for (int w = 1; w < 4; ++w) {
+      v = fmaxf(v, s_max[w]);
+      any_nan |= s_nan[w];
+    }
+    gain[0] = any_nan ? __int_as_float(0x7fc00000) : fmaxf(v, 1e-30f) / 1024.0f;
+  }
 }
 
 static bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -372,20 +463,23 @@ extern "C" int ss_ce_outputs(const float* partial, const int64_t* partial_arg, i
 extern "C" int ss_ce_derivative(const uint16_t* z, int64_t ldz, const int64_t* z_rows,
                                 const int64_t* targets, const float* lse, const float* grad,
                                 uint16_t* dz, uint16_t* dz_global, const float* global_gain,
-                                int64_t n, int64_t width, int64_t start, int64_t ignore_index,
-                                void* stream) {
+                                int64_t n, int64_t global_rows, int64_t width, int64_t start,
+                                int64_t ignore_index, void* stream) {
   SS_CHECK_ARG(n >= 0 && width > 0 && ldz >= width, "ss_ce_derivative: bad sizes");
   SS_CHECK_ARG(!dz_global || global_gain, "ss_ce_derivative: dz_global needs global_gain");
-  if (n == 0) return SS_OK;
+  SS_CHECK_ARG(global_rows >= n && (dz_global || global_rows == n),
+               "ss_ce_derivative: global_rows must be >= n (and n without dz_global)");
+  SS_CHECK_ARG(global_rows < (int64_t)1 << 31, "ss_ce_derivative: too many rows");
+  if (n == 0 && global_rows == 0) return SS_OK;
   SS_CHECK_ARG(z && targets && lse && grad && dz, "ss_ce_derivative: null pointer");
   const int vec = al16(z) && ldz % 8 == 0 && al16(dz) && width % 8 == 0 &&
                   (!dz_global || al16(dz_global));
   SS_CHECK_ARG(cdiv(width, 256 * 8) < 65536, "ss_ce_derivative: width too large");
-  const dim3 grid((unsigned)n, (unsigned)cdiv(width, 256 * 8));
+  const dim3 grid((unsigned)global_rows, (unsigned)cdiv(width, 256 * 8));
   hipLaunchKernelGGL(ce_derivative_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      reinterpret_cast<const half_t*>(z), ldz, z_rows, targets, lse, grad,
                      reinterpret_cast<half_t*>(dz), reinterpret_cast<half_t*>(dz_global),
-                     global_gain, width, start, ignore_index, vec);
+                     global_gain, width, start, ignore_index, vec, n);
   SS_CHECK_LAUNCH("ce_derivative_kernel");
   return SS_OK;
 }
@@ -402,5 +496,26 @@ extern "C" int ss_ce_finalize_dx(const float* acc, int64_t valid_n, const float*
   hipLaunchKernelGGL(ce_finalize_kernel, grid, dim3(256), 0, (hipStream_t)stream, acc, grad,
                      inverse, out, out_dtype, h, valid_n);
   SS_CHECK_LAUNCH("ce_finalize_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_ce_rows(const int64_t* targets, int64_t n, int64_t vocab, int64_t ignore_index,
+                          int64_t* order, int64_t order_len, int64_t* count, uint8_t* ok,
+                          void* stream) {
+  SS_CHECK_ARG(n >= 0 && vocab > 0 && order_len >= n, "ss_ce_rows: bad sizes");
+  SS_CHECK_ARG(count && ok && (n == 0 || targets) && (order_len == 0 || order),
+               "ss_ce_rows: null pointer");
+  hipLaunchKernelGGL(ce_rows_kernel, dim3(1), dim3(kRowsThreads), 0, (hipStream_t)stream,
+                     targets, n, vocab, ignore_index, order, order_len, count, ok);
+  SS_CHECK_LAUNCH("ce_rows_kernel");
+  return SS_OK;
+}
+
+extern "C" int ss_ce_head_gain(const float* grad, int64_t n, float* gain, void* stream) {
+  SS_CHECK_ARG(n >= 0, "ss_ce_head_gain: negative n");
+  SS_CHECK_ARG(gain && (n == 0 || grad), "ss_ce_head_gain: null pointer");
+  hipLaunchKernelGGL(ce_head_gain_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, grad, n,
+                     gain);
+  SS_CHECK_LAUNCH("ce_head_gain_kernel");
   return SS_OK;
 }

@@ -11,8 +11,9 @@ differentiable, ValueError before launch) and its numerics (:1-43):
             order as the online softmax merges (m = max, s = sum s_p
             e^(m_p-m), ...), lse = m + log s, loss = lse - z_target (0 for
             ignored rows), entropy = lse - t/s (ss_ce_outputs);
-  backward  rows with a target only (found in the forward: a stable sort and a
-            count copied to pinned memory early, so no stall); each chunk
+  backward  rows with a target only (found and validated in the forward by one
+            launch, ss_ce_rows, whose count is copied to pinned memory early, so
+            no stall); each chunk
             is recomputed and dz = fp16((softmax - onehot) g / gain) with the
             per-row gain max(|g|, 1e-30)/1024 (ss_ce_derivative); dX = dz . W_c
             accumulated in fp32 over chunks, multiplied back by the gain and
@@ -172,24 +173,33 @@ def _forward(hidden16, weight, targets, ignore_index, chunk, keep):
 
 
 class _KeptRows:
-    """Rows with a target, found in the forward without a host synchronisation.
+    """Rows with a target, found and validated in the forward without a host
+    synchronisation (ss_ce_rows, one launch).
 
-    A stable sort puts the labelled rows first (in row order); their count is
-    copied to pinned host memory as soon as it is computed, ahead of the
-    forward's GEMMs, so by the time the backward needs it the copy has long
-    completed and reading it does not stall the device."""
+    `order` lists the labelled rows in row order, then -1 up to a multiple of 64
+    rows (the gather of the head-gradient product's operand writes zero rows
+    there); their count is copied to pinned host memory as soon as it is
+    computed, ahead of the forward's GEMMs, so by the time the backward needs it
+    the copy has long completed and reading it does not stall the device.  `ok`
+    is False when a target is outside [0, V) and not ignore_index."""
 
-    def __init__(self, targets, ignore_index):
-        kept = targets != ignore_index
-        self.order = torch.argsort((~kept).to(torch.int8), stable=True)
+    def __init__(self, targets, ignore_index, vocab):
+        rows = targets.numel()
+        dev = targets.device
+        self.order = torch.empty(-(-rows // 64) * 64, device=dev, dtype=torch.int64)
+        count = torch.empty((), device=dev, dtype=torch.int64)
+        self.ok = torch.empty((), device=dev, dtype=torch.bool)
+        _lib.call("ss_ce_rows", targets.data_ptr(), rows, vocab, ignore_index,
+                  self.order.data_ptr(), self.order.numel(), count.data_ptr(),
+                  self.ok.data_ptr(), _lib.stream(dev))
         self.count_host = torch.empty((), dtype=torch.int64, pin_memory=True)
-        self.count_host.copy_(kept.sum(), non_blocking=True)
+        self.count_host.copy_(count, non_blocking=True)
         self.ready = torch.cuda.Event()
         self.ready.record()
 
-    def indices(self):
+    def count(self):
         self.ready.synchronize()
-        return self.order[:int(self.count_host)]
+        return int(self.count_host)
 
 
 class _Backward:
@@ -202,17 +212,14 @@ class _Backward:
         self.dev = hidden16.device
         self.stream = _lib.stream(self.dev)
         self.full_grad = grad
-        self.kept = kept.indices()
-        self.count = self.kept.numel()
+        self.count = kept.count()
+        self.kept = kept.order[:self.count]
         if self.count:
-            # Rows with a target, then zero rows up to a multiple of 64: the K of the
-            # head-gradient product.
+            # Rows with a target, then zero rows up to a multiple of 64 (index -1): the
+            # K of the head-gradient product.
             self.padded = -(-self.count // 64) * 64
-            self.h_pad = torch.empty((self.padded, hidden16.shape[1]), device=self.dev,
-                                     dtype=hidden16.dtype)
-            if self.padded > self.count:
-                self.h_pad[self.count:].zero_()
-            self.h = _gather_rows(hidden16, self.kept, out=self.h_pad[:self.count])
+            self.h_pad = _gather_rows(hidden16, kept.order[:self.padded])
+            self.h = self.h_pad[:self.count]
             self.targets = _gather_rows(targets, self.kept)
             self.lse = _gather_rows(lse, self.kept)
             self.grad = _gather_rows(grad, self.kept)
@@ -229,18 +236,20 @@ class _Backward:
         if kept_z is None:
             logits = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
         dz = torch.empty((count, width_max), device=self.dev, dtype=torch.float16)
-        acc = torch.zeros((count, hdim), device=self.dev, dtype=torch.float32) \
+        # dX accumulates over the steps; the first one overwrites.
+        acc = torch.empty((count, hdim), device=self.dev, dtype=torch.float32) \
             if dx is not None else None
         head_gain = None
         if dw is not None:
-            # max_r |g_r| / 1024 as a device scalar: no host round trip between the
-            # forward and the backward's launches
-            head_gain = (self.grad.abs().amax().clamp_min(1e-30) / 1024.0).reshape(1)
-            # dz' per step as [padded, width] (dense rows): the rows past `count` must
-            # read zero.  They are cleared for the first step's width and again when the
-            # width changes (a narrower step's tail rows hold a wider step's rows).
+            # max_r |g_r| / 1024 as a device scalar (ss_ce_head_gain): no host round trip
+            # between the forward and the backward's launches
+            head_gain = torch.empty(1, device=self.dev, dtype=torch.float32)
+            _lib.call("ss_ce_head_gain", self.grad.data_ptr(), count, head_gain.data_ptr(),
+                      self.stream)
+            # dz' per step as [padded, width] (dense rows); the derivative writes the rows
+            # past `count` as zeros.
             dz_head = torch.empty(padded * width_max, device=self.dev, dtype=torch.float16)
-            cleared = None
+        first = True
         for start, width in _vocab_chunks(self.weight.shape[0], span):
             w = _head_rows(self.weight, start, width)
             if kept_z is None:
@@ -253,15 +262,14 @@ class _Backward:
             dh = None
             if dw is not None:
                 dh = dz_head[:padded * width].view(padded, width)
-                if padded > count and width != cleared:
-                    dz_head[count * width:padded * width].zero_()
-                    cleared = width
             _lib.call("ss_ce_derivative", z.data_ptr(), ldz, _lib.ptr(z_rows),
                       self.targets.data_ptr(), self.lse.data_ptr(), self.grad.data_ptr(),
-                      d.data_ptr(), _lib.ptr(dh), _lib.ptr(head_gain), count, width, start,
-                      self.ignore, self.stream)
+                      d.data_ptr(), _lib.ptr(dh), _lib.ptr(head_gain), count,
+                      padded if dh is not None else count, width, start, self.ignore,
+                      self.stream)
             if acc is not None:
-                gemm_f16(d, w, out=acc, accumulate=True, split_k=True)
+                gemm_f16(d, w, out=acc, accumulate=not first, split_k=True)
+            first = False
             if dw is not None:
                 rows_w = dw.narrow(0, start, width)
                 if rows_w.dtype in FLOAT_DTYPES:
@@ -281,11 +289,11 @@ class _Backward:
 
 class LinearCrossEntropy(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, hidden, weight, targets, ignore_index, chunk, weight_grad):
+    def forward(ctx, hidden, weight, targets, ignore_index, chunk, weight_grad, kept):
         hidden16 = hidden.to(torch.float16).contiguous()
         targets = targets.contiguous()
         chunk = chunk or default_chunk(hidden16.shape[0])
-        ctx.kept = _KeptRows(targets, ignore_index) if hidden16.shape[0] else None
+        ctx.kept = kept
         backward_may_run = ctx.needs_input_grad[0] or (weight_grad and ctx.needs_input_grad[1])
         keep = backward_may_run and \
             hidden16.shape[0] * weight.shape[0] * 2 <= KEEP_LOGITS_BUDGET
@@ -304,7 +312,7 @@ class LinearCrossEntropy(torch.autograd.Function):
         logits, ctx.logits = ctx.logits, None  # kept logits serve one backward
         want_x = ctx.needs_input_grad[0]
         want_w = weight_grad and ctx.needs_input_grad[1]
-        nothing = (None,) * 6
+        nothing = (None,) * 7
         if grad_loss is None or not (want_x or want_w):
             return nothing
         hidden16, weight, targets, lse = ctx.saved_tensors
@@ -326,7 +334,7 @@ class LinearCrossEntropy(torch.autograd.Function):
             for g in (dx, dw):
                 if g is not None:
                     g.zero_()
-        return dx, dw, None, None, None, None
+        return dx, dw, None, None, None, None, None
 
 
 CE_RULES = (
@@ -364,8 +372,12 @@ def fused_linear_cross_entropy(hidden, weight, targets, ignore_index=-100, *, ch
     enforce(CE_RULES, hidden=hidden, weight=weight, targets=targets, ignore_index=ignore_index,
             chunk=chunk, weight_grad=weight_grad)
     with torch.cuda.device(hidden.device):
-        out_of_range = (targets != ignore_index) & ((targets < 0) | (targets >= weight.shape[0]))
-        torch._assert_async(torch.logical_not(out_of_range.any()),
-                            "fused_linear_cross_entropy: target outside the vocabulary")
+        targets = targets.contiguous()
+        kept = None
+        if targets.numel():
+            # Labelled rows and the target check in one launch (ss_ce_rows).
+            kept = _KeptRows(targets, ignore_index, weight.shape[0])
+            torch._assert_async(kept.ok, "fused_linear_cross_entropy: target outside the "
+                                         "vocabulary")
         return LinearCrossEntropy.apply(hidden, weight, targets, ignore_index, chunk,
-                                        bool(weight_grad))
+                                        bool(weight_grad), kept)

@@ -73,6 +73,10 @@ def test_workspace_policy_is_host_only(lib):
     ("ss_ce_stats", (None, 8, None, None, None, 2, 8, 4, 0, 0, 1, -100, None), "partial row"),
     ("ss_ce_outputs", (None, None, 0, None, None, None, None, None, 2, -100, None),
      "bad sizes"),
+    ("ss_ce_rows", (None, 4, 10, -100, None, 2, None, None, None), "bad sizes"),
+    ("ss_ce_head_gain", (None, 3, None, None), "null pointer"),
+    ("ss_ce_derivative", (None, 8, None, None, None, None, None, None, None, 4, 2, 8, 0, -100,
+                          None), "global_rows"),
 ])
 def test_invalid_arguments_are_rejected_before_launch(lib, name, args, needle):
     rc = getattr(lib, name)(*args)

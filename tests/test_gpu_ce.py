@@ -193,3 +193,39 @@ def test_kept_logits_equal_recomputed(device, monkeypatch, n, h, v, chunk):
         for a, b in zip(kept[:4] + kept[5:], recomputed[:4] + recomputed[5:]):
             assert torch.equal(a, b)
         assert ((kept[4].float() - dx_r).norm() / dx_r.norm()).item() <= 1e-4
+
+
+@pytest.mark.parametrize("n", [1, 826, 5000])
+def test_rows_and_head_gain_kernels(device, n):
+    """ss_ce_rows: the labelled rows in row order, -1 up to the padded length, their
+    count and the target check; ss_ce_head_gain: max(max |g|, 1e-30) / 1024, NaN when a
+    grad is NaN.  Against torch on the same inputs, through the C ABI."""
+    from soupsuck_amd import _lib
+    gen = torch.Generator(device="cpu").manual_seed(n)
+    vocab = 1000
+    t = torch.randint(0, vocab, (n,), generator=gen)
+    t[torch.rand(n, generator=gen) < 0.4] = -100
+    stream = _lib.stream(device)
+    for bad in (False, True):
+        tt = t.clone()
+        if bad:
+            tt[n // 2] = vocab  # one target outside the vocabulary
+        tt = tt.to(device)
+        pad = -(-n // 64) * 64
+        order = torch.full((pad,), 7, device=device, dtype=torch.int64)
+        count = torch.empty((), device=device, dtype=torch.int64)
+        ok = torch.empty((), device=device, dtype=torch.bool)
+        _lib.call("ss_ce_rows", tt.data_ptr(), n, vocab, -100, order.data_ptr(), pad,
+                  count.data_ptr(), ok.data_ptr(), stream)
+        kept = torch.nonzero(tt != -100).flatten()
+        assert count.item() == kept.numel()
+        assert torch.equal(order[:kept.numel()], kept)
+        assert torch.all(order[kept.numel():] == -1)
+        assert ok.item() is (not bad)
+    g = torch.randn(n, generator=gen).to(device)
+    gain = torch.empty(1, device=device)
+    _lib.call("ss_ce_head_gain", g.data_ptr(), n, gain.data_ptr(), stream)
+    assert gain.item() == (g.abs().amax().clamp_min(1e-30) / 1024.0).item()
+    g[n // 3] = float("nan")
+    _lib.call("ss_ce_head_gain", g.data_ptr(), n, gain.data_ptr(), stream)
+    assert math.isnan(gain.item())

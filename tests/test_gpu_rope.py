@@ -44,6 +44,7 @@ def _exact(t, ref):
 
 
 @pytest.mark.parametrize("qdt,kdt,cdt", [(torch.float16, torch.float16, torch.float16),
+                                         (torch.float16, torch.float16, torch.float32),
                                          (torch.float16, torch.float32, torch.float32),
                                          (torch.float32, torch.float16, torch.float16),
                                          (torch.float32, torch.float32, torch.float32)])
