@@ -7,14 +7,15 @@
 //
 // ce_stats: one 256-thread workgroup per (row, piece), a piece being up to
 // kStatsPiece consecutive logits of the row; one launch covers any number of
-// pieces (a whole product of several vocabulary chunks).  All of a lane's loads
-// (8 consecutive fp16 logits, 16 B, per 2048-logit step) are issued together
-// into registers; pass 1 finds the piece max m_p and its first index, pass 2
-// sums exp(z - m_p) and exp(z - m_p) * z.  The piece's partial state goes to
-// its slot of partial[row, pieces]; ce_outputs folds the slots of a row in
-// vocabulary order (online-softmax merge: rescale both sides to the larger
-// max), so the results depend only on where the pieces start, not on how many
-// a launch covered.
+// pieces (every chunk of the kept logits).  A lane's four 16-byte loads (8
+// consecutive fp16 logits per 2048-logit step) go out together with no branch
+// between them; one pass keeps the lane's running max m and its sums of
+// exp(z - m) and exp(z - m) * z, rescaled when a step raises m; lanes and
+// waves merge as the pieces do.  The piece's partial state goes to its slot of
+// partial[row, slots]; ce_outputs folds a row's slots in a fixed order (one
+// wave per row: lane-strided, then an xor butterfly of a commutative fold), so
+// the results depend only on where the pieces start, not on how many a launch
+// covered.
 
 #include "elementwise.h"
 
@@ -61,29 +62,7 @@ __device__ __forceinline__ Partial fold(Partial a, const Partial& b) {
   return Partial{m, a.s * ra + b.s * rb, a.t * ra + b.t * rb, a.f + b.f, arg};
 }
 
-// Max and first index within one piece (index local to the piece, < 8192); the
-// larger value wins, equal values keep the lower index.
-struct LocalMax {
-  float m;
-  int a;
-};
-
-__device__ __forceinline__ LocalMax better(LocalMax x, LocalMax y) {
-  if (y.m > x.m || (y.m == x.m && y.a < x.a)) return y;
-  return x;
-}
-
-__device__ __forceinline__ LocalMax wave_maxarg(LocalMax v) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    LocalMax o;
-    o.m = __shfl_xor(v.m, s, kWave);
-    o.a = __shfl_xor(v.a, s, kWave);
-    v = better(v, o);
-  }
-  return v;
-}
-
+// Local index standing for "no max": the piece holds no finite logit.
 constexpr int kNoLocal = 0x7fffffff;
 
 // The lane's logits c = 8 tid + 2048 i .. + 7 of one piece (c < w), as fp16.
