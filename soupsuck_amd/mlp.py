@@ -28,15 +28,19 @@ instead of two fp16 results added in fp16 (one rounding fewer).
 ``offload=True`` keeps the saved gate and up in pinned host memory instead of
 HBM (the reference's pinned-host offload, solution/mlp.py:105-359): the
 device-to-host copies run on a copy stream of default priority after the
-producing stream, the backward copies them back on its own stream after that
-copy has finished, and the pinned buffers return to a per-shape free list once
-the copy back has completed.  The default is off (``SOUP_MLP_OFFLOAD=1`` turns it
+producing stream; the copy back runs on that stream too and the backward waits
+for it.  A node's restore also starts the copy back of the node created before
+it (a lookahead of one: in a backward it is the next to restore), so that copy
+overlaps the current node's backward.  The pinned buffers return to a per-shape
+free list once their copy back has completed.  The default is off (``SOUP_MLP_OFFLOAD=1`` turns it
 on; the reference defaults to on): with 288 GB of HBM per MI355X the activations
 fit, and the round trip costs PCIe time.  Recomputation excludes offload, as in
 the reference.  Offload is refused under HIP graph capture.
 """
 
 import os
+import threading
+import weakref
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -192,14 +196,29 @@ def _host_pair(key):
             torch.empty(shape, dtype=torch.float16, pin_memory=True))
 
 
+_LAST_OFFLOAD = {}  # device index -> weakref to the newest HostOffload on that device
+_OFFLOAD_LOCK = threading.Lock()  # forward (main thread) and backward (autograd thread)
+PREFETCHES = [0]    # lookahead copies started (a counter the tests read)
+
+
 class HostOffload:
-    """gate and up of one MLP node held in pinned host memory until its backward."""
+    """gate and up of one MLP node held in pinned host memory until its backward.
+
+    Nodes on a device are chained in creation order.  A backward runs them in the
+    reverse order, so when a node restores its pair it also starts copying the pair
+    of the node created before it back to the device on the copy stream (lookahead
+    of one, the reference's prefetch chain, solution/mlp.py:203-252): that copy
+    overlaps this node's backward and the next restore only waits for it."""
 
     def __init__(self, gate, up):
         device = gate.device
         self.device = device
         self.key = (device.index, gate.shape[0], gate.shape[1])
-        self.pair = _host_pair(self.key)
+        self.prefetched = None  # (gate, up, ready event) once copied back
+        with _OFFLOAD_LOCK:
+            self.pair = _host_pair(self.key)
+            self.previous = _LAST_OFFLOAD.get(device.index)
+            _LAST_OFFLOAD[device.index] = weakref.ref(self)
         producer = torch.cuda.current_stream(device)
         copy = _copy_stream(device)
         copy.wait_stream(producer)
@@ -213,16 +232,36 @@ class HostOffload:
         gate.record_stream(copy)
         up.record_stream(copy)
 
-    def restore(self):
-        """(gate, up) back on the device, ordered on the current stream."""
-        stream = torch.cuda.current_stream(self.device)
-        stream.wait_event(self.stored)
-        gate = self.pair[0].to(self.device, non_blocking=True)
-        up = self.pair[1].to(self.device, non_blocking=True)
-        done = torch.cuda.Event()
-        done.record(stream)
-        _HOST_PENDING.append((done, self.key, self.pair))
+    def _fetch(self):
+        """Copy the pair back to the device on the copy stream (caller holds the lock)."""
+        copy = _copy_stream(self.device)
+        with torch.cuda.stream(copy):
+            copy.wait_event(self.stored)
+            gate = self.pair[0].to(self.device, non_blocking=True)
+            up = self.pair[1].to(self.device, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(copy)
+        _HOST_PENDING.append((ready, self.key, self.pair))
         self.pair = None
+        self.prefetched = (gate, up, ready)
+
+    def restore(self):
+        """(gate, up) back on the device, ordered on the current stream; starts the
+        copy of the previous node's pair."""
+        stream = torch.cuda.current_stream(self.device)
+        with _OFFLOAD_LOCK:
+            if self.prefetched is None:
+                self._fetch()
+            gate, up, ready = self.prefetched
+            self.prefetched = None
+            prev = self.previous() if self.previous is not None else None
+            if prev is not None and prev.pair is not None:
+                prev._fetch()
+                PREFETCHES[0] += 1
+        stream.wait_event(ready)
+        # Allocated on the copy stream, read on this one from here on.
+        gate.record_stream(stream)
+        up.record_stream(stream)
         return gate, up
 
 

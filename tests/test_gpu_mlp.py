@@ -150,6 +150,33 @@ def test_offload_keeps_gate_up_on_host_and_matches_bitwise(device):
     assert out.grad_fn.offloaded is None
 
 
+def test_offload_prefetches_the_previous_node_during_backward(device):
+    """Two offloaded MLP nodes in a row: restoring the second (first in the backward)
+    starts the copy back of the first one's pair on the copy stream; the gradients equal
+    the on-device nodes' bit for bit."""
+    from soupsuck_amd import mlp as fmlp
+
+    torch.manual_seed(779)
+    m1, m2 = _MLP(128, 320).to(device), _MLP(128, 320).to(device)
+    x = torch.randn((2, 90, 128), device=device, dtype=torch.float16)
+    upstream = torch.randn((2, 90, 128), device=device, dtype=torch.float16)
+    results = []
+    for offload in (False, True):
+        xi = x.clone().requires_grad_()
+        h = fused_qwen2_mlp(m1, xi, recompute=False, offload=offload)
+        out = fused_qwen2_mlp(m2, h, recompute=False, offload=offload)
+        first = h.grad_fn.offloaded
+        before = fmlp.PREFETCHES[0]
+        out.backward(upstream)
+        torch.cuda.synchronize()
+        if offload:
+            assert fmlp.PREFETCHES[0] >= before + 1
+            assert first is not None and first.pair is None  # copied back ahead of need
+        results.append((out.detach().clone(), xi.grad.clone()))
+    assert torch.equal(_bits(results[0][0]), _bits(results[1][0]))
+    assert torch.equal(_bits(results[0][1]), _bits(results[1][1]))
+
+
 def test_rejects_ineligible_modules(device):
     mlp = _MLP(128, 320).to(device)
     mlp.down_proj = torch.nn.Linear(320, 128, bias=False).to(device).half()
