@@ -31,11 +31,18 @@ device-to-host copies run on a copy stream of default priority after the
 producing stream; the copy back runs on that stream too and the backward waits
 for it.  A node's restore also starts the copy back of the node created before
 it (a lookahead of one: in a backward it is the next to restore), so that copy
-overlaps the current node's backward.  The pinned buffers return to a per-shape
-free list once their copy back has completed.  The default is off (``SOUP_MLP_OFFLOAD=1`` turns it
-on; the reference defaults to on): with 288 GB of HBM per MI355X the activations
-fit, and the round trip costs PCIe time.  Recomputation excludes offload, as in
-the reference.  Offload is refused under HIP graph capture.
+overlaps the current node's backward.  The pinned buffers come in power-of-two
+row classes and return to a free list once their copy back has completed.  The
+default is off (``SOUP_MLP_OFFLOAD=1`` turns it on; the reference defaults to on):
+with 288 GB of HBM per MI355X the activations fit, and the round trip costs PCIe
+time.  Recomputation excludes offload, as in the reference.  Offload is refused
+under HIP graph capture.
+
+Per-layer placement (solution/mlp.py:362-431): ``SOUP_MLP_RECOMPUTE_LAYERS=k``
+recomputes in the first k MLP layers, ``SOUP_EXP_OFFLOAD_TAIL=k`` keeps the last
+k layers' gate / up on the device when offload is on, and
+``prepare_mlp_offload(model, max_rows)`` numbers the layers and reserves their
+pinned pairs up front.
 """
 
 import os
@@ -169,7 +176,7 @@ def mlp_backward_2d(grad2d, parts, gate, up, fuse=None):
 
 
 _COPY_STREAMS = {}  # device index -> copy stream (default priority)
-_HOST_FREE = {}     # (device index, rows, width) -> free pinned (gate, up) pairs
+_HOST_FREE = {}     # (device index, capacity rows, width) -> free pinned (gate, up) pairs
 _HOST_PENDING = []  # (event, key, pair): pairs whose copy back may still run
 
 
@@ -180,7 +187,15 @@ def _copy_stream(device):
     return stream
 
 
-def _host_pair(key):
+def _capacity(rows):
+    """Pinned rows for `rows` of activations: the next power of two (at least 64), so
+    that packed batches whose T changes every step reuse a few pairs."""
+    return max(64, 1 << (max(rows, 1) - 1).bit_length())
+
+
+def _host_pair(index, rows, width):
+    """((gate, up) pinned pair, its key) holding at least `rows` x `width`: the free
+    pair of the smallest capacity that fits, else a new one of _capacity(rows)."""
     still = []
     for event, k, pair in _HOST_PENDING:
         if event.query():
@@ -188,12 +203,14 @@ def _host_pair(key):
         else:
             still.append((event, k, pair))
     _HOST_PENDING[:] = still
-    free = _HOST_FREE.setdefault(key, [])
-    if free:
-        return free.pop()
-    shape = key[1:]
-    return (torch.empty(shape, dtype=torch.float16, pin_memory=True),
-            torch.empty(shape, dtype=torch.float16, pin_memory=True))
+    fits = [k for k, free in _HOST_FREE.items()
+            if free and k[0] == index and k[2] == width and k[1] >= rows]
+    if fits:
+        key = min(fits)
+        return _HOST_FREE[key].pop(), key
+    key = (index, _capacity(rows), width)
+    return tuple(torch.empty(key[1:], dtype=torch.float16, pin_memory=True)
+                 for _ in range(2)), key
 
 
 _LAST_OFFLOAD = {}  # device index -> weakref to the newest HostOffload on that device
@@ -213,18 +230,18 @@ class HostOffload:
     def __init__(self, gate, up):
         device = gate.device
         self.device = device
-        self.key = (device.index, gate.shape[0], gate.shape[1])
+        self.rows = gate.shape[0]
         self.prefetched = None  # (gate, up, ready event) once copied back
         with _OFFLOAD_LOCK:
-            self.pair = _host_pair(self.key)
+            self.pair, self.key = _host_pair(device.index, self.rows, gate.shape[1])
             self.previous = _LAST_OFFLOAD.get(device.index)
             _LAST_OFFLOAD[device.index] = weakref.ref(self)
         producer = torch.cuda.current_stream(device)
         copy = _copy_stream(device)
         copy.wait_stream(producer)
         with torch.cuda.stream(copy):
-            self.pair[0].copy_(gate, non_blocking=True)
-            self.pair[1].copy_(up, non_blocking=True)
+            self.pair[0][:self.rows].copy_(gate, non_blocking=True)
+            self.pair[1][:self.rows].copy_(up, non_blocking=True)
             self.stored = torch.cuda.Event()
             self.stored.record(copy)
         # The device tensors may be freed by the caller now: keep their memory
@@ -237,8 +254,8 @@ class HostOffload:
         copy = _copy_stream(self.device)
         with torch.cuda.stream(copy):
             copy.wait_event(self.stored)
-            gate = self.pair[0].to(self.device, non_blocking=True)
-            up = self.pair[1].to(self.device, non_blocking=True)
+            gate = self.pair[0][:self.rows].to(self.device, non_blocking=True)
+            up = self.pair[1][:self.rows].to(self.device, non_blocking=True)
             ready = torch.cuda.Event()
             ready.record(copy)
         _HOST_PENDING.append((ready, self.key, self.pair))
@@ -303,15 +320,110 @@ class _FrozenMLP(torch.autograd.Function):
         return dx.reshape(ctx.shape).to(ctx.input_dtype), None, None, None
 
 
+# Per-layer placement of the saved activations (the reference's knobs,
+# solution/mlp.py:360-430): SOUP_MLP_RECOMPUTE_LAYERS = k recomputes gate / up in the
+# backward of the first k MLP layers; with offload on, SOUP_EXP_OFFLOAD_TAIL = k keeps
+# the last k layers' gate / up on the device (their backward comes first).  A layer's
+# index is its position in prepare_mlp_offload's module order, else its order of first
+# forward among the MLPs sharing its config.
+_LAYER_ORDER = {}  # id(config) -> WeakKeyDictionary(mlp -> index)
+
+
+def _layer_index(mlp):
+    index = getattr(mlp, "_soup_mlp_index", None)
+    if index is not None:
+        return index
+    with _OFFLOAD_LOCK:
+        for key in [k for k, group in _LAYER_ORDER.items() if not group]:
+            del _LAYER_ORDER[key]
+        group = _LAYER_ORDER.setdefault(id(getattr(mlp, "config", None)),
+                                        weakref.WeakKeyDictionary())
+        if mlp not in group:
+            group[mlp] = len(group)
+        return group[mlp]
+
+
+def _layer_count(mlp):
+    count = getattr(mlp, "_soup_mlp_count", None)
+    if count is None:
+        count = getattr(getattr(mlp, "config", None), "num_hidden_layers", None)
+    return count
+
+
+def _env_layers(name, mlp):
+    """The layer count in environment variable `name` (0 when unset), checked against
+    the model's depth."""
+    value = os.environ.get(name, "0")
+    try:
+        k = int(value)
+    except ValueError:
+        raise ValueError(f"{name} must be a non-negative integer, got {value!r}") from None
+    total = _layer_count(mlp)
+    if k < 0 or (total is not None and k > total):
+        raise ValueError(f"{name}={k} must be between 0 and the layer count ({total})")
+    return k
+
+
+def _recompute_layer(mlp):
+    k = _env_layers("SOUP_MLP_RECOMPUTE_LAYERS", mlp)
+    return k > 0 and _layer_index(mlp) < k
+
+
+def _tail_layer(mlp):
+    k = _env_layers("SOUP_EXP_OFFLOAD_TAIL", mlp)
+    if k == 0:
+        return False
+    total = _layer_count(mlp)
+    if total is None:
+        raise ValueError("SOUP_EXP_OFFLOAD_TAIL needs the layer count: call "
+                         "prepare_mlp_offload(model) first")
+    return _layer_index(mlp) >= total - k
+
+
+def _mlp_modules(model):
+    names = ("gate_proj", "up_proj", "down_proj")
+    return [m for m in model.modules() if all(hasattr(m, n) for n in names)]
+
+
+def prepare_mlp_offload(model, max_rows=2048):
+    """Number the model's MLP layers in module order and reserve, per (device, width),
+    one pinned (gate, up) pair of `max_rows` capacity for every layer that will
+    offload (neither recomputed nor kept by the tail policy), so steps of up to
+    `max_rows` tokens allocate no pinned memory (solution/mlp.py:360-385)."""
+    if max_rows < 1:
+        raise ValueError("max_rows must be positive")
+    layers = _mlp_modules(model)
+    for index, layer in enumerate(layers):
+        layer._soup_mlp_index = index
+        layer._soup_mlp_count = len(layers)
+    wanted = {}
+    for layer in layers:
+        device = layer.gate_proj.weight.device
+        if device.type != "cuda" or os.environ.get("SOUP_MLP_RECOMPUTE") == "1":
+            continue
+        if _recompute_layer(layer) or _tail_layer(layer):
+            continue
+        key = (device.index, _capacity(max_rows), layer.gate_proj.out_features)
+        wanted[key] = wanted.get(key, 0) + 1
+    with _OFFLOAD_LOCK:
+        for key, count in wanted.items():
+            free = _HOST_FREE.setdefault(key, [])
+            pending = sum(1 for _, k, _ in _HOST_PENDING if k == key)
+            for _ in range(count - len(free) - pending):
+                free.append(tuple(torch.empty(key[1:], dtype=torch.float16, pin_memory=True)
+                                  for _ in range(2)))
+    return len(layers)
+
+
 def fused_qwen2_mlp(mlp, x, recompute=None, offload=None):
     """Run an eligible frozen NF4 MLP; raise ValueError otherwise (solution/mlp.py:579-612)."""
     if not eligible_mlp(mlp, x):
         raise ValueError("Expected frozen bias-free fp16 NF4 Linear4bit projections on CUDA")
     if recompute is None:
-        recompute = os.environ.get("SOUP_MLP_RECOMPUTE") == "1"
+        recompute = os.environ.get("SOUP_MLP_RECOMPUTE") == "1" or _recompute_layer(mlp)
     if offload is None:
         offload = os.environ.get("SOUP_MLP_OFFLOAD") == "1"
-    offload = bool(offload) and not recompute
+    offload = bool(offload) and not recompute and not _tail_layer(mlp)
     if offload and torch.cuda.is_current_stream_capturing():
         raise ValueError("MLP activation offload cannot be captured in a HIP graph; "
                          "pass offload=False (or unset SOUP_MLP_OFFLOAD) for graph capture")
@@ -336,5 +448,6 @@ def mlp_flops(t, hidden, inter):
     return 7 * 2 * t * hidden * inter
 
 
-__all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "eligible_mlp", "gate_up_swiglu", "down_dx_swiglu",
-           "mlp_forward_2d", "mlp_backward_2d", "mlp_flops", "HostOffload"]
+__all__ = ["fused_qwen2_mlp", "patch_qwen2_mlp_fused", "prepare_mlp_offload", "eligible_mlp",
+           "gate_up_swiglu", "down_dx_swiglu", "mlp_forward_2d", "mlp_backward_2d", "mlp_flops",
+           "HostOffload"]

@@ -125,6 +125,15 @@ def test_offload_keeps_gate_up_on_host_and_matches_bitwise(device):
     mlp = _MLP(128, 320).to(device)
     x = torch.randn((3, 77, 128), device=device, dtype=torch.float16)
     upstream = torch.randn((3, 77, 128), device=device, dtype=torch.float16)
+    # 231 rows take a pair of the 256-row capacity class.
+    key = (device.index if device.index is not None else torch.cuda.current_device(), 256, 320)
+
+    def pooled():
+        torch.cuda.synchronize()
+        return len(fmlp._HOST_FREE.get(key, [])) + sum(1 for _, k, _ in fmlp._HOST_PENDING
+                                                        if k == key)
+
+    before = pooled()
     grads = []
     for offload in (False, True, True):
         xi = x.clone().requires_grad_()
@@ -141,10 +150,7 @@ def test_offload_keeps_gate_up_on_host_and_matches_bitwise(device):
         assert torch.equal(_bits(out), _bits(grads[0][0]))
         assert torch.equal(_bits(grad), _bits(grads[0][1]))
     # The second offloaded step took the pair the first one returned.
-    key = (device.index if device.index is not None else torch.cuda.current_device(), 231, 320)
-    pooled = len(fmlp._HOST_FREE.get(key, [])) + sum(1 for _, k, _ in fmlp._HOST_PENDING
-                                                     if k == key)
-    assert pooled == 1
+    assert pooled() == max(before, 1)
     # Recomputation excludes offload.
     out = fused_qwen2_mlp(mlp, x.clone().requires_grad_(), recompute=True, offload=True)
     assert out.grad_fn.offloaded is None
@@ -175,6 +181,63 @@ def test_offload_prefetches_the_previous_node_during_backward(device):
         results.append((out.detach().clone(), xi.grad.clone()))
     assert torch.equal(_bits(results[0][0]), _bits(results[1][0]))
     assert torch.equal(_bits(results[0][1]), _bits(results[1][1]))
+
+
+class _Stack(torch.nn.Module):
+    def __init__(self, depth):
+        super().__init__()
+        self.layers = torch.nn.ModuleList([_MLP(128, 320) for _ in range(depth)])
+
+    def forward(self, x):
+        for layer in self.layers:
+            x = x + fused_qwen2_mlp(layer, x)
+        return x
+
+
+def test_layer_policy_recompute_offload_and_tail(device, monkeypatch):
+    """Four prepared layers under SOUP_MLP_OFFLOAD=1, SOUP_MLP_RECOMPUTE_LAYERS=1 and
+    SOUP_EXP_OFFLOAD_TAIL=1: layer 0 saves only its input, layers 1-2 keep gate / up
+    in pinned pairs reserved by prepare_mlp_offload (taken, not allocated, for a
+    smaller T), layer 3 keeps them on the device; the step's output and input
+    gradient equal the all-on-device step's bit for bit (solution/mlp.py:362-431)."""
+    from soupsuck_amd import mlp as fmlp
+
+    torch.manual_seed(780)
+    model = _Stack(4).to(device)
+    x = torch.randn((2, 60, 128), device=device, dtype=torch.float16)
+    upstream = torch.randn_like(x)
+
+    xi = x.clone().requires_grad_()
+    ref_out = model(xi)
+    ref_out.backward(upstream)
+    ref_grad = xi.grad.clone()
+    monkeypatch.setenv("SOUP_MLP_OFFLOAD", "1")
+    monkeypatch.setenv("SOUP_MLP_RECOMPUTE_LAYERS", "1")
+    monkeypatch.setenv("SOUP_EXP_OFFLOAD_TAIL", "1")
+    torch.cuda.synchronize()
+    monkeypatch.setattr(fmlp, "_HOST_FREE", {})  # a pool of this test's own
+    monkeypatch.setattr(fmlp, "_HOST_PENDING", [])
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    assert fmlp.prepare_mlp_offload(model, max_rows=256) == 4
+    assert list(fmlp._HOST_FREE) == [(index, 256, 320)]
+    reserved = {p[0].data_ptr() for p in fmlp._HOST_FREE[(index, 256, 320)]}
+    assert len(reserved) == 2
+
+    xi = x.clone().requires_grad_()
+    h = [xi]
+    for layer in model.layers:
+        h.append(h[-1] + fused_qwen2_mlp(layer, h[-1]))
+    nodes = [t.grad_fn.next_functions[1][0] for t in h[1:]]
+    assert all("FrozenMLP" in type(n).__name__ for n in nodes)
+    assert [n.recompute for n in nodes] == [True, False, False, False]
+    assert [n.offloaded is not None for n in nodes] == [False, True, True, False]
+    assert [len(n.saved_tensors) for n in nodes] == [1, 0, 0, 2]
+    # 120 rows fit the reserved 256-row pairs: no pinned allocation.
+    assert all(n.offloaded.pair[0].data_ptr() in reserved for n in nodes[1:3])
+    h[-1].backward(upstream)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(h[-1].detach()), _bits(ref_out.detach()))
+    assert torch.equal(_bits(xi.grad), _bits(ref_grad))
 
 
 def test_rejects_ineligible_modules(device):
