@@ -373,7 +373,10 @@ __device__ __forceinline__ void load_bias(const GemmParams& p, int64_t n0, int w
 // (the values and rounding order of nt_epilogue's direct stores) into
 // [WM][BN + 8], then the workgroup stores them as 16-byte row chunks -- one
 // store instruction per 1 KiB instead of per 128 B.  Needs N, ldc and C
-// 16-byte granular (p.c_vec) and the whole workgroup.
+// 16-byte granular (p.c_vec) and the whole workgroup.  The stores are
+// non-temporal (the kernel does not read its output): for a 990 x 8960
+// output (17.7 MB, written when every tile finishes at once) the 256x256
+// product took 38.5 instead of 40.1 us.
 template <class C, int EPI>
 __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t m0, int64_t n0,
                                                    const NtAcc<C>& acc, unsigned char* smem) {
@@ -432,8 +435,9 @@ __device__ __forceinline__ void nt_epilogue_staged(const GemmParams& p, int64_t 
       const int64_t row = m0 + q * C::WM + row_l;
       const int64_t col = n0 + c8;
       if (row < p.M && col < p.N)
-        *reinterpret_cast<half8*>(reinterpret_cast<half_t*>(p.C) + row * p.ldc + col) =
-            *reinterpret_cast<const half8*>(stage + row_l * G::kPitch + c8);
+        __builtin_nontemporal_store(
+            *reinterpret_cast<const half8*>(stage + row_l * G::kPitch + c8),
+            reinterpret_cast<half8*>(reinterpret_cast<half_t*>(p.C) + row * p.ldc + col));
     }
     __syncthreads();
   }
