@@ -101,3 +101,53 @@ def test_graph_replay_after_rank_workspace_growth(device):
         for i, (a, b) in enumerate(zip(graph_out, eager)):
             assert torch.equal(a, b), f"replay {replay}: output {i} differs"
     del scribble
+
+
+def test_decoder_layer_graph_replay_matches_eager(device):
+    """The whole decoder layer (norms, seven QLoRA projections, RoPE, packed causal
+    attention, SwiGLU, residual adds) captured as one HIP graph, as bench.py times it:
+    every replay, with unrelated eager work and synchronisations between replays,
+    reproduces the eager step bit for bit -- output, input gradient and every LoRA
+    gradient -- on the configs[1] batch."""
+    from soupsuck_amd.layer import DecoderLayer
+
+    lengths = [382, 242, 208, 158]
+    layer = DecoderLayer(device, lengths)
+    t = sum(lengths)
+    gen = torch.Generator(device="cpu").manual_seed(3)
+    h = torch.randn((t, 1536), generator=gen).half().to(device).requires_grad_()
+    g = (torch.randn((t, 1536), generator=gen) * 0.05).half().to(device)
+
+    def grads():
+        out = [h.grad]
+        for q in layer.proj.projections:
+            out += [q.lora_a.grad, q.lora_b.grad]
+        return out
+
+    eager_out = layer.step(h, g).detach().clone()
+    eager_grads = [x.clone() for x in grads()]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            layer.step(h, g)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graph_out = layer.step(h, g)
+    graph_grads = grads()
+
+    noise = torch.randn((512, 512), device=device)
+    for replay in range(3):
+        graph_out.detach().zero_()   # same storage; the replay must rewrite it
+        for x in graph_grads:
+            x.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graph_out.detach(), eager_out), f"replay {replay}: output differs"
+        for i, (a, b) in enumerate(zip(graph_grads, eager_grads)):
+            assert torch.equal(a, b), f"replay {replay}: gradient {i} differs"
+        noise = noise @ noise.t() / 512.0   # unrelated eager work between replays
+        torch.cuda.synchronize()
