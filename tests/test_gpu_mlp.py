@@ -268,3 +268,43 @@ def test_patched_qwen2_mlp_routes_through_the_fused_node(device):
         modeling.Qwen2MLP.forward = original
     torch.testing.assert_close(actual, expected, rtol=2e-3, atol=2e-3)
     assert _lib.load() is not None
+
+
+def test_mlp_graph_replay_matches_eager(device):
+    """The frozen NF4 MLP node forward + backward at the configs[1] shapes (T = 990,
+    1536 -> 8960 -> 1536) captured as one HIP graph: every replay, with unrelated eager
+    work between replays, reproduces the eager output and input gradient bit for bit."""
+    torch.manual_seed(781)
+    mlp = _MLP(HIDDEN, INTER).to(device)
+    x = torch.randn((990, HIDDEN), device=device, dtype=torch.float16).requires_grad_()
+    upstream = torch.randn((990, HIDDEN), device=device, dtype=torch.float16)
+
+    def step():
+        x.grad = None
+        out = fused_qwen2_mlp(mlp, x, recompute=False, offload=False)
+        out.backward(upstream)
+        return out
+
+    eager_out = step().detach().clone()
+    eager_grad = x.grad.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graph_out = step()
+    graph_grad = x.grad
+    noise = torch.randn((512, 512), device=device)
+    for replay in range(3):
+        graph_out.detach().zero_()
+        graph_grad.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graph_out.detach(), eager_out), f"replay {replay}: output differs"
+        assert torch.equal(graph_grad, eager_grad), f"replay {replay}: gradient differs"
+        noise = noise @ noise.t() / 512.0
+        torch.cuda.synchronize()
